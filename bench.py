@@ -1,0 +1,210 @@
+"""Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
+
+One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
+Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
+1,048,576 tokens (65,536 pages, 4 GiB of KV); eight block tables over disjoint
+pages rotate across steps, so each step reads 512 MiB the previous seven did
+not touch and the 256 MB MALL cannot serve a repeated working set. Inputs are
+resident in HBM before timing starts.
+
+Printed (rank 0, one JSON line): value = KV-read GB/s of the whole job,
+roofline of the decode kernel (algorithmic KV bytes / average kernel time from
+HIP events on the launch stream, against 8 TB/s), the heterogeneous-batch
+makespan of the static grid and the ticket work queue (W = 2 x CU), and the CPU
+baseline (the oracle's fp32 port of the reference CPU loop, OpenMP, on a
+bounded sample, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sched-pass_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--no-hetero", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--tables", type=int, default=8)
+    return p.parse_args()
+
+
+def time_launches(fn, steps, stream):
+    """Per-launch HIP event pairs on `stream`; returns (mean kernel ms, list)."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fn(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return sum(ms) / len(ms), ms
+
+
+def bench_uniform(args, torch, sched_pd, workloads):
+    b = workloads.workload("llama3_8b_uniform", seed=0, n_tables=args.tables)
+    out = torch.empty(64, 32, 128, dtype=torch.bfloat16, device="cuda")
+    launches = [sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], bt, b["ctx_lens"], out=out)
+                for bt in b["block_tables"]]
+    kind = sched_pd.kernel_kind(launches[0])
+    stream = torch.cuda.current_stream()
+    step = lambda i: sched_pd.launch(launches[i % len(launches)], stream)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = ev0.elapsed_time(ev1)
+    kern_ms, per = time_launches(step, args.steps, stream)
+    kv = b["kv_bytes"]
+    return {
+        "kv_bytes": kv, "ms_per_step": wall_ms / args.steps, "kernel_ms": kern_ms,
+        "kernel_ms_min": min(per), "kernel": kind, "occupancy": sched_pd.occupancy(launches[0]),
+    }
+
+
+def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu):
+    import numpy as np
+    b = workloads.workload("llama3_8b_hetero", seed=0)
+    n = 256 * 8
+    plane = SchedPlane(max_tasks=n)
+    order = np.argsort(-b["urgency"], kind="stable").astype(np.int32)  # pi by urgency q
+    plane.install_order(order, n)
+    plane.set_num_tasks(n)
+    plane.push()
+    W = 2 * cu
+    out = torch.empty(256, 32, 128, dtype=torch.bfloat16, device="cuda")
+    a_static = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                   b["ctx_lens"], out=out, plane=plane, workers=0)
+    a_wq = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                               b["ctx_lens"], out=out, plane=plane, workers=W)
+    stream = torch.cuda.current_stream()
+    plane.reset_queue(W)
+    res = {}
+    for name, a in (("static", a_static), ("ticket_wq", a_wq)):
+        for _ in range(3):
+            sched_pd.launch(a, stream)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):  # min over repeats of 10 back-to-back launches
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(10):
+                sched_pd.launch(a, stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 10)
+        res[name] = best * 1000.0
+    # per-task residency of one work-queue step from the timer rows
+    plane.clear_timer()
+    sched_pd.launch(a_wq, stream)
+    torch.cuda.synchronize()
+    cyc = plane.read_timer()[:n].numpy()
+    kv = b["kv_bytes"]
+    return {
+        "static_us": round(res["static"], 2), "ticket_wq_us": round(res["ticket_wq"], 2),
+        "cut_pct": round(100.0 * (res["static"] - res["ticket_wq"]) / res["static"], 2),
+        "workers": W, "tasks": n, "kv_bytes": kv,
+        "wq_kv_gbs": round(kv / (res["ticket_wq"] * 1e-6) / 1e9, 1),
+        "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
+                             "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())},
+    }
+
+
+def cpu_baseline(torch, workloads):
+    """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
+    2 of the 64 requests of the uniform workload, timed on this host."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    b = workloads.make_batch(np.full(2, 2048), num_q_heads=32, num_kv_heads=8, seed=3,
+                             device="cuda")
+    host = {k: b[k].cpu() for k in ("q", "k_pool", "v_pool", "block_table", "ctx_lens")}
+    threads = len(os.sched_getaffinity(0))
+    oracle.decode(host["q"], host["k_pool"], host["v_pool"], host["block_table"],
+                  host["ctx_lens"], precision=oracle.F32, threads=threads)  # warm
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.decode(host["q"], host["k_pool"], host["v_pool"], host["block_table"],
+                      host["ctx_lens"], precision=oracle.F32, threads=threads)
+        best = min(best, time.perf_counter() - t0)
+    kv = b["kv_bytes"]
+    return {"value": round(kv / best / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"2 of 64 requests x 2048 tokens (KV {kv >> 20} MiB), fp32 oracle port "
+                      f"of the reference CPU loop, {threads} OpenMP threads, min of 3: "
+                      f"{best * 1e3:.1f} ms"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              f"the decode path shards by request / kv-head with no exchange, see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import sched_pd
+    import workloads
+    from sched_rt import SchedPlane
+
+    torch.cuda.set_device(0)
+    cu = sched_pd.cu_count()
+    u = bench_uniform(args, torch, sched_pd, workloads)
+    gbs = u["kv_bytes"] / (u["ms_per_step"] * 1e-3) / 1e9
+    kern_gbs = u["kv_bytes"] / (u["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "paged-decode KV-read GB/s (% HBM peak) + hetero-batch makespan µs",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(u["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1)/sqrt(128) Q/K/V, random page permutation)",
+        "config": {"workload": "llama3_8b_uniform", "requests": 64, "ctx": 2048,
+                   "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page": 16,
+                   "pool_tokens": 1048576, "rotating_tables": args.tables,
+                   "levers": "null (stock)", "parallelism": "1 GPU"},
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": f"decode_{u['kernel']}",
+                     "kernel_us": round(u["kernel_ms"] * 1e3, 2),
+                     "kernel_us_min": round(u["kernel_ms_min"] * 1e3, 2),
+                     "bytes_per_launch": u["kv_bytes"], "wg_per_cu": u["occupancy"]},
+    }
+    if not args.no_hetero:
+        line["hetero_makespan"] = bench_hetero(torch, sched_pd, workloads, SchedPlane, cu)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, workloads)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

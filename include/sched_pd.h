@@ -1,0 +1,241 @@
+/* sched_pd.h -- C ABI of the MI355X (gfx950) paged-KV decode hot path with the
+ * sched-pass scheduling levers built into hand-written HIP kernels.
+ *
+ * Three groups of entry points, all plain C (no HIP or torch types):
+ *
+ *   1. The runtime contract of reference runtime/sched_rt.h:54-275: the
+ *      SchedPolicyRow / SchedCtrl layout with its pinned offsets, and the
+ *      sched_rt_* host API (init/arm, disarm, setters, push, queue reset,
+ *      timer read/clear). The reference defines these `static inline` in a
+ *      header; here they are exported from libschedpd.so.
+ *   2. The decode launcher: sched_paged_decode(const SchedDecodeArgs*, stream).
+ *      One call runs one decode step over a paged batch, with the five levers
+ *      (pi, policy/prefetch, shed, timer, ticket work queue) read from the
+ *      table pointers in the argument block. A NULL table is the stock path.
+ *   3. The reference's JIT-kernel launcher, same name and signature:
+ *      launch_paged_softmax (reference python/kernels/paged_softmax.cu:47-54)
+ *      and paged_softmax_occupancy (:61-67).
+ *
+ * Errors: entry points that return int return 0 on success and a nonzero
+ * hipError_t code on failure; entry points returning bool return false. In
+ * both cases a line "[sched_rt] <call> failed: <reason>" or
+ * "[sched_pd] <reason>" goes to stderr, and sched_pd_last_error() returns the
+ * same text. Nothing aborts.
+ */
+#ifndef SCHED_PD_H
+#define SCHED_PD_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- 1. runtime contract (reference runtime/sched_rt.h) ------------------ */
+
+/* Rows in the order / ctrl / timer tables of the C runtime. Same knob and
+ * default as reference runtime/sched_rt.h:50-52. */
+#ifndef SCHED_MAX_TASKS
+#define SCHED_MAX_TASKS 4096
+#endif
+
+/* Per-task policy row, 8 bytes (reference runtime/sched_rt.h:54-59). */
+typedef struct SchedPolicyRow {
+  float q;        /* urgency, >= 0 */
+  uint16_t tau;   /* shed budget in tokens (0 = unbounded) */
+  uint8_t hint;   /* SCHED_HINT_* */
+  uint8_t _pad;
+} SchedPolicyRow;
+
+/* Per-step control block (reference runtime/sched_rt.h:61-74). The kernels
+ * read num_tasks, lambda[0], flags, order_size and the rows; generation is
+ * written by push and read by no kernel. */
+typedef struct SchedCtrl {
+  uint32_t generation;
+  uint32_t num_tasks;   /* work-queue bound; 0 = stock static path */
+  float lambda[4];      /* shadow prices {bw, l2, smem, comp}; kernels read [0] */
+  uint32_t flags;       /* bit0 = SCHED_CTRL_FLAG_TIMER_OFF */
+  uint32_t order_size;  /* task count the installed pi was built for; 0 = unchecked */
+  SchedPolicyRow task[SCHED_MAX_TASKS];
+} SchedCtrl;
+
+#define SCHED_CTRL_FLAG_TIMER_OFF 1u
+
+/* Byte offsets (reference lib/SchedUtil.h:96-123, python/sched_rt.py:52-61). */
+#define SCHED_CTRL_NUM_TASKS_OFF 4
+#define SCHED_CTRL_LAMBDA_OFF 8
+#define SCHED_CTRL_FLAGS_OFF 24
+#define SCHED_CTRL_ORDER_SIZE_OFF 28
+#define SCHED_CTRL_ROWS_OFF 32
+#define SCHED_CTRL_ROW_SIZE 8
+#define SCHED_CTRL_ROW_TAU_OFF 4
+#define SCHED_CTRL_ROW_HINT_OFF 6
+
+/* Hints (reference lib/SchedUtil.h:119-122). */
+#define SCHED_HINT_AUTO 0   /* urgent iff q*dT - lambda_bw*dR - H > 0 */
+#define SCHED_HINT_URGENT 1 /* deep KV prefetch (pf_dist pages in flight) */
+#define SCHED_HINT_POLITE 2 /* streaming (non-temporal) KV loads */
+
+#ifdef __cplusplus
+static_assert(offsetof(SchedCtrl, num_tasks) == SCHED_CTRL_NUM_TASKS_OFF, "sched ABI: num_tasks");
+static_assert(offsetof(SchedCtrl, lambda) == SCHED_CTRL_LAMBDA_OFF, "sched ABI: lambda");
+static_assert(offsetof(SchedCtrl, flags) == SCHED_CTRL_FLAGS_OFF, "sched ABI: flags");
+static_assert(offsetof(SchedCtrl, order_size) == SCHED_CTRL_ORDER_SIZE_OFF, "sched ABI: order_size");
+static_assert(offsetof(SchedCtrl, task) == SCHED_CTRL_ROWS_OFF, "sched ABI: rows offset");
+static_assert(sizeof(SchedPolicyRow) == SCHED_CTRL_ROW_SIZE, "sched ABI: row size");
+static_assert(offsetof(SchedPolicyRow, tau) == SCHED_CTRL_ROW_TAU_OFF, "sched ABI: row tau");
+static_assert(offsetof(SchedPolicyRow, hint) == SCHED_CTRL_ROW_HINT_OFF, "sched ABI: row hint");
+#endif
+
+/* Replaces reference runtime/sched_rt.h:121-189 (sched_rt_init): allocate the
+ * tables once (identity pi, neutral ctrl, zeroed device-memory timer, queue),
+ * arm the __sched_* device slots, publish /tmp/sched_rt_<pid>.json.
+ * Idempotent; re-arming after disarm reuses the buffers. */
+bool sched_rt_init(void);
+/* runtime/sched_rt.h:192-203: null the slots, keep the buffers. */
+bool sched_rt_disarm(void);
+/* runtime/sched_rt.h:206-212: write order[0..n) (n clamped to the table size),
+ * synchronously. */
+bool sched_rt_set_order(const int32_t *order, unsigned n);
+/* runtime/sched_rt.h:214-249: host-mirror setters; effective at the next push. */
+void sched_rt_set_lambda(float bw, float l2, float smem, float comp);
+void sched_rt_set_task(unsigned i, float q, uint16_t tau, uint8_t hint);
+void sched_rt_set_tau(unsigned i, uint16_t tau);
+void sched_rt_set_num_tasks(uint32_t n);
+void sched_rt_set_order_size(uint32_t n);
+void sched_rt_set_timer_enabled(bool on);
+/* runtime/sched_rt.h:252-257: generation++, then copy the whole struct. */
+bool sched_rt_push_ctrl(void);
+/* runtime/sched_rt.h:261-265: prime the ticket counter to `workers`. */
+bool sched_rt_queue_reset(uint32_t workers);
+/* runtime/sched_rt.h:267-275: timer row read / clear. The rows live in device
+ * memory, so these synchronise with the device. */
+unsigned long long sched_rt_timer(unsigned i);
+void sched_rt_timer_clear(void);
+
+/* Introspection, no counterpart in the reference (its tables are static
+ * globals of the including translation unit): the device addresses the
+ * __sched_* slots hold right now (0 when disarmed), read back from the device
+ * symbols. slots[0..3] = order, ctrl, timer, queue. Returns false on error. */
+bool sched_rt_slots(uint64_t slots[4]);
+/* Bulk timer read, no counterpart in the reference (its rows are host-mapped
+ * and read in place): copies rows [0, n) (n clamped) into dst. */
+bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
+
+/* ---- 2. decode launcher --------------------------------------------------- */
+
+#define SCHED_PD_ABI_VERSION 1u
+
+/* mode */
+#define SCHED_PD_SOFTMAX 0u /* out[r][hq][:] = softmax(scale*q.K^T) V   (online softmax) */
+#define SCHED_PD_LINEAR 1u  /* out[r][hkv][:] = sum_t w[t] V[t]         (linear contraction) */
+
+/* dtypes */
+#define SCHED_PD_F32 0u
+#define SCHED_PD_BF16 1u
+#define SCHED_PD_FP8_E4M3 2u /* OCP e4m3fn, per-(page, kv-head) fp32 scales */
+
+/* tau scope: prefix = the first tau tokens of the request; per_page = the first
+ * tau tokens of every page, the counter of the reference fixtures' woven
+ * innermost loop (test/paged_decode.cu:103,136) */
+#define SCHED_PD_TAU_PREFIX 0u
+#define SCHED_PD_TAU_PER_PAGE 1u
+
+/* flags */
+#define SCHED_PD_FLAG_RT_TABLES 0x1u    /* take order/ctrl/timer/queue from the C runtime's slots */
+#define SCHED_PD_FLAG_WALLCLOCK 0x2u    /* timer counts s_memrealtime (100 MHz) instead of s_memtime */
+#define SCHED_PD_FLAG_FORCE_VALU 0x4u   /* use the VALU kernel even where the MFMA kernel applies */
+#define SCHED_PD_FLAG_CTX_IN_PAGES 0x8u /* ctx_lens counts full pages, not tokens */
+#define SCHED_PD_FLAG_SHED_LOADS 0x10u  /* load shed tokens and mask them (reference weave,
+                                           lib/SchedWeave.cpp:646-651) instead of skipping
+                                           the pages past a prefix budget; same output */
+
+/* One decode step. Element (page, kv-head h, token t, dim j) of the pools:
+ *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
+ *   V: v_pool + page*v_page_stride + h*v_head_stride + t*v_tok_stride + j*v_dim_stride
+ * (strides in elements). Request r's page b is block_table[r*bt_stride + b],
+ * or block_table[page_indptr[r] + b] when page_indptr is not NULL.
+ * Task id = r*num_kv_heads + h; the lever tables are indexed by task. */
+typedef struct SchedDecodeArgs {
+  uint32_t abi_version; /* SCHED_PD_ABI_VERSION */
+  uint32_t mode;
+  uint32_t kv_dtype;
+  uint32_t q_dtype;     /* F32 or BF16 (softmax mode) */
+  uint32_t o_dtype;     /* F32 or BF16 */
+  uint32_t num_requests;
+  uint32_t num_q_heads;  /* softmax: multiple of num_kv_heads */
+  uint32_t num_kv_heads;
+  uint32_t head_dim;     /* 32, 64 or 128 */
+  uint32_t page_size;    /* tokens per page, multiple of 16, <= 256 */
+  uint32_t bt_stride;
+  uint32_t tau_scope;
+  uint32_t workers;      /* 0 = static grid (one workgroup per task); W = ticket queue */
+  uint32_t pf_dist;      /* urgent tasks keep this many pages in flight (0 = default 4) */
+  uint32_t flags;
+  uint32_t max_tasks;    /* rows of order/ctrl/timer; task ids >= max_tasks get no levers */
+  float sm_scale;        /* 0 = 1/sqrt(head_dim) */
+  float policy_dT, policy_dR, policy_H; /* urgent iff q*dT - lambda_bw*dR - H > 0 */
+  uint32_t lin_w_period; /* linear mode: w index = pos % period (0 = pos) */
+  uint32_t _reserved;
+  const void *q;         /* [num_requests][num_q_heads][head_dim] */
+  void *out;             /* softmax: [R][Hq][d]; linear: [R][Hkv][d] */
+  const void *k_pool;
+  const void *v_pool;
+  int64_t k_page_stride, k_head_stride, k_tok_stride;
+  int64_t v_page_stride, v_head_stride, v_tok_stride, v_dim_stride;
+  const float *k_scale;  /* fp8: [num_pages*num_kv_heads], index page*Hkv + h */
+  const float *v_scale;
+  const int32_t *block_table;
+  const int32_t *page_indptr; /* NULL = 2-D block table */
+  const int32_t *ctx_lens;    /* [num_requests] tokens (or pages, see flags) */
+  const float *lin_w;         /* linear mode weights */
+  /* lever tables; NULL = that lever's stock behaviour */
+  const int32_t *order;       /* i32[max_tasks] pi */
+  const void *ctrl;           /* SchedCtrl layout, rows[max_tasks] */
+  unsigned long long *timer;  /* u64[max_tasks] residency accumulators */
+  uint32_t *queue;            /* ticket counter */
+} SchedDecodeArgs;
+
+/* Fill *a with defaults (ABI version, F32, prefix tau, dT=dR=1, H=0.25,
+ * max_tasks=SCHED_MAX_TASKS, everything else 0/NULL). */
+void sched_pd_default_args(SchedDecodeArgs *a);
+
+/* Run one decode step on `stream` (a hipStream_t; NULL = default stream).
+ * Asynchronous. Replaces the launch sites of the reference's decode kernels
+ * (test/paged_decode.cu:207-213, test/hetero_batch.cu:130-134,
+ * python/kernels/paged_softmax.cu:47-54). */
+int sched_paged_decode(const SchedDecodeArgs *a, void *stream);
+
+/* Workgroups per CU of the kernel `a` selects (0 = unknown). Counterpart of
+ * reference paged_softmax_occupancy (python/kernels/paged_softmax.cu:61-67). */
+int sched_paged_decode_occupancy(const SchedDecodeArgs *a);
+
+/* Which kernel `a` selects: 0 = VALU, 1 = MFMA, -1 = invalid args. */
+int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
+
+/* Compute-unit count of the current device (0 on error). */
+int sched_pd_cu_count(void);
+
+/* Last error text of this thread ("" if none). */
+const char *sched_pd_last_error(void);
+
+/* ---- 3. reference JIT-kernel launcher ------------------------------------ */
+
+/* reference python/kernels/paged_softmax.cu:47-54: fp32 online-softmax decode,
+ * one task per request, head dim 32, page layout [token][64] with K in
+ * elements 0..31 and V in 32..63, score scale 0.125, nbl[seq] full pages per
+ * request. Levers come from the C runtime's slots (sched_rt_init); tau counts
+ * tokens within each page, as the reference's woven innermost loop does. */
+void launch_paged_softmax(const void *kv, const void *bt, const void *nbl,
+                          const void *q, void *out, int nseq, int bt_stride,
+                          int page_tokens, void *stream);
+/* python/kernels/paged_softmax.cu:61-67: workgroups per CU, 0 = unknown. */
+int paged_softmax_occupancy(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCHED_PD_H */

@@ -1,0 +1,99 @@
+// common.h -- kernel parameter block and small device helpers shared by the
+// decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "levers.h"
+
+namespace schedpd {
+
+// Everything a decode kernel reads, passed by value as the kernel argument.
+struct KParams {
+  LeverTables L;
+  const void *q;
+  void *out;
+  const void *k_pool;
+  const void *v_pool;
+  int64_t kps, khs, kts;      // K strides (elements): page, head, token
+  int64_t vps, vhs, vts, vds; // V strides (elements): page, head, token, dim
+  const float *k_scale;
+  const float *v_scale;
+  const int32_t *bt;
+  const int32_t *indptr;
+  const int32_t *ctx;
+  const float *lin_w;
+  uint32_t R, Hq, Hkv, G;
+  uint32_t ps, bt_stride, tau_scope;
+  uint32_t q_f32, o_f32, ctx_in_pages, shed_loads, lin_w_period;
+  float scale_log2; // softmax scale * log2(e): scores live in the exp2 domain
+};
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kMInit = -1e30f; // running-max start value (test/paged_decode.cu:94)
+
+__device__ __forceinline__ int32_t page_of(const KParams &P, uint32_t r, uint32_t b) {
+  return P.indptr ? P.bt[P.indptr[r] + b] : P.bt[(int64_t)r * P.bt_stride + b];
+}
+
+__device__ __forceinline__ uint32_t ctx_tokens(const KParams &P, uint32_t r) {
+  uint32_t c = (uint32_t)P.ctx[r];
+  return P.ctx_in_pages ? c * P.ps : c;
+}
+
+// Shed keep test for token position t of a request (budget from task_policy):
+// prefix scope counts t, per-page scope counts t's offset in its page.
+__device__ __forceinline__ bool keep_pos(const KParams &P, uint32_t budget, uint32_t t) {
+  uint32_t ctr = P.tau_scope == SCHED_PD_TAU_PER_PAGE ? t % P.ps : t;
+  return ctr < budget;
+}
+
+// Tokens that need loading: with a prefix budget the pages past it hold only
+// masked tokens, whose contribution is exactly zero, so they are not read
+// (unless shed_loads asks for the reference's load-and-mask behaviour).
+__device__ __forceinline__ uint32_t load_extent(const KParams &P, uint32_t n, uint32_t budget) {
+  if (P.tau_scope == SCHED_PD_TAU_PREFIX && !P.shed_loads && budget < n)
+    return budget;
+  return n;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// OCP e4m3fn decode by bit construction (1 sign, 4 exponent bits bias 7,
+// 3 mantissa bits; S.1111.111 is NaN, there is no infinity).
+__device__ __forceinline__ float fp8e4m3_to_f32(uint32_t b) {
+  uint32_t s = (b & 0x80u) << 24, e = (b >> 3) & 15u, m = b & 7u;
+  float v;
+  if (e == 0u)
+    v = (float)m * 0.001953125f; // m * 2^-9
+  else
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  if (e == 15u && m == 7u)
+    v = __builtin_nanf("");
+  return __uint_as_float(__float_as_uint(v) | s);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u)
+    return (uint16_t)((u >> 16) | 0x40u); // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ void store_out(const KParams &P, int64_t idx, float v) {
+  if (P.o_f32)
+    static_cast<float *>(P.out)[idx] = v;
+  else
+    static_cast<uint16_t *>(P.out)[idx] = f32_to_bf16_rne(v);
+}
+
+__device__ __forceinline__ float load_q(const KParams &P, int64_t idx) {
+  return P.q_f32 ? static_cast<const float *>(P.q)[idx]
+                 : bf16_bits_to_f32(static_cast<const uint16_t *>(P.q)[idx]);
+}
+
+} // namespace schedpd

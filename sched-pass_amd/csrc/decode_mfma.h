@@ -1,0 +1,367 @@
+// decode_mfma.h -- the GQA decode kernel on the CDNA4 matrix cores:
+// bf16 or fp8-e4m3fn KV, head dim 128, page size 16, up to 16 q-heads per
+// kv-head (one MFMA column block), bf16 Q.
+//
+// Layout it reads (one (page, kv-head) chunk each for K and V):
+//   K: 16 token rows x 128 dims, dims contiguous (row stride k_tok_stride);
+//   V: 128 dim rows x 16 tokens, tokens contiguous (v_tok_stride 1, row stride
+//      v_dim_stride) -- the per-page d-major V of vLLM's paged cache.
+// With these, both MFMA operands load straight from HBM into registers:
+//
+//   QK  S^T[16 tok x 16 head] = K[16 x 128] . Q^T[128 x 16]
+//       4 x v_mfma_f32_16x16x32_bf16; A = K rows (lane: token lane%16,
+//       8 dims at slot lane/16 -> one 16-byte load), B = Q (held all task).
+//   The accumulator lane layout (head = lane%16, tokens 4*(lane/16)+0..3) is
+//   exactly the B-operand layout of v_mfma_f32_16x16x16_bf16, so after the
+//   online-softmax update the probabilities feed PV with no data movement:
+//   PV  O^T[128 x 16 head] += V^T[128 x 16 tok] . P^T[16 tok x 16 head]
+//       8 x v_mfma_f32_16x16x16_bf16; A = V^T rows (lane: dim 16*blk+lane%16,
+//       tokens 4*(lane/16)..+3 -> one 8-byte load; 512 contiguous bytes per
+//       wave instruction).
+//
+// A workgroup of NW waves runs one task = (request, kv-head); wave w streams
+// a contiguous slice of the task's pages with DEPTH pages of loads in flight
+// (register ring), and the wave states merge in LDS in fixed order. Nothing
+// in the arithmetic depends on scheduling, so pi, the work queue and the
+// prefetch depth leave every output bit unchanged.
+//
+// Policy lever: urgent tasks stream with DEPTH_U pages in flight instead of
+// DEPTH_S (deeper KV prefetch); polite tasks use non-temporal loads.
+// fp8: values convert exactly to bf16; the per-(page, head) K scale multiplies
+// the score and the V scale multiplies p before PV, so no element is scaled.
+#pragma once
+
+#include "common.h"
+
+namespace schedpd {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
+
+template <bool FP8> struct PageRegs;
+template <> struct PageRegs<false> {
+  u32x4_t k[4]; // 4 x 8 bf16 K
+  u32x2_t v[8]; // 8 x 4 bf16 V^T
+};
+template <> struct PageRegs<true> {
+  u32x4_t k[2]; // 2 x 16 fp8 K
+  unsigned v[8]; // 8 x 4 fp8 V^T
+};
+
+template <bool NT, typename T> __device__ __forceinline__ T gload(const T *p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+// Dim slot of element e of lane-group g4 in QK step kb. bf16: one 16-byte
+// load per step. fp8: one 16-byte load covers steps 2c and 2c+1. Q uses the
+// same map, so the dot product runs over the same dims either way.
+__device__ __forceinline__ uint32_t qk_dim(bool fp8, uint32_t kb, uint32_t g4) {
+  return fp8 ? 64u * (kb >> 1) + 16u * g4 + 8u * (kb & 1u) : 32u * kb + 8u * g4;
+}
+
+// Two floats holding bf16-exact values -> one dword of two bf16 (truncation
+// is exact for them).
+__device__ __forceinline__ unsigned pack_bf16_exact(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+// Round-to-nearest-even pair conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(unsigned, v);
+}
+
+// x from lane (lane ^ 16) / (lane ^ 32), via the LDS crossbar with the byte
+// address precomputed once per lane.
+__device__ __forceinline__ float bperm(float x, int addr) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(x)));
+}
+
+// 4 fp8 bytes -> 4 bf16 (exact), as two dwords.
+__device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
+  auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  u32x2_t r;
+  r.x = pack_bf16_exact(lo[0], lo[1]);
+  r.y = pack_bf16_exact(hi[0], hi[1]);
+  return r;
+}
+
+struct MfmaTask {
+  uint32_t r, h, n, budget, p_begin, p_end;
+  int xor16, xor32;     // ds_bpermute byte addresses of lanes lane^16, lane^32
+  const uint8_t *kbase; // K pool bytes + per-lane offset
+  const uint8_t *vbase;
+  int64_t kpage_bytes, khead_bytes, vpage_bytes, vhead_bytes;
+};
+
+struct MfmaState {
+  float m, lsum;
+  f32x4_t acc[8];
+  bf16x8_t qop[4];
+};
+
+template <bool FP8, bool NT>
+__device__ __forceinline__ void issue_page(const MfmaTask &T, int32_t page, PageRegs<FP8> &B) {
+  const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes;
+  const uint8_t *vp = T.vbase + (int64_t)page * T.vpage_bytes + T.vhead_bytes;
+  if constexpr (!FP8) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+      B.v[blk] = gload<NT>(reinterpret_cast<const u32x2_t *>(vp + 512 * blk));
+  } else {
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+      B.k[cc] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * cc));
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+      B.v[blk] = gload<NT>(reinterpret_cast<const unsigned *>(vp + 256 * blk));
+  }
+}
+
+template <bool FP8>
+__device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T, MfmaState &S,
+                                             const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
+                                             uint32_t g4) {
+  // QK
+  f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    bf16x8_t a;
+    if constexpr (!FP8) {
+      a = __builtin_bit_cast(bf16x8_t, B.k[kb]);
+    } else {
+      const u32x4_t raw = B.k[kb >> 1];
+      const unsigned w0 = (kb & 1) ? raw.z : raw.x, w1 = (kb & 1) ? raw.w : raw.y;
+      const u32x2_t lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
+      const u32x4_t packed = {lo.x, lo.y, hi.x, hi.y};
+      a = __builtin_bit_cast(bf16x8_t, packed);
+    }
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, S.qop[kb], sc, 0, 0, 0);
+  }
+
+  float kscale = P.scale_log2, vs = 1.f;
+  if constexpr (FP8) {
+    if (P.k_scale)
+      kscale *= P.k_scale[(int64_t)page * P.Hkv + T.h];
+    if (P.v_scale)
+      vs = P.v_scale[(int64_t)page * P.Hkv + T.h];
+  }
+
+  // Online softmax over this page (exp2 domain).
+  const uint32_t pos0 = pidx * 16u;
+  const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
+  const bool full = pos0 + 16u <= T.n &&
+                    (T.budget == 0xFFFFFFFFu || (prefix ? pos0 + 16u <= T.budget : T.budget >= 16u));
+  float s[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    s[v] = sc[v] * kscale;
+  if (!full) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t i = 4u * g4 + v; // token in page (page size 16)
+      const uint32_t t = pos0 + i;
+      if (!(t < T.n && (prefix ? t : i) < T.budget))
+        s[v] = kNegInf;
+    }
+  }
+  float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  pm = fmaxf(pm, bperm(pm, T.xor16));
+  pm = fmaxf(pm, bperm(pm, T.xor32));
+  const float mnew = fmaxf(S.m, pm);
+  if (__builtin_amdgcn_ballot_w64(mnew > S.m)) {
+    const float c = __builtin_amdgcn_exp2f(S.m - mnew);
+    S.lsum *= c;
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+      S.acc[blk] *= c;
+  }
+  S.m = mnew;
+  float p[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    p[v] = __builtin_amdgcn_exp2f(s[v] - mnew);
+  S.lsum += (p[0] + p[1]) + (p[2] + p[3]);
+  u32x2_t pk;
+  if constexpr (FP8) {
+    pk.x = pack_bf16_rne(p[0] * vs, p[1] * vs);
+    pk.y = pack_bf16_rne(p[2] * vs, p[3] * vs);
+  } else {
+    pk.x = pack_bf16_rne(p[0], p[1]);
+    pk.y = pack_bf16_rne(p[2], p[3]);
+  }
+  const s16x4_t pop = __builtin_bit_cast(s16x4_t, pk);
+
+  // PV
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) {
+    s16x4_t a;
+    if constexpr (!FP8)
+      a = __builtin_bit_cast(s16x4_t, B.v[blk]);
+    else
+      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(B.v[blk]));
+    S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop, S.acc[blk], 0, 0, 0);
+  }
+}
+
+// Page ids of this wave's slice, 64 at a time in one VGPR (lane j holds the
+// id of slice page 64*blk + j).
+__device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T, uint32_t blk,
+                                            uint32_t lane) {
+  const uint32_t idx = T.p_begin + 64u * blk + lane;
+  return idx < T.p_end ? page_of(P, T.r, idx) : 0;
+}
+
+template <bool FP8, int DEPTH, bool NT>
+__device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
+                                             uint32_t lane, uint32_t g4) {
+  const int npg = (int)T.p_end - (int)T.p_begin;
+  if (npg <= 0)
+    return;
+  int32_t ptA = load_ids(P, T, 0, lane);
+  int32_t ptB = npg > 64 ? load_ids(P, T, 1, lane) : 0;
+  int blk = 0, li = 0;
+  auto next_id = [&]() -> int32_t {
+    if ((li >> 6) != blk) {
+      ptA = ptB;
+      ++blk;
+      ptB = (blk + 1) * 64 < npg ? load_ids(P, T, blk + 1, lane) : 0;
+    }
+    const int32_t id = __builtin_amdgcn_readlane(ptA, li & 63);
+    ++li;
+    return id;
+  };
+
+  PageRegs<FP8> buf[DEPTH];
+  int32_t pid[DEPTH];
+#pragma unroll
+  for (int s = 0; s < DEPTH; ++s)
+    if (s < npg) {
+      pid[s] = next_id();
+      issue_page<FP8, NT>(T, pid[s], buf[s]);
+    }
+  for (int it = 0; it < npg; it += DEPTH) {
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) {
+      const int j = it + s;
+      if (j < npg) {
+        compute_page<FP8>(P, T, S, buf[s], pid[s], T.p_begin + (uint32_t)j, g4);
+        if (j + DEPTH < npg) {
+          pid[s] = next_id();
+          issue_page<FP8, NT>(T, pid[s], buf[s]);
+        }
+      }
+    }
+  }
+}
+
+template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U>
+__global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
+  __shared__ float s_acc[NW][GMAX][128];
+  __shared__ float s_m[NW][GMAX];
+  __shared__ float s_l[NW][GMAX];
+  const uint32_t lane = threadIdx.x & 63u;
+  // Wave index as a scalar: everything per-wave (page slice, loop bounds,
+  // page ids) then stays in SGPRs with uniform branches.
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t c16 = lane & 15u, g4 = lane >> 4;
+  const bool toff = timer_off_latched(P.L);
+  constexpr uint32_t EB = FP8 ? 1u : 2u; // bytes per KV element
+
+  run_tasks(P.L, [&](uint32_t task) {
+    if (task >= P.L.ntasks)
+      return;
+    const unsigned long long t0 = read_clock(P.L.wallclock);
+    MfmaTask T;
+    T.r = task / P.Hkv;
+    T.h = task % P.Hkv;
+    const TaskPolicy pol = task_policy(P.L, task);
+    T.n = ctx_tokens(P, T.r);
+    T.budget = pol.budget;
+    const uint32_t npages = (load_extent(P, T.n, pol.budget) + 15u) / 16u;
+    const uint32_t per = (npages + NW - 1) / NW;
+    T.p_begin = min(npages, w * per);
+    T.p_end = min(npages, T.p_begin + per);
+    T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
+    T.vbase = static_cast<const uint8_t *>(P.v_pool) + (int64_t)c16 * P.vds * EB + 4u * g4 * EB;
+    T.xor16 = (int)((lane ^ 16u) << 2);
+    T.xor32 = (int)((lane ^ 32u) << 2);
+    T.kpage_bytes = P.kps * EB;
+    T.khead_bytes = P.khs * EB * T.h;
+    T.vpage_bytes = P.vps * EB;
+    T.vhead_bytes = P.vhs * EB * T.h;
+
+    MfmaState S;
+    S.m = kMInit;
+    S.lsum = 0.f;
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+      S.acc[blk] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t G = P.G;
+    const int64_t qrow = ((int64_t)T.r * P.Hq + T.h * G + c16) * 128;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      u32x4_t qv = {0u, 0u, 0u, 0u};
+      if (c16 < G) {
+        const uint32_t d0 = qk_dim(FP8, kb, g4);
+        if (P.q_f32) {
+          const float *qf = static_cast<const float *>(P.q) + qrow + d0;
+          qv = u32x4_t{pack_bf16_rne(qf[0], qf[1]), pack_bf16_rne(qf[2], qf[3]),
+                       pack_bf16_rne(qf[4], qf[5]), pack_bf16_rne(qf[6], qf[7])};
+        } else {
+          qv = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(P.q) + qrow + d0);
+        }
+      }
+      S.qop[kb] = __builtin_bit_cast(bf16x8_t, qv);
+    }
+
+    if (pol.urgent)
+      stream_pages<FP8, DEPTH_U, false>(P, T, S, lane, g4);
+    else if (pol.polite)
+      stream_pages<FP8, DEPTH_S, true>(P, T, S, lane, g4);
+    else
+      stream_pages<FP8, DEPTH_S, false>(P, T, S, lane, g4);
+
+    // Merge: l over the 4 lane rows, then the NW wave states in fixed order.
+    float lt = S.lsum + bperm(S.lsum, T.xor16);
+    lt += bperm(lt, T.xor32);
+    if (c16 < G) {
+      if (g4 == 0) {
+        s_m[w][c16] = S.m;
+        s_l[w][c16] = lt;
+      }
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk)
+        *reinterpret_cast<f32x4_t *>(&s_acc[w][c16][16 * blk + 4 * g4]) = S.acc[blk];
+    }
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < G * 128u; idx += NW * 64) {
+      const uint32_t g = idx >> 7, j = idx & 127u;
+      float M = s_m[0][g];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww)
+        M = fmaxf(M, s_m[ww][g]);
+      float Lt = 0.f, A = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        const float e = __builtin_amdgcn_exp2f(s_m[ww][g] - M);
+        Lt += s_l[ww][g] * e;
+        A += s_acc[ww][g][j] * e;
+      }
+      store_out(P, ((int64_t)T.r * P.Hq + T.h * G + g) * 128 + j, A / Lt);
+    }
+    timer_commit(P.L, toff, task, t0);
+  });
+}
+
+} // namespace schedpd

@@ -1,0 +1,249 @@
+// decode_valu.h -- the general decode kernel on the VALU: any kv dtype
+// (fp32 / bf16 / fp8 e4m3fn), head dim 32/64/128, any page size that is a
+// multiple of 16, general K/V strides, up to 16 q-heads per kv-head, and the
+// linear-contraction mode. It serves the fp32 configurations (where the
+// score must stay in fp32), the reference's fixture layouts (interleaved
+// [token][K|V] pages) and every shape the MFMA kernel does not take.
+//
+// One workgroup (4 waves) runs one task = (request r, kv-head h). The tokens
+// of the request are cut into 16-token chunks; wave w takes chunks w, w+4, ...
+// so the split depends only on the context length. Per chunk:
+//   score: lane (i = lane%16, slot = lane/16) owns token i of the chunk and
+//          q-head 4*pass + slot; dot product against its K row (16-byte loads),
+//          running max / sum per head over the 16-lane row (xor shuffles);
+//   PV:    lane owns output element d = lane (+64); it loads V for the 16
+//          tokens once and accumulates every head, broadcasting p and the
+//          rescale factor with v_readlane.
+// The 4 wave states (m, l, acc) merge in LDS in fixed wave order, so the
+// result bits depend only on the task's inputs, never on which workgroup,
+// worker or schedule ran it (pi / work-queue / prefetch invariance).
+// Masked and out-of-context tokens get weight exactly 0 (score -inf, value 0),
+// the reference's skip semantics (test/paged_decode.cu:136-137).
+#pragma once
+
+#include "common.h"
+
+namespace schedpd {
+
+template <typename KVT> struct Vec16;
+template <> struct Vec16<float> { static constexpr int N = 4; };
+template <> struct Vec16<uint16_t> { static constexpr int N = 8; };
+template <> struct Vec16<uint8_t> { static constexpr int N = 16; };
+
+__device__ __forceinline__ void cvt16(const uint4 &raw, float *f, float) {
+  f[0] = __uint_as_float(raw.x);
+  f[1] = __uint_as_float(raw.y);
+  f[2] = __uint_as_float(raw.z);
+  f[3] = __uint_as_float(raw.w);
+}
+__device__ __forceinline__ void cvt16(const uint4 &raw, float *f, uint16_t) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void cvt16(const uint4 &raw, float *f, uint8_t) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      f[4 * k + b] = fp8e4m3_to_f32((w[k] >> (8 * b)) & 0xffu);
+}
+
+__device__ __forceinline__ float ldv(const float *p) { return *p; }
+__device__ __forceinline__ float ldv(const uint16_t *p) { return bf16_bits_to_f32(*p); }
+__device__ __forceinline__ float ldv(const uint8_t *p) { return fp8e4m3_to_f32(*p); }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <typename KVT, int D, int GMAX, bool LINEAR>
+__global__ void __launch_bounds__(256) decode_valu(KParams P) {
+  constexpr int NW = 4;
+  constexpr int GH = LINEAR ? 1 : GMAX;  // head rows of state
+  constexpr int NP = (GH + 3) / 4;       // score passes (4 heads per pass)
+  constexpr int EPL = D >= 64 ? D / 64 : 1;
+  constexpr int VN = Vec16<KVT>::N;
+  __shared__ float s_q[GH][D];
+  __shared__ float s_acc[NW][GH][D];
+  __shared__ float s_m[NW][GH];
+  __shared__ float s_l[NW][GH];
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // scalar wave index
+  const uint32_t i16 = lane & 15u, slot = lane >> 4;
+  const bool toff = timer_off_latched(P.L);
+
+  run_tasks(P.L, [&](uint32_t task) {
+    if (task >= P.L.ntasks)
+      return;
+    const unsigned long long t0 = read_clock(P.L.wallclock);
+    const uint32_t r = task / P.Hkv, h = task % P.Hkv;
+    const TaskPolicy pol = task_policy(P.L, task);
+    const uint32_t n = ctx_tokens(P, r);
+    const uint32_t nload = load_extent(P, n, pol.budget);
+    const uint32_t G = LINEAR ? 1u : P.G;
+    const bool fp8 = sizeof(KVT) == 1;
+
+    if (!LINEAR)
+      for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256) {
+        uint32_t g = idx / D, j = idx % D;
+        s_q[g][j] = load_q(P, ((int64_t)r * P.Hq + h * G + g) * D + j);
+      }
+    __syncthreads();
+
+    float m[NP], lsum[NP];
+    float acc[GH][EPL];
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      m[k] = kMInit;
+      lsum[k] = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < GH; ++g)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+        acc[g][e] = 0.f;
+
+    const uint32_t nchunks = (nload + 15u) / 16u;
+    for (uint32_t c = w; c < nchunks; c += NW) {
+      const uint32_t pos0 = c * 16u, b = pos0 / P.ps, o = pos0 % P.ps;
+      const int64_t page = page_of(P, r, b);
+      const float ks = (fp8 && P.k_scale) ? P.k_scale[page * P.Hkv + h] : 1.f;
+      const float vs = (fp8 && P.v_scale) ? P.v_scale[page * P.Hkv + h] : 1.f;
+      float p_hp[NP], c_hp[NP];
+
+      if (!LINEAR) {
+        const uint32_t t = pos0 + i16;
+        const bool kp = t < n && keep_pos(P, pol.budget, t);
+        const KVT *krow = static_cast<const KVT *>(P.k_pool) + page * P.kps +
+                          (int64_t)h * P.khs + (int64_t)(o + i16) * P.kts;
+#pragma unroll
+        for (int hp = 0; hp < NP; ++hp) {
+          const uint32_t head = 4u * hp + slot;
+          const bool act = kp && head < G;
+          float dot = 0.f;
+          if (act) {
+            const float *qh = s_q[head];
+#pragma unroll 4
+            for (int j0 = 0; j0 < D; j0 += VN) {
+              uint4 raw = *reinterpret_cast<const uint4 *>(krow + j0);
+              float f[VN];
+              cvt16(raw, f, KVT());
+#pragma unroll
+              for (int e = 0; e < VN; ++e)
+                dot += qh[j0 + e] * f[e];
+            }
+          }
+          const float sc = act ? dot * ks * P.scale_log2 : kNegInf;
+          float cmax = sc;
+#pragma unroll
+          for (int x = 1; x < 16; x <<= 1)
+            cmax = fmaxf(cmax, __shfl_xor(cmax, x));
+          const float mnew = fmaxf(m[hp], cmax);
+          const float cf = exp2f(m[hp] - mnew);
+          const float p = exp2f(sc - mnew);
+          float ps = p;
+#pragma unroll
+          for (int x = 1; x < 16; x <<= 1)
+            ps += __shfl_xor(ps, x);
+          lsum[hp] = lsum[hp] * cf + ps;
+          m[hp] = mnew;
+          p_hp[hp] = p;
+          c_hp[hp] = cf;
+        }
+      }
+
+      // PV (or the linear contraction): V for the 16 tokens at my elements.
+      float v[16][EPL];
+      const KVT *vbase = static_cast<const KVT *>(P.v_pool) + page * P.vps + (int64_t)h * P.vhs;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t ti = pos0 + i;
+        const bool ki = ti < n && keep_pos(P, pol.budget, ti);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const uint32_t d = lane + 64u * e;
+          v[i][e] = (ki && d < D) ? ldv(vbase + (int64_t)(o + i) * P.vts + (int64_t)d * P.vds) * vs
+                                  : 0.f;
+        }
+      }
+      if (LINEAR) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t ti = pos0 + i;
+          const bool ki = ti < n && keep_pos(P, pol.budget, ti);
+          const float wi = ki ? P.lin_w[P.lin_w_period ? ti % P.lin_w_period : ti] : 0.f;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e)
+            acc[0][e] += wi * v[i][e];
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GH; ++g) {
+          if ((uint32_t)g < G) {
+            const float cg = readlane_f(c_hp[g / 4], 16 * (g % 4));
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+              acc[g][e] *= cg;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const float pgi = readlane_f(p_hp[g / 4], 16 * (g % 4) + i);
+#pragma unroll
+              for (int e = 0; e < EPL; ++e)
+                acc[g][e] += pgi * v[i][e];
+            }
+          }
+        }
+      }
+    }
+
+    // Merge the 4 wave states in fixed order.
+#pragma unroll
+    for (int g = 0; g < GH; ++g) {
+      if (!LINEAR && lane == 16u * (g % 4)) {
+        s_m[w][g] = m[g / 4];
+        s_l[w][g] = lsum[g / 4];
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const uint32_t d = lane + 64u * e;
+        if (d < D)
+          s_acc[w][g][d] = acc[g][e];
+      }
+    }
+    __syncthreads();
+    if (LINEAR) {
+      for (uint32_t j = threadIdx.x; j < D; j += 256) {
+        float a = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww)
+          a += s_acc[ww][0][j];
+        store_out(P, ((int64_t)r * P.Hkv + h) * D + j, a);
+      }
+    } else {
+      for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256) {
+        const uint32_t g = idx / D, j = idx % D;
+        float M = s_m[0][g];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww)
+          M = fmaxf(M, s_m[ww][g]);
+        float Lt = 0.f, A = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) {
+          const float e = exp2f(s_m[ww][g] - M);
+          Lt += s_l[ww][g] * e;
+          A += s_acc[ww][g][j] * e;
+        }
+        store_out(P, ((int64_t)r * P.Hq + h * G + g) * D + j, A / Lt);
+      }
+    }
+    timer_commit(P.L, toff, task, t0);
+  });
+}
+
+} // namespace schedpd

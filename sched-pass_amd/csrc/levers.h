@@ -1,0 +1,164 @@
+// levers.h -- device side of the five scheduling levers, hand-written for
+// gfx950 (one workgroup = one task at a time, wave64).
+//
+// Each lever reads the table pointers in LeverTables; a NULL pointer is that
+// lever's stock behaviour. The decisions follow the reference weave exactly
+// (file:line of the reference cited per function); only the mechanism is
+// native (no IR weaving: the kernels call these helpers directly).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sched_pd.h"
+
+namespace schedpd {
+
+struct LeverTables {
+  const int32_t *order;      // pi
+  const uint8_t *ctrl;       // SchedCtrl bytes
+  unsigned long long *timer; // residency rows
+  uint32_t *queue;           // ticket counter
+  uint32_t max_tasks;        // rows in order/ctrl/timer
+  uint32_t ntasks;           // tasks of this launch (static grid size)
+  uint32_t wq;               // 1 = launched as W persistent workers
+  uint32_t wallclock;        // timer source: 1 = s_memrealtime, 0 = s_memtime
+  float dT, dR, H;           // policy marginal-exchange constants
+};
+
+struct TaskPolicy {
+  bool urgent;
+  bool polite;
+  uint32_t budget; // tokens; 0xFFFFFFFF = no cap
+};
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
+  return *reinterpret_cast<const uint32_t *>(p);
+}
+__device__ __forceinline__ float ld_f32(const uint8_t *p) {
+  return *reinterpret_cast<const float *>(p);
+}
+
+__device__ __forceinline__ unsigned long long read_clock(uint32_t wallclock) {
+  return wallclock ? __builtin_amdgcn_s_memrealtime() : __builtin_amdgcn_s_memtime();
+}
+
+// pi on the static grid (reference lib/SchedWeave.cpp:444-526):
+//   task = order[pid] if order is armed, pid < max, order[pid] < nctaid and
+//   ctrl.order_size in {0, nctaid} (ctrl unarmed = unchecked); else pid.
+__device__ __forceinline__ uint32_t remap_static(const LeverTables &L, uint32_t pid,
+                                                 uint32_t nctaid) {
+  if (L.order == nullptr || pid >= L.max_tasks)
+    return pid;
+  uint32_t mapped = (uint32_t)L.order[pid];
+  bool size_ok = true;
+  if (L.ctrl) {
+    uint32_t osz = ld_u32(L.ctrl + SCHED_CTRL_ORDER_SIZE_OFF);
+    size_ok = (osz == 0u) || (osz == nctaid);
+  }
+  return (mapped < nctaid && size_ok) ? mapped : pid;
+}
+
+// pi inside the work-queue loop (reference lib/SchedWorkQueue.cpp:305-343):
+// bounded by num_tasks (this claim wave's range) with order_size in
+// {0, num_tasks}. ctrl is armed on this path (the driver checked it).
+__device__ __forceinline__ uint32_t remap_wq(const LeverTables &L, uint32_t raw,
+                                             uint32_t num_tasks) {
+  if (L.order == nullptr || raw >= L.max_tasks)
+    return raw;
+  uint32_t mapped = (uint32_t)L.order[raw];
+  uint32_t osz = ld_u32(L.ctrl + SCHED_CTRL_ORDER_SIZE_OFF);
+  bool ok = mapped < num_tasks && (osz == 0u || osz == num_tasks);
+  return ok ? mapped : raw;
+}
+
+// Policy flags and shed budget of one task (reference lib/SchedWeave.cpp:
+// 532-581 and :585-614). Task-uniform: every lane computes the same values
+// from scalar loads.
+__device__ __forceinline__ TaskPolicy task_policy(const LeverTables &L, uint32_t task) {
+  TaskPolicy P{false, false, 0xFFFFFFFFu};
+  if (L.ctrl == nullptr || task >= L.max_tasks)
+    return P;
+  const uint8_t *row = L.ctrl + SCHED_CTRL_ROWS_OFF + (size_t)task * SCHED_CTRL_ROW_SIZE;
+  float lam = ld_f32(L.ctrl + SCHED_CTRL_LAMBDA_OFF);
+  float q = ld_f32(row);
+  uint32_t w1 = ld_u32(row + 4); // tau (u16) | hint (u8) << 16
+  uint32_t tau = w1 & 0xFFFFu;
+  uint32_t hint = (w1 >> 16) & 0xFFu;
+  float score = (q * L.dT - lam * L.dR) - L.H;
+  P.urgent = hint == SCHED_HINT_URGENT || (hint == SCHED_HINT_AUTO && score > 0.f);
+  P.polite = hint == SCHED_HINT_POLITE;
+  P.budget = tau ? tau : 0xFFFFFFFFu;
+  return P;
+}
+
+// Timer-off gate latched at kernel entry (reference lib/SchedWeave.cpp:
+// 346-356, 979-1002): ctrl unarmed -> timer on.
+__device__ __forceinline__ bool timer_off_latched(const LeverTables &L) {
+  return L.ctrl != nullptr && (ld_u32(L.ctrl + SCHED_CTRL_FLAGS_OFF) & SCHED_CTRL_FLAG_TIMER_OFF);
+}
+
+// Epilogue of one task body (reference lib/SchedWeave.cpp:1004-1049): lane 0
+// of the workgroup adds the residency delta into timer[task], relaxed, device
+// scope; rows accumulate until cleared.
+__device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uint32_t task,
+                                             unsigned long long t0) {
+  if (threadIdx.x == 0 && L.timer != nullptr && task < L.max_tasks && !off) {
+    unsigned long long dt = read_clock(L.wallclock) - t0;
+    __hip_atomic_fetch_add(L.timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Task acquisition: the static grid or the ticket work queue (reference
+// lib/SchedWorkQueue.cpp:345-448). `body(task)` runs one task with the whole
+// workgroup and must end with every thread past its last LDS use.
+//
+// Static launch (wq == 0): one task per workgroup, task = remap_static(ctaid).
+// Work-queue launch (wq == 1, grid = W workers):
+//   stock path if queue or ctrl is NULL, the grid is not 1-D, or num_tasks==0;
+//   otherwise raw = ctaid (exit if >= num_tasks), then loop: body(remap(raw)),
+//   barrier, lane 0 claims raw = atomicAdd(queue, 1), barrier, until
+//   raw >= num_tasks. The claim comes after the body (late binding).
+// On the stock path pi stays live with the static-grid bound (the reference's
+// stated intent, test/hetero_batch.cu:220-225; its num_tasks-bounded remap
+// there degrades to identity, which changes no output).
+// The worker that takes the launch's last ticket (W + num_tasks - 1) stores W
+// back into the counter: every other worker has already made its last claim,
+// so the next launch with the same W needs no host-side reset.
+template <class Body>
+__device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
+  const uint32_t pid = blockIdx.x;
+  if (!L.wq) {
+    body(remap_static(L, pid, gridDim.x));
+    return;
+  }
+  const bool grid1d = gridDim.y == 1 && gridDim.z == 1;
+  const bool armed = L.queue != nullptr && L.ctrl != nullptr && grid1d;
+  const uint32_t ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
+  if (ntasks == 0u) {
+    body(remap_static(L, pid, gridDim.x));
+    return;
+  }
+  __shared__ uint32_t s_next;
+  uint32_t raw = pid;
+  if (raw >= ntasks)
+    return;
+  const uint32_t last_ticket = gridDim.x + ntasks - 1u;
+  while (true) {
+    body(remap_wq(L, raw, ntasks));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t t = __hip_atomic_fetch_add(L.queue, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+      if (t == last_ticket)
+        __hip_atomic_store(L.queue, gridDim.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_next = t;
+    }
+    __syncthreads();
+    raw = s_next;
+    if (raw >= ntasks)
+      break;
+  }
+}
+
+} // namespace schedpd

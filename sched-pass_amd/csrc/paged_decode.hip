@@ -1,0 +1,321 @@
+// paged_decode.hip -- kernel instantiations and the C-ABI launchers:
+// sched_paged_decode (one decode step over a paged batch with the levers),
+// its occupancy query, and the reference's launch_paged_softmax /
+// paged_softmax_occupancy (python/kernels/paged_softmax.cu:47-67).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "decode_mfma.h"
+#include "decode_valu.h"
+#include "rt_internal.h"
+
+using namespace schedpd;
+
+namespace {
+
+typedef void (*KernelFn)(KParams);
+
+struct Selected {
+  KernelFn fn;
+  int block;
+  int mfma;
+};
+
+template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
+  if (linear)
+    return decode_valu<KVT, D, 1, true>;
+  if (G <= 1)
+    return decode_valu<KVT, D, 1, false>;
+  if (G <= 4)
+    return decode_valu<KVT, D, 4, false>;
+  return decode_valu<KVT, D, 16, false>;
+}
+
+template <bool FP8> KernelFn mfma_kernel(uint32_t G) {
+  constexpr int NW = 4, DS = 2, DU = 4;
+  if (G <= 4)
+    return decode_mfma<FP8, NW, 4, DS, DU>;
+  if (G <= 8)
+    return decode_mfma<FP8, NW, 8, DS, DU>;
+  return decode_mfma<FP8, NW, 16, DS, DU>;
+}
+
+uint32_t elem_bytes(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u; }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The MFMA kernel's shape: bf16/fp8 KV, d 128, page 16, K rows dims-contiguous,
+// V d-major 16-token rows, bf16 Q, G <= 16, 16-byte aligned pools.
+bool mfma_applies(const SchedDecodeArgs *a) {
+  if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
+    return false;
+  if (a->mode != SCHED_PD_SOFTMAX || a->q_dtype != SCHED_PD_BF16)
+    return false;
+  if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_FP8_E4M3)
+    return false;
+  const uint32_t G = a->num_q_heads / a->num_kv_heads;
+  if (a->head_dim != 128 || a->page_size != 16 || G > 16)
+    return false;
+  const int64_t eb = elem_bytes(a->kv_dtype);
+  if (a->v_tok_stride != 1 || a->v_dim_stride != 16)
+    return false;
+  if ((a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 || (a->k_head_stride * eb) % 16)
+    return false;
+  if ((a->v_page_stride * eb) % 16 || (a->v_head_stride * eb) % 16)
+    return false;
+  return aligned16(a->k_pool) && aligned16(a->v_pool) && aligned16(a->q);
+}
+
+// Validate `a`; on success fill *kp (tables resolved) and *sel.
+int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
+  if (a == nullptr)
+    return set_error(hipErrorInvalidValue, "args is NULL");
+  if (a->abi_version != SCHED_PD_ABI_VERSION)
+    return set_error(hipErrorInvalidValue, "abi_version %u, library speaks %u", a->abi_version,
+                     SCHED_PD_ABI_VERSION);
+  if (a->mode > SCHED_PD_LINEAR)
+    return set_error(hipErrorInvalidValue, "unknown mode %u", a->mode);
+  if (a->kv_dtype > SCHED_PD_FP8_E4M3 || a->q_dtype > SCHED_PD_BF16 || a->o_dtype > SCHED_PD_BF16)
+    return set_error(hipErrorInvalidValue, "unsupported dtype (kv %u, q %u, out %u)", a->kv_dtype,
+                     a->q_dtype, a->o_dtype);
+  if (a->num_kv_heads == 0)
+    return set_error(hipErrorInvalidValue, "num_kv_heads is 0");
+  const bool linear = a->mode == SCHED_PD_LINEAR;
+  if (!linear && (a->num_q_heads == 0 || a->num_q_heads % a->num_kv_heads))
+    return set_error(hipErrorInvalidValue, "num_q_heads %u is not a multiple of num_kv_heads %u",
+                     a->num_q_heads, a->num_kv_heads);
+  const uint32_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
+  if (G > 16)
+    return set_error(hipErrorInvalidValue, "%u q-heads per kv-head, at most 16 supported", G);
+  if (a->head_dim != 32 && a->head_dim != 64 && a->head_dim != 128)
+    return set_error(hipErrorInvalidValue, "head_dim %u (supported: 32, 64, 128)", a->head_dim);
+  if (a->head_dim == 32 && a->kv_dtype != SCHED_PD_F32)
+    return set_error(hipErrorInvalidValue, "head_dim 32 is supported for fp32 KV only");
+  if (a->page_size == 0 || a->page_size % 16 || a->page_size > 256)
+    return set_error(hipErrorInvalidValue, "page_size %u (multiple of 16, at most 256)",
+                     a->page_size);
+  if (a->tau_scope > SCHED_PD_TAU_PER_PAGE)
+    return set_error(hipErrorInvalidValue, "unknown tau_scope %u", a->tau_scope);
+  if (!a->out || !a->v_pool || !a->block_table || !a->ctx_lens)
+    return set_error(hipErrorInvalidValue, "out, v_pool, block_table and ctx_lens are required");
+  if (!linear && (!a->q || !a->k_pool))
+    return set_error(hipErrorInvalidValue, "softmax mode needs q and k_pool");
+  if (linear && !a->lin_w)
+    return set_error(hipErrorInvalidValue, "linear mode needs lin_w");
+  if (!a->page_indptr && a->bt_stride == 0)
+    return set_error(hipErrorInvalidValue, "bt_stride is 0 with a 2-D block table");
+
+  const int64_t eb = elem_bytes(a->kv_dtype);
+  const bool mfma = mfma_applies(a);
+  if (!mfma && !linear) {
+    // VALU K rows are read with 16-byte vector loads.
+    if (!aligned16(a->k_pool) || (a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 ||
+        (a->k_head_stride * eb) % 16)
+      return set_error(hipErrorInvalidValue,
+                       "K pool and K page/head/token strides must be 16-byte aligned");
+  }
+
+  std::memset(kp, 0, sizeof *kp);
+  const bool rt = (a->flags & SCHED_PD_FLAG_RT_TABLES) != 0;
+  if (rt) {
+    const RtSnapshot s = rt_snapshot();
+    kp->L.order = s.order;
+    kp->L.ctrl = static_cast<const uint8_t *>(s.ctrl);
+    kp->L.timer = s.timer;
+    kp->L.queue = s.queue;
+    kp->L.max_tasks = SCHED_MAX_TASKS;
+  } else {
+    kp->L.order = a->order;
+    kp->L.ctrl = static_cast<const uint8_t *>(a->ctrl);
+    kp->L.timer = a->timer;
+    kp->L.queue = a->queue;
+    kp->L.max_tasks = a->max_tasks;
+  }
+  kp->L.ntasks = a->num_requests * a->num_kv_heads;
+  kp->L.wallclock = (a->flags & SCHED_PD_FLAG_WALLCLOCK) ? 1u : 0u;
+  kp->L.dT = a->policy_dT;
+  kp->L.dR = a->policy_dR;
+  kp->L.H = a->policy_H;
+  kp->q = a->q;
+  kp->out = a->out;
+  kp->k_pool = a->k_pool;
+  kp->v_pool = a->v_pool;
+  kp->kps = a->k_page_stride;
+  kp->khs = a->k_head_stride;
+  kp->kts = a->k_tok_stride;
+  kp->vps = a->v_page_stride;
+  kp->vhs = a->v_head_stride;
+  kp->vts = a->v_tok_stride;
+  kp->vds = a->v_dim_stride;
+  kp->k_scale = a->k_scale;
+  kp->v_scale = a->v_scale;
+  kp->bt = a->block_table;
+  kp->indptr = a->page_indptr;
+  kp->ctx = a->ctx_lens;
+  kp->lin_w = a->lin_w;
+  kp->R = a->num_requests;
+  kp->Hq = linear ? a->num_kv_heads : a->num_q_heads;
+  kp->Hkv = a->num_kv_heads;
+  kp->G = G;
+  kp->ps = a->page_size;
+  kp->bt_stride = a->bt_stride;
+  kp->tau_scope = a->tau_scope;
+  kp->q_f32 = a->q_dtype == SCHED_PD_F32;
+  kp->o_f32 = a->o_dtype == SCHED_PD_F32;
+  kp->ctx_in_pages = (a->flags & SCHED_PD_FLAG_CTX_IN_PAGES) ? 1u : 0u;
+  kp->shed_loads = (a->flags & SCHED_PD_FLAG_SHED_LOADS) ? 1u : 0u;
+  kp->lin_w_period = a->lin_w_period;
+  const float scale = a->sm_scale != 0.f ? a->sm_scale : 1.0f / std::sqrt((float)a->head_dim);
+  kp->scale_log2 = scale * 1.4426950408889634f;
+
+  if (mfma) {
+    sel->fn = a->kv_dtype == SCHED_PD_BF16 ? mfma_kernel<false>(G) : mfma_kernel<true>(G);
+    sel->block = 256;
+    sel->mfma = 1;
+  } else {
+    KernelFn fn = nullptr;
+    switch (a->kv_dtype) {
+    case SCHED_PD_F32:
+      fn = a->head_dim == 32   ? valu_kernel<float, 32>(linear, G)
+           : a->head_dim == 64 ? valu_kernel<float, 64>(linear, G)
+                               : valu_kernel<float, 128>(linear, G);
+      break;
+    case SCHED_PD_BF16:
+      fn = a->head_dim == 64 ? valu_kernel<uint16_t, 64>(linear, G)
+                             : valu_kernel<uint16_t, 128>(linear, G);
+      break;
+    default:
+      fn = a->head_dim == 64 ? valu_kernel<uint8_t, 64>(linear, G)
+                             : valu_kernel<uint8_t, 128>(linear, G);
+      break;
+    }
+    sel->fn = fn;
+    sel->block = 256;
+    sel->mfma = 0;
+  }
+  return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+void sched_pd_default_args(SchedDecodeArgs *a) {
+  if (!a)
+    return;
+  std::memset(a, 0, sizeof *a);
+  a->abi_version = SCHED_PD_ABI_VERSION;
+  a->kv_dtype = SCHED_PD_F32;
+  a->q_dtype = SCHED_PD_F32;
+  a->o_dtype = SCHED_PD_F32;
+  a->tau_scope = SCHED_PD_TAU_PREFIX;
+  a->max_tasks = SCHED_MAX_TASKS;
+  a->policy_dT = 1.f;
+  a->policy_dR = 1.f;
+  a->policy_H = 0.25f;
+}
+
+int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
+  KParams kp;
+  Selected sel;
+  int rc = prepare(a, &kp, &sel);
+  if (rc)
+    return rc;
+  const uint32_t ntasks = kp.L.ntasks;
+  if (ntasks == 0)
+    return 0;
+  uint32_t grid = ntasks;
+  // A work-queue launch needs the queue and ctrl tables; without them the
+  // kernel's stock path serves one task per workgroup, so the grid must then
+  // cover every task. For the runtime's tables the pushed num_tasks is known
+  // here too (0 = the per-step disarm switch).
+  bool wq = a->workers > 0 && kp.L.queue != nullptr && kp.L.ctrl != nullptr;
+  if (wq && (a->flags & SCHED_PD_FLAG_RT_TABLES) && rt_snapshot().num_tasks == 0)
+    wq = false;
+  if (wq)
+    grid = a->workers;
+  kp.L.wq = wq ? 1u : 0u;
+  hipLaunchKernelGGL(sel.fn, dim3(grid), dim3(sel.block), 0, (hipStream_t)stream, kp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(e, "kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int sched_paged_decode_occupancy(const SchedDecodeArgs *a) {
+  KParams kp;
+  Selected sel;
+  if (prepare(a, &kp, &sel))
+    return 0;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, sel.fn, sel.block, 0) != hipSuccess)
+    return 0;
+  return blocks;
+}
+
+int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a) {
+  KParams kp;
+  Selected sel;
+  if (prepare(a, &kp, &sel))
+    return -1;
+  return sel.mfma;
+}
+
+int sched_pd_cu_count(void) {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return n;
+}
+
+// reference python/kernels/paged_softmax.cu:47-54
+static void compat_args(SchedDecodeArgs *a, const void *kv, const void *bt, const void *nbl,
+                        const void *q, void *out, int nseq, int bt_stride, int page_tokens) {
+  sched_pd_default_args(a);
+  a->mode = SCHED_PD_SOFTMAX;
+  a->num_requests = nseq > 0 ? (uint32_t)nseq : 0u;
+  a->num_q_heads = 1;
+  a->num_kv_heads = 1;
+  a->head_dim = 32;
+  a->page_size = page_tokens > 0 ? (uint32_t)page_tokens : 0u;
+  a->bt_stride = bt_stride > 0 ? (uint32_t)bt_stride : 0u;
+  a->tau_scope = SCHED_PD_TAU_PER_PAGE;
+  a->flags = SCHED_PD_FLAG_RT_TABLES | SCHED_PD_FLAG_CTX_IN_PAGES;
+  a->sm_scale = 0.125f;
+  a->q = q;
+  a->out = out;
+  a->k_pool = kv;
+  a->v_pool = static_cast<const float *>(kv) + 32;
+  a->k_page_stride = (int64_t)a->page_size * 64;
+  a->k_tok_stride = 64;
+  a->v_page_stride = (int64_t)a->page_size * 64;
+  a->v_tok_stride = 64;
+  a->v_dim_stride = 1;
+  a->block_table = static_cast<const int32_t *>(bt);
+  a->ctx_lens = static_cast<const int32_t *>(nbl);
+}
+
+void launch_paged_softmax(const void *kv, const void *bt, const void *nbl, const void *q,
+                          void *out, int nseq, int bt_stride, int page_tokens, void *stream) {
+  SchedDecodeArgs a;
+  compat_args(&a, kv, bt, nbl, q, out, nseq, bt_stride, page_tokens);
+  sched_paged_decode(&a, stream);
+}
+
+// reference python/kernels/paged_softmax.cu:61-67
+int paged_softmax_occupancy(void) {
+  // Any valid fixture shape selects the same kernel (fp32, d 32, MHA).
+  alignas(16) static float dummy[64];
+  alignas(16) static int32_t dummy_i[4];
+  SchedDecodeArgs a;
+  compat_args(&a, dummy, dummy_i, dummy_i, dummy, dummy, 1, 1, 16);
+  a.flags &= ~SCHED_PD_FLAG_RT_TABLES;
+  return sched_paged_decode_occupancy(&a);
+}
+
+} // extern "C"

@@ -1,0 +1,25 @@
+// rt_internal.h -- what the launcher needs from the C runtime: the tables the
+// __sched_* slots point at right now, and error reporting shared by both
+// translation units.
+#pragma once
+
+#include <stdint.h>
+
+namespace schedpd {
+
+struct RtSnapshot {
+  const int32_t *order;
+  const void *ctrl;
+  unsigned long long *timer;
+  uint32_t *queue;
+  uint32_t num_tasks; // host mirror of ctrl.num_tasks as last pushed
+  bool armed;
+};
+
+RtSnapshot rt_snapshot();
+
+// Record and print an error ("[sched_pd] ..."); returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void set_error_text(const char *text);
+
+} // namespace schedpd

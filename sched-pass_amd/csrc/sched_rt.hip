@@ -1,0 +1,258 @@
+// sched_rt.hip -- the runtime contract of reference runtime/sched_rt.h, as an
+// exported C library on HIP.
+//
+// Same tables, layout and call semantics as the reference (file:line per
+// function). Differences, all deliberate:
+//   * the timer rows live in device memory (the reference maps pinned host
+//     memory; its own measurement puts host-mapped atomics at +26.5% against
+//     -0.5% for a device buffer, ROADMAP.md:1482-1488), so sched_rt_timer()
+//     is a small device-to-host copy instead of a plain host read;
+//   * the functions are exported, not `static inline` in a header, so the
+//     state is one per process (the library), not one per translation unit.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unistd.h>
+
+#include "../../include/sched_pd.h"
+#include "rt_internal.h"
+
+// --- device-side slots (reference runtime/sched_rt.h:88-94) ---------------
+extern "C" {
+__device__ int32_t *__sched_task_order = nullptr;
+__device__ SchedCtrl *__sched_ctrl = nullptr;
+__device__ unsigned long long *__sched_timer = nullptr;
+__device__ uint32_t *__sched_queue = nullptr;
+}
+
+namespace {
+
+struct RtState {
+  int32_t *d_order = nullptr;
+  SchedCtrl *d_ctrl = nullptr;
+  unsigned long long *d_timer = nullptr;
+  uint32_t *d_queue = nullptr;
+  SchedCtrl h_ctrl;
+  bool armed = false;
+};
+
+RtState g_rt;
+thread_local std::string g_err;
+
+bool rt_check(hipError_t e, const char *what) {
+  if (e == hipSuccess)
+    return true;
+  char buf[512];
+  std::snprintf(buf, sizeof buf, "[sched_rt] %s failed: %s", what, hipGetErrorString(e));
+  schedpd::set_error_text(buf);
+  return false;
+}
+
+#define RT_CHECK(call)                                                         \
+  do {                                                                         \
+    if (!rt_check((call), #call))                                              \
+      return false;                                                            \
+  } while (0)
+
+bool write_slots(int32_t *order, SchedCtrl *ctrl, unsigned long long *timer, uint32_t *queue) {
+  RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_task_order), &order, sizeof(void *)));
+  RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_ctrl), &ctrl, sizeof(void *)));
+  RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_timer), &timer, sizeof(void *)));
+  RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_queue), &queue, sizeof(void *)));
+  return true;
+}
+
+} // namespace
+
+namespace schedpd {
+
+void set_error_text(const char *text) {
+  g_err = text;
+  std::fprintf(stderr, "%s\n", text);
+}
+
+int set_error(int code, const char *fmt, ...) {
+  char buf[512];
+  int n = std::snprintf(buf, sizeof buf, "[sched_pd] ");
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf + n, sizeof buf - n, fmt, ap);
+  va_end(ap);
+  set_error_text(buf);
+  return code;
+}
+
+RtSnapshot rt_snapshot() {
+  RtSnapshot s{};
+  s.armed = g_rt.armed;
+  if (g_rt.armed) {
+    s.order = g_rt.d_order;
+    s.ctrl = g_rt.d_ctrl;
+    s.timer = g_rt.d_timer;
+    s.queue = g_rt.d_queue;
+  }
+  s.num_tasks = g_rt.h_ctrl.num_tasks;
+  return s;
+}
+
+} // namespace schedpd
+
+extern "C" {
+
+const char *sched_pd_last_error(void) { return g_err.c_str(); }
+
+// reference runtime/sched_rt.h:121-189
+bool sched_rt_init(void) {
+  RtState &S = g_rt;
+  if (S.armed)
+    return true;
+  if (S.d_order == nullptr) {
+    RT_CHECK(hipMalloc(&S.d_order, SCHED_MAX_TASKS * sizeof(int32_t)));
+    int32_t *ident = (int32_t *)std::malloc(SCHED_MAX_TASKS * sizeof(int32_t));
+    for (int i = 0; i < SCHED_MAX_TASKS; ++i)
+      ident[i] = i;
+    hipError_t e = hipMemcpy(S.d_order, ident, SCHED_MAX_TASKS * sizeof(int32_t),
+                             hipMemcpyHostToDevice);
+    std::free(ident);
+    RT_CHECK(e);
+    // Neutral policy: lambda = 0, q = 0 -> score = -H < 0 -> stock action.
+    std::memset(&S.h_ctrl, 0, sizeof(SchedCtrl));
+    RT_CHECK(hipMalloc(&S.d_ctrl, sizeof(SchedCtrl)));
+    RT_CHECK(hipMemcpy(S.d_ctrl, &S.h_ctrl, sizeof(SchedCtrl), hipMemcpyHostToDevice));
+    RT_CHECK(hipMalloc(&S.d_timer, SCHED_MAX_TASKS * sizeof(unsigned long long)));
+    RT_CHECK(hipMemset(S.d_timer, 0, SCHED_MAX_TASKS * sizeof(unsigned long long)));
+    RT_CHECK(hipMalloc(&S.d_queue, sizeof(uint32_t)));
+    RT_CHECK(hipMemset(S.d_queue, 0, sizeof(uint32_t)));
+  }
+  if (!write_slots(S.d_order, S.d_ctrl, S.d_timer, S.d_queue))
+    return false;
+
+  char path[256];
+  std::snprintf(path, sizeof path, "/tmp/sched_rt_%d.json", (int)getpid());
+  if (FILE *f = std::fopen(path, "w")) {
+    std::fprintf(f,
+                 "{\"pid\":%d,\"max_tasks\":%d,\"order_dev\":%llu,\"ctrl_dev\":%llu,"
+                 "\"timer_dev\":%llu,\"timer_bytes\":%zu,\"queue_dev\":%llu}\n",
+                 (int)getpid(), SCHED_MAX_TASKS,
+                 (unsigned long long)(uintptr_t)S.d_order, (unsigned long long)(uintptr_t)S.d_ctrl,
+                 (unsigned long long)(uintptr_t)S.d_timer,
+                 (size_t)SCHED_MAX_TASKS * sizeof(unsigned long long),
+                 (unsigned long long)(uintptr_t)S.d_queue);
+    std::fclose(f);
+  }
+  S.armed = true;
+  return true;
+}
+
+// reference runtime/sched_rt.h:192-203
+bool sched_rt_disarm(void) {
+  if (!write_slots(nullptr, nullptr, nullptr, nullptr))
+    return false;
+  g_rt.armed = false;
+  return true;
+}
+
+// reference runtime/sched_rt.h:206-212
+bool sched_rt_set_order(const int32_t *order, unsigned n) {
+  if (g_rt.d_order == nullptr) {
+    schedpd::set_error_text("[sched_rt] sched_rt_set_order failed: runtime not initialised");
+    return false;
+  }
+  if (n > SCHED_MAX_TASKS)
+    n = SCHED_MAX_TASKS;
+  RT_CHECK(hipMemcpy(g_rt.d_order, order, n * sizeof(int32_t), hipMemcpyHostToDevice));
+  return true;
+}
+
+// reference runtime/sched_rt.h:214-249
+void sched_rt_set_lambda(float bw, float l2, float smem, float comp) {
+  g_rt.h_ctrl.lambda[0] = bw;
+  g_rt.h_ctrl.lambda[1] = l2;
+  g_rt.h_ctrl.lambda[2] = smem;
+  g_rt.h_ctrl.lambda[3] = comp;
+}
+void sched_rt_set_task(unsigned i, float q, uint16_t tau, uint8_t hint) {
+  if (i >= SCHED_MAX_TASKS)
+    return;
+  g_rt.h_ctrl.task[i].q = q;
+  g_rt.h_ctrl.task[i].tau = tau;
+  g_rt.h_ctrl.task[i].hint = hint;
+  g_rt.h_ctrl.task[i]._pad = 0;
+}
+void sched_rt_set_tau(unsigned i, uint16_t tau) {
+  if (i < SCHED_MAX_TASKS)
+    g_rt.h_ctrl.task[i].tau = tau;
+}
+void sched_rt_set_num_tasks(uint32_t n) { g_rt.h_ctrl.num_tasks = n; }
+void sched_rt_set_order_size(uint32_t n) { g_rt.h_ctrl.order_size = n; }
+void sched_rt_set_timer_enabled(bool on) {
+  if (on)
+    g_rt.h_ctrl.flags &= ~SCHED_CTRL_FLAG_TIMER_OFF;
+  else
+    g_rt.h_ctrl.flags |= SCHED_CTRL_FLAG_TIMER_OFF;
+}
+
+// reference runtime/sched_rt.h:252-257
+bool sched_rt_push_ctrl(void) {
+  if (g_rt.d_ctrl == nullptr) {
+    schedpd::set_error_text("[sched_rt] sched_rt_push_ctrl failed: runtime not initialised");
+    return false;
+  }
+  g_rt.h_ctrl.generation++;
+  RT_CHECK(hipMemcpy(g_rt.d_ctrl, &g_rt.h_ctrl, sizeof(SchedCtrl), hipMemcpyHostToDevice));
+  return true;
+}
+
+// reference runtime/sched_rt.h:261-265
+bool sched_rt_queue_reset(uint32_t workers) {
+  if (g_rt.d_queue == nullptr) {
+    schedpd::set_error_text("[sched_rt] sched_rt_queue_reset failed: runtime not initialised");
+    return false;
+  }
+  RT_CHECK(hipMemcpy(g_rt.d_queue, &workers, sizeof(uint32_t), hipMemcpyHostToDevice));
+  return true;
+}
+
+// reference runtime/sched_rt.h:267-275
+unsigned long long sched_rt_timer(unsigned i) {
+  if (i >= SCHED_MAX_TASKS || g_rt.d_timer == nullptr)
+    return 0ull;
+  unsigned long long v = 0;
+  if (!rt_check(hipMemcpy(&v, g_rt.d_timer + i, sizeof v, hipMemcpyDeviceToHost),
+                "hipMemcpy(timer row)"))
+    return 0ull;
+  return v;
+}
+void sched_rt_timer_clear(void) {
+  if (g_rt.d_timer)
+    rt_check(hipMemset(g_rt.d_timer, 0, SCHED_MAX_TASKS * sizeof(unsigned long long)),
+             "hipMemset(timer)");
+}
+
+bool sched_rt_timer_read(unsigned long long *dst, unsigned n) {
+  if (g_rt.d_timer == nullptr || dst == nullptr) {
+    schedpd::set_error_text("[sched_rt] sched_rt_timer_read failed: runtime not initialised");
+    return false;
+  }
+  if (n > SCHED_MAX_TASKS)
+    n = SCHED_MAX_TASKS;
+  RT_CHECK(hipMemcpy(dst, g_rt.d_timer, n * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  return true;
+}
+
+bool sched_rt_slots(uint64_t slots[4]) {
+  void *p[4] = {nullptr, nullptr, nullptr, nullptr};
+  RT_CHECK(hipMemcpyFromSymbol(&p[0], HIP_SYMBOL(__sched_task_order), sizeof(void *)));
+  RT_CHECK(hipMemcpyFromSymbol(&p[1], HIP_SYMBOL(__sched_ctrl), sizeof(void *)));
+  RT_CHECK(hipMemcpyFromSymbol(&p[2], HIP_SYMBOL(__sched_timer), sizeof(void *)));
+  RT_CHECK(hipMemcpyFromSymbol(&p[3], HIP_SYMBOL(__sched_queue), sizeof(void *)));
+  for (int i = 0; i < 4; ++i)
+    slots[i] = (uint64_t)(uintptr_t)p[i];
+  return true;
+}
+
+} // extern "C"

@@ -1,0 +1,175 @@
+"""paged_decode(): one decode step on torch-ROCm tensors through the C ABI
+(`sched_paged_decode` in include/sched_pd.h).
+
+Pool layout (HND pages; the MFMA kernel's layout):
+    k_pool [num_pages, Hkv, page_size, d]    token rows, dims contiguous
+    v_pool [num_pages, Hkv, d, page_size]    d-major ("dmajor", default)
+        or [num_pages, Hkv, page_size, d]    token-major ("tokmajor", VALU only)
+Any strides are accepted as long as the innermost listed dim is contiguous;
+they are passed to the kernel in elements.
+
+The call goes straight to the HIP library; there is no CPU path. Levers come
+from a SchedPlane (its device tables), from the C runtime's armed slots
+(rt_tables=True), or are absent (stock decode).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+import sched_abi as abi
+
+_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16}
+if hasattr(torch, "float8_e4m3fn"):
+    _DT[torch.float8_e4m3fn] = abi.FP8_E4M3
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    if t.dtype not in _DT:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need_cuda(t: torch.Tensor, what: str) -> None:
+    if t is not None and not t.is_cuda:
+        raise ValueError(f"{what} must be a device tensor (got {t.device})")
+
+
+def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
+               mode=abi.SOFTMAX, v_layout="dmajor", page_indptr=None,
+               sm_scale=None, k_scale=None, v_scale=None,
+               tau_scope=abi.TAU_PREFIX, lin_w=None, lin_w_period=0,
+               plane=None, rt_tables=False, workers=0, pf_dist=0, flags=0,
+               policy=(1.0, 1.0, 0.25)) -> abi.SchedDecodeArgs:
+    """Fill a SchedDecodeArgs from tensors (no launch)."""
+    a = abi.default_args()
+    linear = mode == abi.LINEAR
+    a.mode = mode
+    a.kv_dtype = _dtype_code(v_pool, "v_pool")
+    num_pages, hkv = v_pool.shape[0], v_pool.shape[1]
+    if v_layout == "dmajor":
+        d, ps = v_pool.shape[2], v_pool.shape[3]
+        a.v_page_stride, a.v_head_stride = v_pool.stride(0), v_pool.stride(1)
+        a.v_dim_stride, a.v_tok_stride = v_pool.stride(2), v_pool.stride(3)
+    elif v_layout == "tokmajor":
+        ps, d = v_pool.shape[2], v_pool.shape[3]
+        a.v_page_stride, a.v_head_stride = v_pool.stride(0), v_pool.stride(1)
+        a.v_tok_stride, a.v_dim_stride = v_pool.stride(2), v_pool.stride(3)
+    else:
+        raise ValueError(f"v_layout {v_layout!r}")
+    a.num_kv_heads, a.head_dim, a.page_size = hkv, d, ps
+    a.num_requests = ctx_lens.numel()
+    if not linear:
+        if k_pool.dtype != v_pool.dtype or tuple(k_pool.shape) != (num_pages, hkv, ps, d):
+            raise ValueError(f"k_pool {tuple(k_pool.shape)} {k_pool.dtype} does not match "
+                             f"v_pool ({num_pages}, {hkv}, {ps}, {d}) {v_pool.dtype}")
+        if k_pool.stride(3) != 1:
+            raise ValueError("k_pool dims must be contiguous")
+        a.k_page_stride, a.k_head_stride, a.k_tok_stride = (
+            k_pool.stride(0), k_pool.stride(1), k_pool.stride(2))
+        if q.dim() != 3 or q.shape[0] != a.num_requests or q.shape[2] != d:
+            raise ValueError(f"q must be [num_requests, Hq, {d}], got {tuple(q.shape)}")
+        if not q.is_contiguous():
+            raise ValueError("q must be contiguous")
+        a.num_q_heads = q.shape[1]
+        a.q_dtype = _dtype_code(q, "q")
+        a.q = _ptr(q)
+        a.k_pool = _ptr(k_pool)
+        rows = a.num_q_heads
+    else:
+        if lin_w is None:
+            raise ValueError("linear mode needs lin_w")
+        a.num_q_heads = hkv
+        a.lin_w = _ptr(lin_w)
+        a.lin_w_period = lin_w_period
+        rows = hkv
+    if tuple(out.shape) != (a.num_requests, rows, d) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{a.num_requests}, {rows}, {d}], "
+                         f"got {tuple(out.shape)}")
+    a.o_dtype = _dtype_code(out, "out")
+    a.out = _ptr(out)
+    a.v_pool = _ptr(v_pool)
+    for t, what in ((q, "q"), (k_pool, "k_pool"), (v_pool, "v_pool"), (out, "out"),
+                    (block_table, "block_table"), (ctx_lens, "ctx_lens"),
+                    (page_indptr, "page_indptr"), (k_scale, "k_scale"),
+                    (v_scale, "v_scale"), (lin_w, "lin_w")):
+        if t is not None and (linear is False or what not in ("q", "k_pool")):
+            _need_cuda(t, what)
+    for t, what in ((block_table, "block_table"), (ctx_lens, "ctx_lens"),
+                    (page_indptr, "page_indptr")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"{what} must be contiguous int32")
+    a.block_table = _ptr(block_table)
+    a.ctx_lens = _ptr(ctx_lens)
+    if page_indptr is not None:
+        a.page_indptr = _ptr(page_indptr)
+    else:
+        if block_table.dim() != 2:
+            raise ValueError("block_table must be [num_requests, max_pages] without page_indptr")
+        a.bt_stride = block_table.stride(0)
+    a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
+    a.sm_scale = 0.0 if sm_scale is None else float(sm_scale)
+    a.tau_scope = tau_scope
+    a.pf_dist = pf_dist
+    a.policy_dT, a.policy_dR, a.policy_H = (float(x) for x in policy)
+    a.flags = flags
+    if rt_tables:
+        a.flags |= abi.FLAG_RT_TABLES
+        a.workers = workers
+    elif plane is not None:
+        t = plane.tables()
+        a.order, a.ctrl, a.timer, a.queue = (ctypes.c_void_p(t[k]) for k in
+                                             ("order", "ctrl", "timer", "queue"))
+        a.max_tasks = plane.N
+        # num_tasks == 0 is the per-step disarm of the claim loop; the stock
+        # path serves one task per workgroup, so launch the full grid then.
+        a.workers = workers if plane.num_tasks > 0 else 0
+    else:
+        a.max_tasks = 0
+        a.workers = 0
+    return a
+
+
+def launch(args: abi.SchedDecodeArgs, stream=None) -> None:
+    """Launch one decode step described by `args` on `stream` (default: the
+    current torch stream). Raises RuntimeError with the library's message."""
+    lib = abi.load_library()
+    s = torch.cuda.current_stream() if stream is None else stream
+    rc = lib.sched_paged_decode(ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"sched_paged_decode failed ({rc}): {abi.last_error()}")
+
+
+def paged_decode(q, k_pool, v_pool, block_table, ctx_lens, *, out=None,
+                 out_dtype=None, mode=abi.SOFTMAX, stream=None, **kw) -> torch.Tensor:
+    """One decode step; returns `out` ([R, Hq, d] softmax, [R, Hkv, d] linear).
+    Keyword arguments are those of build_args()."""
+    if out is None:
+        d = v_pool.shape[2] if kw.get("v_layout", "dmajor") == "dmajor" else v_pool.shape[3]
+        rows = q.shape[1] if mode == abi.SOFTMAX else v_pool.shape[1]
+        dt = out_dtype or (q.dtype if q is not None else torch.float32)
+        out = torch.empty(ctx_lens.numel(), rows, d, dtype=dt, device=v_pool.device)
+    args = build_args(q, k_pool, v_pool, block_table, ctx_lens, out=out, mode=mode, **kw)
+    launch(args, stream)
+    return out
+
+
+def kernel_kind(args: abi.SchedDecodeArgs) -> str:
+    """'mfma' or 'valu': which kernel the library picks for `args`."""
+    k = abi.load_library().sched_paged_decode_kernel_kind(ctypes.byref(args))
+    if k < 0:
+        raise RuntimeError(abi.last_error())
+    return "mfma" if k == 1 else "valu"
+
+
+def occupancy(args: abi.SchedDecodeArgs) -> int:
+    return abi.load_library().sched_paged_decode_occupancy(ctypes.byref(args))
+
+
+def cu_count() -> int:
+    return abi.load_library().sched_pd_cu_count()

@@ -1,0 +1,236 @@
+"""sched_rt.py -- the per-step scheduling control plane on torch-ROCm, with the
+API of reference python/sched_rt.py:287-609 (SchedPlane).
+
+The reference keeps its tables in a fixed-VA host mapping registered with the
+driver (so a JIT-compiled kernel can bake the addresses). The kernels here take
+the table addresses as launch arguments instead, so the tables live in device
+memory: one 1 MiB device arena with the reference's offsets (ORDER 0x0,
+CTRL 0x40000, TIMER 0x80000, QUEUE 0xC0000). Consequences:
+  * setters write a host mirror; push() copies it to the device in stream
+    order (rows first, the generation word last, as the reference does);
+  * the timer rows are device memory already (the reference's own verdict for
+    the observation channel: device atomics are ~free, host-mapped ones cost
+    +26.5%); read_timer() is a device-to-host copy on a side stream;
+  * clear_timer() is a fill kernel, so it is safe inside captured graphs.
+Out of scope on purpose (they exist for the reference's clang-JIT cache or
+inspect NVIDIA binaries): bake_env, arm_process_env, compute_bake_env,
+_weave_tag, the fixed-VA guarantee, r_for_cached_so.
+"""
+from __future__ import annotations
+
+import struct
+
+import torch
+
+from sched_abi import (CTRL_FLAGS_OFF, CTRL_LAMBDA_OFF, CTRL_NUM_TASKS_OFF,
+                       CTRL_ORDER_SIZE_OFF, CTRL_ROWS_OFF, FLAG_TIMER_OFF,
+                       HINT_AUTO, HINT_POLITE, HINT_URGENT, ROW_SIZE)
+
+__all__ = ["SchedPlane", "SchedArenaError", "HINT_AUTO", "HINT_URGENT",
+           "HINT_POLITE", "FLAG_TIMER_OFF", "MANIFEST"]
+
+# Arena layout (reference python/sched_rt.py:84-89).
+ORDER_OFF = 0x00000
+CTRL_OFF = 0x40000
+TIMER_OFF = 0x80000
+QUEUE_OFF = 0xC0000
+ARENA_BYTES = 0x100000
+MAX_TASKS_LIMIT = 16384
+
+# Lever manifest (reference include/sched/SchedManifest.h:76-105 and its
+# mirror python/sched_rt.py:72-79): name, effect type, what it reads, and how
+# this build arms it. Order = the order the kernels apply them in.
+MANIFEST = [
+    ("workqueue", "acquire", "ctrl,queue", "launch with workers=W and num_tasks>0"),
+    ("pi", "E1/permute", "order,ctrl", "order table (identity by default)"),
+    ("shed", "E2/budget", "ctrl", "row tau > 0"),
+    ("policy", "E0/hint", "ctrl", "row hint / q*dT - lambda_bw*dR - H > 0"),
+    ("timer", "O/observe", "timer,ctrl", "timer table + flags bit0 clear"),
+]
+
+
+class SchedArenaError(RuntimeError):
+    """The device arena could not be created."""
+
+
+class SchedPlane:
+    """Per-step scheduling tables for the decode kernels (one per device)."""
+
+    def __init__(self, max_tasks: int = 4096, device: str = "cuda"):
+        if max_tasks > MAX_TASKS_LIMIT:
+            raise ValueError(f"max_tasks {max_tasks} > {MAX_TASKS_LIMIT} "
+                             f"(the arena's per-table window)")
+        self.N = int(max_tasks)
+        self.dev = torch.device(device)
+        try:
+            self.arena = torch.zeros(ARENA_BYTES, dtype=torch.uint8, device=self.dev)
+        except RuntimeError as e:
+            raise SchedArenaError(f"arena allocation failed: {e}") from e
+        self._order_arena = self.arena[ORDER_OFF:ORDER_OFF + 4 * self.N].view(torch.int32)
+        self.ctrl_bytes = CTRL_ROWS_OFF + ROW_SIZE * self.N
+        self._ctrl_dev = self.arena[CTRL_OFF:CTRL_OFF + self.ctrl_bytes]
+        self._timer_arena = self.arena[TIMER_OFF:TIMER_OFF + 8 * self.N].view(torch.int64)
+        self._queue = self.arena[QUEUE_OFF:QUEUE_OFF + 4].view(torch.int32)
+        self._ctrl_host = bytearray(self.ctrl_bytes)
+        self._generation = 0
+        self._timer_dev = None      # separate device row buffer (use_device_timer)
+        self._timer_stream = None
+        self._order_dev = None      # separate device order table (use_device_order)
+        self.reset_order()
+        self.push()
+
+    # -- table addresses for the launcher ------------------------------------
+    def _order_view(self) -> torch.Tensor:
+        return self._order_dev if self._order_dev is not None else self._order_arena
+
+    def _timer_view(self) -> torch.Tensor:
+        return self._timer_dev if self._timer_dev is not None else self._timer_arena
+
+    def tables(self) -> dict:
+        return {"order": self._order_view().data_ptr(),
+                "ctrl": self._ctrl_dev.data_ptr(),
+                "timer": self._timer_view().data_ptr(),
+                "queue": self._queue.data_ptr()}
+
+    @property
+    def num_tasks(self) -> int:
+        return struct.unpack_from("<I", self._ctrl_host, CTRL_NUM_TASKS_OFF)[0]
+
+    def use_device_timer(self) -> None:
+        """Move the observation rows to their own device buffer, read back on
+        a side stream (reference python/sched_rt.py:319-331)."""
+        if self._timer_dev is None:
+            self._timer_dev = torch.zeros(self.N, dtype=torch.int64, device=self.dev)
+            self._timer_stream = torch.cuda.Stream(device=self.dev)
+
+    def use_device_order(self) -> None:
+        """Kernel-resident order table in its own device tensor, installable
+        device-to-device without a host sync (python/sched_rt.py:333-347).
+        Starts as identity."""
+        if self._order_dev is None:
+            self._order_dev = torch.arange(self.N, dtype=torch.int32, device=self.dev)
+
+    # -- pi (python/sched_rt.py:365-395) ---------------------------------------
+    def set_order(self, tasks) -> None:
+        """tasks[i] = the task the i-th claim / workgroup serves (a prefix;
+        the tail keeps its current entries)."""
+        t = torch.as_tensor(tasks, dtype=torch.int32)
+        n = min(t.numel(), self.N)
+        self._order_view()[:n].copy_(t[:n].to(self.dev, non_blocking=t.is_cuda))
+
+    def reset_order(self) -> None:
+        self.set_order(torch.arange(self.N, dtype=torch.int32))
+
+    def set_order_size(self, n: int) -> None:
+        struct.pack_into("<I", self._ctrl_host, CTRL_ORDER_SIZE_OFF, int(n))
+
+    def install_order(self, tasks, n: int) -> None:
+        """Table first, validity stamp second (published by the next push)."""
+        self.set_order(tasks)
+        self.set_order_size(n)
+
+    # -- ctrl mirror (python/sched_rt.py:397-443) -------------------------------
+    def set_lambda(self, bw=0.0, l2=0.0, smem=0.0, comp=0.0) -> None:
+        struct.pack_into("<4f", self._ctrl_host, CTRL_LAMBDA_OFF,
+                         float(bw), float(l2), float(smem), float(comp))
+
+    def set_num_tasks(self, n: int) -> None:
+        """Also the per-step work-queue switch: 0 = stock static path."""
+        struct.pack_into("<I", self._ctrl_host, CTRL_NUM_TASKS_OFF, int(n))
+
+    def set_timer_enabled(self, on: bool) -> None:
+        (flags,) = struct.unpack_from("<I", self._ctrl_host, CTRL_FLAGS_OFF)
+        flags = (flags & ~FLAG_TIMER_OFF) | (0 if on else FLAG_TIMER_OFF)
+        struct.pack_into("<I", self._ctrl_host, CTRL_FLAGS_OFF, flags)
+
+    def set_row(self, i: int, q: float = 0.0, tau: int = 0, hint: int = HINT_AUTO) -> None:
+        if not 0 <= i < self.N:
+            raise IndexError(f"row {i} outside [0, {self.N})")
+        struct.pack_into("<fHBB", self._ctrl_host, CTRL_ROWS_OFF + ROW_SIZE * i,
+                         float(q), int(tau) & 0xFFFF, int(hint) & 0xFF, 0)
+
+    def set_rows(self, q=None, tau=None, hint=None, n: int | None = None) -> None:
+        """Vectorised set_row over rows [0, n)."""
+        import numpy as np
+        n = self.N if n is None else int(n)
+        rows = np.zeros(n, dtype=[("q", "<f4"), ("tau", "<u2"), ("hint", "u1"), ("pad", "u1")])
+        if q is not None:
+            rows["q"] = np.asarray(torch.as_tensor(q, dtype=torch.float32).cpu())[:n]
+        if tau is not None:
+            rows["tau"] = np.asarray(torch.as_tensor(tau, dtype=torch.int64).cpu())[:n] & 0xFFFF
+        if hint is not None:
+            rows["hint"] = np.asarray(torch.as_tensor(hint, dtype=torch.int64).cpu())[:n] & 0xFF
+        self._ctrl_host[CTRL_ROWS_OFF:CTRL_ROWS_OFF + ROW_SIZE * n] = rows.tobytes()
+
+    def push(self) -> None:
+        """Publish the mirror (generation++): rows and header body first, the
+        generation word last, in stream order."""
+        self._generation += 1
+        struct.pack_into("<I", self._ctrl_host, 0, self._generation)
+        host = torch.frombuffer(bytearray(self._ctrl_host), dtype=torch.uint8)
+        self._ctrl_dev[4:].copy_(host[4:])
+        self._ctrl_dev[:4].copy_(host[:4])
+
+    # -- timer (python/sched_rt.py:446-462) -------------------------------------
+    def clear_timer(self) -> None:
+        self._timer_view().zero_()
+
+    def read_timer(self) -> torch.Tensor:
+        """Per-task cycles as an int64 CPU tensor. The caller guarantees the
+        writing launches are complete (after a sync or an event)."""
+        t = self._timer_view()
+        if self._timer_stream is not None:
+            with torch.cuda.stream(self._timer_stream):
+                out = t.to("cpu", non_blocking=True)
+            self._timer_stream.synchronize()
+            return out
+        return t.cpu()
+
+    # -- work queue (python/sched_rt.py:464-471) --------------------------------
+    def reset_queue(self, workers: int) -> None:
+        self._queue.fill_(int(workers))
+
+    # -- resident-prefix sizing (python/sched_rt.py:478-487) --------------------
+    def sm_count(self) -> int:
+        return torch.cuda.get_device_properties(self.dev).multi_processor_count
+
+    def r_from_occupancy(self, blocks_per_sm: int) -> int:
+        return int(blocks_per_sm) * self.sm_count()
+
+    # -- pi builders (python/sched_rt.py:557-609) --------------------------------
+    @staticmethod
+    def _grouped_lpt(c, block: int) -> torch.Tensor:
+        """Blocks of `block` adjacent tiles ordered by descending summed cost,
+        ascending index order kept inside a block; block <= 1 is plain LPT.
+        Ties keep ascending index order (stable sort)."""
+        c = torch.as_tensor(c).float().flatten()
+        n = c.numel()
+        if block <= 1 or n <= block:
+            return torch.sort(c, descending=True, stable=True).indices.to(torch.int32)
+        nb = -(-n // block)
+        pad = nb * block - n
+        cc = torch.cat([c, c.new_zeros(pad)]) if pad else c
+        bcost = cc.reshape(nb, block).sum(1)
+        border = torch.sort(bcost, descending=True, stable=True).indices
+        order = (border[:, None] * block + torch.arange(block)[None, :]).flatten()
+        return order[order < n].to(torch.int32)
+
+    @staticmethod
+    def region_order(cost, R: int, block: int | None = None) -> torch.Tensor:
+        """Region-aware pi: with n <= R every tile starts at once, so use
+        grouped LPT (block default 16). Otherwise the first R slots alternate
+        heaviest and lightest tiles and the rest follow heaviest first."""
+        c = torch.as_tensor(cost).float().flatten()
+        n = c.numel()
+        if R <= 0 or n <= int(R):
+            return SchedPlane._grouped_lpt(c, 16 if block is None else block)
+        R = int(R)
+        lpt = torch.sort(c, descending=True, stable=True).indices.to(torch.int32)
+        nh = (R + 1) // 2
+        nl = R - nh
+        pre = torch.empty(R, dtype=torch.int32)
+        pre[0::2] = lpt[:nh]
+        if nl:
+            pre[1::2] = lpt[n - nl:].flip(0)
+        suf = lpt[nh:n - nl] if nl else lpt[nh:]
+        return torch.cat([pre, suf])

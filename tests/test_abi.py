@@ -1,0 +1,151 @@
+"""The C ABI without a GPU: the library loads, exports exactly what
+include/sched_pd.h declares, the ctypes mirror matches the C layout, and the
+host-side argument validation / kernel selection behave (no device calls)."""
+import ctypes
+import os
+import re
+import struct
+import subprocess
+
+import pytest
+
+import oracle
+import sched_abi as abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sched_pd.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^\s*[A-Za-z_][\w \*]*?\b(\w+)\s*\([^;{]*\)\s*;", src, re.M)
+    return sorted(set(n for n in names if n not in ("static_assert",)))
+
+
+def test_header_declares_what_the_mirror_binds():
+    assert header_functions() == sorted(abi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(schedlib):
+    out = subprocess.run(["nm", "-D", "--defined-only", abi.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    missing = [f for f in header_functions() if f not in exported]
+    assert not missing, missing
+    for f in header_functions():
+        assert getattr(schedlib, f) is not None
+
+
+def test_device_slot_symbols_exist(schedlib):
+    # the __sched_* slots live in the device code object; the host side keeps
+    # their shadow symbols for hipMemcpyToSymbol.
+    out = subprocess.run(["nm", "-C", abi.LIB_PATH], capture_output=True, text=True).stdout
+    for s in ("__sched_task_order", "__sched_ctrl", "__sched_timer", "__sched_queue"):
+        assert s in out, s
+
+
+def test_struct_layout_matches_c():
+    lib = oracle.load()
+    buf = (ctypes.c_int64 * 16)()
+    n = lib.oracle_args_layout(buf, 16)
+    A = abi.SchedDecodeArgs
+    expect = [ctypes.sizeof(A), A.sm_scale.offset, A.lin_w_period.offset, A.q.offset,
+              A.k_page_stride.offset, A.v_dim_stride.offset, A.k_scale.offset,
+              A.block_table.offset, A.lin_w.offset, A.order.offset, A.queue.offset,
+              32 + 8 * abi.SCHED_MAX_TASKS]
+    assert list(buf[:n]) == expect
+
+
+def test_default_args_match(schedlib):
+    c = abi.SchedDecodeArgs()
+    schedlib.sched_pd_default_args(ctypes.byref(c))
+    p = abi.default_args()
+    assert bytes(c) == bytes(p)
+
+
+def test_plane_constants_mirror_header():
+    src = open(HEADER).read()
+    def define(name):
+        return int(re.search(rf"#define {name} (\w+)", src).group(1).rstrip("u"), 0)
+    assert define("SCHED_MAX_TASKS") == abi.SCHED_MAX_TASKS
+    assert define("SCHED_CTRL_ROWS_OFF") == abi.CTRL_ROWS_OFF
+    assert define("SCHED_CTRL_FLAGS_OFF") == abi.CTRL_FLAGS_OFF
+    assert define("SCHED_CTRL_ORDER_SIZE_OFF") == abi.CTRL_ORDER_SIZE_OFF
+    assert define("SCHED_PD_ABI_VERSION") == abi.ABI_VERSION
+    assert define("SCHED_PD_FLAG_SHED_LOADS") == abi.FLAG_SHED_LOADS
+    import sched_rt
+    assert (sched_rt.ORDER_OFF, sched_rt.CTRL_OFF, sched_rt.TIMER_OFF, sched_rt.QUEUE_OFF) == \
+        (0, 0x40000, 0x80000, 0xC0000)
+
+
+def fake_args(**kw):
+    """Argument block with fake (never dereferenced) 256-aligned addresses."""
+    a = abi.default_args()
+    a.mode = abi.SOFTMAX
+    a.kv_dtype = a.q_dtype = a.o_dtype = abi.BF16
+    a.num_requests, a.num_q_heads, a.num_kv_heads = 4, 32, 8
+    a.head_dim, a.page_size, a.bt_stride = 128, 16, 8
+    a.k_page_stride, a.k_head_stride, a.k_tok_stride = 8 * 16 * 128, 16 * 128, 128
+    a.v_page_stride, a.v_head_stride, a.v_tok_stride, a.v_dim_stride = 8 * 16 * 128, 16 * 128, 1, 16
+    for i, f in enumerate(("q", "out", "k_pool", "v_pool", "block_table", "ctx_lens")):
+        setattr(a, f, ctypes.c_void_p(0x10000 * (i + 1)))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def kind(lib, a):
+    return lib.sched_paged_decode_kernel_kind(ctypes.byref(a))
+
+
+def test_kernel_selection(schedlib):
+    assert kind(schedlib, fake_args()) == 1                               # bf16 GQA -> MFMA
+    assert kind(schedlib, fake_args(kv_dtype=abi.FP8_E4M3)) == 1          # fp8 -> MFMA
+    assert kind(schedlib, fake_args(flags=abi.FLAG_FORCE_VALU)) == 0
+    assert kind(schedlib, fake_args(q_dtype=abi.F32)) == 0                # fp32 Q keeps fp32 scores
+    assert kind(schedlib, fake_args(kv_dtype=abi.F32, q_dtype=abi.F32)) == 0
+    assert kind(schedlib, fake_args(v_tok_stride=128, v_dim_stride=1)) == 0  # token-major V
+    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32)) == 0
+    assert kind(schedlib, fake_args(num_q_heads=28, num_kv_heads=4)) == 1   # G = 7
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("abi_version", 7, "abi_version"),
+    ("num_q_heads", 33, "multiple"),
+    ("num_q_heads", 8 * 17, "at most 16"),
+    ("head_dim", 96, "head_dim"),
+    ("page_size", 8, "page_size"),
+    ("tau_scope", 5, "tau_scope"),
+    ("kv_dtype", 9, "dtype"),
+    ("ctx_lens", None, "required"),
+    ("bt_stride", 0, "bt_stride"),
+])
+def test_invalid_arguments_fail_loudly_without_launching(schedlib, field, value, msg):
+    a = fake_args(**{field: value})
+    rc = schedlib.sched_paged_decode(ctypes.byref(a), None)
+    assert rc != 0
+    assert msg in abi.last_error()
+    assert kind(schedlib, a) == -1
+
+
+def test_linear_mode_needs_weights(schedlib):
+    a = fake_args(mode=abi.LINEAR)
+    assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
+    assert "lin_w" in abi.last_error()
+
+
+def test_misaligned_k_pool_rejected_for_valu(schedlib):
+    a = fake_args(kv_dtype=abi.F32, q_dtype=abi.F32, k_pool=ctypes.c_void_p(0x10004))
+    assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
+    assert "16-byte" in abi.last_error()
+
+
+def test_missing_library_is_an_error(tmp_path):
+    saved = abi._LIB
+    abi._LIB = None
+    try:
+        with pytest.raises(abi.SchedLibraryError):
+            abi.load_library(str(tmp_path / "nope.so"))
+    finally:
+        abi._LIB = saved

@@ -1,0 +1,318 @@
+"""GPU parity of the decode kernels against the oracle, and bitwise invariance
+of every lever that must not change outputs. All launches go through the C ABI
+(sched_paged_decode) via sched_pd.build_args/launch."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sched_abi as abi
+import sched_pd
+import workloads
+from sched_rt import SchedPlane
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5   # fp32 tolerance, mixed form |a-r| <= tol (1 + |r|)
+TOL_BF16 = 2e-3  # bf16 tolerance, same form
+
+
+def mixed_err(a, r):
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    return float(np.max(np.abs(a - r) / (1 + np.abs(r))))
+
+
+def run(b, plane=None, out_dtype=torch.float32, **kw):
+    torch.cuda.synchronize()
+    out = torch.full((b["ctx_lens"].numel(), b["q"].shape[1] if kw.get("mode", 0) == 0
+                      else b["v_pool"].shape[1], b["v_pool"].shape[2]), float("nan"),
+                     dtype=out_dtype, device="cuda")
+    sched_pd.paged_decode(b["q"], b["k_pool"], b["v_pool"], kw.pop("bt", b["block_table"]),
+                          b["ctx_lens"], out=out, k_scale=b["k_scale"], v_scale=b["v_scale"],
+                          plane=plane, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def ref(b, plane=None, **kw):
+    ctrl = None
+    if plane is not None:
+        ctrl = bytes(plane._ctrl_host)
+    return oracle.decode(b["q"], b["k_pool"], b["v_pool"], kw.pop("bt", b["block_table"]),
+                         b["ctx_lens"], k_scale=b["k_scale"], v_scale=b["v_scale"], ctrl=ctrl,
+                         max_tasks=plane.N if plane is not None else 4096, **kw)
+
+
+def batch(ctx, hq=32, hkv=8, d=128, kv=torch.bfloat16, qd=torch.bfloat16, seed=0):
+    return workloads.make_batch(np.asarray(ctx), num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                                kv_dtype=kv, q_dtype=qd, seed=seed, device="cuda")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib(schedlib):
+    torch.cuda.init()
+    return schedlib
+
+
+# --- parity -------------------------------------------------------------------
+
+def test_mha_fp32_small_parity_tau_and_pi():
+    """fp32, 16 requests, MHA 8 heads, d 64, page 16, ctx ~ U[64,512];
+    pi identity vs reversed bitwise; tau 0 and tau = ctx/2 vs the oracle."""
+    b = workloads.workload("mha_fp32_small", seed=1)
+    R, H = 16, 8
+    plane = SchedPlane(max_tasks=R * H)
+    plane.set_num_tasks(R * H)
+    plane.push()
+    a = run(b, plane=plane)
+    assert sched_pd.kernel_kind(sched_pd.build_args(
+        b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"], out=a)) == "valu"
+    e = mixed_err(a.cpu(), ref(b, plane))
+    print(f"fp32 tau=0 err {e:.3g}")
+    assert e <= TOL_F32
+    plane.set_order(torch.arange(R * H - 1, -1, -1))
+    assert torch.equal(run(b, plane=plane), a)
+    plane.reset_order()
+    ctx = b["ctx_lens"].cpu().numpy()
+    plane.set_rows(tau=np.repeat(ctx // 2, H), n=R * H)
+    plane.push()
+    s = run(b, plane=plane)
+    e = mixed_err(s.cpu(), ref(b, plane))
+    print(f"fp32 tau=ctx/2 err {e:.3g}")
+    assert e <= TOL_F32
+    assert not torch.equal(s, a)
+    plane.set_order(torch.arange(R * H - 1, -1, -1))
+    assert torch.equal(run(b, plane=plane), s)
+
+
+@pytest.mark.parametrize("ctx", [[2048] * 4, [1, 15, 16, 17, 33, 100, 511, 5000]])
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_bf16_gqa_parity(ctx, force_valu):
+    b = batch(ctx, seed=len(ctx))
+    flags = abi.FLAG_FORCE_VALU if force_valu else 0
+    out = run(b, flags=flags)
+    args = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                               b["ctx_lens"], out=out, flags=flags)
+    assert sched_pd.kernel_kind(args) == ("valu" if force_valu else "mfma")
+    e = mixed_err(out.cpu(), ref(b))
+    print(f"bf16 {'valu' if force_valu else 'mfma'} err {e:.3g}")
+    assert e <= TOL_BF16
+    o16 = run(b, flags=flags, out_dtype=torch.bfloat16)
+    assert mixed_err(o16.float().cpu(), ref(b)) <= TOL_BF16
+
+
+def test_bf16_output_is_rne_of_fp32_output():
+    b = batch([300, 2048, 17], seed=3)
+    f = run(b)
+    h = run(b, out_dtype=torch.bfloat16)
+    assert torch.equal(f.to(torch.bfloat16), h)
+
+
+@pytest.mark.parametrize("hq,hkv", [(28, 4), (32, 8), (16, 16), (64, 4)])
+def test_fp8_parity(hq, hkv):
+    b = batch([16, 700, 2048, 3, 257], hq=hq, hkv=hkv, kv=torch.float8_e4m3fn, seed=hq)
+    out = run(b)
+    e = mixed_err(out.cpu(), ref(b))
+    print(f"fp8 G={hq // hkv} err {e:.3g}")
+    assert e <= TOL_BF16
+
+
+@pytest.mark.parametrize("scope", [abi.TAU_PREFIX, abi.TAU_PER_PAGE])
+@pytest.mark.parametrize("kvt", [torch.bfloat16, torch.float8_e4m3fn])
+def test_shed_softmax_matches_truncated_reference(scope, kvt):
+    rng = np.random.default_rng(4)
+    ctx = rng.integers(1024, 4097, size=6)
+    b = batch(ctx, kv=kvt, seed=5)
+    n = len(ctx) * 8
+    plane = SchedPlane(max_tasks=n)
+    if scope == abi.TAU_PREFIX:
+        tau = np.repeat([rng.integers(-(-c // 4), c + 1) for c in ctx], 8)
+    else:
+        tau = rng.integers(1, 17, size=n)
+    tau[::7] = 0  # some tasks unshed
+    plane.set_rows(tau=tau, n=n)
+    plane.push()
+    out = run(b, plane=plane, tau_scope=scope)
+    e = mixed_err(out.cpu(), ref(b, plane, tau_scope=scope))
+    print(f"shed scope {scope} {kvt} err {e:.3g}")
+    assert e <= TOL_BF16
+    # loading the shed pages and masking them gives the same bits
+    same = run(b, plane=plane, tau_scope=scope, flags=abi.FLAG_SHED_LOADS)
+    assert torch.equal(out, same)
+
+
+@pytest.mark.parametrize("kvt", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("period", [0, 16])
+def test_linear_contraction_and_value_shed(kvt, period):
+    ctx = [64, 1000, 5, 2048]
+    b = batch(ctx, hq=8, hkv=8, d=64 if kvt == torch.float32 else 128, kv=kvt,
+              qd=torch.float32 if kvt == torch.float32 else torch.bfloat16, seed=6)
+    w = torch.randn(4096, device="cuda")
+    n = len(ctx) * 8
+    plane = SchedPlane(max_tasks=n)
+    tau = np.random.default_rng(7).integers(0, 2048, size=n)
+    plane.set_rows(tau=tau, n=n)
+    plane.push()
+    out = run(b, plane=plane, mode=abi.LINEAR, lin_w=w, lin_w_period=period)
+    r = ref(b, plane, mode=abi.LINEAR, lin_w=w.cpu().numpy(), lin_w_period=period)
+    tol = TOL_F32 if kvt == torch.float32 else TOL_BF16
+    e = mixed_err(out.cpu(), r)
+    print(f"linear {kvt} err {e:.3g}")
+    assert e <= tol
+
+
+def test_empty_request_gives_nan_like_the_reference():
+    b = batch([0, 64, 0])
+    out = run(b)
+    assert torch.isnan(out[0]).all() and torch.isnan(out[2]).all()
+    assert torch.isfinite(out[1]).all()
+
+
+def test_csr_page_table():
+    b = batch([100, 2048, 33], seed=8)
+    ctx = b["ctx_lens"].cpu().numpy()
+    npg = (ctx + 15) // 16
+    bt = b["block_table"].cpu().numpy()
+    indptr = torch.tensor(np.concatenate([[0], np.cumsum(npg)]), dtype=torch.int32, device="cuda")
+    flat = torch.tensor(np.concatenate([bt[r, :npg[r]] for r in range(3)]), dtype=torch.int32,
+                        device="cuda")
+    a = run(b)
+    c = run(b, bt=flat, page_indptr=indptr)
+    assert torch.equal(a, c)
+
+
+# --- levers that must not change a bit ---------------------------------------
+
+def _hetero(seed=9):
+    ctx = np.random.default_rng(seed).integers(1, 3000, size=24)
+    return batch(ctx, seed=seed)
+
+
+@pytest.mark.parametrize("pi", ["reversed", "random", "lpt"])
+def test_pi_is_bit_invariant(pi):
+    b = _hetero()
+    n = 24 * 8
+    plane = SchedPlane(max_tasks=n)
+    base = run(b, plane=plane)
+    if pi == "reversed":
+        order = torch.arange(n - 1, -1, -1)
+    elif pi == "random":
+        order = torch.randperm(n)
+    else:
+        order = SchedPlane._grouped_lpt(torch.repeat_interleave(b["ctx_lens"].cpu(), 8).float(), 1)
+    plane.install_order(order, n)
+    plane.push()
+    assert torch.equal(run(b, plane=plane), base)
+
+
+@pytest.mark.parametrize("W", [1, 7, 192, 197, 512])
+def test_work_queue_is_bit_invariant_and_times_every_task(W):
+    b = _hetero(10)
+    n = 24 * 8
+    plane = SchedPlane(max_tasks=n)
+    base = run(b, plane=plane)
+    plane.set_num_tasks(n)
+    plane.install_order(torch.randperm(n), n)
+    plane.push()
+    plane.reset_queue(W)
+    plane.clear_timer()
+    out = run(b, plane=plane, workers=W)
+    assert torch.equal(out, base)
+    rows = plane.read_timer()[:n]
+    assert int((rows > 0).sum()) == n
+    # the counter reset itself: a second launch without a host reset is exact too
+    plane.clear_timer()
+    assert torch.equal(run(b, plane=plane, workers=W), base)
+    assert int((plane.read_timer()[:n] > 0).sum()) == n
+
+
+def test_policy_levers_are_bit_invariant():
+    b = _hetero(11)
+    n = 24 * 8
+    plane = SchedPlane(max_tasks=n)
+    base = run(b, plane=plane)
+    rng = np.random.default_rng(0)
+    plane.set_lambda(0.5)
+    plane.set_rows(q=rng.uniform(0, 1, n), hint=rng.integers(0, 3, n), n=n)
+    plane.push()
+    assert torch.equal(run(b, plane=plane, policy=(1.0, 1.0, 0.1)), base)
+    plane.set_rows(hint=np.full(n, abi.HINT_URGENT), n=n)
+    plane.push()
+    assert torch.equal(run(b, plane=plane), base)
+    plane.set_rows(hint=np.full(n, abi.HINT_POLITE), n=n)
+    plane.push()
+    assert torch.equal(run(b, plane=plane), base)
+
+
+def test_timer_rows_gate_and_cost_ranking():
+    ctx = np.array([16] * 16 + [8192] * 2)
+    b = batch(ctx, seed=12)
+    n = len(ctx) * 8
+    plane = SchedPlane(max_tasks=n)
+    plane.use_device_timer()
+    base = run(b)
+    plane.clear_timer()
+    assert torch.equal(run(b, plane=plane), base)
+    cyc = plane.read_timer()[:n].numpy()
+    assert (cyc > 0).all()
+    long_c = cyc[16 * 8:].mean()
+    short_c = cyc[:16 * 8].mean()
+    print(f"timer long {long_c:.0f} short {short_c:.0f}")
+    assert long_c > 2 * short_c
+    plane.set_timer_enabled(False)
+    plane.push()
+    plane.clear_timer()
+    assert torch.equal(run(b, plane=plane), base)
+    assert int((plane.read_timer() != 0).sum()) == 0
+
+
+def test_remap_edge_cases_follow_the_emulator():
+    import levers
+    b = _hetero(13)
+    n = 24 * 8
+    plane = SchedPlane(max_tasks=n)
+    base = run(b, plane=plane)
+    # out-of-range and negative entries fall back to the workgroup's own id
+    order = np.arange(n)
+    order[3], order[5] = n + 7, -2
+    plane.set_order(torch.tensor(order, dtype=torch.int32))
+    assert torch.equal(run(b, plane=plane), base)
+    # duplicates under a stale order_size stamp: whole launch takes identity
+    dup = np.arange(n)
+    dup[10] = 11
+    plane.set_order(torch.tensor(dup, dtype=torch.int32))
+    plane.set_order_size(n + 1)
+    plane.push()
+    assert torch.equal(run(b, plane=plane), base)
+    # duplicates unchecked (order_size 0): task 10 never runs, 11 runs twice
+    plane.set_order_size(0)
+    plane.push()
+    plane.clear_timer()
+    out = run(b, plane=plane)
+    ex, rows = levers.run_launch(ntasks=n, grid=n, wq=False, order=list(dup),
+                                 ctrl={"order_size": 0}, max_tasks=n)
+    missing = sorted(set(range(n)) - set(ex))
+    assert missing == [10]
+    r, h = divmod(10, 8)
+    assert torch.isnan(out[r, h * 4:(h + 1) * 4]).all()
+    keep = torch.ones(n, dtype=torch.bool)
+    keep[10] = False
+    o = out.view(24, 8, 4, 128)[:].reshape(n, 4, 128)
+    assert torch.equal(o[keep], base.view(n, 4, 128)[keep])
+    t = plane.read_timer()[:n].numpy()
+    assert t[10] == 0 and t[11] > 0
+
+
+def test_num_tasks_zero_takes_the_static_path():
+    b = _hetero(14)
+    n = 24 * 8
+    plane = SchedPlane(max_tasks=n)
+    base = run(b, plane=plane)
+    plane.set_num_tasks(0)
+    plane.set_order(torch.arange(n - 1, -1, -1))
+    plane.push()
+    plane.clear_timer()
+    # workers requested, but num_tasks 0 disarms the claim loop: full grid
+    assert torch.equal(run(b, plane=plane, workers=16), base)
+    assert int((plane.read_timer()[:n] > 0).sum()) == n
