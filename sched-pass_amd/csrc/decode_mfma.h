@@ -20,8 +20,8 @@
 //       wave instruction).
 //
 // A workgroup of NW waves runs one task = (request, kv-head); wave w streams
-// a contiguous slice of the task's pages with DEPTH pages of loads in flight
-// (register ring), and the wave states merge in LDS in fixed order. Nothing
+// pages w, w+NW, ... with DEPTH pages of loads in flight (register ring), and
+// the wave states merge in LDS in fixed order. Nothing
 // in the arithmetic depends on scheduling, so pi, the work queue and the
 // prefetch depth leave every output bit unchanged.
 //
@@ -77,10 +77,26 @@ __device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
   return __builtin_bit_cast(unsigned, v);
 }
 
-// x from lane (lane ^ 16) / (lane ^ 32), via the LDS crossbar with the byte
-// address precomputed once per lane.
-__device__ __forceinline__ float bperm(float x, int addr) {
-  return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(x)));
+// Reductions across the four 16-lane rows with the gfx950 row swaps (VALU,
+// no LDS traffic). v_permlane16_swap(x, x) leaves {x[row], x[row ^ 1]} in its
+// two results on every lane, v_permlane32_swap(x, x) {x[half], x[half ^ 1]};
+// combining the pair gives the pairwise max / sum, in the same operand order on
+// every lane.
+__device__ __forceinline__ float max_rows(float x) {
+  const unsigned u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+  const unsigned u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // 4 fp8 bytes -> 4 bf16 (exact), as two dwords.
@@ -94,8 +110,9 @@ __device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
 }
 
 struct MfmaTask {
-  uint32_t r, h, n, budget, p_begin, p_end;
-  int xor16, xor32;     // ds_bpermute byte addresses of lanes lane^16, lane^32
+  uint32_t r, h, n, budget;
+  uint32_t npages; // pages of the task that are read
+  uint32_t w;      // this wave: pages w, w + NW, w + 2 NW, ...
   const uint8_t *kbase; // K pool bytes + per-lane offset
   const uint8_t *vbase;
   int64_t kpage_bytes, khead_bytes, vpage_bytes, vhead_bytes;
@@ -175,9 +192,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
         s[v] = kNegInf;
     }
   }
-  float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  pm = fmaxf(pm, bperm(pm, T.xor16));
-  pm = fmaxf(pm, bperm(pm, T.xor32));
+  const float pm = max_rows(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
   const float mnew = fmaxf(S.m, pm);
   if (__builtin_amdgcn_ballot_w64(mnew > S.m)) {
     const float c = __builtin_amdgcn_exp2f(S.m - mnew);
@@ -214,28 +229,33 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   }
 }
 
-// Page ids of this wave's slice, 64 at a time in one VGPR (lane j holds the
-// id of slice page 64*blk + j).
+// Page ids of this wave's pages, 64 at a time in one VGPR (lane j holds the id
+// of the wave's page 64*blk + j, i.e. task page w + NW*(64*blk + j)).
+template <int NW>
 __device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T, uint32_t blk,
                                             uint32_t lane) {
-  const uint32_t idx = T.p_begin + 64u * blk + lane;
-  return idx < T.p_end ? page_of(P, T.r, idx) : 0;
+  const uint32_t idx = T.w + NW * (64u * blk + lane);
+  return idx < T.npages ? page_of(P, T.r, idx) : 0;
 }
 
-template <bool FP8, int DEPTH, bool NT>
+// Pages go to waves round-robin, so the assignment (and with it every
+// summation order) depends only on the page index, not on how many pages are
+// read: a task whose shed pages are loaded and masked gives the same bits as
+// one that skips them, and shed tasks stay balanced across the waves.
+template <bool FP8, int NW, int DEPTH, bool NT>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
-  const int npg = (int)T.p_end - (int)T.p_begin;
+  const int npg = T.npages > T.w ? (int)((T.npages - T.w + NW - 1) / NW) : 0;
   if (npg <= 0)
     return;
-  int32_t ptA = load_ids(P, T, 0, lane);
-  int32_t ptB = npg > 64 ? load_ids(P, T, 1, lane) : 0;
+  int32_t ptA = load_ids<NW>(P, T, 0, lane);
+  int32_t ptB = npg > 64 ? load_ids<NW>(P, T, 1, lane) : 0;
   int blk = 0, li = 0;
   auto next_id = [&]() -> int32_t {
     if ((li >> 6) != blk) {
       ptA = ptB;
       ++blk;
-      ptB = (blk + 1) * 64 < npg ? load_ids(P, T, blk + 1, lane) : 0;
+      ptB = (blk + 1) * 64 < npg ? load_ids<NW>(P, T, blk + 1, lane) : 0;
     }
     const int32_t id = __builtin_amdgcn_readlane(ptA, li & 63);
     ++li;
@@ -255,7 +275,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     for (int s = 0; s < DEPTH; ++s) {
       const int j = it + s;
       if (j < npg) {
-        compute_page<FP8>(P, T, S, buf[s], pid[s], T.p_begin + (uint32_t)j, g4);
+        compute_page<FP8>(P, T, S, buf[s], pid[s], T.w + NW * (uint32_t)j, g4);
         if (j + DEPTH < npg) {
           pid[s] = next_id();
           issue_page<FP8, NT>(T, pid[s], buf[s]);
@@ -288,14 +308,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     const TaskPolicy pol = task_policy(P.L, task);
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;
-    const uint32_t npages = (load_extent(P, T.n, pol.budget) + 15u) / 16u;
-    const uint32_t per = (npages + NW - 1) / NW;
-    T.p_begin = min(npages, w * per);
-    T.p_end = min(npages, T.p_begin + per);
+    T.npages = (load_extent(P, T.n, pol.budget) + 15u) / 16u;
+    T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
     T.vbase = static_cast<const uint8_t *>(P.v_pool) + (int64_t)c16 * P.vds * EB + 4u * g4 * EB;
-    T.xor16 = (int)((lane ^ 16u) << 2);
-    T.xor32 = (int)((lane ^ 32u) << 2);
     T.kpage_bytes = P.kps * EB;
     T.khead_bytes = P.khs * EB * T.h;
     T.vpage_bytes = P.vps * EB;
@@ -326,15 +342,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
 
     if (pol.urgent)
-      stream_pages<FP8, DEPTH_U, false>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, false>(P, T, S, lane, g4);
     else if (pol.polite)
-      stream_pages<FP8, DEPTH_S, true>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, true>(P, T, S, lane, g4);
     else
-      stream_pages<FP8, DEPTH_S, false>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, false>(P, T, S, lane, g4);
 
     // Merge: l over the 4 lane rows, then the NW wave states in fixed order.
-    float lt = S.lsum + bperm(S.lsum, T.xor16);
-    lt += bperm(lt, T.xor32);
+    const float lt = sum_rows(S.lsum);
     if (c16 < G) {
       if (g4 == 0) {
         s_m[w][c16] = S.m;

@@ -21,6 +21,8 @@
 // the reference's skip semantics (test/paged_decode.cu:136-137).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace schedpd {
@@ -69,7 +71,10 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
   constexpr int EPL = D >= 64 ? D / 64 : 1;
   constexpr int VN = Vec16<KVT>::N;
   __shared__ float s_q[GH][D];
-  __shared__ float s_acc[NW][GH][D];
+  // Linear mode accumulates in double: an unnormalised sum of thousands of
+  // products loses the fp32 tolerance in float; the mode is bandwidth-bound.
+  using Acc = typename std::conditional<LINEAR, double, float>::type;
+  __shared__ Acc s_acc[NW][GH][D];
   __shared__ float s_m[NW][GH];
   __shared__ float s_l[NW][GH];
 
@@ -97,7 +102,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
     __syncthreads();
 
     float m[NP], lsum[NP];
-    float acc[GH][EPL];
+    Acc acc[GH][EPL];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       m[k] = kMInit;
@@ -107,7 +112,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
     for (int g = 0; g < GH; ++g)
 #pragma unroll
       for (int e = 0; e < EPL; ++e)
-        acc[g][e] = 0.f;
+        acc[g][e] = Acc(0);
 
     const uint32_t nchunks = (nload + 15u) / 16u;
     for (uint32_t c = w; c < nchunks; c += NW) {
@@ -180,7 +185,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
           const float wi = ki ? P.lin_w[P.lin_w_period ? ti % P.lin_w_period : ti] : 0.f;
 #pragma unroll
           for (int e = 0; e < EPL; ++e)
-            acc[0][e] += wi * v[i][e];
+            acc[0][e] += (double)wi * (double)v[i][e];
         }
       } else {
 #pragma unroll
@@ -219,11 +224,11 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
     __syncthreads();
     if (LINEAR) {
       for (uint32_t j = threadIdx.x; j < D; j += 256) {
-        float a = 0.f;
+        double a = 0.0;
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
           a += s_acc[ww][0][j];
-        store_out(P, ((int64_t)r * P.Hkv + h) * D + j, a);
+        store_out(P, ((int64_t)r * P.Hkv + h) * D + j, (float)a);
       }
     } else {
       for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256) {
@@ -237,7 +242,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
         for (int ww = 0; ww < NW; ++ww) {
           const float e = exp2f(s_m[ww][g] - M);
           Lt += s_l[ww][g] * e;
-          A += s_acc[ww][g][j] * e;
+          A += (float)s_acc[ww][g][j] * e;
         }
         store_out(P, ((int64_t)r * P.Hq + h * G + g) * D + j, A / Lt);
       }

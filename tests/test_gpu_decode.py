@@ -137,9 +137,13 @@ def test_shed_softmax_matches_truncated_reference(scope, kvt):
     e = mixed_err(out.cpu(), ref(b, plane, tau_scope=scope))
     print(f"shed scope {scope} {kvt} err {e:.3g}")
     assert e <= TOL_BF16
-    # loading the shed pages and masking them gives the same bits
+    # loading the shed pages and masking them gives the same bits (MFMA and VALU)
     same = run(b, plane=plane, tau_scope=scope, flags=abi.FLAG_SHED_LOADS)
     assert torch.equal(out, same)
+    v = run(b, plane=plane, tau_scope=scope, flags=abi.FLAG_FORCE_VALU)
+    assert mixed_err(v.cpu(), ref(b, plane, tau_scope=scope)) <= TOL_BF16
+    assert torch.equal(v, run(b, plane=plane, tau_scope=scope,
+                              flags=abi.FLAG_FORCE_VALU | abi.FLAG_SHED_LOADS))
 
 
 @pytest.mark.parametrize("kvt", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
