@@ -82,49 +82,78 @@ def bench_uniform(args, torch, sched_pd, workloads):
     }
 
 
-def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu):
+TILE_PAGES = 64  # split-KV tile (pages) for the heterogeneous batch
+
+
+def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):
+    """Min over `reps` of the mean of `launches` back-to-back launches (HIP
+    events on the launch stream), microseconds."""
+    for _ in range(3):
+        sched_pd.launch(a, stream)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(launches):
+            sched_pd.launch(a, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / launches)
+    return best * 1000.0
+
+
+def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES):
+    """256 requests, lognormal contexts; pi by a uniform-random urgency per
+    task. Static grid (one workgroup per task) against the ticket work queue
+    with W = 2 x CU persistent workers; the queue claims split-KV tiles of
+    `tile_pages` pages. The other two corners are reported as well."""
     import numpy as np
     b = workloads.workload("llama3_8b_hetero", seed=0)
-    n = 256 * 8
-    plane = SchedPlane(max_tasks=n)
-    order = np.argsort(-b["urgency"], kind="stable").astype(np.int32)  # pi by urgency q
-    plane.install_order(order, n)
-    plane.set_num_tasks(n)
-    plane.push()
+    ntask = 256 * 8
+    q = b["urgency"]
     W = 2 * cu
     out = torch.empty(256, 32, 128, dtype=torch.bfloat16, device="cuda")
-    a_static = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
-                                   b["ctx_lens"], out=out, plane=plane, workers=0)
-    a_wq = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
-                               b["ctx_lens"], out=out, plane=plane, workers=W)
+    tiles = sched_pd.plan_tiles(b["ctx_lens"], 16, tile_pages, 8)
+    nt = tiles.shape[0]
+    if nt > 16384:
+        raise ValueError(f"{nt} tiles exceed the 16384-row plane; use larger tiles")
+    p_task = SchedPlane(max_tasks=ntask)
+    p_task.install_order(np.argsort(-q, kind="stable").astype(np.int32), ntask)
+    p_task.set_num_tasks(ntask)
+    p_task.push()
+    p_tile = SchedPlane(max_tasks=max(nt, ntask))
+    p_tile.install_order(sched_pd.tile_order_by_task_key(tiles, q), nt)
+    p_tile.set_num_tasks(nt)
+    p_tile.push()
+    p_task.reset_queue(W)
+    p_tile.reset_queue(W)
+    common = dict(out=out)
+    A = {
+        "static_task": sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                           b["ctx_lens"], plane=p_task, workers=0, **common),
+        "wq_task": sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                       b["ctx_lens"], plane=p_task, workers=W, **common),
+        "static_tiles": sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                            b["ctx_lens"], plane=p_tile, workers=0, tiles=tiles,
+                                            tile_pages=tile_pages, **common),
+        "wq_tiles": sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                        b["ctx_lens"], plane=p_tile, workers=W, tiles=tiles,
+                                        tile_pages=tile_pages, **common),
+    }
     stream = torch.cuda.current_stream()
-    plane.reset_queue(W)
-    res = {}
-    for name, a in (("static", a_static), ("ticket_wq", a_wq)):
-        for _ in range(3):
-            sched_pd.launch(a, stream)
-        torch.cuda.synchronize()
-        best = float("inf")
-        for _ in range(5):  # min over repeats of 10 back-to-back launches
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(10):
-                sched_pd.launch(a, stream)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            best = min(best, e0.elapsed_time(e1) / 10)
-        res[name] = best * 1000.0
+    res = {k: round(_makespan_us(torch, sched_pd, a, stream), 2) for k, a in A.items()}
     # per-task residency of one work-queue step from the timer rows
-    plane.clear_timer()
-    sched_pd.launch(a_wq, stream)
+    p_tile.clear_timer()
+    sched_pd.launch(A["wq_tiles"], stream)
     torch.cuda.synchronize()
-    cyc = plane.read_timer()[:n].numpy()
+    cyc = p_tile.read_timer()[:ntask].numpy()
     kv = b["kv_bytes"]
     return {
-        "static_us": round(res["static"], 2), "ticket_wq_us": round(res["ticket_wq"], 2),
-        "cut_pct": round(100.0 * (res["static"] - res["ticket_wq"]) / res["static"], 2),
-        "workers": W, "tasks": n, "kv_bytes": kv,
-        "wq_kv_gbs": round(kv / (res["ticket_wq"] * 1e-6) / 1e9, 1),
+        "static_us": res["static_task"], "ticket_wq_us": res["wq_tiles"],
+        "cut_pct": round(100.0 * (res["static_task"] - res["wq_tiles"]) / res["static_task"], 2),
+        "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
+        "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
         "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                              "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())},
     }

@@ -178,7 +178,7 @@ typedef struct SchedDecodeArgs {
   float sm_scale;        /* 0 = 1/sqrt(head_dim) */
   float policy_dT, policy_dR, policy_H; /* urgent iff q*dT - lambda_bw*dR - H > 0 */
   uint32_t lin_w_period; /* linear mode: w index = pos % period (0 = pos) */
-  uint32_t _reserved;
+  uint32_t tile_pages;   /* split-KV tile size in pages (with `tiles`) */
   const void *q;         /* [num_requests][num_q_heads][head_dim] */
   void *out;             /* softmax: [R][Hq][d]; linear: [R][Hkv][d] */
   const void *k_pool;
@@ -196,6 +196,21 @@ typedef struct SchedDecodeArgs {
   const void *ctrl;           /* SchedCtrl layout, rows[max_tasks] */
   unsigned long long *timer;  /* u64[max_tasks] residency accumulators */
   uint32_t *queue;            /* ticket counter */
+  /* Split-KV work items (NULL = one work item per task). tiles[2*i],
+   * tiles[2*i+1] = (task, chunk) of work item i; chunk c of a task covers
+   * its pages [c*tile_pages, (c+1)*tile_pages). The list is task-major: the
+   * ceil(ceil(ctx/page_size)/tile_pages) chunks of a task (at least 1) are
+   * consecutive and in chunk order. pi, num_tasks, order_size and the ticket
+   * queue count work items; policy rows and timer rows stay per task. */
+  const int32_t *tiles;
+  uint32_t num_tiles;
+  uint32_t _pad0;
+  /* Device scratch for split tasks (sched_paged_decode_workspace_bytes):
+   * per-task arrival counters, then per-work-item partial results. The
+   * counters must be zero before the first launch; each launch leaves them
+   * zero. Launches sharing one workspace must not overlap. */
+  void *workspace;
+  uint64_t workspace_bytes;
 } SchedDecodeArgs;
 
 /* Fill *a with defaults (ABI version, F32, prefix tau, dT=dR=1, H=0.25,
@@ -207,6 +222,10 @@ void sched_pd_default_args(SchedDecodeArgs *a);
  * (test/paged_decode.cu:207-213, test/hetero_batch.cu:130-134,
  * python/kernels/paged_softmax.cu:47-54). */
 int sched_paged_decode(const SchedDecodeArgs *a, void *stream);
+
+/* Bytes of workspace a launch with these arguments needs (0 without tiles,
+ * or -1 on invalid arguments). */
+int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a);
 
 /* Workgroups per CU of the kernel `a` selects (0 = unknown). Counterpart of
  * reference paged_softmax_occupancy (python/kernels/paged_softmax.cu:61-67). */

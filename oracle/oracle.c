@@ -298,6 +298,11 @@ int oracle_args_layout(int64_t *out, int n) {
       (int64_t)offsetof(SchedDecodeArgs, order),
       (int64_t)offsetof(SchedDecodeArgs, queue),
       (int64_t)sizeof(SchedCtrl),
+      (int64_t)offsetof(SchedDecodeArgs, tile_pages),
+      (int64_t)offsetof(SchedDecodeArgs, tiles),
+      (int64_t)offsetof(SchedDecodeArgs, num_tiles),
+      (int64_t)offsetof(SchedDecodeArgs, workspace),
+      (int64_t)offsetof(SchedDecodeArgs, workspace_bytes),
   };
   int m = (int)(sizeof v / sizeof v[0]);
   for (int i = 0; i < m && i < n; ++i)

@@ -1,0 +1,165 @@
+// combine.h -- end of one work item: merge the wave states of the workgroup
+// (fixed wave order), then either write the task's output (the task is one
+// work item) or publish the work item's partial and, in the work item that
+// completes the task, merge all partials of the task in chunk order.
+//
+// The merge order depends only on the task's chunking, never on which
+// workgroup finished last, so split tasks stay bit-reproducible under any pi
+// or work-queue schedule.
+//
+// Cross-XCD handoff: every thread publishes its partial, then an agent-scope
+// release fence (L2 write-back) precedes the arrival atomic; the completing
+// work item takes an agent-scope acquire fence (L2 invalidate) before reading
+// the other partials. The arrival counter is reset to 0 by the work item that
+// completes the task: every other chunk has already arrived.
+#pragma once
+
+#include "common.h"
+
+namespace schedpd {
+
+// Softmax: acc is unnormalised with running max m and sum l per head.
+// Linear: acc is a plain sum (m, l unused).
+template <int NW, int GMAX, int D, typename AccT, bool LINEAR>
+__device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint32_t task,
+                                            uint32_t chunk, uint32_t nchunks, uint32_t r,
+                                            uint32_t h, uint32_t G, AccT (*s_acc)[GMAX][D],
+                                            float (*s_m)[GMAX], float (*s_l)[GMAX]) {
+  constexpr uint32_t NT = NW * 64;
+  const int64_t orow = LINEAR ? ((int64_t)r * P.Hkv + h) : ((int64_t)r * P.Hq + h * G);
+  if (nchunks <= 1) {
+    for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
+      const uint32_t g = idx / D, j = idx % D;
+      if (LINEAR) {
+        AccT a = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+          a += s_acc[w][0][j];
+        store_out(P, orow * D + j, (float)a);
+      } else {
+        float M = s_m[0][g];
+#pragma unroll
+        for (int w = 1; w < NW; ++w)
+          M = fmaxf(M, s_m[w][g]);
+        float Lt = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float e = __builtin_amdgcn_exp2f(s_m[w][g] - M);
+          Lt += s_l[w][g] * e;
+          A += (float)s_acc[w][g][j] * e;
+        }
+        store_out(P, (orow + g) * D + j, A / Lt);
+      }
+    }
+    return;
+  }
+
+  // Publish this work item's partial.
+  AccT *pacc = static_cast<AccT *>(P.ws_acc) + (size_t)wi * G * D;
+  float *pml = P.ws_ml + (size_t)wi * G * 2;
+  for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
+    const uint32_t g = idx / D, j = idx % D;
+    if (LINEAR) {
+      AccT a = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        a += s_acc[w][0][j];
+      pacc[j] = a;
+    } else {
+      float M = s_m[0][g];
+#pragma unroll
+      for (int w = 1; w < NW; ++w)
+        M = fmaxf(M, s_m[w][g]);
+      float Lt = 0.f, A = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float e = __builtin_amdgcn_exp2f(s_m[w][g] - M);
+        Lt += s_l[w][g] * e;
+        A += (float)s_acc[w][g][j] * e;
+      }
+      pacc[g * D + j] = A;
+      if (j == 0) {
+        pml[2 * g] = M;
+        pml[2 * g + 1] = Lt;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  __shared__ uint32_t s_last;
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(P.ws_count + task, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == nchunks - 1u;
+    if (last)
+      __hip_atomic_store(P.ws_count + task, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last)
+    return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const uint32_t base = wi - chunk; // task-major list: chunk c is work item base + c
+  for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
+    const uint32_t g = idx / D, j = idx % D;
+    if (LINEAR) {
+      AccT a = 0;
+      for (uint32_t c = 0; c < nchunks; ++c)
+        a += static_cast<const AccT *>(P.ws_acc)[(size_t)(base + c) * G * D + j];
+      store_out(P, orow * D + j, (float)a);
+    } else {
+      float M = P.ws_ml[(size_t)base * G * 2 + 2 * g];
+      for (uint32_t c = 1; c < nchunks; ++c)
+        M = fmaxf(M, P.ws_ml[(size_t)(base + c) * G * 2 + 2 * g]);
+      float Lt = 0.f, A = 0.f;
+      for (uint32_t c = 0; c < nchunks; ++c) {
+        const float *ml = P.ws_ml + (size_t)(base + c) * G * 2 + 2 * g;
+        const float e = __builtin_amdgcn_exp2f(ml[0] - M);
+        Lt += ml[1] * e;
+        A += (float)static_cast<const AccT *>(P.ws_acc)[(size_t)(base + c) * G * D + g * D + j] * e;
+      }
+      store_out(P, (orow + g) * D + j, A / Lt);
+    }
+  }
+}
+
+// Work item -> (task, chunk): the tile list, or work item = task.
+__device__ __forceinline__ void item_task(const KParams &P, uint32_t wi, uint32_t &task,
+                                          uint32_t &chunk) {
+  if (P.tiles == nullptr) {
+    task = wi;
+    chunk = 0u;
+  } else {
+    task = (uint32_t)P.tiles[2 * wi];
+    chunk = (uint32_t)P.tiles[2 * wi + 1];
+  }
+}
+
+// Chunks of a task with n context tokens, and the page range [p0, p1) of
+// chunk `chunk` within the npages_load pages that are read.
+struct ItemRange {
+  uint32_t nchunks, p0, p1;
+};
+
+__device__ __forceinline__ ItemRange item_range(const KParams &P, uint32_t chunk, uint32_t n,
+                                                uint32_t npages_load) {
+  if (P.tiles == nullptr)
+    return ItemRange{1u, 0u, npages_load};
+  const uint32_t npages_ctx = (n + P.ps - 1) / P.ps;
+  ItemRange it;
+  it.nchunks = npages_ctx ? (npages_ctx + P.tile_pages - 1) / P.tile_pages : 1u;
+  it.p0 = min(chunk * P.tile_pages, npages_load);
+  it.p1 = min(it.p0 + P.tile_pages, npages_load);
+  return it;
+}
+
+// A work item whose chunk cannot belong to a task-major list (chunk past the
+// task's chunk count, before the start of the list, or a task whose chunks
+// would run past the end) is skipped: the merge only ever reads work items
+// [wi - chunk, wi - chunk + nchunks), which this keeps inside the list.
+__device__ __forceinline__ bool item_ok(const KParams &P, uint32_t wi, uint32_t chunk,
+                                        const ItemRange &R) {
+  return chunk < R.nchunks && chunk <= wi && (wi - chunk) + R.nchunks <= P.L.nitems;
+}
+
+} // namespace schedpd

@@ -28,6 +28,13 @@ struct KParams {
   uint32_t ps, bt_stride, tau_scope;
   uint32_t q_f32, o_f32, ctx_in_pages, shed_loads, lin_w_period;
   float scale_log2; // softmax scale * log2(e): scores live in the exp2 domain
+  // split-KV work items (tiles == nullptr: one work item per task)
+  const int32_t *tiles;
+  uint32_t ntasks;     // requests x kv-heads
+  uint32_t tile_pages;
+  uint32_t *ws_count;  // per-task arrival counters
+  float *ws_ml;        // per-work-item (m, l) per head
+  void *ws_acc;        // per-work-item partial accumulators
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();

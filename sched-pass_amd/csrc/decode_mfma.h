@@ -31,7 +31,7 @@
 // the score and the V scale multiplies p before PV, so no element is scaled.
 #pragma once
 
-#include "common.h"
+#include "combine.h"
 
 namespace schedpd {
 
@@ -111,8 +111,8 @@ __device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
 
 struct MfmaTask {
   uint32_t r, h, n, budget;
-  uint32_t npages; // pages of the task that are read
-  uint32_t w;      // this wave: pages w, w + NW, w + 2 NW, ...
+  uint32_t p0, p1; // pages [p0, p1) of the task are read by this work item
+  uint32_t w;      // this wave: pages p0 + w, p0 + w + NW, ...
   const uint8_t *kbase; // K pool bytes + per-lane offset
   const uint8_t *vbase;
   int64_t kpage_bytes, khead_bytes, vpage_bytes, vhead_bytes;
@@ -230,12 +230,12 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 }
 
 // Page ids of this wave's pages, 64 at a time in one VGPR (lane j holds the id
-// of the wave's page 64*blk + j, i.e. task page w + NW*(64*blk + j)).
+// of the wave's page 64*blk + j, i.e. task page p0 + w + NW*(64*blk + j)).
 template <int NW>
 __device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T, uint32_t blk,
                                             uint32_t lane) {
-  const uint32_t idx = T.w + NW * (64u * blk + lane);
-  return idx < T.npages ? page_of(P, T.r, idx) : 0;
+  const uint32_t idx = T.p0 + T.w + NW * (64u * blk + lane);
+  return idx < T.p1 ? page_of(P, T.r, idx) : 0;
 }
 
 // Pages go to waves round-robin, so the assignment (and with it every
@@ -245,7 +245,8 @@ __device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T,
 template <bool FP8, int NW, int DEPTH, bool NT>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
-  const int npg = T.npages > T.w ? (int)((T.npages - T.w + NW - 1) / NW) : 0;
+  const uint32_t span = T.p1 - T.p0;
+  const int npg = span > T.w ? (int)((span - T.w + NW - 1) / NW) : 0;
   if (npg <= 0)
     return;
   int32_t ptA = load_ids<NW>(P, T, 0, lane);
@@ -275,7 +276,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     for (int s = 0; s < DEPTH; ++s) {
       const int j = it + s;
       if (j < npg) {
-        compute_page<FP8>(P, T, S, buf[s], pid[s], T.w + NW * (uint32_t)j, g4);
+        compute_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, g4);
         if (j + DEPTH < npg) {
           pid[s] = next_id();
           issue_page<FP8, NT>(T, pid[s], buf[s]);
@@ -298,17 +299,25 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
   const bool toff = timer_off_latched(P.L);
   constexpr uint32_t EB = FP8 ? 1u : 2u; // bytes per KV element
 
-  run_tasks(P.L, [&](uint32_t task) {
-    if (task >= P.L.ntasks)
+  run_tasks(P.L, [&](uint32_t wi) {
+    if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
+    uint32_t task, chunk;
+    item_task(P, wi, task, chunk);
+    if (task >= P.ntasks)
+      return;
     MfmaTask T;
     T.r = task / P.Hkv;
     T.h = task % P.Hkv;
     const TaskPolicy pol = task_policy(P.L, task);
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;
-    T.npages = (load_extent(P, T.n, pol.budget) + 15u) / 16u;
+    const ItemRange R = item_range(P, chunk, T.n, (load_extent(P, T.n, pol.budget) + 15u) / 16u);
+    if (!item_ok(P, wi, chunk, R))
+      return;
+    T.p0 = R.p0;
+    T.p1 = R.p1;
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
     T.vbase = static_cast<const uint8_t *>(P.v_pool) + (int64_t)c16 * P.vds * EB + 4u * g4 * EB;
@@ -348,7 +357,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     else
       stream_pages<FP8, NW, DEPTH_S, false>(P, T, S, lane, g4);
 
-    // Merge: l over the 4 lane rows, then the NW wave states in fixed order.
+    // Wave states to LDS (l summed over the 4 lane rows first), then the
+    // work item's result: output, or partial + fixed-order task merge.
     const float lt = sum_rows(S.lsum);
     if (c16 < G) {
       if (g4 == 0) {
@@ -360,21 +370,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
         *reinterpret_cast<f32x4_t *>(&s_acc[w][c16][16 * blk + 4 * g4]) = S.acc[blk];
     }
     __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < G * 128u; idx += NW * 64) {
-      const uint32_t g = idx >> 7, j = idx & 127u;
-      float M = s_m[0][g];
-#pragma unroll
-      for (int ww = 1; ww < NW; ++ww)
-        M = fmaxf(M, s_m[ww][g]);
-      float Lt = 0.f, A = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < NW; ++ww) {
-        const float e = __builtin_amdgcn_exp2f(s_m[ww][g] - M);
-        Lt += s_l[ww][g] * e;
-        A += s_acc[ww][g][j] * e;
-      }
-      store_out(P, ((int64_t)T.r * P.Hq + T.h * G + g) * 128 + j, A / Lt);
-    }
+    finish_item<NW, GMAX, 128, float, false>(P, wi, task, chunk, R.nchunks, T.r, T.h, G, s_acc,
+                                             s_m, s_l);
     timer_commit(P.L, toff, task, t0);
   });
 }

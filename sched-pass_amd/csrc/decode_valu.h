@@ -23,7 +23,7 @@
 
 #include <type_traits>
 
-#include "common.h"
+#include "combine.h"
 
 namespace schedpd {
 
@@ -83,14 +83,21 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
   const uint32_t i16 = lane & 15u, slot = lane >> 4;
   const bool toff = timer_off_latched(P.L);
 
-  run_tasks(P.L, [&](uint32_t task) {
-    if (task >= P.L.ntasks)
+  run_tasks(P.L, [&](uint32_t wi) {
+    if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
+    uint32_t task, chunk;
+    item_task(P, wi, task, chunk);
+    if (task >= P.ntasks)
+      return;
     const uint32_t r = task / P.Hkv, h = task % P.Hkv;
     const TaskPolicy pol = task_policy(P.L, task);
     const uint32_t n = ctx_tokens(P, r);
     const uint32_t nload = load_extent(P, n, pol.budget);
+    const ItemRange R = item_range(P, chunk, n, (nload + P.ps - 1) / P.ps);
+    if (!item_ok(P, wi, chunk, R))
+      return;
     const uint32_t G = LINEAR ? 1u : P.G;
     const bool fp8 = sizeof(KVT) == 1;
 
@@ -114,8 +121,10 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
       for (int e = 0; e < EPL; ++e)
         acc[g][e] = Acc(0);
 
-    const uint32_t nchunks = (nload + 15u) / 16u;
-    for (uint32_t c = w; c < nchunks; c += NW) {
+    // 16-token chunks of this work item's pages [p0, p1), round-robin over waves
+    const uint32_t cpp = P.ps / 16u;
+    const uint32_t c_end = (min(R.p1 * P.ps, nload) + 15u) / 16u;
+    for (uint32_t c = R.p0 * cpp + w; c < c_end; c += NW) {
       const uint32_t pos0 = c * 16u, b = pos0 / P.ps, o = pos0 % P.ps;
       const int64_t page = page_of(P, r, b);
       const float ks = (fp8 && P.k_scale) ? P.k_scale[page * P.Hkv + h] : 1.f;
@@ -222,31 +231,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
       }
     }
     __syncthreads();
-    if (LINEAR) {
-      for (uint32_t j = threadIdx.x; j < D; j += 256) {
-        double a = 0.0;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-          a += s_acc[ww][0][j];
-        store_out(P, ((int64_t)r * P.Hkv + h) * D + j, (float)a);
-      }
-    } else {
-      for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256) {
-        const uint32_t g = idx / D, j = idx % D;
-        float M = s_m[0][g];
-#pragma unroll
-        for (int ww = 1; ww < NW; ++ww)
-          M = fmaxf(M, s_m[ww][g]);
-        float Lt = 0.f, A = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-          const float e = exp2f(s_m[ww][g] - M);
-          Lt += s_l[ww][g] * e;
-          A += (float)s_acc[ww][g][j] * e;
-        }
-        store_out(P, ((int64_t)r * P.Hq + h * G + g) * D + j, A / Lt);
-      }
-    }
+    finish_item<NW, GH, D, Acc, LINEAR>(P, wi, task, chunk, R.nchunks, r, h, G, s_acc, s_m, s_l);
     timer_commit(P.L, toff, task, t0);
   });
 }

@@ -47,6 +47,27 @@ uint32_t elem_bytes(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+uint64_t round256(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
+
+// Workspace layout for split tasks: [counters: ntasks u32][(m, l): items x G
+// x 2 f32][partials: items x G x d x (f32 softmax | f64 linear)], each region
+// 256-byte aligned.
+struct WsLayout {
+  uint64_t count_off, ml_off, acc_off, total;
+};
+
+WsLayout ws_layout(const SchedDecodeArgs *a) {
+  const bool linear = a->mode == SCHED_PD_LINEAR;
+  const uint64_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
+  const uint64_t ntasks = (uint64_t)a->num_requests * a->num_kv_heads;
+  WsLayout L;
+  L.count_off = 0;
+  L.ml_off = round256(ntasks * 4u);
+  L.acc_off = L.ml_off + round256((uint64_t)a->num_tiles * G * 8u);
+  L.total = L.acc_off + (uint64_t)a->num_tiles * G * a->head_dim * (linear ? 8u : 4u);
+  return L;
+}
+
 // The MFMA kernel's shape: bf16/fp8 KV, d 128, page 16, K rows dims-contiguous,
 // V d-major 16-token rows, bf16 Q, G <= 16, 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
@@ -134,7 +155,24 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     kp->L.queue = a->queue;
     kp->L.max_tasks = a->max_tasks;
   }
-  kp->L.ntasks = a->num_requests * a->num_kv_heads;
+  kp->ntasks = a->num_requests * a->num_kv_heads;
+  kp->L.nitems = kp->ntasks;
+  if (a->tiles) {
+    if (a->num_tiles == 0 || a->tile_pages == 0)
+      return set_error(hipErrorInvalidValue, "tiles need num_tiles > 0 and tile_pages > 0");
+    const WsLayout W = ws_layout(a);
+    if (!a->workspace || a->workspace_bytes < W.total || ((uintptr_t)a->workspace & 255u))
+      return set_error(hipErrorInvalidValue,
+                       "split tasks need a 256-byte aligned workspace of %llu bytes (got %llu)",
+                       (unsigned long long)W.total, (unsigned long long)a->workspace_bytes);
+    uint8_t *ws = static_cast<uint8_t *>(a->workspace);
+    kp->tiles = a->tiles;
+    kp->tile_pages = a->tile_pages;
+    kp->L.nitems = a->num_tiles;
+    kp->ws_count = reinterpret_cast<uint32_t *>(ws + W.count_off);
+    kp->ws_ml = reinterpret_cast<float *>(ws + W.ml_off);
+    kp->ws_acc = ws + W.acc_off;
+  }
   kp->L.wallclock = (a->flags & SCHED_PD_FLAG_WALLCLOCK) ? 1u : 0u;
   kp->L.dT = a->policy_dT;
   kp->L.dR = a->policy_dR;
@@ -224,10 +262,10 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   int rc = prepare(a, &kp, &sel);
   if (rc)
     return rc;
-  const uint32_t ntasks = kp.L.ntasks;
-  if (ntasks == 0)
+  const uint32_t nitems = kp.L.nitems;
+  if (nitems == 0 || kp.ntasks == 0)
     return 0;
-  uint32_t grid = ntasks;
+  uint32_t grid = nitems;
   // A work-queue launch needs the queue and ctrl tables; without them the
   // kernel's stock path serves one task per workgroup, so the grid must then
   // cover every task. For the runtime's tables the pushed num_tasks is known
@@ -243,6 +281,15 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   if (e != hipSuccess)
     return set_error(e, "kernel launch failed: %s", hipGetErrorString(e));
   return 0;
+}
+
+int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a) {
+  if (a == nullptr || a->num_kv_heads == 0 ||
+      (a->mode == SCHED_PD_SOFTMAX && (a->num_q_heads == 0 || a->num_q_heads % a->num_kv_heads)))
+    return -1;
+  if (a->tiles == nullptr)
+    return 0;
+  return (int64_t)ws_layout(a).total;
 }
 
 int sched_paged_decode_occupancy(const SchedDecodeArgs *a) {

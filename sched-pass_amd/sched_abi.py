@@ -51,7 +51,7 @@ class SchedDecodeArgs(ctypes.Structure):
         ("max_tasks", _u32),
         ("sm_scale", _f32), ("policy_dT", _f32), ("policy_dR", _f32),
         ("policy_H", _f32),
-        ("lin_w_period", _u32), ("_reserved", _u32),
+        ("lin_w_period", _u32), ("tile_pages", _u32),
         ("q", _p), ("out", _p), ("k_pool", _p), ("v_pool", _p),
         ("k_page_stride", _i64), ("k_head_stride", _i64), ("k_tok_stride", _i64),
         ("v_page_stride", _i64), ("v_head_stride", _i64), ("v_tok_stride", _i64),
@@ -60,6 +60,8 @@ class SchedDecodeArgs(ctypes.Structure):
         ("block_table", _p), ("page_indptr", _p), ("ctx_lens", _p),
         ("lin_w", _p),
         ("order", _p), ("ctrl", _p), ("timer", _p), ("queue", _p),
+        ("tiles", _p), ("num_tiles", _u32), ("_pad0", _u32),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_uint64),
     ]
 
 
@@ -97,6 +99,7 @@ SIGNATURES = {
     "sched_pd_default_args": (None, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),
     "sched_paged_decode_occupancy": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
+    "sched_paged_decode_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_kernel_kind": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_pd_cu_count": (ctypes.c_int, []),
     "sched_pd_last_error": (ctypes.c_char_p, []),

@@ -15,7 +15,9 @@ from a SchedPlane (its device tables), from the C runtime's armed slots
 from __future__ import annotations
 
 import ctypes
+import math
 
+import numpy as np
 import torch
 
 import sched_abi as abi
@@ -45,8 +47,11 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                sm_scale=None, k_scale=None, v_scale=None,
                tau_scope=abi.TAU_PREFIX, lin_w=None, lin_w_period=0,
                plane=None, rt_tables=False, workers=0, pf_dist=0, flags=0,
-               policy=(1.0, 1.0, 0.25)) -> abi.SchedDecodeArgs:
-    """Fill a SchedDecodeArgs from tensors (no launch)."""
+               policy=(1.0, 1.0, 0.25), tiles=None, tile_pages=0,
+               workspace=None) -> abi.SchedDecodeArgs:
+    """Fill a SchedDecodeArgs from tensors (no launch). With `tiles` (from
+    plan_tiles) long tasks run as several work items; the workspace is taken
+    from a per-device cache unless one is given."""
     a = abi.default_args()
     linear = mode == abi.LINEAR
     a.mode = mode
@@ -98,7 +103,7 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                     (block_table, "block_table"), (ctx_lens, "ctx_lens"),
                     (page_indptr, "page_indptr"), (k_scale, "k_scale"),
                     (v_scale, "v_scale"), (lin_w, "lin_w")):
-        if t is not None and (linear is False or what not in ("q", "k_pool")):
+        if t is not None and not (linear and what in ("q", "k_pool")):
             _need_cuda(t, what)
     for t, what in ((block_table, "block_table"), (ctx_lens, "ctx_lens"),
                     (page_indptr, "page_indptr")):
@@ -118,6 +123,24 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
     a.pf_dist = pf_dist
     a.policy_dT, a.policy_dR, a.policy_H = (float(x) for x in policy)
     a.flags = flags
+    if tiles is not None:
+        _need_cuda(tiles, "tiles")
+        if tiles.dtype != torch.int32 or tiles.dim() != 2 or tiles.shape[1] != 2 \
+                or not tiles.is_contiguous():
+            raise ValueError("tiles must be a contiguous int32 [num_tiles, 2] tensor")
+        a.tiles = _ptr(tiles)
+        a.num_tiles = tiles.shape[0]
+        a.tile_pages = int(tile_pages)
+        need = abi.load_library().sched_paged_decode_workspace_bytes(ctypes.byref(a))
+        if need < 0:
+            raise RuntimeError(abi.last_error())
+        if workspace is None:
+            workspace = workspace_for(need, v_pool.device,
+                                      count_bytes=4 * a.num_requests * a.num_kv_heads)
+        elif workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace holds {workspace.numel()} bytes, needs {need}")
+        a.workspace = _ptr(workspace)
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
     if rt_tables:
         a.flags |= abi.FLAG_RT_TABLES
         a.workers = workers
@@ -133,6 +156,57 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
         a.max_tasks = 0
         a.workers = 0
     return a
+
+
+_WS = {}
+
+
+def workspace_for(nbytes: int, device, count_bytes: int = 0) -> torch.Tensor:
+    """A device workspace of at least `nbytes` whose first `count_bytes` (the
+    per-task arrival counters) are zero, cached per device. A launch leaves
+    its counters zero but writes partials right after them, so the zeroed
+    prefix is tracked and cleared again when a launch needs more counters.
+    Launches that share the workspace must not overlap."""
+    dev = torch.device(device)
+    key = (dev.type, dev.index)
+    ent = _WS.get(key)
+    if ent is None or ent[0].numel() < nbytes:
+        ent = [torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev), 0]
+        ent[1] = ent[0].numel()
+        _WS[key] = ent
+    need_zero = -(-count_bytes // 256) * 256
+    if need_zero > ent[1]:
+        ent[0][:need_zero].zero_()
+    ent[1] = need_zero
+    return ent[0]
+
+
+def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
+               device="cuda") -> torch.Tensor:
+    """Task-major split-KV plan: one (task, chunk) row per work item, chunk c
+    of task (r, h) covering pages [c*tile_pages, (c+1)*tile_pages). A task has
+    max(1, ceil(ceil(ctx/page_size) / tile_pages)) chunks. ctx_lens: host
+    sequence (the plan is built where the lengths are known, like a serving
+    scheduler's plan step)."""
+    ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
+                     dtype=np.int64)
+    npg = (ctx + page_size - 1) // page_size
+    nch = np.maximum(1, (npg + tile_pages - 1) // tile_pages)
+    per_task = np.repeat(nch, num_kv_heads)
+    tasks = np.repeat(np.arange(per_task.size, dtype=np.int64), per_task)
+    starts = np.cumsum(per_task) - per_task
+    chunks = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, per_task)
+    return torch.tensor(np.stack([tasks, chunks], 1), dtype=torch.int32, device=device)
+
+
+def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.Tensor:
+    """pi over work items that follows a per-task key (e.g. urgency or
+    predicted cost): tiles of higher-key tasks first, chunk order kept."""
+    t = tiles[:, 0].cpu().numpy()
+    k = np.asarray(key, dtype=np.float64)[t]
+    idx = np.arange(t.size)
+    order = np.lexsort((idx, -k if descending else k))
+    return torch.tensor(order, dtype=torch.int32)
 
 
 def launch(args: abi.SchedDecodeArgs, stream=None) -> None:

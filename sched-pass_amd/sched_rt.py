@@ -125,7 +125,12 @@ class SchedPlane:
         struct.pack_into("<I", self._ctrl_host, CTRL_ORDER_SIZE_OFF, int(n))
 
     def install_order(self, tasks, n: int) -> None:
-        """Table first, validity stamp second (published by the next push)."""
+        """Table first, validity stamp second (published by the next push).
+        A permutation of more than max_tasks work items cannot be installed:
+        the items past the table would keep their own ids while the table
+        maps others onto them (duplicated and missing work)."""
+        if int(n) > self.N:
+            raise ValueError(f"order for {n} work items exceeds the plane's {self.N} rows")
         self.set_order(tasks)
         self.set_order_size(n)
 

@@ -47,13 +47,14 @@ def test_device_slot_symbols_exist(schedlib):
 
 def test_struct_layout_matches_c():
     lib = oracle.load()
-    buf = (ctypes.c_int64 * 16)()
-    n = lib.oracle_args_layout(buf, 16)
+    buf = (ctypes.c_int64 * 32)()
+    n = lib.oracle_args_layout(buf, 32)
     A = abi.SchedDecodeArgs
     expect = [ctypes.sizeof(A), A.sm_scale.offset, A.lin_w_period.offset, A.q.offset,
               A.k_page_stride.offset, A.v_dim_stride.offset, A.k_scale.offset,
               A.block_table.offset, A.lin_w.offset, A.order.offset, A.queue.offset,
-              32 + 8 * abi.SCHED_MAX_TASKS]
+              32 + 8 * abi.SCHED_MAX_TASKS, A.tile_pages.offset, A.tiles.offset,
+              A.num_tiles.offset, A.workspace.offset, A.workspace_bytes.offset]
     assert list(buf[:n]) == expect
 
 
@@ -149,3 +150,33 @@ def test_missing_library_is_an_error(tmp_path):
             abi.load_library(str(tmp_path / "nope.so"))
     finally:
         abi._LIB = saved
+
+
+def test_split_arguments_validated(schedlib):
+    a = fake_args(tiles=ctypes.c_void_p(0x90000), num_tiles=8, tile_pages=4)
+    need = schedlib.sched_paged_decode_workspace_bytes(ctypes.byref(a))
+    # counters (32 tasks) + (m, l) for 8 items x 4 heads + partials 8 x 4 x 128 f32
+    assert need == 256 + 256 + 8 * 4 * 128 * 4
+    assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
+    assert "workspace" in abi.last_error()
+    a.workspace, a.workspace_bytes = ctypes.c_void_p(0xA0000), need - 1
+    assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
+    a.tile_pages = 0
+    assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
+    assert "tile_pages" in abi.last_error()
+
+
+def test_plan_tiles_is_task_major():
+    import numpy as np
+    import sched_pd
+    t = sched_pd.plan_tiles([0, 16, 17, 100], 16, 2, 2, device="cpu").numpy()
+    # pages per request: 0, 1, 2, 7 -> chunks 1, 1, 1, 4; two kv-heads each
+    assert t[:, 0].tolist() == [0, 1, 2, 3, 4, 5, 6, 6, 6, 6, 7, 7, 7, 7]
+    assert t[:, 1].tolist() == [0, 0, 0, 0, 0, 0, 0, 1, 2, 3, 0, 1, 2, 3]
+    o = sched_pd.tile_order_by_task_key(torch_tiles(t), np.arange(8.0)).numpy()
+    assert o[:4].tolist() == [10, 11, 12, 13] and o[-1] == 0
+
+
+def torch_tiles(t):
+    import torch
+    return torch.from_numpy(t)

@@ -320,3 +320,76 @@ def test_num_tasks_zero_takes_the_static_path():
     # workers requested, but num_tasks 0 disarms the claim loop: full grid
     assert torch.equal(run(b, plane=plane, workers=16), base)
     assert int((plane.read_timer()[:n] > 0).sum()) == n
+
+
+# --- split-KV work items ------------------------------------------------------
+
+SPLIT_CTX = [1, 16, 17, 300, 2048, 5000, 0, 777]
+
+
+@pytest.mark.parametrize("tp", [1, 3, 16, 64])
+@pytest.mark.parametrize("kvt", [torch.bfloat16, torch.float8_e4m3fn])
+def test_split_kv_parity_and_schedule_invariance(tp, kvt):
+    b = batch(SPLIT_CTX, kv=kvt, seed=tp)
+    ntask = len(SPLIT_CTX) * 8
+    tiles = sched_pd.plan_tiles(SPLIT_CTX, 16, tp, 8)
+    n = tiles.shape[0]
+    plane = SchedPlane(max_tasks=max(n, ntask))
+    out = run(b, plane=plane, tiles=tiles, tile_pages=tp)
+    r = ref(b)
+    fin = np.isfinite(r)
+    assert np.array_equal(np.isnan(out.cpu().numpy()), ~fin)  # the empty request is 0/0
+    e = mixed_err(out.cpu().numpy()[fin], r[fin])
+    print(f"split tp={tp} {kvt} items={n} err {e:.3g}")
+    assert e <= TOL_BF16
+    # pi over work items
+    plane.install_order(torch.arange(n - 1, -1, -1), n)
+    plane.push()
+    assert _same(run(b, plane=plane, tiles=tiles, tile_pages=tp), out)
+    plane.install_order(torch.randperm(n), n)
+    plane.set_num_tasks(n)
+    plane.push()
+    for W in (3, 100, n + 9):
+        plane.reset_queue(W)
+        plane.clear_timer()
+        o = run(b, plane=plane, tiles=tiles, tile_pages=tp, workers=W)
+        assert _same(o, out)
+        rows = plane.read_timer()[:ntask].numpy()
+        assert (rows > 0).all()  # every task's chunks add into its own row
+    # relaunch without a host reset: arrival counters and queue reset themselves
+    assert _same(run(b, plane=plane, tiles=tiles, tile_pages=tp, workers=100), out)
+    ws = sched_pd._WS[("cuda", torch.cuda.current_device())][0]
+    assert int(ws[:4 * ntask].view(torch.int32).abs().sum()) == 0
+
+
+def _same(a, b):
+    return bool(torch.equal(torch.nan_to_num(a, nan=7.0), torch.nan_to_num(b, nan=7.0))) and \
+        bool(torch.equal(torch.isnan(a), torch.isnan(b)))
+
+
+def test_split_kv_with_shed_valu_and_linear():
+    ctx = [40, 3000, 1000, 4096]
+    b = batch(ctx, seed=31)
+    ntask = len(ctx) * 8
+    tiles = sched_pd.plan_tiles(ctx, 16, 32, 8)
+    plane = SchedPlane(max_tasks=max(tiles.shape[0], ntask))
+    tau = np.random.default_rng(3).integers(0, 3000, size=ntask)
+    plane.set_rows(tau=tau, n=ntask)
+    plane.push()
+    for flags in (0, abi.FLAG_FORCE_VALU):
+        o = run(b, plane=plane, tiles=tiles, tile_pages=32, flags=flags)
+        assert mixed_err(o.cpu(), ref(b, plane)) <= TOL_BF16
+    w = torch.randn(4096, device="cuda")
+    o = run(b, plane=plane, tiles=tiles, tile_pages=32, mode=abi.LINEAR, lin_w=w)
+    r = ref(b, plane, mode=abi.LINEAR, lin_w=w.cpu().numpy())
+    assert mixed_err(o.cpu(), r) <= TOL_BF16
+
+
+def test_split_workspace_counters_grow_safely():
+    small = batch([3000, 40], seed=41)
+    big = batch([3000] * 12, seed=42)
+    for b in (small, big, small, big):
+        ctx = b["ctx_lens"].cpu().numpy()
+        tiles = sched_pd.plan_tiles(ctx, 16, 16, 8)
+        o = run(b, tiles=tiles, tile_pages=16)
+        assert mixed_err(o.cpu(), ref(b)) <= TOL_BF16
