@@ -82,7 +82,7 @@ def bench_uniform(args, torch, sched_pd, workloads):
     }
 
 
-TILE_PAGES = 64  # split-KV tile (pages) for the heterogeneous batch
+TILE_PAGES = 128  # split-KV tile (pages) for the heterogeneous batch (sweep: 32..256)
 
 
 def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):

@@ -7,16 +7,26 @@
 // workgroup finished last, so split tasks stay bit-reproducible under any pi
 // or work-queue schedule.
 //
-// Cross-XCD handoff: every thread publishes its partial, then an agent-scope
-// release fence (L2 write-back) precedes the arrival atomic; the completing
-// work item takes an agent-scope acquire fence (L2 invalidate) before reading
-// the other partials. The arrival counter is reset to 0 by the work item that
-// completes the task: every other chunk has already arrived.
+// Cross-XCD handoff without L2 maintenance: partials are written and read
+// with agent-scope relaxed atomic stores / loads (sc1: coherent at device
+// scope, so the per-XCD L2s are not involved), and each wave waits for its
+// stores to complete (s_waitcnt vmcnt(0)) before the barrier that precedes the
+// arrival atomic. A release/acquire fence pair would do the same job with a
+// write-back and an invalidate of the whole XCD L2 per work item, which costs
+// more than the tile's own KV stream. The arrival counter is reset to 0 by the
+// work item that completes the task: every other chunk has already arrived.
 #pragma once
 
 #include "common.h"
 
 namespace schedpd {
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), GFX9 encoding.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+template <typename T> __device__ __forceinline__ T ld_coherent(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Softmax: acc is unnormalised with running max m and sum l per head.
 // Linear: acc is a plain sum (m, l unused).
@@ -64,7 +74,7 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
 #pragma unroll
       for (int w = 0; w < NW; ++w)
         a += s_acc[w][0][j];
-      pacc[j] = a;
+      __hip_atomic_store(pacc + j, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
       float M = s_m[0][g];
 #pragma unroll
@@ -77,14 +87,14 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
         Lt += s_l[w][g] * e;
         A += (float)s_acc[w][g][j] * e;
       }
-      pacc[g * D + j] = A;
+      __hip_atomic_store(pacc + g * D + j, (AccT)A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (j == 0) {
-        pml[2 * g] = M;
-        pml[2 * g + 1] = Lt;
+        __hip_atomic_store(pml + 2 * g, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pml + 2 * g + 1, Lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   __shared__ uint32_t s_last;
   if (threadIdx.x == 0) {
@@ -98,25 +108,25 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
   __syncthreads();
   if (!s_last)
     return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const uint32_t base = wi - chunk; // task-major list: chunk c is work item base + c
   for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
     const uint32_t g = idx / D, j = idx % D;
     if (LINEAR) {
       AccT a = 0;
       for (uint32_t c = 0; c < nchunks; ++c)
-        a += static_cast<const AccT *>(P.ws_acc)[(size_t)(base + c) * G * D + j];
+        a += ld_coherent(static_cast<const AccT *>(P.ws_acc) + (size_t)(base + c) * G * D + j);
       store_out(P, orow * D + j, (float)a);
     } else {
-      float M = P.ws_ml[(size_t)base * G * 2 + 2 * g];
+      float M = ld_coherent(P.ws_ml + (size_t)base * G * 2 + 2 * g);
       for (uint32_t c = 1; c < nchunks; ++c)
-        M = fmaxf(M, P.ws_ml[(size_t)(base + c) * G * 2 + 2 * g]);
+        M = fmaxf(M, ld_coherent(P.ws_ml + (size_t)(base + c) * G * 2 + 2 * g));
       float Lt = 0.f, A = 0.f;
       for (uint32_t c = 0; c < nchunks; ++c) {
         const float *ml = P.ws_ml + (size_t)(base + c) * G * 2 + 2 * g;
-        const float e = __builtin_amdgcn_exp2f(ml[0] - M);
-        Lt += ml[1] * e;
-        A += (float)static_cast<const AccT *>(P.ws_acc)[(size_t)(base + c) * G * D + g * D + j] * e;
+        const float e = __builtin_amdgcn_exp2f(ld_coherent(ml) - M);
+        Lt += ld_coherent(ml + 1) * e;
+        A += (float)ld_coherent(static_cast<const AccT *>(P.ws_acc) +
+                                (size_t)(base + c) * G * D + g * D + j) * e;
       }
       store_out(P, (orow + g) * D + j, A / Lt);
     }

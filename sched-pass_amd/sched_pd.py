@@ -152,6 +152,8 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
         # num_tasks == 0 is the per-step disarm of the claim loop; the stock
         # path serves one task per workgroup, so launch the full grid then.
         a.workers = workers if plane.num_tasks > 0 else 0
+        if a.workers:
+            plane.prime_queue(a.workers)
     else:
         a.max_tasks = 0
         a.workers = 0

@@ -194,6 +194,15 @@ class SchedPlane:
     # -- work queue (python/sched_rt.py:464-471) --------------------------------
     def reset_queue(self, workers: int) -> None:
         self._queue.fill_(int(workers))
+        self._queue_w = int(workers)
+
+    def prime_queue(self, workers: int) -> None:
+        """Prime the ticket counter for a launch of `workers` workers unless it
+        already holds that value: a launch that took its last ticket leaves the
+        counter at its own worker count, so only a change of W needs a write
+        (a stream-ordered fill, safe in captured graphs)."""
+        if getattr(self, "_queue_w", None) != int(workers):
+            self.reset_queue(workers)
 
     # -- resident-prefix sizing (python/sched_rt.py:478-487) --------------------
     def sm_count(self) -> int:

@@ -356,8 +356,13 @@ def test_split_kv_parity_and_schedule_invariance(tp, kvt):
         assert _same(o, out)
         rows = plane.read_timer()[:ntask].numpy()
         assert (rows > 0).all()  # every task's chunks add into its own row
-    # relaunch without a host reset: arrival counters and queue reset themselves
-    assert _same(run(b, plane=plane, tiles=tiles, tile_pages=tp, workers=100), out)
+    # relaunch with the same W and no host reset: arrival counters and the
+    # ticket counter reset themselves
+    q0 = int(plane._queue.item())
+    assert q0 == n + 9
+    plane._queue_w = n + 9
+    assert _same(run(b, plane=plane, tiles=tiles, tile_pages=tp, workers=n + 9), out)
+    assert int(plane._queue.item()) == n + 9
     ws = sched_pd._WS[("cuda", torch.cuda.current_device())][0]
     assert int(ws[:4 * ntask].view(torch.int32).abs().sum()) == 0
 
