@@ -55,6 +55,28 @@ def time_launches(fn, steps, stream):
     return sum(ms) / len(ms), ms
 
 
+def read_ceiling_gbs(torch, sched_pd, buf):
+    """Achievable streaming-read bandwidth: the library's read probe over
+    `buf` (>= 2 GiB, far beyond the 256 MB MALL), min time of 5 launches."""
+    import ctypes
+    import sched_abi
+    lib = sched_abi.load_library()
+    nbytes = buf.numel() * buf.element_size()
+    stream = torch.cuda.current_stream()
+    s = ctypes.c_void_p(stream.cuda_stream)
+    best = float("inf")
+    for _ in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rc = lib.sched_pd_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, None, s)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if rc:
+            raise RuntimeError(sched_abi.last_error())
+        best = min(best, e0.elapsed_time(e1))
+    return nbytes / (best * 1e-3) / 1e9
+
+
 def bench_uniform(args, torch, sched_pd, workloads):
     b = workloads.workload("llama3_8b_uniform", seed=0, n_tables=args.tables)
     out = torch.empty(64, 32, 128, dtype=torch.bfloat16, device="cuda")
@@ -76,8 +98,10 @@ def bench_uniform(args, torch, sched_pd, workloads):
     wall_ms = ev0.elapsed_time(ev1)
     kern_ms, per = time_launches(step, args.steps, stream)
     kv = b["kv_bytes"]
+    ceiling = read_ceiling_gbs(torch, sched_pd, b["k_pool"])
     return {
         "kv_bytes": kv, "ms_per_step": wall_ms / args.steps, "kernel_ms": kern_ms,
+        "read_ceiling_gbs": ceiling,
         "kernel_ms_min": min(per), "kernel": kind, "occupancy": sched_pd.occupancy(launches[0]),
     }
 
@@ -148,6 +172,10 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     sched_pd.launch(A["wq_tiles"], stream)
     torch.cuda.synchronize()
     cyc = p_tile.read_timer()[:ntask].numpy()
+    # closed loop: pi over tiles by the measured per-task cost, longest first
+    p_tile.install_order(sched_pd.tile_order_by_task_key(tiles, cyc.astype(np.float64)), nt)
+    p_tile.push()
+    res["wq_tiles_lpt_timer"] = round(_makespan_us(torch, sched_pd, A["wq_tiles"], stream), 2)
     kv = b["kv_bytes"]
     return {
         "static_us": res["static_task"], "ticket_wq_us": res["wq_tiles"],
@@ -157,6 +185,98 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
         "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                              "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())},
     }
+
+
+def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES):
+    """128 requests, ctx ~ U{1024..8192}, per-task tau ~ U{ctx/4..ctx}; policy
+    armed (q ~ U(0,1), lambda_bw 0.5, H 0.1: urgent tasks stream 4 pages
+    ahead). Online softmax (score -> -inf) and linear contraction (value -> 0)
+    variants; pages past the budget skipped (default) or loaded and masked
+    (the reference weave's behaviour). Work queue over split tiles."""
+    import numpy as np
+    import sched_abi as abi
+    b = workloads.workload("llama3_8b_shed", seed=0)
+    R, ntask = 128, 128 * 8
+    ctx = b["ctx_lens"].cpu().numpy()
+    tiles = sched_pd.plan_tiles(ctx, 16, tile_pages, 8)
+    nt = tiles.shape[0]
+    plane = SchedPlane(max_tasks=max(nt, ntask))
+    plane.set_lambda(0.5)
+    plane.set_rows(q=b["urgency"], tau=b["tau"], n=ntask)
+    plane.install_order(sched_pd.tile_order_by_task_key(tiles, b["urgency"]), nt)
+    plane.set_num_tasks(nt)
+    plane.push()
+    W = 2 * cu
+    plane.reset_queue(W)
+    stream = torch.cuda.current_stream()
+    full = workloads.kv_bytes(ctx, 8, 128, torch.bfloat16)
+    kept = workloads.kv_bytes(ctx, 8, 128, torch.bfloat16, tau=b["tau"][::8])
+    res = {"tasks": ntask, "tiles": nt, "urgent_frac": round(float((b["urgency"] > 0.6).mean()), 3),
+           "kv_bytes_ctx": full, "kv_bytes_kept": kept}
+    out = torch.empty(R, 32, 128, dtype=torch.bfloat16, device="cuda")
+    lout = torch.empty(R, 8, 128, dtype=torch.bfloat16, device="cuda")
+    w = torch.randn(8192, device="cuda")
+    for name, kw, o, vb in (
+            ("softmax_skip", {}, out, 1.0),
+            ("softmax_shed_loads", {"flags": abi.FLAG_SHED_LOADS}, out, 1.0),
+            ("linear_skip", {"mode": abi.LINEAR, "lin_w": w}, lout, 0.5)):
+        a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                out=o, plane=plane, workers=W, tiles=tiles, tile_pages=tile_pages,
+                                policy=(1.0, 1.0, 0.1), **kw)
+        us = _makespan_us(torch, sched_pd, a, stream)
+        loaded = (full if "loads" in name else kept) * vb
+        res[name] = {"us": round(us, 2), "gbs_loaded": round(loaded / us / 1e3, 1),
+                     "gbs_ctx_equiv": round(full * vb / us / 1e3, 1)}
+    return res
+
+
+def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES):
+    """Qwen2-7B shape (Hq 28 / Hkv 4), fp8-e4m3fn KV with per-(page, head)
+    scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
+    max 16384); ticket work queue over split tiles, timer on."""
+    import numpy as np
+    b = workloads.workload("qwen2_7b_fp8", seed=0)
+    R, ntask = 512, 512 * 4
+    ctx = b["ctx_lens"].cpu().numpy()
+    tiles = sched_pd.plan_tiles(ctx, 16, tile_pages, 4)
+    nt = tiles.shape[0]
+    plane = SchedPlane(max_tasks=max(nt, ntask))
+    plane.set_num_tasks(nt)
+    plane.push()
+    W = 2 * cu
+    plane.reset_queue(W)
+    out = torch.empty(R, 28, 128, dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+    a_wq = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                               out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane,
+                               workers=W, tiles=tiles, tile_pages=tile_pages)
+    plane2 = SchedPlane(max_tasks=ntask)
+    a_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                               out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane2)
+    us_wq = _makespan_us(torch, sched_pd, a_wq, stream)
+    us_st = _makespan_us(torch, sched_pd, a_st, stream)
+    plane.clear_timer()
+    sched_pd.launch(a_wq, stream)
+    torch.cuda.synchronize()
+    cyc = plane.read_timer()[:ntask].numpy()
+    kv = b["kv_bytes"]
+    return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
+            "gbs": round(kv / us_wq / 1e3, 1), "tiles": nt, "workers": W,
+            "max_ctx": int(ctx.max()),
+            "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
+                                 "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())}}
+
+
+def profiled_traffic():
+    """HBM bytes per decode launch from the committed PMC summary (two
+    rocprofv3 --pmc runs, FETCH_SIZE calibrated on the read probe), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "decode_mfma_llama3_8b_uniform_pmc.md")
+    try:
+        m = re.search(r"^traffic_bytes_per_launch: (\d+)$", open(path).read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(torch, workloads):
@@ -226,10 +346,15 @@ def main():
                      "traffic": None, "kernel": f"decode_{u['kernel']}",
                      "kernel_us": round(u["kernel_ms"] * 1e3, 2),
                      "kernel_us_min": round(u["kernel_ms_min"] * 1e3, 2),
-                     "bytes_per_launch": u["kv_bytes"], "wg_per_cu": u["occupancy"]},
+                     "bytes_per_launch": u["kv_bytes"], "wg_per_cu": u["occupancy"],
+                     "measured_read_ceiling_gbs": round(u["read_ceiling_gbs"], 1),
+                     "frac_of_measured_ceiling": round(kern_gbs / u["read_ceiling_gbs"], 4)},
     }
+    line["roofline"]["traffic"] = profiled_traffic()
     if not args.no_hetero:
         line["hetero_makespan"] = bench_hetero(torch, sched_pd, workloads, SchedPlane, cu)
+        line["shed_policy"] = bench_shed(torch, sched_pd, workloads, SchedPlane, cu)
+        line["fp8_qwen2_7b"] = bench_fp8(torch, sched_pd, workloads, SchedPlane, cu)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, workloads)
     print(json.dumps(line), flush=True)

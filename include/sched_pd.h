@@ -237,6 +237,12 @@ int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
 /* Compute-unit count of the current device (0 on error). */
 int sched_pd_cu_count(void);
 
+/* Streaming-read ceiling probe, no counterpart in the reference: reads
+ * `bytes` (16-byte aligned) of `buf` once on `stream`, writes nothing (sink
+ * may be NULL). Timing it gives the device's achievable read bandwidth, the
+ * measured peak beside the vendor figure. Returns 0 or a hipError_t code. */
+int sched_pd_read_probe(const void *buf, uint64_t bytes, void *sink, void *stream);
+
 /* Last error text of this thread ("" if none). */
 const char *sched_pd_last_error(void);
 

@@ -34,8 +34,20 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
   return decode_valu<KVT, D, 16, false>;
 }
 
+// MFMA kernel shape: waves per workgroup, pages in flight per wave (stock,
+// urgent). Overridable at build time for tuning sweeps.
+#ifndef SCHED_PD_MFMA_NW
+#define SCHED_PD_MFMA_NW 4
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH
+#define SCHED_PD_MFMA_DEPTH 2
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH_URGENT
+#define SCHED_PD_MFMA_DEPTH_URGENT 4
+#endif
+
 template <bool FP8> KernelFn mfma_kernel(uint32_t G) {
-  constexpr int NW = 4, DS = 2, DU = 4;
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = SCHED_PD_MFMA_DEPTH, DU = SCHED_PD_MFMA_DEPTH_URGENT;
   if (G <= 4)
     return decode_mfma<FP8, NW, 4, DS, DU>;
   if (G <= 8)
@@ -211,7 +223,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
 
   if (mfma) {
     sel->fn = a->kv_dtype == SCHED_PD_BF16 ? mfma_kernel<false>(G) : mfma_kernel<true>(G);
-    sel->block = 256;
+    sel->block = SCHED_PD_MFMA_NW * 64;
     sel->mfma = 1;
   } else {
     KernelFn fn = nullptr;

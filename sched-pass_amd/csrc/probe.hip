@@ -1,0 +1,49 @@
+// probe.hip -- streaming-read ceiling of the device, the measured counterpart
+// of the vendor HBM peak that decode bandwidth is reported against. Every
+// workgroup strides over the buffer with 16-byte loads, 4 in flight per lane;
+// the XOR of the data is written only when it equals a value it cannot take
+// for the benchmark's inputs, so the loads are kept and nothing is stored.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/sched_pd.h"
+#include "rt_internal.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+
+__global__ void __launch_bounds__(256) read_probe(const u32x4 *__restrict__ p, uint64_t n16,
+                                                  unsigned *sink) {
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    const u32x4 b = __builtin_nontemporal_load(p + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(p + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(p + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride)
+    acc ^= __builtin_nontemporal_load(p + i);
+  const unsigned x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (x == 0x9E3779B9u && sink)
+    sink[0] = x;
+}
+
+} // namespace
+
+extern "C" int sched_pd_read_probe(const void *buf, uint64_t bytes, void *sink, void *stream) {
+  if (!buf || (bytes & 15u) || ((uintptr_t)buf & 15u))
+    return schedpd::set_error(hipErrorInvalidValue, "read probe needs a 16-byte aligned buffer");
+  int dev = 0, cus = 0;
+  hipGetDevice(&dev);
+  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const unsigned grid = (unsigned)(cus > 0 ? cus : 256) * 8u;
+  hipLaunchKernelGGL(read_probe, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const u32x4 *>(buf), bytes / 16u, static_cast<unsigned *>(sink));
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : schedpd::set_error(e, "read probe launch: %s", hipGetErrorString(e));
+}

@@ -102,6 +102,7 @@ SIGNATURES = {
     "sched_paged_decode_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_kernel_kind": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_pd_cu_count": (ctypes.c_int, []),
+    "sched_pd_read_probe": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _p]),
     "sched_pd_last_error": (ctypes.c_char_p, []),
     "launch_paged_softmax": (None, [_p, _p, _p, _p, _p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, _p]),
