@@ -1,6 +1,7 @@
 // decode_mfma.h -- the GQA decode kernel on the CDNA4 matrix cores:
 // bf16 or fp8-e4m3fn KV, head dim 128, page size 16, up to 16 q-heads per
-// kv-head (one MFMA column block), bf16 Q.
+// kv-head (one MFMA column block), bf16 Q; and the linear contraction over the
+// same V stream (LINEAR: no K, weights as MFMA column 0).
 //
 // Layout it reads (one (page, kv-head) chunk each for K and V):
 //   K: 16 token rows x 128 dims, dims contiguous (row stride k_tok_stride);
@@ -124,21 +125,23 @@ struct MfmaState {
   bf16x8_t qop[4];
 };
 
-template <bool FP8, bool NT>
+template <bool FP8, bool NT, bool LINEAR>
 __device__ __forceinline__ void issue_page(const MfmaTask &T, int32_t page, PageRegs<FP8> &B) {
   const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes;
   const uint8_t *vp = T.vbase + (int64_t)page * T.vpage_bytes + T.vhead_bytes;
   if constexpr (!FP8) {
+    if constexpr (!LINEAR)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
+      for (int kb = 0; kb < 4; ++kb)
+        B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk)
       B.v[blk] = gload<NT>(reinterpret_cast<const u32x2_t *>(vp + 512 * blk));
   } else {
+    if constexpr (!LINEAR)
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-      B.k[cc] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * cc));
+      for (int cc = 0; cc < 2; ++cc)
+        B.k[cc] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * cc));
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk)
       B.v[blk] = gload<NT>(reinterpret_cast<const unsigned *>(vp + 256 * blk));
@@ -229,6 +232,47 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   }
 }
 
+// Linear contraction of one page: acc[:, 0] += V^T . w over the page's kept
+// tokens. w enters PV as column 0 of the B operand, split into bf16 hi + lo
+// halves (two MFMAs) so the weights keep ~16 mantissa bits; V is exact.
+template <bool FP8>
+__device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T, MfmaState &S,
+                                            const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
+                                            uint32_t c16, uint32_t g4) {
+  float vs = 1.f;
+  if constexpr (FP8) {
+    if (P.v_scale)
+      vs = P.v_scale[(int64_t)page * P.Hkv + T.h];
+  }
+  const uint32_t pos0 = pidx * 16u;
+  const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
+  float wv[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t i = 4u * g4 + v, t = pos0 + i;
+    const bool keep = c16 == 0u && t < T.n && (prefix ? t : i) < T.budget;
+    wv[v] = keep ? P.lin_w[P.lin_w_period ? t % P.lin_w_period : t] * vs : 0.f;
+  }
+  u32x2_t hi, lo;
+  hi.x = pack_bf16_rne(wv[0], wv[1]);
+  hi.y = pack_bf16_rne(wv[2], wv[3]);
+  const float r0 = wv[0] - __uint_as_float(hi.x << 16), r1 = wv[1] - __uint_as_float(hi.x & 0xffff0000u);
+  const float r2 = wv[2] - __uint_as_float(hi.y << 16), r3 = wv[3] - __uint_as_float(hi.y & 0xffff0000u);
+  lo.x = pack_bf16_rne(r0, r1);
+  lo.y = pack_bf16_rne(r2, r3);
+  const s16x4_t bhi = __builtin_bit_cast(s16x4_t, hi), blo = __builtin_bit_cast(s16x4_t, lo);
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) {
+    s16x4_t a;
+    if constexpr (!FP8)
+      a = __builtin_bit_cast(s16x4_t, B.v[blk]);
+    else
+      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(B.v[blk]));
+    S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, bhi, S.acc[blk], 0, 0, 0);
+    S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, blo, S.acc[blk], 0, 0, 0);
+  }
+}
+
 // Page ids of this wave's pages, 64 at a time in one VGPR (lane j holds the id
 // of the wave's page 64*blk + j, i.e. task page p0 + w + NW*(64*blk + j)).
 template <int NW>
@@ -242,7 +286,7 @@ __device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T,
 // summation order) depends only on the page index, not on how many pages are
 // read: a task whose shed pages are loaded and masked gives the same bits as
 // one that skips them, and shed tasks stay balanced across the waves.
-template <bool FP8, int NW, int DEPTH, bool NT>
+template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
   const uint32_t span = T.p1 - T.p0;
@@ -269,24 +313,27 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   for (int s = 0; s < DEPTH; ++s)
     if (s < npg) {
       pid[s] = next_id();
-      issue_page<FP8, NT>(T, pid[s], buf[s]);
+      issue_page<FP8, NT, LINEAR>(T, pid[s], buf[s]);
     }
   for (int it = 0; it < npg; it += DEPTH) {
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s) {
       const int j = it + s;
       if (j < npg) {
-        compute_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, g4);
+        if constexpr (LINEAR)
+          linear_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, lane & 15u, g4);
+        else
+          compute_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, g4);
         if (j + DEPTH < npg) {
           pid[s] = next_id();
-          issue_page<FP8, NT>(T, pid[s], buf[s]);
+          issue_page<FP8, NT, LINEAR>(T, pid[s], buf[s]);
         }
       }
     }
   }
 }
 
-template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U>
+template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
   __shared__ float s_acc[NW][GMAX][128];
   __shared__ float s_m[NW][GMAX];
@@ -332,12 +379,12 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk)
       S.acc[blk] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const uint32_t G = P.G;
+    const uint32_t G = LINEAR ? 1u : P.G;
     const int64_t qrow = ((int64_t)T.r * P.Hq + T.h * G + c16) * 128;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       u32x4_t qv = {0u, 0u, 0u, 0u};
-      if (c16 < G) {
+      if (!LINEAR && c16 < G) {
         const uint32_t d0 = qk_dim(FP8, kb, g4);
         if (P.q_f32) {
           const float *qf = static_cast<const float *>(P.q) + qrow + d0;
@@ -351,11 +398,11 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
 
     if (pol.urgent)
-      stream_pages<FP8, NW, DEPTH_U, false>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, false, LINEAR>(P, T, S, lane, g4);
     else if (pol.polite)
-      stream_pages<FP8, NW, DEPTH_S, true>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, true, LINEAR>(P, T, S, lane, g4);
     else
-      stream_pages<FP8, NW, DEPTH_S, false>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, false, LINEAR>(P, T, S, lane, g4);
 
     // Wave states to LDS (l summed over the 4 lane rows first), then the
     // work item's result: output, or partial + fixed-order task merge.
@@ -370,8 +417,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
         *reinterpret_cast<f32x4_t *>(&s_acc[w][c16][16 * blk + 4 * g4]) = S.acc[blk];
     }
     __syncthreads();
-    finish_item<NW, GMAX, 128, float, false>(P, wi, task, chunk, R.nchunks, T.r, T.h, G, s_acc,
-                                             s_m, s_l);
+    finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, chunk, R.nchunks, T.r, T.h, G, s_acc,
+                                              s_m, s_l);
     timer_commit(P.L, toff, task, t0);
   });
 }

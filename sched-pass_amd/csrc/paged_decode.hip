@@ -45,9 +45,20 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
 #ifndef SCHED_PD_MFMA_DEPTH_URGENT
 #define SCHED_PD_MFMA_DEPTH_URGENT 4
 #endif
+// fp8 pages are half the bytes: twice the pages in flight for the same bytes.
+#ifndef SCHED_PD_MFMA_DEPTH_FP8
+#define SCHED_PD_MFMA_DEPTH_FP8 4
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH_FP8_URGENT
+#define SCHED_PD_MFMA_DEPTH_FP8_URGENT 6
+#endif
 
-template <bool FP8> KernelFn mfma_kernel(uint32_t G) {
-  constexpr int NW = SCHED_PD_MFMA_NW, DS = SCHED_PD_MFMA_DEPTH, DU = SCHED_PD_MFMA_DEPTH_URGENT;
+template <bool FP8> KernelFn mfma_kernel(uint32_t G, bool linear) {
+  constexpr int NW = SCHED_PD_MFMA_NW;
+  constexpr int DS = FP8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH;
+  constexpr int DU = FP8 ? SCHED_PD_MFMA_DEPTH_FP8_URGENT : SCHED_PD_MFMA_DEPTH_URGENT;
+  if (linear)
+    return decode_mfma<FP8, NW, 4, DS, DU, true>;
   if (G <= 4)
     return decode_mfma<FP8, NW, 4, DS, DU>;
   if (G <= 8)
@@ -85,11 +96,12 @@ WsLayout ws_layout(const SchedDecodeArgs *a) {
 bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
     return false;
-  if (a->mode != SCHED_PD_SOFTMAX || a->q_dtype != SCHED_PD_BF16)
+  const bool linear = a->mode == SCHED_PD_LINEAR;
+  if (!linear && a->q_dtype != SCHED_PD_BF16)
     return false;
   if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_FP8_E4M3)
     return false;
-  const uint32_t G = a->num_q_heads / a->num_kv_heads;
+  const uint32_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
   if (a->head_dim != 128 || a->page_size != 16 || G > 16)
     return false;
   const int64_t eb = elem_bytes(a->kv_dtype);
@@ -99,6 +111,8 @@ bool mfma_applies(const SchedDecodeArgs *a) {
     return false;
   if ((a->v_page_stride * eb) % 16 || (a->v_head_stride * eb) % 16)
     return false;
+  if (linear)
+    return aligned16(a->v_pool);
   return aligned16(a->k_pool) && aligned16(a->v_pool) && aligned16(a->q);
 }
 
@@ -222,7 +236,8 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->scale_log2 = scale * 1.4426950408889634f;
 
   if (mfma) {
-    sel->fn = a->kv_dtype == SCHED_PD_BF16 ? mfma_kernel<false>(G) : mfma_kernel<true>(G);
+    sel->fn = a->kv_dtype == SCHED_PD_BF16 ? mfma_kernel<false>(G, linear)
+                                           : mfma_kernel<true>(G, linear);
     sel->block = SCHED_PD_MFMA_NW * 64;
     sel->mfma = 1;
   } else {

@@ -148,7 +148,8 @@ def test_shed_softmax_matches_truncated_reference(scope, kvt):
 
 @pytest.mark.parametrize("kvt", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("period", [0, 16])
-def test_linear_contraction_and_value_shed(kvt, period):
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_linear_contraction_and_value_shed(kvt, period, force_valu):
     ctx = [64, 1000, 5, 2048]
     b = batch(ctx, hq=8, hkv=8, d=64 if kvt == torch.float32 else 128, kv=kvt,
               qd=torch.float32 if kvt == torch.float32 else torch.bfloat16, seed=6)
@@ -158,7 +159,12 @@ def test_linear_contraction_and_value_shed(kvt, period):
     tau = np.random.default_rng(7).integers(0, 2048, size=n)
     plane.set_rows(tau=tau, n=n)
     plane.push()
-    out = run(b, plane=plane, mode=abi.LINEAR, lin_w=w, lin_w_period=period)
+    flags = abi.FLAG_FORCE_VALU if force_valu else 0
+    out = run(b, plane=plane, mode=abi.LINEAR, lin_w=w, lin_w_period=period, flags=flags)
+    args = sched_pd.build_args(None, None, b["v_pool"], b["block_table"], b["ctx_lens"],
+                               out=out, mode=abi.LINEAR, lin_w=w, flags=flags)
+    expect = "valu" if (force_valu or kvt == torch.float32) else "mfma"
+    assert sched_pd.kernel_kind(args) == expect
     r = ref(b, plane, mode=abi.LINEAR, lin_w=w.cpu().numpy(), lin_w_period=period)
     tol = TOL_F32 if kvt == torch.float32 else TOL_BF16
     e = mixed_err(out.cpu(), r)
