@@ -50,6 +50,9 @@ template <> struct PageRegs<false> {
 template <> struct PageRegs<true> {
   u32x4_t k[2]; // 2 x 16 fp8 K
   unsigned v[8]; // 8 x 4 fp8 V^T
+  float ks, vs;  // the page's K / V scales, loaded with its KV so that no
+                 // load is consumed right after issue (which would drain the
+                 // whole prefetch ring with s_waitcnt vmcnt(0))
 };
 
 template <bool NT, typename T> __device__ __forceinline__ T gload(const T *p) {
@@ -112,6 +115,7 @@ __device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
 
 struct MfmaTask {
   uint32_t r, h, n, budget;
+  int64_t row; // block-table index of the request's first page
   uint32_t p0, p1; // pages [p0, p1) of the task are read by this work item
   uint32_t w;      // this wave: pages p0 + w, p0 + w + NW, ...
   const uint8_t *kbase; // K pool bytes + per-lane offset
@@ -126,7 +130,8 @@ struct MfmaState {
 };
 
 template <bool FP8, bool NT, bool LINEAR>
-__device__ __forceinline__ void issue_page(const MfmaTask &T, int32_t page, PageRegs<FP8> &B) {
+__device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, int32_t page,
+                                           PageRegs<FP8> &B) {
   const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes;
   const uint8_t *vp = T.vbase + (int64_t)page * T.vpage_bytes + T.vhead_bytes;
   if constexpr (!FP8) {
@@ -142,6 +147,9 @@ __device__ __forceinline__ void issue_page(const MfmaTask &T, int32_t page, Page
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
         B.k[cc] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * cc));
+    const int64_t si = (int64_t)page * P.Hkv + T.h;
+    B.ks = (!LINEAR && P.k_scale) ? P.k_scale[si] : 1.f;
+    B.vs = P.v_scale ? P.v_scale[si] : 1.f;
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk)
       B.v[blk] = gload<NT>(reinterpret_cast<const unsigned *>(vp + 256 * blk));
@@ -171,10 +179,8 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 
   float kscale = P.scale_log2, vs = 1.f;
   if constexpr (FP8) {
-    if (P.k_scale)
-      kscale *= P.k_scale[(int64_t)page * P.Hkv + T.h];
-    if (P.v_scale)
-      vs = P.v_scale[(int64_t)page * P.Hkv + T.h];
+    kscale *= B.ks;
+    vs = B.vs;
   }
 
   // Online softmax over this page (exp2 domain).
@@ -240,10 +246,8 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
                                             const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                             uint32_t c16, uint32_t g4) {
   float vs = 1.f;
-  if constexpr (FP8) {
-    if (P.v_scale)
-      vs = P.v_scale[(int64_t)page * P.Hkv + T.h];
-  }
+  if constexpr (FP8)
+    vs = B.vs;
   const uint32_t pos0 = pidx * 16u;
   const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
   float wv[4];
@@ -273,19 +277,25 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
   }
 }
 
-// Page ids of this wave's pages, 64 at a time in one VGPR (lane j holds the id
-// of the wave's page 64*blk + j, i.e. task page p0 + w + NW*(64*blk + j)).
+// Page id of the wave's i-th page (task page p0 + w + NW*i), read through the
+// constant address space so it is a scalar load: it is counted by lgkmcnt, not
+// by the vmcnt of the KV ring, and the ring's waits stay exact.
 template <int NW>
-__device__ __forceinline__ int32_t load_ids(const KParams &P, const MfmaTask &T, uint32_t blk,
-                                            uint32_t lane) {
-  const uint32_t idx = T.p0 + T.w + NW * (64u * blk + lane);
-  return idx < T.p1 ? page_of(P, T.r, idx) : 0;
+__device__ __forceinline__ int32_t page_id(const KParams &P, const MfmaTask &T, int i) {
+  typedef const __attribute__((address_space(4))) int32_t cint32;
+  const cint32 *bt = (const cint32 *)P.bt;
+  return bt[T.row + T.p0 + T.w + (int64_t)NW * i];
 }
 
-// Pages go to waves round-robin, so the assignment (and with it every
-// summation order) depends only on the page index, not on how many pages are
-// read: a task whose shed pages are loaded and masked gives the same bits as
-// one that skips them, and shed tasks stay balanced across the waves.
+// Stream the wave's pages with DEPTH pages of loads in flight. The steady
+// loop has no branches: each computed page is followed by exactly one page's
+// loads, so the compiler's s_waitcnt vmcnt values keep DEPTH-1 pages in flight
+// (a conditional load in the loop makes it fall back to vmcnt(0), which
+// drains the ring every page). Page ids come one group ahead from scalar
+// loads at clamped indices (always inside the wave's table row). Pages go to
+// waves round-robin, so the assignment (and with it every summation order)
+// depends only on the page index, not on how many pages are read: a task whose
+// shed pages are loaded and masked gives the same bits as one that skips them.
 template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
@@ -293,40 +303,46 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   const int npg = span > T.w ? (int)((span - T.w + NW - 1) / NW) : 0;
   if (npg <= 0)
     return;
-  int32_t ptA = load_ids<NW>(P, T, 0, lane);
-  int32_t ptB = npg > 64 ? load_ids<NW>(P, T, 1, lane) : 0;
-  int blk = 0, li = 0;
-  auto next_id = [&]() -> int32_t {
-    if ((li >> 6) != blk) {
-      ptA = ptB;
-      ++blk;
-      ptB = (blk + 1) * 64 < npg ? load_ids<NW>(P, T, blk + 1, lane) : 0;
-    }
-    const int32_t id = __builtin_amdgcn_readlane(ptA, li & 63);
-    ++li;
-    return id;
-  };
-
+  const int last = npg - 1;
   PageRegs<FP8> buf[DEPTH];
-  int32_t pid[DEPTH];
+  int32_t pid[DEPTH], idn[DEPTH];
+#pragma unroll
+  for (int s = 0; s < DEPTH; ++s) {
+    pid[s] = page_id<NW>(P, T, min(s, last));
+    idn[s] = page_id<NW>(P, T, min(DEPTH + s, last));
+  }
+  // Unconditional prologue: a wave with fewer than DEPTH pages re-reads its
+  // last page into the unused slots (same lines, L2 hits) so that the loop is
+  // entered with the same DEPTH pages outstanding as on every back edge.
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s)
-    if (s < npg) {
-      pid[s] = next_id();
-      issue_page<FP8, NT, LINEAR>(T, pid[s], buf[s]);
-    }
-  for (int it = 0; it < npg; it += DEPTH) {
+    issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
+
+  auto compute = [&](int s, int j) {
+    const uint32_t pidx = T.p0 + T.w + NW * (uint32_t)j;
+    if constexpr (LINEAR)
+      linear_page<FP8>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
+    else
+      compute_page<FP8>(P, T, S, buf[s], pid[s], pidx, g4);
+  };
+  int j = 0;
+  for (; j + 2 * DEPTH <= npg; j += DEPTH) {
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s) {
-      const int j = it + s;
-      if (j < npg) {
-        if constexpr (LINEAR)
-          linear_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, lane & 15u, g4);
-        else
-          compute_page<FP8>(P, T, S, buf[s], pid[s], T.p0 + T.w + NW * (uint32_t)j, g4);
-        if (j + DEPTH < npg) {
-          pid[s] = next_id();
-          issue_page<FP8, NT, LINEAR>(T, pid[s], buf[s]);
+      compute(s, j + s);
+      pid[s] = idn[s];
+      issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
+      idn[s] = page_id<NW>(P, T, min(j + 2 * DEPTH + s, last));
+    }
+  }
+  for (; j < npg; j += DEPTH) {
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) {
+      if (j + s < npg) {
+        compute(s, j + s);
+        if (j + DEPTH + s < npg) {
+          pid[s] = idn[s];
+          issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
         }
       }
     }
@@ -357,6 +373,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     MfmaTask T;
     T.r = task / P.Hkv;
     T.h = task % P.Hkv;
+    T.row = P.indptr ? (int64_t)P.indptr[T.r] : (int64_t)T.r * P.bt_stride;
     const TaskPolicy pol = task_policy(P.L, task);
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;
