@@ -1,0 +1,100 @@
+/* sched_kv.h -- paged KV-cache writer for the decode pools of sched_pd.h.
+ *
+ * The reference has no writer of its own: its decode paths read caches that
+ * FlashInfer (flashinfer-python==0.6.12, requirements.txt:6) or the serving
+ * engine filled, in the CSR format its tests build (kv_indptr, kv_indices,
+ * last_page_len; test/py/eval_pi_makespan.py:46-60). sched_kv_append is the
+ * counterpart of FlashInfer's append_paged_kv_cache with its
+ * (append_indptr, seq_lens) position rule, writing the pools in the layout
+ * the decode kernels read, and quantising on write for an fp8 cache.
+ *
+ * Append rule. Request r appends n_r = append_indptr[r+1] - append_indptr[r]
+ * tokens, source rows append_indptr[r] .. append_indptr[r+1]-1, at token
+ * positions ctx_lens[r] - n_r .. ctx_lens[r] - 1 (ctx_lens counts tokens
+ * after the append). Position p lives in page table entry p / page_size,
+ * slot p % page_size; the page table is the decode's (block_table with
+ * bt_stride, or CSR through page_indptr).
+ *
+ * fp8 cache (OCP e4m3fn). Every (page, kv-head) has one fp32 scale for K and
+ * one for V (index page*num_kv_heads + h); stored code c means c * scale.
+ * Scales are powers of two: for the amax a of the tokens an append writes
+ * into a (page, head), P(a) = the least 2^k (k >= -126) with a <= 448 * 2^k,
+ * and P(0) = 0. A page's first append (it writes slot 0) sets scale = P(a);
+ * a later append sets scale = max(old, P(a)), and when that grows the scale
+ * the page's earlier codes are re-encoded at the new scale, which for a
+ * power-of-two ratio moves only their exponent (exact unless a code drops
+ * into e4m3's subnormal range). Each value x is written as
+ * e4m3(clamp(x * (1/scale), -448, 448)), round-to-nearest-even; 1/0 counts
+ * as 0. Non-finite inputs are not supported.
+ *
+ * bf16 / fp32 caches: values are converted (fp32 -> bf16 round-to-nearest-
+ * even) and scales are not touched.
+ */
+#ifndef SCHED_KV_H
+#define SCHED_KV_H
+
+#include <stdint.h>
+
+#include "sched_pd.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SCHED_KV_ABI_VERSION 1u
+
+/* Element (page, kv-head h, slot t, dim j) of the pools, strides in elements:
+ *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
+ *   V: v_pool + page*v_page_stride + h*v_head_stride + t*v_tok_stride + j*v_dim_stride
+ * with v_tok_stride == 1 (d-major V, the MFMA kernel's layout) or
+ * v_dim_stride == 1 (token-major V). Source row i, head h, dim j:
+ *   k_src[i*src_tok_stride + h*src_head_stride + j] (v_src alike). */
+typedef struct SchedKvAppendArgs {
+  uint32_t abi_version;   /* SCHED_KV_ABI_VERSION */
+  uint32_t src_dtype;     /* SCHED_PD_F32 or SCHED_PD_BF16 */
+  uint32_t kv_dtype;      /* SCHED_PD_F32, SCHED_PD_BF16 or SCHED_PD_FP8_E4M3 */
+  uint32_t num_requests;
+  uint32_t num_kv_heads;
+  uint32_t head_dim;      /* multiple of 4, <= 256 */
+  uint32_t page_size;     /* multiple of 4, <= 256 */
+  uint32_t bt_stride;     /* 2-D block table row stride (page_indptr == NULL) */
+  uint32_t max_append;    /* >= every n_r (sizes the grid; 0 = num_tokens) */
+  uint32_t num_tokens;    /* source rows = append_indptr[num_requests] */
+  uint64_t num_pages;     /* pool pages; ids outside [0, num_pages) are errors */
+  const void *k_src;
+  const void *v_src;
+  int64_t src_tok_stride, src_head_stride;
+  const int32_t *append_indptr; /* [num_requests + 1] */
+  const int32_t *ctx_lens;      /* [num_requests], tokens after the append */
+  const int32_t *block_table;
+  const int32_t *page_indptr;   /* NULL = 2-D block table */
+  void *k_pool;
+  void *v_pool;
+  int64_t k_page_stride, k_head_stride, k_tok_stride;
+  int64_t v_page_stride, v_head_stride, v_tok_stride, v_dim_stride;
+  float *k_scale;         /* fp8: [num_pages * num_kv_heads], read and written */
+  float *v_scale;
+  /* Optional u32 error counter (NULL = none): the kernel adds one per
+   * (token, kv-head) it could not write (a page id outside the pool, a table
+   * entry past the request's pages, or n_r > ctx_lens[r]) and skips it. */
+  uint32_t *errors;
+  uint32_t _pad0;
+  uint32_t _pad1;
+} SchedKvAppendArgs;
+
+/* Fill *a with defaults (ABI version, BF16 source and cache, the rest 0/NULL). */
+void sched_kv_default_args(SchedKvAppendArgs *a);
+
+/* Append on `stream` (hipStream_t; NULL = default). Asynchronous; returns 0,
+ * or -1 with sched_pd_last_error() set for invalid arguments. Pages written
+ * by one call must belong to one request each; calls that write the same
+ * pages must be stream-ordered. Replaces FlashInfer's append_paged_kv_cache
+ * at the serving engine's cache-write site (no call site in the reference's
+ * own tree). */
+int sched_kv_append(const SchedKvAppendArgs *a, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCHED_KV_H */

@@ -4,6 +4,9 @@ Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import
 this module, and only as the checker / the timed CPU baseline; no product code
 path imports, loads or calls anything under oracle/.
 
+The KV-cache writer's restatement is kv_append() (kv_oracle.c), with the
+fp8 encoder and scale rule it uses exposed for their own pins.
+
 Two independent CPU restatements of the reference's truncated attention:
   * decode(): liboracle.so (oracle.c), the reference's online-softmax loop
     (test/paged_decode.cu:124-153, test/py/test_dynamic_loop.py:77-100) in
@@ -41,8 +44,9 @@ def build() -> str:
 def load():
     global _lib
     if _lib is None:
+        srcs = [os.path.join(HERE, f) for f in ("oracle.c", "kv_oracle.c")]
         if not os.path.exists(LIB_PATH) or (
-                os.path.getmtime(LIB_PATH) < os.path.getmtime(os.path.join(HERE, "oracle.c"))):
+                os.path.getmtime(LIB_PATH) < max(os.path.getmtime(f) for f in srcs)):
             build()
         lib = ctypes.CDLL(LIB_PATH)
         lib.oracle_decode.restype = ctypes.c_int
@@ -56,6 +60,16 @@ def load():
         lib.oracle_max_threads.restype = ctypes.c_int
         lib.oracle_args_layout.restype = ctypes.c_int
         lib.oracle_args_layout.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int]
+        lib.oracle_kv_args_layout.restype = ctypes.c_int
+        lib.oracle_kv_args_layout.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int]
+        lib.oracle_kv_append.restype = ctypes.c_long
+        lib.oracle_kv_append.argtypes = [ctypes.POINTER(abi.SchedKvAppendArgs)]
+        lib.oracle_fp8_e4m3_from_float.restype = ctypes.c_uint8
+        lib.oracle_fp8_e4m3_from_float.argtypes = [ctypes.c_float]
+        lib.oracle_float_to_bf16.restype = ctypes.c_uint16
+        lib.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+        lib.oracle_pow2_scale.restype = ctypes.c_float
+        lib.oracle_pow2_scale.argtypes = [ctypes.c_float]
         _lib = lib
     return _lib
 
@@ -234,3 +248,59 @@ def numpy_decode(q, k_pool, v_pool, block_table, ctx_lens, *, mode=abi.SOFTMAX,
                 e = np.exp(s - s.max())
                 out[r, h * G + g] = (e[:, None] * Vt[kept]).sum(0) / e.sum()
     return out
+
+
+def fp8_e4m3_encode(x) -> np.ndarray:
+    """The oracle's e4m3fn encoder (RNE, saturating at 448) over an array."""
+    lib = load()
+    x = np.asarray(x, np.float32).ravel()
+    return np.array([lib.oracle_fp8_e4m3_from_float(float(v)) for v in x], np.uint8)
+
+
+def pow2_scale(a: float) -> float:
+    return load().oracle_pow2_scale(float(a))
+
+
+def kv_append(k_src, v_src, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
+              page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
+              num_tokens=None):
+    """Restated sched_kv_append on host copies. Pools: k [P, Hkv, ps, d];
+    v [P, Hkv, d, ps] (dmajor) or [P, Hkv, ps, d] (tokmajor); sources
+    [T, Hkv, d]. Returns (k_pool, v_pool, k_scale, v_scale, errors) as numpy
+    arrays of the pools' raw element bits (uint16 for bf16, uint8 for fp8)
+    and float32 scales (None without scales)."""
+    lib = load()
+    ks, src_code = _host(k_src)
+    vs, _ = _host(v_src)
+    kp, kv_code = _host(k_pool)
+    vp, _ = _host(v_pool)
+    kp, vp = kp.copy(), vp.copy()
+    app, _ = _host(append_indptr, np.int32)
+    ctx, _ = _host(ctx_lens, np.int32)
+    bt, _ = _host(block_table, np.int32)
+    pi, _ = _host(page_indptr, np.int32)
+    ksc = None if k_scale is None else _host(k_scale, np.float32)[0].copy()
+    vsc = None if v_scale is None else _host(v_scale, np.float32)[0].copy()
+    a = abi.default_kv_args()
+    a.src_dtype, a.kv_dtype = src_code, kv_code
+    P, hkv, ps, d = kp.shape
+    a.num_requests = ctx.size
+    a.num_kv_heads, a.head_dim, a.page_size = hkv, d, ps
+    a.num_tokens = ks.shape[0] if num_tokens is None else num_tokens
+    a.num_pages = P
+    a.src_tok_stride, a.src_head_stride = hkv * d, d
+    a.k_page_stride, a.k_head_stride, a.k_tok_stride = hkv * ps * d, ps * d, d
+    a.v_page_stride, a.v_head_stride = hkv * ps * d, ps * d
+    if v_layout == "dmajor":
+        a.v_tok_stride, a.v_dim_stride = 1, ps
+    else:
+        a.v_tok_stride, a.v_dim_stride = d, 1
+    a.bt_stride = bt.shape[1] if bt.ndim == 2 else 0
+    vp_ = lambda x: None if x is None else ctypes.c_void_p(x.ctypes.data)  # noqa: E731
+    a.k_src, a.v_src = vp_(ks), vp_(vs)
+    a.append_indptr, a.ctx_lens, a.block_table = vp_(app), vp_(ctx), vp_(bt)
+    a.page_indptr = vp_(pi)
+    a.k_pool, a.v_pool = vp_(kp), vp_(vp)
+    a.k_scale, a.v_scale = vp_(ksc), vp_(vsc)
+    errors = lib.oracle_kv_append(ctypes.byref(a))
+    return kp, vp, ksc, vsc, int(errors)

@@ -18,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libschedpd.so")
-SOURCES = ["sched_rt.hip", "paged_decode.hip", "probe.hip"]
+SOURCES = ["sched_rt.hip", "paged_decode.hip", "probe.hip", "kv_append.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

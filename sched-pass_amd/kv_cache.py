@@ -1,0 +1,273 @@
+"""The paged KV cache the decode kernels read: page allocator, per-request
+page lists, and the append path (`sched_kv_append` in include/sched_kv.h).
+
+Formats (what the reference's tests build around FlashInfer,
+test/py/eval_pi_makespan.py:46-60):
+  * CSR page table: page_indptr [R+1], page indices, last_page_len [R]
+    (ctx = (pages - 1) * page_size + last_page_len);
+  * 2-D block table [R, max_pages] (vLLM style) with ctx_lens [R];
+  * pools k [P, Hkv, page, d] and v [P, Hkv, d, page] (d-major, the MFMA
+    kernel's layout) or v [P, Hkv, page, d] (token-major);
+  * FlashInfer's NHD cache [P, 2, page, Hkv, d] is readable in place through
+    nhd_views() (strided pools, token-major V).
+
+Appends run on the GPU through the C ABI; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+import sched_abi as abi
+import sched_pd
+
+_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16}
+if hasattr(torch, "float8_e4m3fn"):
+    _DT[torch.float8_e4m3fn] = abi.FP8_E4M3
+
+
+class OutOfPages(RuntimeError):
+    """The pool has fewer free pages than an allocation needs."""
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
+           page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
+           max_append=0, errors=None, stream=None) -> None:
+    """Write source rows k_new/v_new [T, Hkv, d] (bf16 or fp32, dims
+    contiguous) into the pools: request r's rows append_indptr[r] ..
+    append_indptr[r+1]-1 go to positions ctx_lens[r] - n_r .. ctx_lens[r]-1
+    (ctx_lens counts tokens after the append). An fp8 pool needs k_scale /
+    v_scale [P * Hkv] float32 (read and written). `errors` (int32/uint32 [1],
+    optional) counts (token, kv-head) pairs the kernel could not place."""
+    a = abi.default_kv_args()
+    if k_new.dtype not in (torch.float32, torch.bfloat16) or v_new.dtype != k_new.dtype:
+        raise TypeError(f"sources must both be float32 or bfloat16, got {k_new.dtype}, "
+                        f"{v_new.dtype}")
+    if k_pool.dtype not in _DT or v_pool.dtype != k_pool.dtype:
+        raise TypeError(f"pool dtypes {k_pool.dtype}, {v_pool.dtype}")
+    if k_new.dim() != 3 or k_new.shape != v_new.shape or k_new.stride() != v_new.stride():
+        raise ValueError("k_new and v_new must be [T, Hkv, d] with the same strides")
+    if k_new.stride(2) != 1:
+        raise ValueError("source dims must be contiguous")
+    P, hkv, ps, d = k_pool.shape
+    if k_new.shape[1:] != (hkv, d):
+        raise ValueError(f"sources {tuple(k_new.shape)} vs pool heads/dims ({hkv}, {d})")
+    if k_pool.stride(3) != 1:
+        raise ValueError("k_pool dims must be contiguous")
+    a.src_dtype = _DT[k_new.dtype]
+    a.kv_dtype = _DT[k_pool.dtype]
+    a.num_requests = ctx_lens.numel()
+    a.num_kv_heads, a.head_dim, a.page_size = hkv, d, ps
+    a.num_tokens = k_new.shape[0]
+    a.max_append = int(max_append)
+    a.num_pages = P
+    a.src_tok_stride, a.src_head_stride = k_new.stride(0), k_new.stride(1)
+    a.k_page_stride, a.k_head_stride, a.k_tok_stride = k_pool.stride()[:3]
+    if v_layout == "dmajor":
+        if tuple(v_pool.shape) != (P, hkv, d, ps):
+            raise ValueError(f"d-major v_pool must be {(P, hkv, d, ps)}, got {tuple(v_pool.shape)}")
+        a.v_page_stride, a.v_head_stride = v_pool.stride(0), v_pool.stride(1)
+        a.v_dim_stride, a.v_tok_stride = v_pool.stride(2), v_pool.stride(3)
+    elif v_layout == "tokmajor":
+        if tuple(v_pool.shape) != (P, hkv, ps, d):
+            raise ValueError(f"token-major v_pool must be {(P, hkv, ps, d)}, "
+                             f"got {tuple(v_pool.shape)}")
+        a.v_page_stride, a.v_head_stride = v_pool.stride(0), v_pool.stride(1)
+        a.v_tok_stride, a.v_dim_stride = v_pool.stride(2), v_pool.stride(3)
+    else:
+        raise ValueError(f"v_layout {v_layout!r}")
+    for t, what in ((k_new, "k_new"), (v_new, "v_new"), (k_pool, "k_pool"), (v_pool, "v_pool"),
+                    (append_indptr, "append_indptr"), (ctx_lens, "ctx_lens"),
+                    (block_table, "block_table"), (page_indptr, "page_indptr"),
+                    (k_scale, "k_scale"), (v_scale, "v_scale"), (errors, "errors")):
+        if t is not None and not t.is_cuda:
+            raise ValueError(f"{what} must be a device tensor (got {t.device})")
+    for t, what in ((append_indptr, "append_indptr"), (ctx_lens, "ctx_lens"),
+                    (block_table, "block_table"), (page_indptr, "page_indptr")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"{what} must be contiguous int32")
+    if append_indptr.numel() != a.num_requests + 1:
+        raise ValueError("append_indptr needs num_requests + 1 entries")
+    if page_indptr is None:
+        if block_table.dim() != 2:
+            raise ValueError("block_table must be [num_requests, max_pages] without page_indptr")
+        a.bt_stride = block_table.stride(0)
+    elif page_indptr.numel() != a.num_requests + 1:
+        raise ValueError("page_indptr needs num_requests + 1 entries")
+    if a.kv_dtype == abi.FP8_E4M3:
+        for t, what in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+            if t is None or t.dtype != torch.float32 or t.numel() < P * hkv \
+                    or not t.is_contiguous():
+                raise ValueError(f"an fp8 pool needs contiguous float32 {what} [P * Hkv]")
+    if errors is not None and (errors.dtype not in (torch.int32, torch.uint32)
+                               or errors.numel() < 1):
+        raise ValueError("errors must be a 32-bit integer tensor")
+    a.k_src, a.v_src = _ptr(k_new), _ptr(v_new)
+    a.append_indptr, a.ctx_lens = _ptr(append_indptr), _ptr(ctx_lens)
+    a.block_table, a.page_indptr = _ptr(block_table), _ptr(page_indptr)
+    a.k_pool, a.v_pool = _ptr(k_pool), _ptr(v_pool)
+    if a.kv_dtype == abi.FP8_E4M3:
+        a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
+    a.errors = _ptr(errors)
+    if stream is None:
+        stream = torch.cuda.current_stream(k_pool.device)
+    lib = abi.load_library()
+    if lib.sched_kv_append(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream)) != 0:
+        raise RuntimeError(abi.last_error())
+
+
+def ctx_lens_from_last_page_len(page_indptr, last_page_len, page_size: int):
+    """CSR page counts + last-page fill -> token counts (0 pages -> 0)."""
+    pages = page_indptr[1:] - page_indptr[:-1]
+    ctx = (pages - 1) * page_size + last_page_len
+    return torch.where(pages > 0, ctx, torch.zeros_like(ctx)).to(torch.int32)
+
+
+def nhd_views(kv):
+    """FlashInfer's NHD paged cache [P, 2, page, Hkv, d] as (k_pool, v_pool)
+    views [P, Hkv, page, d] for paged_decode(..., v_layout="tokmajor")."""
+    if kv.dim() != 5 or kv.shape[1] != 2:
+        raise ValueError(f"expected [P, 2, page, Hkv, d], got {tuple(kv.shape)}")
+    return kv[:, 0].permute(0, 2, 1, 3), kv[:, 1].permute(0, 2, 1, 3)
+
+
+class PageAllocator:
+    """LIFO free list over page ids 0..num_pages-1 (host side). Freed pages
+    are reused first, which keeps a steady-state batch on recently touched
+    pages."""
+
+    def __init__(self, num_pages: int):
+        self.num_pages = int(num_pages)
+        self._stack = np.arange(self.num_pages - 1, -1, -1, dtype=np.int32)
+        self._top = self.num_pages
+        self._used = np.zeros(self.num_pages, dtype=bool)
+
+    @property
+    def num_free(self) -> int:
+        return self._top
+
+    def alloc(self, n: int) -> np.ndarray:
+        n = int(n)
+        if n < 0:
+            raise ValueError("negative page count")
+        if n > self._top:
+            raise OutOfPages(f"need {n} pages, {self._top} free of {self.num_pages}")
+        pages = self._stack[self._top - n:self._top][::-1].copy()
+        self._top -= n
+        self._used[pages] = True
+        return pages
+
+    def free(self, pages) -> None:
+        pages = np.asarray(pages, dtype=np.int32).ravel()
+        if pages.size == 0:
+            return
+        if pages.min() < 0 or pages.max() >= self.num_pages:
+            raise ValueError("page id outside the pool")
+        if np.unique(pages).size != pages.size or not self._used[pages].all():
+            raise ValueError("freeing a page that is not allocated (double free?)")
+        self._used[pages] = False
+        self._stack[self._top:self._top + pages.size] = pages[::-1]
+        self._top += pages.size
+
+
+class PagedKvCache:
+    """Pools + allocator + per-request page lists for one layer's KV.
+
+    k_pool [P, Hkv, page, d], v_pool [P, Hkv, d, page] (d-major), and for an
+    fp8 cache k_scale / v_scale [P * Hkv] (index page * Hkv + head)."""
+
+    def __init__(self, num_pages: int, num_kv_heads: int, head_dim: int, page_size: int = 16,
+                 dtype=torch.bfloat16, device="cuda"):
+        self.page_size, self.num_kv_heads, self.head_dim = page_size, num_kv_heads, head_dim
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.k_pool = torch.zeros(num_pages, num_kv_heads, page_size, head_dim, dtype=dtype,
+                                  device=self.device)
+        self.v_pool = torch.zeros(num_pages, num_kv_heads, head_dim, page_size, dtype=dtype,
+                                  device=self.device)
+        fp8 = dtype == getattr(torch, "float8_e4m3fn", None)
+        self.k_scale = torch.zeros(num_pages * num_kv_heads, dtype=torch.float32,
+                                   device=self.device) if fp8 else None
+        self.v_scale = torch.zeros_like(self.k_scale) if fp8 else None
+        self.allocator = PageAllocator(num_pages)
+        self.pages: dict = {}
+        self.lens: dict = {}
+
+    # -- bookkeeping ----------------------------------------------------------
+    def add_request(self, rid) -> None:
+        if rid in self.pages:
+            raise KeyError(f"request {rid!r} already present")
+        self.pages[rid] = []
+        self.lens[rid] = 0
+
+    def release(self, rid) -> None:
+        self.allocator.free(self.pages.pop(rid))
+        del self.lens[rid]
+
+    def reserve(self, rids, counts) -> None:
+        """Allocate pages so that each request has room for counts[i] more
+        tokens; all or nothing."""
+        need = []
+        for rid, n in zip(rids, counts):
+            want = math.ceil((self.lens[rid] + int(n)) / self.page_size)
+            need.append(max(0, want - len(self.pages[rid])))
+        total = sum(need)
+        if total > self.allocator.num_free:
+            raise OutOfPages(f"need {total} pages, {self.allocator.num_free} free")
+        fresh = self.allocator.alloc(total)
+        at = 0
+        for rid, k in zip(rids, need):
+            self.pages[rid].extend(fresh[at:at + k].tolist())
+            at += k
+
+    # -- tables ---------------------------------------------------------------
+    def block_table(self, rids):
+        """(block_table [R, max_pages] int32, ctx_lens [R] int32) on the device;
+        unused entries are -1."""
+        width = max([len(self.pages[r]) for r in rids] + [1])
+        bt = np.full((len(rids), width), -1, dtype=np.int32)
+        for i, r in enumerate(rids):
+            bt[i, :len(self.pages[r])] = self.pages[r]
+        ctx = np.array([self.lens[r] for r in rids], dtype=np.int32)
+        return (torch.from_numpy(bt).to(self.device), torch.from_numpy(ctx).to(self.device))
+
+    def csr(self, rids):
+        """(page_indptr [R+1], indices, last_page_len [R]) int32 on the device."""
+        counts = np.array([len(self.pages[r]) for r in rids], dtype=np.int64)
+        indptr = np.zeros(len(rids) + 1, dtype=np.int32)
+        indptr[1:] = np.cumsum(counts)
+        indices = np.array([p for r in rids for p in self.pages[r]], dtype=np.int32)
+        last = np.array([self.lens[r] - (len(self.pages[r]) - 1) * self.page_size
+                         if self.pages[r] else 0 for r in rids], dtype=np.int32)
+        to = lambda x: torch.from_numpy(x).to(self.device)  # noqa: E731
+        return to(indptr), to(indices if indices.size else np.zeros(1, np.int32)), to(last)
+
+    # -- writes and reads -----------------------------------------------------
+    def append(self, rids, k_new, v_new, counts=None, errors=None) -> None:
+        """Append counts[i] rows (default 1 each) of k_new / v_new [T, Hkv, d]
+        to request rids[i], rows in request order."""
+        counts = [1] * len(rids) if counts is None else [int(c) for c in counts]
+        if sum(counts) != k_new.shape[0]:
+            raise ValueError(f"counts sum to {sum(counts)}, sources have {k_new.shape[0]} rows")
+        self.reserve(rids, counts)
+        for rid, n in zip(rids, counts):
+            self.lens[rid] += n
+        bt, ctx = self.block_table(rids)
+        app = np.zeros(len(rids) + 1, dtype=np.int32)
+        app[1:] = np.cumsum(counts)
+        append(k_new, v_new, torch.from_numpy(app).to(self.device), ctx, self.k_pool,
+               self.v_pool, bt, k_scale=self.k_scale, v_scale=self.v_scale,
+               max_append=max(counts + [0]), errors=errors)
+
+    def decode(self, q, rids, **kw):
+        """One decode step over the requests' current contexts."""
+        bt, ctx = self.block_table(rids)
+        return sched_pd.paged_decode(q, self.k_pool, self.v_pool, bt, ctx, k_scale=self.k_scale,
+                                     v_scale=self.v_scale, **kw)

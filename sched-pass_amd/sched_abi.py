@@ -1,4 +1,5 @@
-"""ctypes mirror of include/sched_pd.h and the loader of libschedpd.so.
+"""ctypes mirror of include/sched_pd.h and include/sched_kv.h, and the
+loader of libschedpd.so.
 
 Pure ctypes: importing this module touches no GPU. The library is loaded from
 next to this file (built in-tree by build_lib.py); a missing library is an
@@ -78,7 +79,39 @@ def default_args() -> SchedDecodeArgs:
     return a
 
 
-# Every function include/sched_pd.h declares: name -> (restype, argtypes).
+# --- KV-cache writer (include/sched_kv.h) --------------------------------------
+KV_ABI_VERSION = 1
+
+
+class SchedKvAppendArgs(ctypes.Structure):
+    """Field-for-field mirror of `SchedKvAppendArgs` in include/sched_kv.h."""
+    _fields_ = [
+        ("abi_version", _u32), ("src_dtype", _u32), ("kv_dtype", _u32),
+        ("num_requests", _u32), ("num_kv_heads", _u32), ("head_dim", _u32),
+        ("page_size", _u32), ("bt_stride", _u32), ("max_append", _u32),
+        ("num_tokens", _u32), ("num_pages", ctypes.c_uint64),
+        ("k_src", _p), ("v_src", _p),
+        ("src_tok_stride", _i64), ("src_head_stride", _i64),
+        ("append_indptr", _p), ("ctx_lens", _p), ("block_table", _p),
+        ("page_indptr", _p),
+        ("k_pool", _p), ("v_pool", _p),
+        ("k_page_stride", _i64), ("k_head_stride", _i64), ("k_tok_stride", _i64),
+        ("v_page_stride", _i64), ("v_head_stride", _i64), ("v_tok_stride", _i64),
+        ("v_dim_stride", _i64),
+        ("k_scale", _p), ("v_scale", _p), ("errors", _p),
+        ("_pad0", _u32), ("_pad1", _u32),
+    ]
+
+
+def default_kv_args() -> SchedKvAppendArgs:
+    """Same defaults as sched_kv_default_args() in C."""
+    a = SchedKvAppendArgs()
+    a.abi_version = KV_ABI_VERSION
+    a.src_dtype = a.kv_dtype = BF16
+    return a
+
+
+# Every function include/*.h declares: name -> (restype, argtypes).
 _c_bool = ctypes.c_bool
 SIGNATURES = {
     "sched_rt_init": (_c_bool, []),
@@ -104,6 +137,8 @@ SIGNATURES = {
     "sched_pd_cu_count": (ctypes.c_int, []),
     "sched_pd_read_probe": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _p]),
     "sched_pd_last_error": (ctypes.c_char_p, []),
+    "sched_kv_default_args": (None, [ctypes.POINTER(SchedKvAppendArgs)]),
+    "sched_kv_append": (ctypes.c_int, [ctypes.POINTER(SchedKvAppendArgs), _p]),
     "launch_paged_softmax": (None, [_p, _p, _p, _p, _p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, _p]),
     "paged_softmax_occupancy": (ctypes.c_int, []),

@@ -1,5 +1,5 @@
 """The C ABI without a GPU: the library loads, exports exactly what
-include/sched_pd.h declares, the ctypes mirror matches the C layout, and the
+include/*.h declare, the ctypes mirror matches the C layout, and the
 host-side argument validation / kernel selection behave (no device calls)."""
 import ctypes
 import os
@@ -13,11 +13,16 @@ import oracle
 import sched_abi as abi
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "sched_pd.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("sched_pd.h", "sched_kv.h")]
+
+
+def test_every_header_is_listed():
+    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == sorted(
+        os.path.basename(h) for h in HEADERS)
 
 
 def header_functions():
-    src = open(HEADER).read()
+    src = "".join(open(h).read() for h in HEADERS)
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = re.findall(r"^\s*[A-Za-z_][\w \*]*?\b(\w+)\s*\([^;{]*\)\s*;", src, re.M)
     return sorted(set(n for n in names if n not in ("static_assert",)))
@@ -66,7 +71,7 @@ def test_default_args_match(schedlib):
 
 
 def test_plane_constants_mirror_header():
-    src = open(HEADER).read()
+    src = open(HEADERS[0]).read()
     def define(name):
         return int(re.search(rf"#define {name} (\w+)", src).group(1).rstrip("u"), 0)
     assert define("SCHED_MAX_TASKS") == abi.SCHED_MAX_TASKS

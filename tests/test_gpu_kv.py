@@ -1,0 +1,233 @@
+"""The KV-cache writer on the GPU: sched_kv_append through the C ABI against
+the oracle, bit for bit (pools, scales, error count), the hardware fp8
+encoder on every tie, the cache manager's decode loop, and size-independent
+readback properties at the full Llama-3-8B decode size."""
+import numpy as np
+import pytest
+import torch
+
+import kv_cache
+import oracle
+import sched_pd
+from kv_cases import FP8, append_case, random_pool
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib(schedlib):
+    torch.cuda.init()
+    return schedlib
+
+
+def raw(t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == FP8:
+        return t.view(torch.uint8).numpy()
+    return t.numpy()
+
+
+def run_gpu(c):
+    dev = "cuda"
+    k_pool, v_pool = c["k_pool"].to(dev), c["v_pool"].to(dev)
+    ks = None if c["k_scale"] is None else c["k_scale"].to(dev)
+    vs = None if c["v_scale"] is None else c["v_scale"].to(dev)
+    errors = torch.zeros(1, dtype=torch.int32, device=dev)
+    pind = None if c["pind"] is None else torch.from_numpy(c["pind"]).to(dev)
+    torch.cuda.synchronize()
+    kv_cache.append(c["k_src"].to(dev), c["v_src"].to(dev), torch.from_numpy(c["app"]).to(dev),
+                    torch.from_numpy(c["ctx"].astype(np.int32)).to(dev), k_pool, v_pool,
+                    torch.from_numpy(c["table"]).to(dev), page_indptr=pind,
+                    v_layout=c["v_layout"], k_scale=ks, v_scale=vs, errors=errors)
+    torch.cuda.synchronize()
+    return (raw(k_pool), raw(v_pool), None if ks is None else ks.cpu().numpy(),
+            None if vs is None else vs.cpu().numpy(), int(errors.item()))
+
+
+def assert_same(got, ref):
+    for g, r, what in zip(got, ref, ("k_pool", "v_pool", "k_scale", "v_scale", "errors")):
+        if r is None:
+            assert g is None, what
+        elif what == "errors":
+            assert g == r, what
+        else:
+            assert np.array_equal(g, r), (what, int(np.sum(g != r)))
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8])
+@pytest.mark.parametrize("v_layout", ["dmajor", "tokmajor"])
+@pytest.mark.parametrize("csr", [False, True])
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
+def test_append_is_bit_exact_with_the_oracle(kv, v_layout, csr, src):
+    for seed, (hkv, d) in enumerate([(8, 128), (4, 64), (2, 32)]):
+        print(f"case kv={kv} v={v_layout} csr={csr} src={src} hkv={hkv} d={d}", flush=True)
+        c = append_case(100 + seed, kv, v_layout, csr, hkv=hkv, d=d, src_dtype=src)
+        assert_same(run_gpu(c), c["out"])
+
+
+def test_append_into_partial_pages_regrows_fp8_scales():
+    # every request already holds a partial page; the new rows are 16x larger
+    c = append_case(7, FP8, "dmajor", prior=[3, 5, 17, 30, 1], n=[1, 4, 9, 20, 15], hkv=8, d=128)
+    got = run_gpu(c)
+    assert_same(got, c["out"])
+    assert np.any(got[2] != c["k_scale"].numpy())
+
+
+def test_page_size_32_and_64():
+    for ps in (32, 64):
+        c = append_case(11, FP8, "dmajor", hkv=4, d=128, ps=ps)
+        assert_same(run_gpu(c), c["out"])
+        c = append_case(12, torch.bfloat16, "tokmajor", hkv=4, d=128, ps=ps, csr=True)
+        assert_same(run_gpu(c), c["out"])
+
+
+def test_errors_are_counted_and_nothing_else_is_written():
+    rng = np.random.default_rng(9)
+    hkv, d, ps = 2, 8, 8
+    c = dict(k_src=torch.ones(12, hkv, d, dtype=torch.bfloat16),
+             v_src=torch.full((12, hkv, d), 2.0, dtype=torch.bfloat16),
+             app=np.array([0, 3, 8, 11, 12], np.int32), ctx=np.array([3, 2, 3, 1]),
+             table=np.array([[9, 0], [1, 0], [-1, 0], [2, 0]], np.int32), pind=None,
+             k_pool=random_pool((4, hkv, ps, d), torch.bfloat16, rng),
+             v_pool=random_pool((4, hkv, d, ps), torch.bfloat16, rng),
+             k_scale=None, v_scale=None, v_layout="dmajor", ps=ps)
+    c["out"] = oracle.kv_append(c["k_src"], c["v_src"], c["app"], c["ctx"], c["k_pool"],
+                                c["v_pool"], c["table"])
+    got = run_gpu(c)
+    assert got[4] == (3 + 5 + 3) * hkv
+    assert_same(got, c["out"])
+
+
+def test_hardware_fp8_encoder_on_every_tie_and_neighbour():
+    """One page whose K amax is exactly 448 (scale 1): the kernel's codes for
+    every e4m3 value, every midpoint between neighbours and the floats just
+    either side of each midpoint equal torch's RNE cast."""
+    vals = oracle.fp8_e4m3_table()
+    vals = np.unique(vals[np.isfinite(vals)])
+    mids = (vals[:-1] + vals[1:]) / 2
+    x = np.concatenate([vals, mids, np.nextafter(mids, np.float32(np.inf)),
+                        np.nextafter(mids, np.float32(-np.inf))]).astype(np.float32)
+    x = np.concatenate([x, [448.0]])
+    d = 128
+    T = -(-x.size // d)
+    padded = np.zeros(T * d, np.float32)
+    padded[:x.size] = x
+    ps = 16 * -(-T // 16)
+    src = torch.from_numpy(padded.reshape(T, 1, d)).cuda()
+    k_pool = torch.zeros(1, 1, ps, d, dtype=FP8, device="cuda")
+    v_pool = torch.zeros(1, 1, d, ps, dtype=FP8, device="cuda")
+    ks = torch.zeros(1, device="cuda")
+    vs = torch.zeros(1, device="cuda")
+    kv_cache.append(src, src, torch.tensor([0, T], dtype=torch.int32, device="cuda"),
+                    torch.tensor([T], dtype=torch.int32, device="cuda"), k_pool, v_pool,
+                    torch.zeros(1, 1, dtype=torch.int32, device="cuda"), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert ks.item() == 1.0
+    got = raw(k_pool)[0, 0, :T].reshape(-1)[:x.size]
+    ref = torch.from_numpy(x).to(FP8).view(torch.uint8).numpy()
+    assert np.array_equal(got, ref), int(np.sum(got != ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
+def test_cache_prefill_then_decode_loop(dtype):
+    """PagedKvCache: a prefill append, then 20 one-token appends per request
+    (page boundaries crossed), mirrored on the oracle; then a decode step over
+    the cache against the oracle decode on the same pools."""
+    rng = np.random.default_rng(21)
+    hkv, hq, d, ps, R = 8, 32, 128, 16, 6
+    cache = kv_cache.PagedKvCache(64, hkv, d, ps, dtype=dtype)
+    rids = list(range(R))
+    for r in rids:
+        cache.add_request(r)
+    host = [raw(cache.k_pool), raw(cache.v_pool),
+            None if cache.k_scale is None else cache.k_scale.cpu().numpy(),
+            None if cache.v_scale is None else cache.v_scale.cpu().numpy()]
+
+    def step(counts):
+        T = int(sum(counts))
+        k = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).bfloat16()
+        v = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).bfloat16()
+        cache.append(rids, k.cuda(), v.cuda(), counts)
+        bt, ctx = cache.block_table(rids)
+        app = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        as_t = (lambda a: torch.from_numpy(a).view(FP8)) if dtype == FP8 else \
+               (lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16))
+        kp, vp, ks, vs, err = oracle.kv_append(k, v, app, ctx.cpu().numpy(), as_t(host[0]),
+                                               as_t(host[1]), bt.cpu().numpy(),
+                                               k_scale=host[2], v_scale=host[3])
+        assert err == 0
+        host[:] = [kp, vp, ks, vs]
+
+    step(rng.integers(1, 100, R).tolist())
+    for _ in range(20):
+        step([1] * R)
+    torch.cuda.synchronize()
+    assert np.array_equal(raw(cache.k_pool), host[0])
+    assert np.array_equal(raw(cache.v_pool), host[1])
+    if dtype == FP8:
+        assert np.array_equal(cache.k_scale.cpu().numpy(), host[2])
+        assert np.array_equal(cache.v_scale.cpu().numpy(), host[3])
+    q = torch.randn(R, hq, d, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(R, hq, d, dtype=torch.float32, device="cuda")
+    cache.decode(q, rids, out=out)
+    bt, ctx = cache.block_table(rids)
+    ref = oracle.decode(q, cache.k_pool, cache.v_pool, bt, ctx, k_scale=cache.k_scale,
+                        v_scale=cache.v_scale)
+    r = np.asarray(ref, np.float64)
+    err = float(np.max(np.abs(out.cpu().double().numpy() - r) / (1 + np.abs(r))))
+    assert err <= TOL_BF16
+    args = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out,
+                               k_scale=cache.k_scale, v_scale=cache.v_scale)
+    assert sched_pd.kernel_kind(args) == "mfma"
+
+
+def _full_size(dtype):
+    """Llama-3-8B decode KV (64 requests x 2048 tokens, Hkv 8, d 128, page 16)
+    written by one bulk append into a shuffled pool."""
+    R, T, hkv, d, ps = 64, 2048, 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    k = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
+    v = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
+    npg = R * T // ps
+    pages = torch.randperm(npg + 512, device="cuda", generator=g)[:npg].int().view(R, T // ps)
+    kp = torch.zeros(npg + 512, hkv, ps, d, dtype=dtype, device="cuda")
+    vp = torch.zeros(npg + 512, hkv, d, ps, dtype=dtype, device="cuda")
+    ks = vs = None
+    if dtype == FP8:
+        ks = torch.zeros((npg + 512) * hkv, device="cuda")
+        vs = torch.zeros_like(ks)
+    app = torch.arange(0, R * T + 1, T, dtype=torch.int32, device="cuda")
+    ctx = torch.full((R,), T, dtype=torch.int32, device="cuda")
+    errors = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kv_cache.append(k, v, app, ctx, kp, vp, pages, k_scale=ks, v_scale=vs, max_append=T,
+                    errors=errors)
+    torch.cuda.synchronize()
+    assert errors.item() == 0
+    # gather back into [R*T, hkv, d] through the table
+    flat = pages.reshape(-1).long()
+    kb = kp[flat].permute(0, 2, 1, 3).reshape(R * T, hkv, d)
+    vb = vp[flat].permute(0, 3, 1, 2).reshape(R * T, hkv, d)
+    return k, v, kb, vb, flat, ks, vs, hkv, ps
+
+
+def test_full_size_bf16_append_reads_back_identically():
+    k, v, kb, vb, *_ = _full_size(torch.bfloat16)
+    assert torch.equal(kb, k) and torch.equal(vb, v)
+
+
+def test_full_size_fp8_append_scales_and_error_bound():
+    k, v, kb, vb, flat, ks, vs, hkv, ps = _full_size(FP8)
+    for src, back, sc in ((k, kb, ks), (v, vb, vs)):
+        amax = src.float().abs().view(-1, ps, hkv, 128).amax(dim=(1, 3))      # [pages, hkv]
+        s = sc.view(-1, hkv)[flat]                                             # [pages, hkv]
+        # the least power of two with amax <= 448 s
+        assert torch.all(amax <= 448 * s) and torch.all(amax > 224 * s)
+        assert torch.all(torch.frexp(s).mantissa == 0.5)
+        deq = back.float().view(-1, ps, hkv, 128) * s[:, None, :, None]
+        x = src.float().view(-1, ps, hkv, 128)
+        bound = x.abs() * 2 ** -4 + s[:, None, :, None] * 2 ** -10
+        assert torch.all((deq - x).abs() <= bound)
