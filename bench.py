@@ -267,6 +267,61 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES)
                                  "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())}}
 
 
+def bench_kv_append(torch, steps=20):
+    """The cache writer (sched_kv_append) on the Llama-3-8B decode shape
+    (Hkv 8, d 128, page 16, d-major V), bf16 K/V rows in:
+      decode_step: one token for each of 64 requests at ragged positions
+        (ctx after the append ~ U[1024, 2048]), into a bf16 and an fp8 cache;
+      bulk: the whole 64 x 2048-token KV of the uniform batch in one call.
+    Bytes per call = source rows read + cache bytes written (+ fp8 scales);
+    the d-major V's read-merge of a partial 4-slot group is not counted."""
+    import numpy as np
+    import kv_cache
+    R, T, hkv, d, ps = 64, 2048, 8, 128, 16
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    res = {}
+    fp8 = torch.float8_e4m3fn
+    npg = R * T // ps
+    bt = torch.randperm(npg, device="cuda", generator=g).int().view(R, T // ps)
+    k_big = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
+    v_big = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
+    rng = np.random.default_rng(5)
+    ctx_step = torch.from_numpy(rng.integers(1024, 2049, R).astype(np.int32)).cuda()
+    k1, v1 = k_big[:R].contiguous(), v_big[:R].contiguous()
+    app_step = torch.arange(R + 1, dtype=torch.int32, device="cuda")
+    app_bulk = torch.arange(0, R * T + 1, T, dtype=torch.int32, device="cuda")
+    ctx_bulk = torch.full((R,), T, dtype=torch.int32, device="cuda")
+    for name, dt in (("bf16", torch.bfloat16), ("fp8", fp8)):
+        kp = torch.zeros(npg, hkv, ps, d, dtype=dt, device="cuda")
+        vp = torch.zeros(npg, hkv, d, ps, dtype=dt, device="cuda")
+        ks = vs = None
+        if dt == fp8:
+            ks = torch.zeros(npg * hkv, device="cuda")
+            vs = torch.zeros_like(ks)
+        esz = kp.element_size()
+        scale_b = 0 if ks is None else 2 * 4
+        for label, src_k, src_v, app, ctx, ntok, max_app in (
+                ("bulk", k_big, v_big, app_bulk, ctx_bulk, R * T, T),
+                ("decode_step", k1, v1, app_step, ctx_step, R, 1)):
+            a = kv_cache.build_append_args(src_k, src_v, app, ctx, kp, vp, bt, k_scale=ks,
+                                           v_scale=vs, max_append=max_app)
+            step = lambda i: kv_cache.launch_append(a, stream)  # noqa: E731
+            for i in range(3):
+                step(i)
+            torch.cuda.synchronize()
+            ms, per = time_launches(step, steps, stream)
+            pages_touched = R * hkv * (-(-max_app // ps))
+            nbytes = ntok * hkv * d * 2 * (2 + esz) + pages_touched * scale_b
+            res[f"{label}_{name}"] = {"us": round(ms * 1e3, 2), "us_min": round(min(per) * 1e3, 2),
+                                      "bytes": nbytes,
+                                      "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                      "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9
+                                                             / HBM_PEAK_GBS, 4)}
+        del kp, vp, ks, vs
+    return res
+
+
 def profiled_traffic():
     """HBM bytes per decode launch from the committed PMC summary (two
     rocprofv3 --pmc runs, FETCH_SIZE calibrated on the read probe), or None."""
@@ -355,6 +410,7 @@ def main():
         line["hetero_makespan"] = bench_hetero(torch, sched_pd, workloads, SchedPlane, cu)
         line["shed_policy"] = bench_shed(torch, sched_pd, workloads, SchedPlane, cu)
         line["fp8_qwen2_7b"] = bench_fp8(torch, sched_pd, workloads, SchedPlane, cu)
+        line["kv_append"] = bench_kv_append(torch)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, workloads)
     print(json.dumps(line), flush=True)

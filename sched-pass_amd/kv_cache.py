@@ -46,6 +46,24 @@ def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *
     (ctx_lens counts tokens after the append). An fp8 pool needs k_scale /
     v_scale [P * Hkv] float32 (read and written). `errors` (int32/uint32 [1],
     optional) counts (token, kv-head) pairs the kernel could not place."""
+    a = build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table,
+                          page_indptr=page_indptr, v_layout=v_layout, k_scale=k_scale,
+                          v_scale=v_scale, max_append=max_append, errors=errors)
+    launch_append(a, stream if stream is not None else torch.cuda.current_stream(k_pool.device))
+
+
+def launch_append(a: abi.SchedKvAppendArgs, stream) -> None:
+    """Launch a prepared append on a torch stream (the tensors behind `a`
+    must stay alive until it has run)."""
+    lib = abi.load_library()
+    if lib.sched_kv_append(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream)) != 0:
+        raise RuntimeError(abi.last_error())
+
+
+def build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
+                      page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
+                      max_append=0, errors=None) -> abi.SchedKvAppendArgs:
+    """Validate and fill a SchedKvAppendArgs (no launch); see append()."""
     a = abi.default_kv_args()
     if k_new.dtype not in (torch.float32, torch.bfloat16) or v_new.dtype != k_new.dtype:
         raise TypeError(f"sources must both be float32 or bfloat16, got {k_new.dtype}, "
@@ -116,11 +134,7 @@ def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *
     if a.kv_dtype == abi.FP8_E4M3:
         a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
     a.errors = _ptr(errors)
-    if stream is None:
-        stream = torch.cuda.current_stream(k_pool.device)
-    lib = abi.load_library()
-    if lib.sched_kv_append(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream)) != 0:
-        raise RuntimeError(abi.last_error())
+    return a
 
 
 def ctx_lens_from_last_page_len(page_indptr, last_page_len, page_size: int):

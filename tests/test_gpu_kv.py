@@ -231,3 +231,46 @@ def test_full_size_fp8_append_scales_and_error_bound():
         x = src.float().view(-1, ps, hkv, 128)
         bound = x.abs() * 2 ** -4 + s[:, None, :, None] * 2 ** -10
         assert torch.all((deq - x).abs() <= bound)
+
+
+def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
+    """A FlashInfer NHD cache [P, 2, page, Hkv, d] with its CSR table
+    (indptr, indices, last_page_len; test/py/eval_pi_makespan.py:46-60) is
+    decoded in place (strided views, token-major V) and, imported through the
+    writer into the d-major layout, by the MFMA kernel; both match the oracle
+    on the same cache."""
+    rng = np.random.default_rng(31)
+    P, ps, hkv, hq, d = 64, 16, 4, 16, 128
+    pages = np.array([3, 1, 7, 2, 9, 5], np.int32)
+    R = pages.size
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)).cuda()
+    indices = torch.from_numpy(rng.permutation(P)[:pages.sum()].astype(np.int32)).cuda()
+    last = torch.from_numpy(rng.integers(1, ps + 1, R).astype(np.int32)).cuda()
+    ctx = kv_cache.ctx_lens_from_last_page_len(indptr, last, ps)
+    kv = (torch.randn(P, 2, ps, hkv, d, device="cuda") / d ** 0.5).bfloat16()
+    q = (torch.randn(R, hq, d, device="cuda") / d ** 0.5).bfloat16()
+    kview, vview = kv_cache.nhd_views(kv)
+    out = torch.empty(R, hq, d, dtype=torch.float32, device="cuda")
+    sched_pd.paged_decode(q, kview, vview, indices, ctx, out=out, page_indptr=indptr,
+                          v_layout="tokmajor")
+    torch.cuda.synchronize()
+    ref = np.asarray(oracle.decode(q, kview, vview, indices, ctx, page_indptr=indptr,
+                                   v_layout="tokmajor"), np.float64)
+    err = lambda o: float(np.max(np.abs(o.cpu().double().numpy() - ref) / (1 + np.abs(ref))))  # noqa: E731
+    assert err(out) <= TOL_BF16
+    # import: gather each request's tokens in order and append them
+    rows_k, rows_v = [], []
+    for r in range(R):
+        pg = indices[int(indptr[r]):int(indptr[r + 1])].long()
+        n = int(ctx[r])
+        rows_k.append(kv[pg, 0].reshape(-1, hkv, d)[:n])
+        rows_v.append(kv[pg, 1].reshape(-1, hkv, d)[:n])
+    cache = kv_cache.PagedKvCache(P, hkv, d, ps, dtype=torch.bfloat16)
+    for r in range(R):
+        cache.add_request(r)
+    cache.append(list(range(R)), torch.cat(rows_k), torch.cat(rows_v),
+                 ctx.cpu().tolist())
+    out2 = torch.empty_like(out)
+    cache.decode(q, list(range(R)), out=out2)
+    torch.cuda.synchronize()
+    assert err(out2) <= TOL_BF16
