@@ -47,7 +47,9 @@ extern "C" {
  *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
  *   V: v_pool + page*v_page_stride + h*v_head_stride + t*v_tok_stride + j*v_dim_stride
  * with v_tok_stride == 1 (d-major V, the MFMA kernel's layout) or
- * v_dim_stride == 1 (token-major V). Source row i, head h, dim j:
+ * v_dim_stride == 1 (token-major V). A d-major V is written in groups of 4
+ * slots: the unused slots after a request's last token, up to its group's
+ * end, are written as zero. Source row i, head h, dim j:
  *   k_src[i*src_tok_stride + h*src_head_stride + j] (v_src alike). */
 typedef struct SchedKvAppendArgs {
   uint32_t abi_version;   /* SCHED_KV_ABI_VERSION */
@@ -78,8 +80,10 @@ typedef struct SchedKvAppendArgs {
    * (token, kv-head) it could not write (a page id outside the pool, a table
    * entry past the request's pages, or n_r > ctx_lens[r]) and skips it. */
   uint32_t *errors;
+  /* kv-heads one workgroup writes (divides num_kv_heads, <= 64); 0 = chosen
+   * from the append size. Does not change the result. */
+  uint32_t heads_per_group;
   uint32_t _pad0;
-  uint32_t _pad1;
 } SchedKvAppendArgs;
 
 /* Fill *a with defaults (ABI version, BF16 source and cache, the rest 0/NULL). */

@@ -2,15 +2,16 @@
 // source token rows into the decode pools, converting to bf16 / fp32 or
 // quantising to fp8 e4m3fn with per-(page, kv-head) power-of-two scales.
 //
-// One workgroup serves one (request, kv-head) pair and a strided subset of
-// the pages that request's append touches (grid.y covers the pages of the
-// longest append, so a bulk append runs one page per workgroup). Per page it
-// handles K, then V:
-//   1. fp8: block max of |x| over the appended slots -> the new scale;
-//   2. one pass over the page's slots [lo, o1) in storage order, four
+// One workgroup serves one request and a group of its kv-heads (all of them
+// unless a small append needs more workgroups), over a strided subset of the
+// pages the append touches (grid.y covers the pages of the longest append,
+// so a bulk append runs one page per workgroup). Per page:
+//   1. fp8: max |x| of each head's appended K and V slots (LDS atomics, one
+//      per wave when its lanes share a head) -> the new scales;
+//   2. K, then V: one pass over the group's slots in storage order, four
 //      elements per lane along the contiguous dimension (one 4/8/16-byte
-//      store): earlier slots are re-encoded when the scale grew (fp8) or
-//      kept, appended slots are converted from the source.
+//      store): earlier slots are re-encoded when their head's scale grew
+//      (fp8) or skipped, appended slots are converted from the source.
 // Every address is bounds-checked against the pool, the page table and the
 // source rows; a slot that cannot be written is counted in `errors`.
 #include <hip/hip_runtime.h>
@@ -40,6 +41,7 @@ struct AParams {
   int64_t kps, khs, kts, vps, vhs, vts, vds;
   float *k_scale, *v_scale;
   uint32_t *errors;
+  uint32_t hpw; // kv-heads per workgroup, divides Hkv
 };
 
 template <bool SRC_F32>
@@ -145,122 +147,468 @@ template <> struct Codec<SCHED_PD_FP8_E4M3> {
   }
 };
 
-__device__ __forceinline__ float block_max(float v, float *red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1)
-    v = fmaxf(v, __shfl_xor(v, off));
-  const int w = threadIdx.x >> 6;
-  __syncthreads(); // red[] may still be read by a previous call
-  if ((threadIdx.x & 63) == 0)
-    red[w] = v;
-  __syncthreads();
-  float m = red[0];
-#pragma unroll
-  for (int i = 1; i < kBlock / 64; ++i)
-    m = fmaxf(m, red[i]);
-  return m;
+constexpr uint32_t kMaxGroup = 64; // kv-heads one workgroup serves at most
+
+// Per-head fp8 state of the page being written, for K (0) and V (1).
+struct PageScales {
+  uint32_t amax[2][kMaxGroup]; // max |x| as bits (non-negative floats order as integers)
+  float inv[2][kMaxGroup];     // 1 / new scale, 0 for a zero scale
+  float prev[2][kMaxGroup];    // old scale, to re-encode earlier slots
+  uint32_t regrow[2][kMaxGroup];
+  uint32_t any_regrow[2];
+};
+
+template <int KVD>
+using PoolElem = typename std::conditional<
+    KVD == SCHED_PD_F32, float,
+    typename std::conditional<KVD == SCHED_PD_BF16, uint16_t, uint8_t>::type>::type;
+
+// Max over the 64 lanes of a wave (all lanes active), in VALU cross-lane
+// moves: quad permutes and row rotations (DPP) within each row of 16, then
+// v_permlane16/32_swap across rows. Every lane gets the result.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF,
+                                                          false))); // quad [1,0,3,2]
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF,
+                                                          false))); // quad [2,3,0,1]
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF,
+                                                          false))); // row_ror:4
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF,
+                                                          false))); // row_ror:8
+  const unsigned u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// One tensor (K or V) of one (page, head): slots [o0, o1) are appended from
-// source rows row0 + (o - o0).
-template <bool SRC_F32, int KVD>
-__device__ void write_page(const AParams &P, const void *src, void *pool_v, int64_t base,
-                           int64_t tok_stride, int64_t dim_stride, float *scale_slot,
-                           uint32_t o0, uint32_t o1, int64_t row0, uint32_t h, float *red) {
-  typedef Codec<KVD> C;
-  typedef typename C::Vec Vec;
-  typedef typename std::conditional<KVD == SCHED_PD_F32, float,
-          typename std::conditional<KVD == SCHED_PD_BF16, uint16_t, uint8_t>::type>::type E;
-  E *pool = static_cast<E *>(pool_v);
-  const uint32_t d = P.d;
-  const int64_t shead = (int64_t)h * P.s_head;
+// max into an LDS slot per head (all lanes active). When a head's chunks
+// are at least a wave long, a wave's lanes hold at most two consecutive
+// heads: two wave maxima and one or two atomics per wave. Otherwise one
+// atomic per lane.
+__device__ __forceinline__ void lds_max(uint32_t *slots, uint32_t hh, float v, bool wide) {
+  if (!wide) {
+    atomicMax(&slots[hh], __float_as_uint(v));
+    return;
+  }
+  const uint32_t h_lo = __builtin_amdgcn_readfirstlane(hh);
+  const bool two = __builtin_amdgcn_ballot_w64(hh != h_lo) != 0;
+  const float lo = wave_max(hh == h_lo ? v : 0.f);
+  const float hi = two ? wave_max(hh == h_lo ? 0.f : v) : 0.f;
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&slots[h_lo], __float_as_uint(lo));
+    if (two)
+      atomicMax(&slots[h_lo + 1], __float_as_uint(hi));
+  }
+}
 
-  float inv = 0.f, s_prev = 0.f;
-  bool requant = false;
-  if (KVD == SCHED_PD_FP8_E4M3) {
-    const float s_old = *scale_slot;
-    float a = 0.f;
-    const uint32_t groups = (o1 - o0) * (d / 4);
-    for (uint32_t g = threadIdx.x; g < groups; g += kBlock) {
-      const uint32_t o = o0 + g / (d / 4), j = (g % (d / 4)) * 4;
-      float x[4];
-      load_src4<SRC_F32>(src, (row0 + (o - o0)) * P.s_tok + shead + j, x);
+// Chunks in flight per lane: every lane issues the loads of kBatch chunks
+// before any store, so a workgroup keeps kBatch x 256 loads outstanding (a
+// store to the pool may alias the source as far as the compiler knows, so
+// it would not hoist the next load above it by itself).
+#ifndef SCHED_KV_BATCH
+#define SCHED_KV_BATCH 4
+#endif
+constexpr uint32_t kBatch = SCHED_KV_BATCH;
+
+// fp8: the new scale of each (page, head) of the group from the appended
+// slots [o0, o1), written back; per-head encode state into S.
+__device__ void clear_amax(PageScales &S, uint32_t hpw) {
+  __syncthreads(); // S may still be read for the previous page
+  for (uint32_t i = threadIdx.x; i < 2 * hpw; i += kBlock)
+    S.amax[i / hpw][i % hpw] = 0u;
+  if (threadIdx.x < 2)
+    S.any_regrow[threadIdx.x] = 0u;
+  __syncthreads();
+}
+
+// One (page, head)'s new scale from its amax (written back), its encode
+// state in S; the amax slot is left at zero for the next page.
+__device__ __forceinline__ void set_scale(PageScales &S, uint32_t x, uint32_t hh, float *slot,
+                                          float s_old, uint32_t o0) {
+  const float p = pow2_scale(__uint_as_float(S.amax[x][hh]));
+  S.amax[x][hh] = 0u;
+  const float s_new = o0 == 0 ? p : fmaxf(s_old, p);
+  const uint32_t rq = (o0 > 0 && s_new != s_old) ? 1u : 0u;
+  S.inv[x][hh] = s_new > 0.f ? 1.f / s_new : 0.f;
+  S.prev[x][hh] = s_old;
+  S.regrow[x][hh] = rq;
+  if (rq)
+    S.any_regrow[x] = 1u;
+  *slot = s_new;
+}
+
+// After the amax pass: each (page, head)'s new scale (written back) and its
+// encode state in S.
+__device__ void scales_from_amax(const AParams &P, PageScales &S, int64_t page, uint32_t h0,
+                                 uint32_t hpw, uint32_t o0) {
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < 2 * hpw; i += kBlock) {
+    const uint32_t x = i / hpw, hh = i % hpw;
+    float *slot = (x ? P.v_scale : P.k_scale) + page * P.Hkv + h0 + hh;
+    set_scale(S, x, hh, slot, *slot, o0);
+  }
+  __syncthreads();
+}
+
+template <bool SRC_F32>
+__device__ void page_scales(const AParams &P, PageScales &S, int64_t page, uint32_t h0,
+                            uint32_t hpw, uint32_t o0, uint32_t o1, int64_t row0) {
+  const uint32_t q = P.d / 4, per_head = (o1 - o0) * q, total = hpw * per_head;
+  clear_amax(S, hpw);
+  for (uint32_t c0 = 0; c0 < total; c0 += kBlock * kBatch) {
+    float xk[kBatch][4], xv[kBatch][4];
+    uint32_t hh[kBatch];
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      const uint32_t c = c0 + u * kBlock + threadIdx.x;
+      hh[u] = hpw - 1; // lanes past the end add 0 to the last head
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        a = fmaxf(a, fabsf(x[i]));
-    }
-    a = block_max(a, red);
-    const float p = pow2_scale(a);
-    const float s_new = o0 == 0 ? p : fmaxf(s_old, p);
-    requant = o0 > 0 && s_new != s_old;
-    inv = s_new > 0.f ? 1.f / s_new : 0.f;
-    s_prev = s_old; // re-encode: (code * s_old) * inv
-    if (threadIdx.x == 0)
-      *scale_slot = s_new;
-  }
-
-  if (dim_stride == 1) {
-    // token rows: groups of four dims, never straddling a slot
-    const uint32_t lo = requant ? 0u : o0;
-    const uint32_t groups = (o1 - lo) * (d / 4);
-    for (uint32_t g = threadIdx.x; g < groups; g += kBlock) {
-      const uint32_t o = lo + g / (d / 4), j = (g % (d / 4)) * 4;
-      Vec *dst = reinterpret_cast<Vec *>(pool + base + (int64_t)o * tok_stride + j);
-      float x[4];
-      if (o < o0) {
-        const Vec old = *dst;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          x[i] = C::dec(old, i) * s_prev;
-      } else {
-        load_src4<SRC_F32>(src, (row0 + (o - o0)) * P.s_tok + shead + j, x);
+        xk[u][i] = xv[u][i] = 0.f;
+      if (c < total) {
+        hh[u] = c / per_head;
+        const uint32_t rem = c - hh[u] * per_head;
+        const uint32_t t = rem / q, j = (rem - t * q) * 4;
+        const int64_t s = (row0 + t) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j;
+        load_src4<SRC_F32>(P.k_src, s, xk[u]);
+        load_src4<SRC_F32>(P.v_src, s, xv[u]);
       }
-      *dst = C::enc(x, inv);
     }
-  } else {
-    // d-major: groups of four slots of one dim; slots past o1 in the last
-    // group are unused positions and are written as zero
-    const uint32_t lo = (requant ? 0u : o0) & ~3u;
-    const uint32_t hi = (o1 + 3u) & ~3u;
-    const uint32_t per_dim = (hi - lo) / 4;
-    const uint32_t groups = per_dim * d;
-    for (uint32_t g = threadIdx.x; g < groups; g += kBlock) {
-      const uint32_t j = g / per_dim, o = lo + (g % per_dim) * 4;
-      Vec *dst = reinterpret_cast<Vec *>(pool + base + (int64_t)j * dim_stride + o);
-      Vec old{};
-      if (o < o0)
-        old = *dst;
-      float x[4];
-      uint32_t kept = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      float mk = 0.f, mv = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t t = o + i;
-        if (t < o0) {
-          // earlier slot: re-encoded at the grown scale, else kept bit for bit
-          x[i] = requant ? C::dec(old, i) * s_prev : 0.f;
-          kept |= requant ? 0u : 1u << i;
-        } else if (t < o1) {
-          x[i] = load_src<SRC_F32>(src, (row0 + (t - o0)) * P.s_tok + shead + j);
-        } else {
-          x[i] = 0.f;
+        mk = fmaxf(mk, fabsf(xk[u][i]));
+        mv = fmaxf(mv, fabsf(xv[u][i]));
+      }
+      lds_max(S.amax[0], hh[u], mk, per_head >= 64);
+      lds_max(S.amax[1], hh[u], mv, per_head >= 64);
+    }
+  }
+  scales_from_amax(P, S, page, h0, hpw, o0);
+}
+
+// One tensor (K: x = 0, V: x = 1) of heads [h0, h0 + hpw) of one page:
+// slots [o0, o1) appended from source rows row0 + (t - o0); with fp8, the
+// earlier slots of heads whose scale grew are re-encoded.
+template <bool SRC_F32, int KVD>
+__device__ void write_tensor(const AParams &P, const PageScales &S, int x, const void *src,
+                             void *pool_v, int64_t base, int64_t head_stride, int64_t tok_stride,
+                             int64_t dim_stride, uint32_t h0, uint32_t hpw, uint32_t o0,
+                             uint32_t o1, int64_t row0) {
+  typedef Codec<KVD> C;
+  typedef typename C::Vec Vec;
+  constexpr bool FP8 = KVD == SCHED_PD_FP8_E4M3;
+  PoolElem<KVD> *pool = static_cast<PoolElem<KVD> *>(pool_v) + base;
+  const uint32_t d = P.d, lo = (FP8 && S.any_regrow[x]) ? 0u : o0;
+
+  if (dim_stride == 1) {
+    // token rows: chunks of four dims, never straddling a slot
+    const uint32_t q = d / 4, per_head = (o1 - lo) * q, total = hpw * per_head;
+    for (uint32_t c0 = 0; c0 < total; c0 += kBlock * kBatch) {
+      Vec *dst[kBatch];
+      Vec old[kBatch];
+      float v[kBatch][4];
+      uint32_t state[kBatch]; // 0 skip, 1 append, 2 re-encode
+      uint32_t hh[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t c = c0 + u * kBlock + threadIdx.x;
+        state[u] = 0;
+        hh[u] = 0;
+        dst[u] = nullptr;
+        if (c < total) {
+          hh[u] = c / per_head;
+          const uint32_t rem = c - hh[u] * per_head;
+          const uint32_t t = lo + rem / q, j = (rem % q) * 4;
+          dst[u] = reinterpret_cast<Vec *>(pool + (int64_t)(h0 + hh[u]) * head_stride +
+                                           (int64_t)t * tok_stride + j);
+          if (t >= o0) {
+            state[u] = 1;
+            load_src4<SRC_F32>(
+                src, (row0 + (t - o0)) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j, v[u]);
+          } else if (FP8 && S.regrow[x][hh[u]]) {
+            state[u] = 2;
+            old[u] = *dst[u];
+          }
         }
       }
-      *dst = C::keep(C::enc(x, inv), old, kept);
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        if (!state[u])
+          continue;
+        if (state[u] == 2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[u][i] = C::dec(old[u], i) * S.prev[x][hh[u]];
+        }
+        *dst[u] = C::enc(v[u], FP8 ? S.inv[x][hh[u]] : 0.f);
+      }
+    }
+  } else {
+    // d-major: chunks of four slots of one dim; slots past o1 in the last
+    // chunk are unused positions and are written as zero
+    const uint32_t lo4 = lo & ~3u, hi4 = (o1 + 3u) & ~3u;
+    const uint32_t per_dim = (hi4 - lo4) / 4, per_head = per_dim * d, total = hpw * per_head;
+    for (uint32_t c0 = 0; c0 < total; c0 += kBlock * kBatch) {
+      Vec *dst[kBatch];
+      Vec old[kBatch];
+      float v[kBatch][4];
+      uint32_t kept[kBatch], hh[kBatch], o[kBatch];
+      bool act[kBatch], rq[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t c = c0 + u * kBlock + threadIdx.x;
+        act[u] = false;
+        rq[u] = false;
+        kept[u] = 0;
+        hh[u] = 0;
+        o[u] = 0;
+        dst[u] = nullptr;
+        old[u] = Vec{};
+        if (c < total) {
+          hh[u] = c / per_head;
+          const uint32_t rem = c - hh[u] * per_head;
+          const uint32_t j = rem / per_dim;
+          o[u] = lo4 + (rem % per_dim) * 4;
+          rq[u] = FP8 && S.regrow[x][hh[u]];
+          act[u] = o[u] + 3u >= o0 || rq[u]; // else four earlier slots, kept as they are
+          if (act[u]) {
+            dst[u] = reinterpret_cast<Vec *>(pool + (int64_t)(h0 + hh[u]) * head_stride +
+                                             (int64_t)j * dim_stride + o[u]);
+            if (o[u] < o0)
+              old[u] = *dst[u];
+            const int64_t s = (int64_t)(h0 + hh[u]) * P.s_head + j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t t = o[u] + i;
+              v[u][i] = (t >= o0 && t < o1) ? load_src<SRC_F32>(src, (row0 + (t - o0)) * P.s_tok + s)
+                                            : 0.f;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        if (!act[u])
+          continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (o[u] + i < o0) {
+            // earlier slot: re-encoded at the grown scale, else kept bit for bit
+            if (rq[u])
+              v[u][i] = C::dec(old[u], i) * S.prev[x][hh[u]];
+            else
+              kept[u] |= 1u << i;
+          }
+        }
+        *dst[u] = C::keep(C::enc(v[u], FP8 ? S.inv[x][hh[u]] : 0.f), old[u], kept[u]);
+      }
     }
   }
 }
 
+// Chunks one lane holds in the one-round path, and the LDS stage that
+// transposes a d-major V: rows (head, appended slot) of d floats, padded by
+// one float so the four slot rows a chunk reads fall in different banks.
+constexpr uint32_t kFastChunks = kBlock * kBatch;
+constexpr uint32_t kStageFloats = kFastChunks * 4 + kFastChunks;
+
+// Re-encodes slots [0, o0) of token rows for the heads whose scale grew.
+template <int KVD>
+__device__ void regrow_rows(const AParams &P, const PageScales &S, int x, PoolElem<KVD> *pool,
+                            int64_t head_stride, int64_t tok_stride, uint32_t h0, uint32_t hpw,
+                            uint32_t o0) {
+  typedef Codec<KVD> C;
+  typedef typename C::Vec Vec;
+  const uint32_t q = P.d / 4, per_head = o0 * q, total = hpw * per_head;
+  for (uint32_t c = threadIdx.x; c < total; c += kBlock) {
+    const uint32_t hh = c / per_head, rem = c - hh * per_head;
+    if (!S.regrow[x][hh])
+      continue;
+    const uint32_t t = rem / q, j = (rem - t * q) * 4;
+    Vec *dst = reinterpret_cast<Vec *>(pool + (int64_t)(h0 + hh) * head_stride +
+                                       (int64_t)t * tok_stride + j);
+    const Vec old = *dst;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = C::dec(old, i) * S.prev[x][hh];
+    *dst = C::enc(v, S.inv[x][hh]);
+  }
+}
+
+// One page of a head group whose appended chunks (per tensor) fit one round:
+// every lane loads its K and V chunks once, keeps them in registers through
+// the fp8 amax, and stores them; a d-major V goes through the LDS stage so
+// that the source is read in rows and the pool written in slot groups.
+template <bool SRC_F32, int KVD>
+__device__ void page_one_round(const AParams &P, PageScales &S, float *stage, int64_t page,
+                               uint32_t h0, uint32_t hpw, uint32_t o0, uint32_t o1,
+                               int64_t row0) {
+  typedef Codec<KVD> C;
+  typedef typename C::Vec Vec;
+  constexpr bool FP8 = KVD == SCHED_PD_FP8_E4M3;
+  const uint32_t d = P.d, q = d / 4, nn = o1 - o0, per_head = nn * q, total = hpw * per_head;
+  const bool vdm = P.vds != 1;
+  const uint32_t row_len = d + 1;
+  // fp8: lanes [0, hpw) own the K scales of the group, [hpw, 2 hpw) the V
+  // scales; the old values load together with the source
+  float *slot = nullptr, s_old = 0.f;
+  if (FP8 && threadIdx.x < 2 * hpw) {
+    slot = (threadIdx.x < hpw ? P.k_scale : P.v_scale) + page * P.Hkv + h0 + threadIdx.x % hpw;
+    s_old = *slot;
+  }
+  float xk[kBatch][4], xv[kBatch][4];
+  uint32_t hh[kBatch], t[kBatch], j[kBatch];
+#pragma unroll
+  for (uint32_t u = 0; u < kBatch; ++u) {
+    const uint32_t c = u * kBlock + threadIdx.x;
+    hh[u] = hpw - 1; // lanes past the end add 0 to the last head
+    t[u] = j[u] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xk[u][i] = xv[u][i] = 0.f;
+    if (c < total) {
+      hh[u] = c / per_head;
+      const uint32_t rem = c - hh[u] * per_head;
+      t[u] = rem / q;
+      j[u] = (rem - t[u] * q) * 4;
+      const int64_t s = (row0 + t[u]) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j[u];
+      load_src4<SRC_F32>(P.k_src, s, xk[u]);
+      load_src4<SRC_F32>(P.v_src, s, xv[u]);
+    }
+  }
+  __syncthreads(); // the stage and S are free: the previous page is written
+  if (FP8 && threadIdx.x == 0)
+    S.any_regrow[0] = S.any_regrow[1] = 0u;
+  if (vdm) {
+    // d-major V: stage the appended rows for the slot-group writes below
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      if (u * kBlock + threadIdx.x < total) {
+        float *row = stage + (hh[u] * nn + t[u]) * row_len + j[u];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          row[i] = xv[u][i];
+      }
+    }
+  }
+  if (FP8) {
+    // per lane, a running max over its chunks of one head; flushed to LDS
+    // when some lane's next chunk starts a new head, and at the end
+    const bool wide = per_head >= 64;
+    float mk = 0.f, mv = 0.f;
+    uint32_t h_run = hh[0];
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      if (u > 0 && __builtin_amdgcn_ballot_w64(hh[u] != h_run) != 0) {
+        lds_max(S.amax[0], h_run, mk, wide);
+        lds_max(S.amax[1], h_run, mv, wide);
+        mk = mv = 0.f;
+        h_run = hh[u];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mk = fmaxf(mk, fabsf(xk[u][i]));
+        mv = fmaxf(mv, fabsf(xv[u][i]));
+      }
+    }
+    lds_max(S.amax[0], h_run, mk, wide);
+    lds_max(S.amax[1], h_run, mv, wide);
+  }
+  __syncthreads();
+  if (FP8) {
+    if (slot)
+      set_scale(S, threadIdx.x / hpw, threadIdx.x % hpw, slot, s_old, o0);
+    __syncthreads();
+  }
+
+  // K: token rows
+  PoolElem<KVD> *kpool = static_cast<PoolElem<KVD> *>(P.k_pool) + page * P.kps;
+#pragma unroll
+  for (uint32_t u = 0; u < kBatch; ++u) {
+    if (u * kBlock + threadIdx.x < total) {
+      Vec *dst = reinterpret_cast<Vec *>(kpool + (int64_t)(h0 + hh[u]) * P.khs +
+                                         (int64_t)(o0 + t[u]) * P.kts + j[u]);
+      *dst = C::enc(xk[u], FP8 ? S.inv[0][hh[u]] : 0.f);
+    }
+  }
+  if (FP8 && S.any_regrow[0])
+    regrow_rows<KVD>(P, S, 0, kpool, P.khs, P.kts, h0, hpw, o0);
+
+  PoolElem<KVD> *vpool = static_cast<PoolElem<KVD> *>(P.v_pool) + page * P.vps;
+  if (!vdm) {
+    // token-major V: as K
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      if (u * kBlock + threadIdx.x < total) {
+        Vec *dst = reinterpret_cast<Vec *>(vpool + (int64_t)(h0 + hh[u]) * P.vhs +
+                                           (int64_t)(o0 + t[u]) * P.vts + j[u]);
+        *dst = C::enc(xv[u], FP8 ? S.inv[1][hh[u]] : 0.f);
+      }
+    }
+    if (FP8 && S.any_regrow[1])
+      regrow_rows<KVD>(P, S, 1, vpool, P.vhs, P.vts, h0, hpw, o0);
+    return;
+  }
+
+  // d-major V: groups of four slots from the stage
+  const uint32_t lo4 = ((FP8 && S.any_regrow[1]) ? 0u : o0) & ~3u, hi4 = (o1 + 3u) & ~3u;
+  const uint32_t per_dim = (hi4 - lo4) / 4, vper_head = per_dim * d, vtotal = hpw * vper_head;
+  for (uint32_t c = threadIdx.x; c < vtotal; c += kBlock) {
+    const uint32_t g = c / vper_head, rem = c - g * vper_head;
+    const uint32_t jj = rem / per_dim, o = lo4 + (rem - jj * per_dim) * 4;
+    const bool rq = FP8 && S.regrow[1][g];
+    if (o + 3u < o0 && !rq)
+      continue; // four earlier slots, kept as they are
+    Vec *dst = reinterpret_cast<Vec *>(vpool + (int64_t)(h0 + g) * P.vhs +
+                                       (int64_t)jj * P.vds + o);
+    Vec old{};
+    if (o < o0)
+      old = *dst;
+    float v[4];
+    uint32_t kept = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t ts = o + i;
+      if (ts < o0) {
+        v[i] = rq ? C::dec(old, i) * S.prev[1][g] : 0.f;
+        kept |= rq ? 0u : 1u << i;
+      } else if (ts < o1) {
+        v[i] = stage[(g * nn + (ts - o0)) * row_len + jj];
+      } else {
+        v[i] = 0.f;
+      }
+    }
+    *dst = C::keep(C::enc(v, FP8 ? S.inv[1][g] : 0.f), old, kept);
+  }
+}
+
+// grid.x = requests x head groups, grid.y strides over the pages of the
+// longest append.
 template <bool SRC_F32, int KVD>
 __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
-  __shared__ float red[kBlock / 64];
-  const uint32_t r = blockIdx.x / P.Hkv, h = blockIdx.x % P.Hkv;
+  __shared__ PageScales S;
+  __shared__ float stage[kStageFloats];
+  if (KVD == SCHED_PD_FP8_E4M3) {
+    // amax slots are zero between pages: set here, reset by each scale update
+    for (uint32_t i = threadIdx.x; i < 2 * kMaxGroup; i += kBlock)
+      S.amax[i / kMaxGroup][i % kMaxGroup] = 0u;
+    __syncthreads();
+  }
+  const uint32_t groups = P.Hkv / P.hpw;
+  const uint32_t r = blockIdx.x / groups, h0 = (blockIdx.x % groups) * P.hpw, hpw = P.hpw;
   const int32_t a0 = P.app[r], a1 = P.app[r + 1];
   if (a1 <= a0)
     return;
   const int64_t n = (int64_t)a1 - a0, ctx = P.ctx[r], pos0 = ctx - n;
   if (a0 < 0 || (uint32_t)a1 > P.num_tokens || pos0 < 0) {
     if (threadIdx.x == 0 && blockIdx.y == 0 && P.errors)
-      atomicAdd(P.errors, (uint32_t)n);
+      atomicAdd(P.errors, (uint32_t)(n * hpw));
     return;
   }
   const int64_t row = P.pind ? (int64_t)P.pind[r] : (int64_t)r * P.bt_stride;
@@ -273,15 +621,20 @@ __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
     const int32_t page = b < cap ? P.table[row + b] : -1;
     if (page < 0 || (uint64_t)page >= P.num_pages) {
       if (threadIdx.x == 0 && P.errors)
-        atomicAdd(P.errors, o1 - o0);
+        atomicAdd(P.errors, (o1 - o0) * hpw);
       continue;
     }
-    const int64_t src_row0 = a0 + (pbase + o0 - pos0);
-    const int64_t sidx = (int64_t)page * P.Hkv + h;
-    write_page<SRC_F32, KVD>(P, P.k_src, P.k_pool, page * P.kps + h * P.khs, P.kts, 1,
-                             P.k_scale ? P.k_scale + sidx : nullptr, o0, o1, src_row0, h, red);
-    write_page<SRC_F32, KVD>(P, P.v_src, P.v_pool, page * P.vps + h * P.vhs, P.vts, P.vds,
-                             P.v_scale ? P.v_scale + sidx : nullptr, o0, o1, src_row0, h, red);
+    const int64_t row0 = a0 + (pbase + o0 - pos0);
+    if ((uint64_t)hpw * (o1 - o0) * (P.d / 4) <= kFastChunks) {
+      page_one_round<SRC_F32, KVD>(P, S, stage, page, h0, hpw, o0, o1, row0);
+      continue;
+    }
+    if (KVD == SCHED_PD_FP8_E4M3)
+      page_scales<SRC_F32>(P, S, page, h0, hpw, o0, o1, row0);
+    write_tensor<SRC_F32, KVD>(P, S, 0, P.k_src, P.k_pool, page * P.kps, P.khs, P.kts, 1, h0, hpw,
+                               o0, o1, row0);
+    write_tensor<SRC_F32, KVD>(P, S, 1, P.v_src, P.v_pool, page * P.vps, P.vhs, P.vts, P.vds, h0,
+                               hpw, o0, o1, row0);
   }
 }
 
@@ -374,10 +727,31 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   P.errors = a->errors;
 
   const uint32_t max_app = a->max_append ? a->max_append : a->num_tokens;
+  uint32_t hpw = a->heads_per_group;
+  if (hpw == 0) {
+    // Page-filling appends: the largest group whose appended chunks fit one
+    // round, so every lane streams kBatch chunks. Small appends (a few tokens
+    // per request, as in a decode step) are latency-bound: groups of at most
+    // kBlock / head_dim heads, so a d-major V needs one slot group per lane.
+    const uint32_t span = max_app < a->page_size ? max_app : a->page_size;
+    const uint64_t per_head = (uint64_t)span * (a->head_dim / 4);
+    const bool small = 2 * span < a->page_size;
+    hpw = 1;
+    while (hpw * 2 <= kMaxGroup && a->num_kv_heads % (hpw * 2) == 0) {
+      const uint32_t next = hpw * 2;
+      if (next * per_head > kFastChunks || (small && next * a->head_dim > kBlock))
+        break;
+      hpw = next;
+    }
+  } else if (hpw > kMaxGroup || a->num_kv_heads % hpw) {
+    return set_error(-1, "sched_kv_append: heads_per_group %u must divide num_kv_heads %u "
+                         "and be <= %u", hpw, a->num_kv_heads, kMaxGroup);
+  }
+  P.hpw = hpw;
   uint64_t gy = (uint64_t)(max_app + a->page_size - 1) / a->page_size + 1;
   if (gy > 65535)
     gy = 65535;
-  const dim3 grid(a->num_requests * a->num_kv_heads, (uint32_t)gy);
+  const dim3 grid(a->num_requests * (a->num_kv_heads / hpw), (uint32_t)gy);
   AppendFn fn = a->src_dtype == SCHED_PD_F32 ? pick<true>(a->kv_dtype) : pick<false>(a->kv_dtype);
   hipLaunchKernelGGL(fn, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), P);
   hipError_t e = hipGetLastError();

@@ -39,7 +39,7 @@ def _ptr(t):
 
 def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
            page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
-           max_append=0, errors=None, stream=None) -> None:
+           max_append=0, errors=None, heads_per_group=0, stream=None) -> None:
     """Write source rows k_new/v_new [T, Hkv, d] (bf16 or fp32, dims
     contiguous) into the pools: request r's rows append_indptr[r] ..
     append_indptr[r+1]-1 go to positions ctx_lens[r] - n_r .. ctx_lens[r]-1
@@ -48,7 +48,8 @@ def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *
     optional) counts (token, kv-head) pairs the kernel could not place."""
     a = build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table,
                           page_indptr=page_indptr, v_layout=v_layout, k_scale=k_scale,
-                          v_scale=v_scale, max_append=max_append, errors=errors)
+                          v_scale=v_scale, max_append=max_append, errors=errors,
+                          heads_per_group=heads_per_group)
     launch_append(a, stream if stream is not None else torch.cuda.current_stream(k_pool.device))
 
 
@@ -62,7 +63,7 @@ def launch_append(a: abi.SchedKvAppendArgs, stream) -> None:
 
 def build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
                       page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
-                      max_append=0, errors=None) -> abi.SchedKvAppendArgs:
+                      max_append=0, errors=None, heads_per_group=0) -> abi.SchedKvAppendArgs:
     """Validate and fill a SchedKvAppendArgs (no launch); see append()."""
     a = abi.default_kv_args()
     if k_new.dtype not in (torch.float32, torch.bfloat16) or v_new.dtype != k_new.dtype:
@@ -134,6 +135,7 @@ def build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, blo
     if a.kv_dtype == abi.FP8_E4M3:
         a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
     a.errors = _ptr(errors)
+    a.heads_per_group = int(heads_per_group)
     return a
 
 

@@ -99,7 +99,7 @@ class SchedKvAppendArgs(ctypes.Structure):
         ("v_page_stride", _i64), ("v_head_stride", _i64), ("v_tok_stride", _i64),
         ("v_dim_stride", _i64),
         ("k_scale", _p), ("v_scale", _p), ("errors", _p),
-        ("_pad0", _u32), ("_pad1", _u32),
+        ("heads_per_group", _u32), ("_pad0", _u32),
     ]
 
 

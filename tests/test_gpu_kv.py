@@ -31,7 +31,7 @@ def raw(t):
     return t.numpy()
 
 
-def run_gpu(c):
+def run_gpu(c, heads_per_group=0):
     dev = "cuda"
     k_pool, v_pool = c["k_pool"].to(dev), c["v_pool"].to(dev)
     ks = None if c["k_scale"] is None else c["k_scale"].to(dev)
@@ -42,7 +42,8 @@ def run_gpu(c):
     kv_cache.append(c["k_src"].to(dev), c["v_src"].to(dev), torch.from_numpy(c["app"]).to(dev),
                     torch.from_numpy(c["ctx"].astype(np.int32)).to(dev), k_pool, v_pool,
                     torch.from_numpy(c["table"]).to(dev), page_indptr=pind,
-                    v_layout=c["v_layout"], k_scale=ks, v_scale=vs, errors=errors)
+                    v_layout=c["v_layout"], k_scale=ks, v_scale=vs, errors=errors,
+                    heads_per_group=heads_per_group)
     torch.cuda.synchronize()
     return (raw(k_pool), raw(v_pool), None if ks is None else ks.cpu().numpy(),
             None if vs is None else vs.cpu().numpy(), int(errors.item()))
@@ -67,6 +68,13 @@ def test_append_is_bit_exact_with_the_oracle(kv, v_layout, csr, src):
         print(f"case kv={kv} v={v_layout} csr={csr} src={src} hkv={hkv} d={d}", flush=True)
         c = append_case(100 + seed, kv, v_layout, csr, hkv=hkv, d=d, src_dtype=src)
         assert_same(run_gpu(c), c["out"])
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, FP8])
+@pytest.mark.parametrize("hpw", [1, 2, 4, 8])
+def test_every_head_grouping_gives_the_same_bytes(kv, hpw):
+    c = append_case(41, kv, "dmajor", hkv=8, d=128, prior=[3, 0, 17, 30, 9], n=[1, 40, 9, 20, 3])
+    assert_same(run_gpu(c, heads_per_group=hpw), c["out"])
 
 
 def test_append_into_partial_pages_regrows_fp8_scales():

@@ -232,6 +232,8 @@ def kv_fake(**kw):
     (dict(v_tok_stride=2, v_dim_stride=16), "d-major"),
     (dict(k_tok_stride=130), "multiples of 4"),
     (dict(k_pool=ctypes.c_void_p(0x10002)), "aligned"),
+    (dict(heads_per_group=3), "heads_per_group"),
+    (dict(heads_per_group=128), "heads_per_group"),
 ])
 def test_kv_append_rejects_invalid_args(schedlib, kw, msg):
     a = kv_fake(**kw)
