@@ -153,6 +153,12 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
         # path serves one task per workgroup, so launch the full grid then.
         a.workers = workers if plane.num_tasks > 0 else 0
         if a.workers:
+            nitems = a.num_tiles if tiles is not None else a.num_requests * a.num_kv_heads
+            if plane.num_tasks != nitems:
+                # the queue hands out items [0, num_tasks): any other count
+                # would skip items or leave workers idle on missing ones
+                raise ValueError(f"plane.num_tasks is {plane.num_tasks}, this launch has "
+                                 f"{nitems} work items: push the item count (or 0) first")
             plane.prime_queue(a.workers)
     else:
         a.max_tasks = 0

@@ -1,0 +1,230 @@
+"""serving.py -- the per-step control loop around a decode step, for any
+serving engine (reference python/sched_sglang_plugin.py:148-342, whose
+on_batch_begin / on_batch_end / _consume_probe are bound to SGLang's batch
+objects; here the engine passes request ids and KV lengths).
+
+Per step, as in the reference:
+  on_batch_begin(rids, kv_lens) -> launch arguments for sched_pd.paged_decode
+    * cadence gate: re-plan only every `plan_every` steps (and on probe
+      steps); in between the installed tables stay and nothing is read back;
+    * bind work items to requests (one per (request, kv-head) task, or the
+      split-KV tiles of plan_tiles);
+    * fold the last probe's timer rows into the controller once the GPU has
+      passed that step (event query, never a synchronize);
+    * predict per-request cost, spread it over the work items;
+    * regime gate: ticket queue armed (W = resident workgroups) when the
+      batch has more items than resident slots, a heavy tail
+      (max/mean > clc_imbalance) and uncertain predictions
+      (> clc_resid); one wave (items <= R): any live order retired, stock
+      grid; otherwise the grouped LPT order over items when the previous
+      step's kernels are done, stock grid;
+    * hints when the batch's KV exceeds the L2: long requests polite, short
+      ones urgent, q = predicted cost;
+    * push; clear the timer on probe steps.
+  on_batch_end()
+    * record the step's completion event; on a probe step keep (event,
+      binding) pending and switch the timer off for the following steps.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from sched_controller import SchedControlPlane
+from sched_rt import HINT_POLITE, HINT_URGENT, SchedPlane
+
+
+@dataclass
+class HookConfig:
+    """Knobs of the reference plugin's _STATE (python/sched_sglang_plugin.py:
+    36-106), with the same defaults."""
+    plan_every: int = 8          # re-plan cadence (steps)
+    timer_every: int = 8         # probe cadence (steps)
+    clc: str = "auto"            # ticket-queue arming: off | on | auto
+    clc_resid: float = 0.75      # auto: arm above this prediction uncertainty
+    clc_imbalance: float = 3.0   # auto: and above this max/mean item cost
+    resident: int = 0            # R, workgroups resident at once (0 = unknown)
+    observe_only: bool = False   # bind and measure, never change the schedule
+    kv_bytes_per_token: int = 0  # 0 = no hints
+    l2_bytes: int = 0            # hint threshold (0 = the device's L2 size)
+    page_size: int = 16
+    tile_pages: int = 0          # split-KV tile (pages); 0 = one item per task
+    policy: str = "lpt"
+
+
+class ServingHooks:
+    """Owns the controller and drives one SchedPlane through the steps."""
+
+    def __init__(self, plane: SchedPlane, num_kv_heads: int, config: HookConfig | None = None,
+                 controller: SchedControlPlane | None = None, event_factory=None):
+        self.plane = plane
+        self.hkv = int(num_kv_heads)
+        self.cfg = config or HookConfig()
+        self.ctl = controller or SchedControlPlane(policy=self.cfg.policy)
+        self._event = event_factory or (lambda: torch.cuda.Event())
+        self.step = 0
+        self.timer_armed = False
+        self.pending = None      # (event, binding) of an unread probe step
+        self.inflight = None     # completion event of the last step
+        self.binding = None      # (rids, kv_lens, item_to_req, nitems)
+        self.order_n = None      # items of the live order, None = identity
+        self.armed_n = None      # items the armed ticket queue covers
+        self.launch = {"plane": plane, "workers": 0, "tiles": None, "tile_pages": 0}
+        self.probes_folded = 0
+
+    # -- helpers ---------------------------------------------------------------
+    def _items(self, kv_lens):
+        """(tiles or None, item -> request index, pages per item)."""
+        n = len(kv_lens)
+        ps = self.cfg.page_size
+        pages = -(-np.asarray(kv_lens, np.int64) // ps)
+        if self.cfg.tile_pages > 0:
+            import sched_pd
+            tiles = sched_pd.plan_tiles(kv_lens, ps, self.cfg.tile_pages, self.hkv,
+                                        device=self.plane.dev)
+            t = tiles.cpu().numpy()
+            req = t[:, 0] // self.hkv
+            first = t[:, 1] * self.cfg.tile_pages
+            item_pages = np.clip(pages[req] - first, 0, self.cfg.tile_pages)
+            return tiles, req, item_pages
+        req = np.repeat(np.arange(n), self.hkv)
+        return None, req, pages[req]
+
+    def _consume_probe(self) -> None:
+        """Fold the pending probe's timer rows (per task) into per-request
+        cost once its event has fired (python/sched_sglang_plugin.py:
+        345-377)."""
+        if self.pending is None:
+            return
+        ev, b = self.pending
+        if not ev.query():
+            return
+        self.pending = None
+        rids, kv_list = b[0], b[1]
+        n = len(rids)
+        cyc = torch.as_tensor(self.plane.read_timer()).to(torch.int64)
+        m = min(n * self.hkv, cyc.numel())
+        per_req = torch.zeros(n, dtype=torch.int64).scatter_add_(
+            0, torch.arange(m) // self.hkv, cyc[:m])
+        self.ctl.observe(rids, kv_list, per_req.tolist())
+        self.probes_folded += 1
+
+    # -- the hooks ---------------------------------------------------------------
+    def on_batch_begin(self, rids, kv_lens) -> dict:
+        """Tables for this step; returns the launch arguments to pass to
+        sched_pd.paged_decode (plane, workers, tiles, tile_pages)."""
+        cfg, p = self.cfg, self.plane
+        step = self.step
+        self.step += 1
+        probe = step % cfg.timer_every == 0 and self.pending is None
+        kv_list = [int(x) for x in kv_lens]
+        if step % cfg.plan_every != 0 and not probe:
+            # off cadence: the tables stay. The split plan is rebuilt (it is
+            # the engine's per-step plan, from host lengths), and an armed
+            # queue whose item count no longer matches is switched off.
+            self.timer_armed = False
+            tiles = self._items(kv_list)[0] if cfg.tile_pages > 0 else None
+            nitems = tiles.shape[0] if tiles is not None else len(kv_list) * self.hkv
+            workers = self.launch["workers"]
+            if workers and nitems != self.armed_n:
+                p.set_num_tasks(0)
+                p.push()
+                workers = 0
+            self.launch = dict(self.launch, workers=workers, tiles=tiles)
+            return self.launch
+        rids = list(rids)
+        n = len(rids)
+        tiles, item_req, item_pages = self._items(kv_list)
+        nitems = int(item_req.size)
+        self._consume_probe()
+
+        alpha, beta = self.ctl._fit.coeffs()
+        resid = np.array([self.ctl._resid.get(r, 0.0) for r in rids], np.float64)
+        cost_req = np.maximum(alpha * np.asarray(kv_list, np.float64) + beta + resid, 0.0)
+        req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
+        cost_item = torch.as_tensor(cost_req[item_req] * item_pages / req_pages[item_req],
+                                    dtype=torch.float32)
+
+        p.set_timer_enabled(probe)
+        self.timer_armed = probe
+        workers = 0
+        if not cfg.observe_only and nitems <= p.N:
+            R = cfg.resident
+            imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6)) \
+                if nitems else 1.0
+            arm = cfg.clc == "on" or (
+                cfg.clc == "auto" and R > 0 and nitems > R and imbalance > cfg.clc_imbalance
+                and self.ctl.uncertainty(rids, kv_list) > cfg.clc_resid)
+            if arm:
+                p.install_order(SchedPlane.region_order(cost_item, R), nitems)
+                self.order_n = nitems
+                p.set_num_tasks(nitems)
+                self.armed_n = nitems
+                workers = R if R > 0 else 2 * p.sm_count()
+            elif R > 0 and nitems <= R:
+                self._retire_order()
+                p.set_num_tasks(0)
+            else:
+                if self.inflight is None or self.inflight.query():
+                    p.install_order(SchedPlane.region_order(cost_item, 0), nitems)
+                    self.order_n = nitems
+                p.set_num_tasks(0)
+            self._hints(kv_list, cost_req, item_req, cost_item)
+        else:
+            self._retire_order()
+            p.set_num_tasks(0)
+        p.push()
+        if probe:
+            p.clear_timer()
+        self.binding = (rids, kv_list, item_req, nitems)
+        self.launch = {"plane": p, "workers": workers, "tiles": tiles,
+                       "tile_pages": cfg.tile_pages if tiles is not None else 0}
+        return self.launch
+
+    def on_batch_end(self) -> None:
+        """After the step's launches (python/sched_sglang_plugin.py:311-342):
+        no synchronize; the completion event gates the next table writes and
+        the probe readout."""
+        ev = self._event()
+        ev.record()
+        self.inflight = ev
+        if self.timer_armed:
+            self.pending = (ev, self.binding)
+            self.plane.set_timer_enabled(False)
+            self.plane.push()
+
+    # -- pieces ----------------------------------------------------------------
+    def _retire_order(self) -> None:
+        if self.order_n is not None:
+            self.plane.reset_order()
+            self.plane.set_order_size(0)
+            self.order_n = None
+
+    def _hints(self, kv_list, cost_req, item_req, cost_item) -> None:
+        """Residency hints when the batch's KV exceeds the L2 (reference
+        python/sched_sglang_plugin.py:290-301). Rows are per task: the
+        kernels read policy rows by task, not by split item."""
+        bpt = self.cfg.kv_bytes_per_token
+        if not bpt or not kv_list:
+            return
+        l2 = self.cfg.l2_bytes or torch.cuda.get_device_properties(self.plane.dev).L2_cache_size
+        if float(sum(kv_list)) * bpt <= l2:
+            return
+        thr = float(np.median(cost_req))
+        ntask = len(kv_list) * self.hkv
+        if ntask > self.plane.N:
+            return
+        task_req = np.repeat(np.arange(len(kv_list)), self.hkv)
+        long_ = cost_req[task_req] >= thr
+        self.plane.set_rows(q=cost_req[task_req].astype(np.float32),
+                            hint=np.where(long_, HINT_POLITE, HINT_URGENT), n=ntask)
+
+    def stats(self) -> str:
+        """One status line (python/sched_sglang_plugin.py:302-309)."""
+        b = self.binding
+        u = self.ctl.uncertainty(b[0], b[1]) if b and b[0] else 0.0
+        return (f"[sched-serving] step={self.step} items={b[3] if b else 0} "
+                f"R={self.cfg.resident} probes={self.probes_folded} uncert={u:.2f} "
+                f"mode={'observe' if self.cfg.observe_only else 'enforce'}")

@@ -1,0 +1,171 @@
+"""The engine-agnostic serving hooks on the CPU (a SchedPlane in host memory,
+events faked): cadence, probes, the timer fold, each regime of the gate and
+the hints, against the reference plugin's rules
+(python/sched_sglang_plugin.py:148-377)."""
+import struct
+
+import numpy as np
+import torch
+
+import sched_abi as abi
+from sched_rt import HINT_POLITE, HINT_URGENT, SchedPlane
+from serving import HookConfig, ServingHooks
+
+
+class Ev:
+    def __init__(self, done=True):
+        self.done = done
+
+    def record(self):
+        pass
+
+    def query(self):
+        return self.done
+
+
+def plane(n=256):
+    return SchedPlane(max_tasks=n, device="cpu")
+
+
+def ctrl_u32(p, off):
+    return struct.unpack_from("<I", bytes(p._ctrl_dev[:64].numpy()), off)[0]
+
+
+def order(p, n):
+    return p._order_view()[:n].tolist()
+
+
+def test_cadence_gate_and_probe_timer():
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(plan_every=4, timer_every=4), event_factory=Ev)
+    rids, kv = [10, 11, 12], [100, 900, 300]
+    gen0 = p._generation
+    h.on_batch_begin(rids, kv)               # step 0: plan + probe
+    assert h.timer_armed and p._generation == gen0 + 1
+    assert ctrl_u32(p, abi.CTRL_FLAGS_OFF) & abi.FLAG_TIMER_OFF == 0
+    h.on_batch_end()                         # probe pending, timer off pushed
+    assert h.pending is not None
+    assert ctrl_u32(p, abi.CTRL_FLAGS_OFF) & abi.FLAG_TIMER_OFF
+    g = p._generation
+    for _ in range(3):                       # steps 1..3: off cadence, no writes
+        h.on_batch_begin(rids, kv)
+        h.on_batch_end()
+        assert not h.timer_armed
+    assert p._generation == g
+
+
+def test_probe_fold_is_per_request_sum_over_kv_heads():
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(plan_every=1, timer_every=1), event_factory=Ev)
+    rids, kv = [7, 8], [64, 512]
+    h.on_batch_begin(rids, kv)
+    p._timer_view()[:4] = torch.tensor([10, 20, 300, 400])   # tasks (r, h)
+    h.on_batch_end()
+    seen = {}
+    h.ctl.observe = lambda r, k, c: seen.update(r=r, k=k, c=c)
+    h.on_batch_begin(rids, kv)
+    assert seen == {"r": [7, 8], "k": [64, 512], "c": [30, 700]}
+    assert h.probes_folded == 1
+
+
+def test_probe_waits_for_its_event():
+    p = plane()
+    ev = Ev(done=False)
+    h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=1), event_factory=lambda: ev)
+    h.on_batch_begin([1], [16])
+    h.on_batch_end()
+    h.on_batch_begin([1], [16])              # GPU not done: stays pending
+    assert h.pending is not None and h.probes_folded == 0
+    ev.done = True
+    h.on_batch_begin([1], [16])
+    assert h.probes_folded == 1
+
+
+def test_one_wave_retires_order_and_stays_static():
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(plan_every=1, timer_every=100, resident=64),
+                     event_factory=Ev)
+    h.order_n = 6
+    p.set_order(torch.tensor([5, 4, 3, 2, 1, 0]))
+    p.set_order_size(6)
+    launch = h.on_batch_begin([1, 2, 3], [10, 20, 30])
+    assert launch["workers"] == 0 and h.order_n is None
+    assert order(p, 6) == list(range(6)) and ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 0
+    assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 0
+
+
+def test_queued_regime_installs_grouped_lpt_only_when_idle():
+    p = plane()
+    ev = Ev(done=False)
+    h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=100, resident=2, clc="off"),
+                     event_factory=lambda: ev)
+    kv = [16, 4096, 512, 64]
+    h.on_batch_end()                         # a step in flight
+    h.on_batch_begin([0, 1, 2, 3], kv)
+    assert h.order_n is None                 # busy: table left alone
+    ev.done = True
+    h.on_batch_begin([0, 1, 2, 3], kv)
+    assert h.order_n == 4
+    assert order(p, 4) == SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32),
+                                                  0).tolist()
+    assert ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 4
+
+
+def test_auto_arms_the_queue_only_for_an_uncertain_heavy_tail():
+    kv_tail = [16] * 31 + [16384]
+    kv_flat = [1024] * 32
+    for kv, expect in ((kv_tail, True), (kv_flat, False)):
+        p = plane()
+        h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=100, resident=8),
+                         event_factory=Ev)
+        launch = h.on_batch_begin(list(range(32)), kv)   # cold estimator: uncertainty 1.0
+        assert (launch["workers"] == 8) == expect
+        assert (ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 32) == expect
+        if expect:
+            ref = SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32), 8)
+            assert order(p, 32) == ref.tolist()
+
+
+def test_observe_only_never_orders_or_arms():
+    p = plane()
+    h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=1, resident=2, clc="on",
+                                      observe_only=True), event_factory=Ev)
+    launch = h.on_batch_begin([0, 1, 2, 3], [16, 4096, 512, 64])
+    assert launch["workers"] == 0 and h.order_n is None and h.timer_armed
+
+
+def test_hints_when_kv_exceeds_l2():
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(plan_every=1, timer_every=100, resident=64,
+                                      kv_bytes_per_token=4096, l2_bytes=1 << 20),
+                     event_factory=Ev)
+    h.on_batch_begin([0, 1, 2], [4096, 16, 1024])   # 21 MB > 1 MB
+    rows = np.frombuffer(bytes(p._ctrl_host[abi.CTRL_ROWS_OFF:abi.CTRL_ROWS_OFF + 6 * 8]),
+                         dtype=np.dtype([("q", "<f4"), ("tau", "<u2"), ("hint", "u1"),
+                                         ("pad", "u1")]))
+    assert list(rows["hint"]) == [HINT_POLITE] * 2 + [HINT_URGENT] * 2 + [HINT_POLITE] * 2
+    assert rows["q"][0] > rows["q"][4] > rows["q"][2]
+
+
+def test_split_items_spread_cost_by_pages():
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(plan_every=1, timer_every=100, resident=2, clc="off",
+                                      tile_pages=4), event_factory=Ev)
+    launch = h.on_batch_begin([0, 1], [16 * 10, 16])   # 3 + 1 chunks per task
+    assert launch["tiles"].shape[0] == 2 * 3 + 2 * 1 and launch["tile_pages"] == 4
+    assert h.order_n == 8
+    o = order(p, 8)
+    assert sorted(o) == list(range(8))
+
+
+def test_off_cadence_rebuilds_tiles_and_disarms_a_mismatched_queue():
+    p = plane()
+    h = ServingHooks(p, 1, HookConfig(plan_every=4, timer_every=100, resident=2, clc="on",
+                                      tile_pages=1), event_factory=Ev)
+    first = h.on_batch_begin([0, 1, 2], [32, 32, 32])           # 2 one-page chunks each
+    assert first["workers"] == 2 and first["tiles"].shape[0] == 6
+    same = h.on_batch_begin([0, 1, 2], [32, 32, 32])
+    assert same["workers"] == 2                                 # still matches
+    grown = h.on_batch_begin([0, 1, 2], [33, 32, 32])           # 3 chunks for r0
+    assert grown["tiles"].shape[0] == 7 and grown["workers"] == 0
+    assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 0
