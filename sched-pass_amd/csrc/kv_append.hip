@@ -51,13 +51,21 @@ __device__ __forceinline__ float load_src(const void *src, int64_t idx) {
   return bf16_bits_to_f32(static_cast<const uint16_t *>(src)[idx]);
 }
 
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
+
+// Source rows are read once: non-temporal loads (bulk bf16 append measured
+// 280 -> 252 us).
 template <bool SRC_F32>
 __device__ __forceinline__ void load_src4(const void *src, int64_t idx, float x[4]) {
   if (SRC_F32) {
-    float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + idx);
-    x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+    const u32x4_t v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx));
+    x[0] = __uint_as_float(v.x), x[1] = __uint_as_float(v.y);
+    x[2] = __uint_as_float(v.z), x[3] = __uint_as_float(v.w);
   } else {
-    uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(src) + idx);
+    const u32x2_t v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2_t *>(static_cast<const uint16_t *>(src) + idx));
     x[0] = __uint_as_float(v.x << 16), x[1] = __uint_as_float(v.x & 0xffff0000u);
     x[2] = __uint_as_float(v.y << 16), x[3] = __uint_as_float(v.y & 0xffff0000u);
   }
