@@ -14,7 +14,9 @@ Printed (rank 0, one JSON line): value = KV-read GB/s of the whole job,
 roofline of the decode kernel (algorithmic KV bytes / average kernel time:
 HIP events on the launch stream around the timed region of back-to-back
 launches, divided by the steps; against 8 TB/s), the heterogeneous-batch
-makespan of the static grid and the ticket work queue (W = 2 x CU), and the CPU
+makespan of the static grid and the ticket work queue (W = 2 x CU), two
+measured read ceilings (contiguous streaming, and random 4 KB blocks -- the
+decode's own access pattern -- for one step's bytes), and the CPU
 baseline (the oracle's fp32 port of the reference CPU loop, OpenMP, on a
 bounded sample, timed on this host).
 """
@@ -95,6 +97,34 @@ def read_ceiling_gbs(torch, sched_pd, buf):
     return nbytes / (best * 1e-3) / 1e9
 
 
+def random_block_ceiling_gbs(torch, buf, nbytes, block=4096, seed=7):
+    """Read ceiling for the decode's access pattern: `nbytes` of random
+    4 KB blocks of `buf` (one step's worth of (page, kv-head) blocks), read
+    by the library's block probe; min time of 5 launches."""
+    import ctypes
+    import sched_abi
+    lib = sched_abi.load_library()
+    total = buf.numel() * buf.element_size()
+    g = torch.Generator(device=buf.device).manual_seed(seed)
+    ids = torch.randperm(total // block, device=buf.device, generator=g)[:nbytes // block]
+    ids = ids.to(torch.int32).contiguous()
+    stream = torch.cuda.current_stream()
+    s = ctypes.c_void_p(stream.cuda_stream)
+    best = float("inf")
+    for _ in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rc = lib.sched_pd_read_probe_blocks(ctypes.c_void_p(buf.data_ptr()), total,
+                                            ctypes.c_void_p(ids.data_ptr()), ids.numel(), block,
+                                            None, s)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if rc:
+            raise RuntimeError(sched_abi.last_error())
+        best = min(best, e0.elapsed_time(e1))
+    return ids.numel() * block / (best * 1e-3) / 1e9
+
+
 def bench_uniform(args, torch, sched_pd, workloads):
     b = workloads.workload("llama3_8b_uniform", seed=0, n_tables=args.tables)
     out = torch.empty(64, 32, 128, dtype=torch.bfloat16, device="cuda")
@@ -117,8 +147,10 @@ def bench_uniform(args, torch, sched_pd, workloads):
     kern_ms, per = time_launches(step, args.steps, stream)
     kv = b["kv_bytes"]
     ceiling = read_ceiling_gbs(torch, sched_pd, b["k_pool"])
+    ceiling_4k = random_block_ceiling_gbs(torch, b["k_pool"], kv)
     return {
         "kv_bytes": kv, "ms_per_step": wall_ms / args.steps,
+        "random_4k_ceiling_gbs": ceiling_4k,
         # the timed region holds only this kernel's launches, queued back to
         # back: its event span / steps is the kernel's average duration (the
         # per-launch event pairs below add their own gaps)
@@ -428,7 +460,9 @@ def main():
                      "single_launch_events_min_us": round(u["kernel_ms_min"] * 1e3, 2),
                      "bytes_per_launch": u["kv_bytes"], "wg_per_cu": u["occupancy"],
                      "measured_read_ceiling_gbs": round(u["read_ceiling_gbs"], 1),
-                     "frac_of_measured_ceiling": round(kern_gbs / u["read_ceiling_gbs"], 4)},
+                     "frac_of_measured_ceiling": round(kern_gbs / u["read_ceiling_gbs"], 4),
+                     "measured_random_4k_ceiling_gbs": round(u["random_4k_ceiling_gbs"], 1),
+                     "frac_of_random_4k_ceiling": round(kern_gbs / u["random_4k_ceiling_gbs"], 4)},
     }
     line["roofline"]["traffic"] = profiled_traffic()
     sections = set() if args.no_hetero else set(x for x in args.sections.split(",") if x)

@@ -243,6 +243,14 @@ int sched_pd_cu_count(void);
  * measured peak beside the vendor figure. Returns 0 or a hipError_t code. */
 int sched_pd_read_probe(const void *buf, uint64_t bytes, void *sink, void *stream);
 
+/* Random-block read ceiling, no counterpart in the reference: reads blocks
+ * block_ids[0..nblocks) of block_bytes each (16-byte multiple) from `buf`
+ * (`bytes` long; ids outside it are skipped) with non-temporal loads, the
+ * access pattern of a decode over scattered (page, kv-head) blocks. Writes
+ * nothing (sink may be NULL). Returns 0 or a hipError_t code. */
+int sched_pd_read_probe_blocks(const void *buf, uint64_t bytes, const int32_t *block_ids,
+                               uint32_t nblocks, uint32_t block_bytes, void *sink, void *stream);
+
 /* Last error text of this thread ("" if none). */
 const char *sched_pd_last_error(void);
 

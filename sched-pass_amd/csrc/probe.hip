@@ -41,7 +41,63 @@ __global__ void __launch_bounds__(256) read_probe(const u32x4 *__restrict__ p, u
     sink[0] = x;
 }
 
+// Random-block variant: the decode reads its KV as (page, kv-head) blocks of
+// 4 KB scattered over the pool. Workgroup w reads list entries w, w + grid,
+// ..., 4 in flight per lane; each entry is block16 16-byte units, read by the
+// workgroup's 256 lanes in turn. Entries outside the buffer are skipped.
+__global__ void __launch_bounds__(256) read_probe_blocks(const u32x4 *__restrict__ p,
+                                                         uint64_t n16, const int32_t *ids,
+                                                         uint32_t nblk, uint32_t block16,
+                                                         unsigned *sink) {
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (uint32_t e = blockIdx.x; e < nblk; e += 4 * gridDim.x) {
+    uint64_t base[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t k = e + u * gridDim.x;
+      const int64_t id = k < nblk ? (int64_t)ids[k] : -1;
+      base[u] = id < 0 ? 0 : (uint64_t)id * block16;
+      ok[u] = id >= 0 && base[u] + block16 <= n16;
+    }
+    for (uint32_t j = threadIdx.x; j < block16; j += 256) {
+      u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = ok[u] ? __builtin_nontemporal_load(p + base[u] + j) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        acc ^= v[u];
+    }
+  }
+  const unsigned x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (x == 0x9E3779B9u && sink)
+    sink[0] = x;
+}
+
 } // namespace
+
+extern "C" int sched_pd_read_probe_blocks(const void *buf, uint64_t bytes, const int32_t *block_ids,
+                                          uint32_t nblocks, uint32_t block_bytes, void *sink,
+                                          void *stream) {
+  if (!buf || !block_ids || (bytes & 15u) || ((uintptr_t)buf & 15u) || block_bytes == 0 ||
+      (block_bytes & 15u))
+    return schedpd::set_error(hipErrorInvalidValue,
+                              "block probe needs a 16-byte aligned buffer, block ids and "
+                              "16-byte multiple blocks");
+  if (nblocks == 0)
+    return 0;
+  int dev = 0, cus = 0;
+  hipGetDevice(&dev);
+  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const unsigned grid = (unsigned)(cus > 0 ? cus : 256) * 16u;
+  hipLaunchKernelGGL(read_probe_blocks, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const u32x4 *>(buf), bytes / 16u, block_ids, nblocks,
+                     block_bytes / 16u, static_cast<unsigned *>(sink));
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0
+                         : schedpd::set_error(e, "block probe launch: %s", hipGetErrorString(e));
+}
 
 extern "C" int sched_pd_read_probe(const void *buf, uint64_t bytes, void *sink, void *stream) {
   if (!buf || (bytes & 15u) || ((uintptr_t)buf & 15u))

@@ -136,6 +136,7 @@ SIGNATURES = {
     "sched_paged_decode_kernel_kind": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_pd_cu_count": (ctypes.c_int, []),
     "sched_pd_read_probe": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _p]),
+    "sched_pd_read_probe_blocks": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _u32, _u32, _p, _p]),
     "sched_pd_last_error": (ctypes.c_char_p, []),
     "sched_kv_default_args": (None, [ctypes.POINTER(SchedKvAppendArgs)]),
     "sched_kv_append": (ctypes.c_int, [ctypes.POINTER(SchedKvAppendArgs), _p]),

@@ -185,3 +185,12 @@ def test_plan_tiles_is_task_major():
 def torch_tiles(t):
     import torch
     return torch.from_numpy(t)
+
+
+def test_block_probe_validates_arguments_without_the_gpu(schedlib):
+    buf = ctypes.c_void_p(0x10000)
+    ids = (ctypes.c_int32 * 4)(0, 1, 2, 3)
+    assert schedlib.sched_pd_read_probe_blocks(buf, 1 << 20, None, 4, 4096, None, None) != 0
+    assert "block probe" in abi.last_error()
+    assert schedlib.sched_pd_read_probe_blocks(buf, 1 << 20, ids, 4, 4095, None, None) != 0
+    assert schedlib.sched_pd_read_probe_blocks(buf, 1 << 20, ids, 0, 4096, None, None) == 0
