@@ -15,7 +15,7 @@ roofline of the decode kernel (algorithmic KV bytes / average kernel time:
 HIP events on the launch stream around the timed region of back-to-back
 launches, divided by the steps; against 8 TB/s), the heterogeneous-batch
 makespan of the static grid and the ticket work queue (W = 2 x CU), two
-measured read ceilings (contiguous streaming, and random 4 KB blocks -- the
+measured read ceilings (contiguous streaming, and random whole pages -- the
 decode's own access pattern -- for one step's bytes), and the CPU
 baseline (the oracle's fp32 port of the reference CPU loop, OpenMP, on a
 bounded sample, timed on this host).
@@ -77,30 +77,33 @@ def time_region(fn, steps, stream):
 
 def read_ceiling_gbs(torch, sched_pd, buf):
     """Achievable streaming-read bandwidth: the library's read probe over
-    `buf` (>= 2 GiB, far beyond the 256 MB MALL), min time of 5 launches."""
+    `buf` (>= 2 GiB, far beyond the 256 MB MALL); min over 3 repeats of 3
+    back-to-back launches per event pair."""
     import ctypes
     import sched_abi
     lib = sched_abi.load_library()
     nbytes = buf.numel() * buf.element_size()
     stream = torch.cuda.current_stream()
     s = ctypes.c_void_p(stream.cuda_stream)
+    if lib.sched_pd_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, None, s):
+        raise RuntimeError(sched_abi.last_error())
     best = float("inf")
-    for _ in range(6):
+    for _ in range(3):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        rc = lib.sched_pd_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, None, s)
+        for _ in range(3):
+            lib.sched_pd_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, None, s)
         e1.record(stream)
         torch.cuda.synchronize()
-        if rc:
-            raise RuntimeError(sched_abi.last_error())
-        best = min(best, e0.elapsed_time(e1))
+        best = min(best, e0.elapsed_time(e1) / 3)
     return nbytes / (best * 1e-3) / 1e9
 
 
-def random_block_ceiling_gbs(torch, buf, nbytes, block=4096, seed=7):
+def random_block_ceiling_gbs(torch, buf, nbytes, block, seed=7, launches=5):
     """Read ceiling for the decode's access pattern: `nbytes` of random
-    4 KB blocks of `buf` (one step's worth of (page, kv-head) blocks), read
-    by the library's block probe; min time of 5 launches."""
+    `block`-byte blocks of `buf` (one step's worth of pages, each a page of
+    every kv-head), read by the library's block probe. Min over 3 repeats of
+    `launches` back-to-back launches per event pair."""
     import ctypes
     import sched_abi
     lib = sched_abi.load_library()
@@ -110,18 +113,20 @@ def random_block_ceiling_gbs(torch, buf, nbytes, block=4096, seed=7):
     ids = ids.to(torch.int32).contiguous()
     stream = torch.cuda.current_stream()
     s = ctypes.c_void_p(stream.cuda_stream)
+    call = lambda: lib.sched_pd_read_probe_blocks(ctypes.c_void_p(buf.data_ptr()), total,  # noqa: E731
+                                                  ctypes.c_void_p(ids.data_ptr()), ids.numel(),
+                                                  block, None, s)
+    if call():
+        raise RuntimeError(sched_abi.last_error())
     best = float("inf")
-    for _ in range(6):
+    for _ in range(3):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        rc = lib.sched_pd_read_probe_blocks(ctypes.c_void_p(buf.data_ptr()), total,
-                                            ctypes.c_void_p(ids.data_ptr()), ids.numel(), block,
-                                            None, s)
+        for _ in range(launches):
+            call()
         e1.record(stream)
         torch.cuda.synchronize()
-        if rc:
-            raise RuntimeError(sched_abi.last_error())
-        best = min(best, e0.elapsed_time(e1))
+        best = min(best, e0.elapsed_time(e1) / launches)
     return ids.numel() * block / (best * 1e-3) / 1e9
 
 
@@ -147,10 +152,11 @@ def bench_uniform(args, torch, sched_pd, workloads):
     kern_ms, per = time_launches(step, args.steps, stream)
     kv = b["kv_bytes"]
     ceiling = read_ceiling_gbs(torch, sched_pd, b["k_pool"])
-    ceiling_4k = random_block_ceiling_gbs(torch, b["k_pool"], kv)
+    page_bytes = b["k_pool"][0].numel() * b["k_pool"].element_size()   # one page, all kv-heads
+    ceiling_pages = random_block_ceiling_gbs(torch, b["k_pool"], kv, page_bytes)
     return {
         "kv_bytes": kv, "ms_per_step": wall_ms / args.steps,
-        "random_4k_ceiling_gbs": ceiling_4k,
+        "random_page_ceiling_gbs": ceiling_pages, "page_bytes": page_bytes,
         # the timed region holds only this kernel's launches, queued back to
         # back: its event span / steps is the kernel's average duration (the
         # per-launch event pairs below add their own gaps)
@@ -461,8 +467,9 @@ def main():
                      "bytes_per_launch": u["kv_bytes"], "wg_per_cu": u["occupancy"],
                      "measured_read_ceiling_gbs": round(u["read_ceiling_gbs"], 1),
                      "frac_of_measured_ceiling": round(kern_gbs / u["read_ceiling_gbs"], 4),
-                     "measured_random_4k_ceiling_gbs": round(u["random_4k_ceiling_gbs"], 1),
-                     "frac_of_random_4k_ceiling": round(kern_gbs / u["random_4k_ceiling_gbs"], 4)},
+                     "measured_random_page_ceiling_gbs": round(u["random_page_ceiling_gbs"], 1),
+                     "random_page_bytes": u["page_bytes"],
+                     "frac_of_random_page_ceiling": round(kern_gbs / u["random_page_ceiling_gbs"], 4)},
     }
     line["roofline"]["traffic"] = profiled_traffic()
     sections = set() if args.no_hetero else set(x for x in args.sections.split(",") if x)
