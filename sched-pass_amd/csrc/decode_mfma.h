@@ -27,7 +27,8 @@
 // prefetch depth leave every output bit unchanged.
 //
 // Policy lever: urgent tasks stream with DEPTH_U pages in flight instead of
-// DEPTH_S (deeper KV prefetch); polite tasks use non-temporal loads.
+// DEPTH_S (deeper KV prefetch); polite tasks use non-temporal loads, as every
+// task does by default (KV is read once per step).
 // fp8: values convert exactly to bf16; the per-(page, head) K scale multiplies
 // the score and the V scale multiplies p before PV, so no element is scaled.
 #pragma once
