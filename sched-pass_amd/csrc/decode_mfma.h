@@ -28,7 +28,8 @@
 //
 // Policy lever: urgent tasks stream with DEPTH_U pages in flight instead of
 // DEPTH_S (deeper KV prefetch); polite tasks use non-temporal loads, as every
-// task does by default (KV is read once per step).
+// task does by default (KV is read once per step) except work items longer
+// than kLongItemPages, which take the deep pipeline with ordinary loads.
 // fp8: values convert exactly to bf16; the per-(page, head) K scale multiplies
 // the score and the V scale multiplies p before PV, so no element is scaled.
 #pragma once
@@ -64,6 +65,16 @@ template <> struct PageRegs<true> {
 #define SCHED_PD_MFMA_STOCK_NT 1
 #endif
 constexpr bool kStockNT = SCHED_PD_MFMA_STOCK_NT != 0;
+
+// A work item of more pages than this is the step's straggler: it streams
+// alone at the end, where a deep pipeline of ordinary (temporal) loads runs
+// faster than non-temporal ones (heterogeneous batch, one workgroup per task:
+// 828 -> 662 us; 64-page threshold slows the 128-page tasks of the uniform
+// batch, 83 -> 94 us). Polite items keep their non-temporal loads.
+#ifndef SCHED_PD_MFMA_LONG_ITEM_PAGES
+#define SCHED_PD_MFMA_LONG_ITEM_PAGES 256u
+#endif
+constexpr uint32_t kLongItemPages = SCHED_PD_MFMA_LONG_ITEM_PAGES;
 
 template <bool NT, typename T> __device__ __forceinline__ T gload(const T *p) {
   if constexpr (NT)
@@ -419,7 +430,9 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       S.qop[kb] = __builtin_bit_cast(bf16x8_t, qv);
     }
 
-    if (pol.urgent)
+    if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
+      stream_pages<FP8, NW, DEPTH_U, false, LINEAR>(P, T, S, lane, g4);
+    else if (pol.urgent)
       stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR>(P, T, S, lane, g4);
     else if (pol.polite)
       stream_pages<FP8, NW, DEPTH_S, true, LINEAR>(P, T, S, lane, g4);
