@@ -166,7 +166,16 @@ def bench_uniform(args, torch, sched_pd, workloads):
     }
 
 
-TILE_PAGES = 128  # split-KV tile (pages) for the heterogeneous batch (sweep: 32..256)
+# Split-KV tiles hold 1 MiB of one kv-head's KV: 128 pages of bf16, 256 of
+# fp8 (d 128, page 16). Swept: bf16 32..256 pages, fp8 64..512.
+TILE_BYTES = 1 << 20
+
+
+def tile_pages_for(elem_bytes, page=16, head_dim=128):
+    return TILE_BYTES // (page * head_dim * 2 * elem_bytes)
+
+
+TILE_PAGES = tile_pages_for(2)
 
 
 def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):
@@ -290,10 +299,11 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     return res
 
 
-def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES):
+def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_for(1)):
     """Qwen2-7B shape (Hq 28 / Hkv 4), fp8-e4m3fn KV with per-(page, head)
     scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
-    max 16384); ticket work queue over split tiles, timer on."""
+    max 16384); ticket work queue over split tiles, timer on; then the same
+    queue with pi over tiles by the timer's per-task cycles, longest first."""
     import numpy as np
     b = workloads.workload("qwen2_7b_fp8", seed=0)
     R, ntask = 512, 512 * 4
@@ -319,9 +329,15 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES)
     sched_pd.launch(a_wq, stream)
     torch.cuda.synchronize()
     cyc = plane.read_timer()[:ntask].numpy()
+    # closed loop: pi over tiles by the measured per-task cost, longest first
+    plane.install_order(sched_pd.tile_order_by_task_key(tiles, cyc.astype(np.float64)), nt)
+    plane.push()
+    us_lpt = _makespan_us(torch, sched_pd, a_wq, stream)
     kv = b["kv_bytes"]
     return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
-            "gbs": round(kv / us_wq / 1e3, 1), "tiles": nt, "workers": W,
+            "wq_tiles_lpt_timer_us": round(us_lpt, 2),
+            "gbs": round(kv / us_wq / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
+            "tiles": nt, "tile_pages": tile_pages, "workers": W,
             "max_ctx": int(ctx.max()),
             "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                                  "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())}}
