@@ -51,7 +51,7 @@ template <> struct PageRegs<false> {
 };
 template <> struct PageRegs<true> {
   u32x4_t k[2]; // 2 x 16 fp8 K
-  unsigned v[8]; // 8 x 4 fp8 V^T
+  u32x4_t v[2]; // V rows lane and lane + 64 (16 fp8 tokens each), see fp8_v_operands
   float ks, vs;  // the page's K / V scales, loaded with its KV so that no
                  // load is consumed right after issue (which would drain the
                  // whole prefetch ring with s_waitcnt vmcnt(0))
@@ -129,6 +129,33 @@ __device__ __forceinline__ u32x2_t fp8x4_to_bf16x4(unsigned w) {
   return r;
 }
 
+// fp8 V: a lane loads two whole 16-byte V rows (rows lane and lane + 64 of
+// the page's 128 dims), a quarter of the load instructions of taking each
+// 4-token slice separately. The PV A-operand of lane (g4, c16) for dim block
+// blk is dword g4 (tokens 4*g4..+3) of row 16*blk + c16, which the lane in
+// row group blk % 4 holds: a 4x4 transpose of (dword, lane row) per load,
+// done with two v_permlane32_swap and two v_permlane16_swap (the first swaps
+// the upper rows of its first operand with the lower rows of the second, the
+// second swaps odd rows of the first with even rows of the second).
+__device__ __forceinline__ void rows_transpose4(unsigned d[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto e = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  d[0] = c[0];
+  d[1] = c[1];
+  d[2] = e[0];
+  d[3] = e[1];
+}
+
+// The eight fp8 PV A-operands (4 tokens of one dim, one per dim block).
+__device__ __forceinline__ void fp8_v_operands(const u32x4_t v[2], unsigned out[8]) {
+  out[0] = v[0].x, out[1] = v[0].y, out[2] = v[0].z, out[3] = v[0].w;
+  out[4] = v[1].x, out[5] = v[1].y, out[6] = v[1].z, out[7] = v[1].w;
+  rows_transpose4(out);
+  rows_transpose4(out + 4);
+}
+
 struct MfmaTask {
   uint32_t r, h, n, budget;
   int64_t row; // block-table index of the request's first page
@@ -166,9 +193,8 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
     const int64_t si = (int64_t)page * P.Hkv + T.h;
     B.ks = (!LINEAR && P.k_scale) ? P.k_scale[si] : 1.f;
     B.vs = P.v_scale ? P.v_scale[si] : 1.f;
-#pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
-      B.v[blk] = gload<NT>(reinterpret_cast<const unsigned *>(vp + 256 * blk));
+    B.v[0] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp));
+    B.v[1] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 64 * 16));
   }
 }
 
@@ -243,13 +269,16 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   const s16x4_t pop = __builtin_bit_cast(s16x4_t, pk);
 
   // PV
+  unsigned v8[8];
+  if constexpr (FP8)
+    fp8_v_operands(B.v, v8);
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
     if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, B.v[blk]);
     else
-      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(B.v[blk]));
+      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
     S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop, S.acc[blk], 0, 0, 0);
   }
 }
@@ -281,13 +310,16 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
   lo.x = pack_bf16_rne(r0, r1);
   lo.y = pack_bf16_rne(r2, r3);
   const s16x4_t bhi = __builtin_bit_cast(s16x4_t, hi), blo = __builtin_bit_cast(s16x4_t, lo);
+  unsigned v8[8];
+  if constexpr (FP8)
+    fp8_v_operands(B.v, v8);
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
     if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, B.v[blk]);
     else
-      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(B.v[blk]));
+      a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
     S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, bhi, S.acc[blk], 0, 0, 0);
     S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, blo, S.acc[blk], 0, 0, 0);
   }
@@ -400,7 +432,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.p1 = R.p1;
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
-    T.vbase = static_cast<const uint8_t *>(P.v_pool) + (int64_t)c16 * P.vds * EB + 4u * g4 * EB;
+    // bf16: the lane's 4-token slice of dim c16; fp8: whole row 16*g4 + c16
+    T.vbase = static_cast<const uint8_t *>(P.v_pool) +
+              (FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
+                   : (int64_t)c16 * P.vds * EB + 4u * g4 * EB);
     T.kpage_bytes = P.kps * EB;
     T.khead_bytes = P.khs * EB * T.h;
     T.vpage_bytes = P.vps * EB;
