@@ -47,7 +47,7 @@ typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
 template <bool FP8> struct PageRegs;
 template <> struct PageRegs<false> {
   u32x4_t k[4]; // 4 x 8 bf16 K
-  u32x2_t v[8]; // 8 x 4 bf16 V^T
+  u32x4_t v[4]; // V row halves, see bf16_v_operands
 };
 template <> struct PageRegs<true> {
   u32x4_t k[2]; // 2 x 16 fp8 K
@@ -156,6 +156,22 @@ __device__ __forceinline__ void fp8_v_operands(const u32x4_t v[2], unsigned out[
   rows_transpose4(out + 4);
 }
 
+// bf16 V: load i of a lane in row group g4 is the 16-byte half g4 / 2
+// (tokens 8*(g4/2)..+7) of V row 16*(2i + g4 % 2) + c16: even lane rows hold
+// dim block 2i, odd ones block 2i + 1, each as the two 4-token slices of the
+// half. One v_permlane16_swap per dword pair trades the odd rows' first slice
+// for the even rows' second, after which every lane holds its own slice
+// (tokens 4*g4..+3) of both blocks: four 16-byte loads and eight swaps per
+// page instead of eight 8-byte loads.
+__device__ __forceinline__ void bf16_v_operands(u32x4_t v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto a = __builtin_amdgcn_permlane16_swap(v[i].x, v[i].z, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(v[i].y, v[i].w, false, false);
+    v[i] = u32x4_t{a[0], b[0], a[1], b[1]}; // (block 2i slice, block 2i + 1 slice)
+  }
+}
+
 struct MfmaTask {
   uint32_t r, h, n, budget;
   int64_t row; // block-table index of the request's first page
@@ -183,8 +199,8 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
       for (int kb = 0; kb < 4; ++kb)
         B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
-      B.v[blk] = gload<NT>(reinterpret_cast<const u32x2_t *>(vp + 512 * blk));
+    for (int i = 0; i < 4; ++i)
+      B.v[i] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 1024 * i));
   } else {
     if constexpr (!LINEAR)
 #pragma unroll
@@ -270,13 +286,21 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 
   // PV
   unsigned v8[8];
-  if constexpr (FP8)
+  u32x4_t vb[4];
+  if constexpr (FP8) {
     fp8_v_operands(B.v, v8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vb[i] = B.v[i];
+    bf16_v_operands(vb);
+  }
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
     if constexpr (!FP8)
-      a = __builtin_bit_cast(s16x4_t, B.v[blk]);
+      a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
+                                                : u32x2_t{vb[blk >> 1].x, vb[blk >> 1].y});
     else
       a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
     S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop, S.acc[blk], 0, 0, 0);
@@ -311,13 +335,21 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
   lo.y = pack_bf16_rne(r2, r3);
   const s16x4_t bhi = __builtin_bit_cast(s16x4_t, hi), blo = __builtin_bit_cast(s16x4_t, lo);
   unsigned v8[8];
-  if constexpr (FP8)
+  u32x4_t vb[4];
+  if constexpr (FP8) {
     fp8_v_operands(B.v, v8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vb[i] = B.v[i];
+    bf16_v_operands(vb);
+  }
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
     if constexpr (!FP8)
-      a = __builtin_bit_cast(s16x4_t, B.v[blk]);
+      a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
+                                                : u32x2_t{vb[blk >> 1].x, vb[blk >> 1].y});
     else
       a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
     S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, bhi, S.acc[blk], 0, 0, 0);
@@ -432,10 +464,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.p1 = R.p1;
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
-    // bf16: the lane's 4-token slice of dim c16; fp8: whole row 16*g4 + c16
+    // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16
     T.vbase = static_cast<const uint8_t *>(P.v_pool) +
               (FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
-                   : (int64_t)c16 * P.vds * EB + 4u * g4 * EB);
+                   : (int64_t)(c16 + 16u * (g4 & 1u)) * P.vds * EB + 16u * (g4 >> 1));
     T.kpage_bytes = P.kps * EB;
     T.khead_bytes = P.khs * EB * T.h;
     T.vpage_bytes = P.vps * EB;
