@@ -17,8 +17,9 @@
 //   online-softmax update the probabilities feed PV with no data movement:
 //   PV  O^T[128 x 16 head] += V^T[128 x 16 tok] . P^T[16 tok x 16 head]
 //       8 x v_mfma_f32_16x16x16_bf16; A = V^T rows (lane: dim 16*blk+lane%16,
-//       tokens 4*(lane/16)..+3 -> one 8-byte load; 512 contiguous bytes per
-//       wave instruction).
+//       tokens 4*(lane/16)..+3). Lanes load 16-byte V row halves (bf16) or
+//       whole rows (fp8) and trade these 4-token slices across lane rows
+//       with v_permlane16/32_swap (bf16_v_operands, fp8_v_operands).
 //
 // A workgroup of NW waves runs one task = (request, kv-head); wave w streams
 // pages w, w+NW, ... with DEPTH pages of loads in flight (register ring), and
