@@ -270,17 +270,28 @@ class PagedKvCache:
         """Append counts[i] rows (default 1 each) of k_new / v_new [T, Hkv, d]
         to request rids[i], rows in request order."""
         counts = [1] * len(rids) if counts is None else [int(c) for c in counts]
-        if sum(counts) != k_new.shape[0]:
+        if len(set(rids)) != len(rids):
+            raise ValueError("a request appears twice in one append")
+        if any(c < 0 for c in counts) or sum(counts) != k_new.shape[0]:
             raise ValueError(f"counts sum to {sum(counts)}, sources have {k_new.shape[0]} rows")
+        held = {rid: len(self.pages[rid]) for rid in rids}
         self.reserve(rids, counts)
-        for rid, n in zip(rids, counts):
-            self.lens[rid] += n
-        bt, ctx = self.block_table(rids)
-        app = np.zeros(len(rids) + 1, dtype=np.int32)
-        app[1:] = np.cumsum(counts)
-        append(k_new, v_new, torch.from_numpy(app).to(self.device), ctx, self.k_pool,
-               self.v_pool, bt, k_scale=self.k_scale, v_scale=self.v_scale,
-               max_append=max(counts + [0]), errors=errors)
+        try:
+            for rid, n in zip(rids, counts):
+                self.lens[rid] += n
+            bt, ctx = self.block_table(rids)
+            app = np.zeros(len(rids) + 1, dtype=np.int32)
+            app[1:] = np.cumsum(counts)
+            append(k_new, v_new, torch.from_numpy(app).to(self.device), ctx, self.k_pool,
+                   self.v_pool, bt, k_scale=self.k_scale, v_scale=self.v_scale,
+                   max_append=max(counts + [0]), errors=errors)
+        except Exception:
+            # a rejected launch leaves the cache as it was
+            for rid, n in zip(rids, counts):
+                self.lens[rid] -= n
+                self.allocator.free(self.pages[rid][held[rid]:])
+                del self.pages[rid][held[rid]:]
+            raise
 
     def decode(self, q, rids, **kw):
         """One decode step over the requests' current contexts."""

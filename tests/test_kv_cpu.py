@@ -283,3 +283,16 @@ def test_cache_bookkeeping_and_tables_on_cpu():
     assert c.allocator.num_free == 7               # all or nothing
     c.release("a")
     assert c.allocator.num_free == 9
+
+
+def test_cache_append_rolls_back_a_rejected_launch():
+    c = PagedKvCache(8, 2, 8, page_size=4, dtype=torch.bfloat16, device="cpu")
+    c.add_request("a")
+    c.add_request("b")
+    rows = torch.zeros(5, 2, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):          # host tensors: the launcher refuses them
+        c.append(["a", "b"], rows, rows, [2, 3])
+    assert c.lens == {"a": 0, "b": 0} and c.pages == {"a": [], "b": []}
+    assert c.allocator.num_free == 8
+    with pytest.raises(ValueError):
+        c.append(["a", "a"], rows, rows, [2, 3])
