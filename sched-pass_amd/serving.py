@@ -24,6 +24,10 @@ Per step, as in the reference:
   on_batch_end()
     * record the step's completion event; on a probe step keep (event,
       binding) pending and switch the timer off for the following steps.
+
+begin() / end() wrap the two hooks for an engine loop: a failure is counted,
+logged once per site, and that step runs the stock decode. A batch larger
+than the plane's tables raises (loudly) instead of being truncated.
 """
 from __future__ import annotations
 
@@ -73,6 +77,8 @@ class ServingHooks:
         self.armed_n = None      # items the armed ticket queue covers
         self.launch = {"plane": plane, "workers": 0, "tiles": None, "tile_pages": 0}
         self.probes_folded = 0
+        self.hook_errors = 0
+        self._err_sites = set()
 
     # -- helpers ---------------------------------------------------------------
     def _items(self, kv_lens):
@@ -138,6 +144,11 @@ class ServingHooks:
         n = len(rids)
         tiles, item_req, item_pages = self._items(kv_list)
         nitems = int(item_req.size)
+        if max(nitems, n * self.hkv) > p.N:
+            # never truncate a batch to the tables (python/sched_sglang_plugin.py:
+            # 99-118): a larger plane is the fix
+            raise RuntimeError(f"batch of {nitems} work items / {n * self.hkv} tasks exceeds "
+                               f"the plane's max_tasks {p.N}")
         self._consume_probe()
 
         alpha, beta = self.ctl._fit.coeffs()
@@ -150,7 +161,7 @@ class ServingHooks:
         p.set_timer_enabled(probe)
         self.timer_armed = probe
         workers = 0
-        if not cfg.observe_only and nitems <= p.N:
+        if not cfg.observe_only:
             R = cfg.resident
             imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6)) \
                 if nitems else 1.0
@@ -195,6 +206,32 @@ class ServingHooks:
             self.plane.set_timer_enabled(False)
             self.plane.push()
 
+    # -- engine-facing wrappers: a hook never takes the serving loop down --------
+    STOCK = {"plane": None, "workers": 0, "tiles": None, "tile_pages": 0}
+
+    def begin(self, rids, kv_lens) -> dict:
+        """on_batch_begin for an engine loop: an exception is counted and
+        logged (first per site), and the step runs the stock decode (no
+        levers) instead (python/sched_sglang_plugin.py:594-606, 648-662)."""
+        try:
+            return self.on_batch_begin(rids, kv_lens)
+        except Exception as e:  # noqa: BLE001 -- any failure degrades to stock
+            self._hook_error("begin", e)
+            return dict(self.STOCK)
+
+    def end(self) -> None:
+        try:
+            self.on_batch_end()
+        except Exception as e:  # noqa: BLE001
+            self._hook_error("end", e)
+
+    def _hook_error(self, where: str, exc: Exception) -> None:
+        self.hook_errors += 1
+        if where not in self._err_sites:
+            self._err_sites.add(where)
+            print(f"[sched-serving] {where} hook error (control plane degraded; serving "
+                  f"continues with the stock decode): {exc!r}", flush=True)
+
     # -- pieces ----------------------------------------------------------------
     def _retire_order(self) -> None:
         if self.order_n is not None:
@@ -227,4 +264,5 @@ class ServingHooks:
         u = self.ctl.uncertainty(b[0], b[1]) if b and b[0] else 0.0
         return (f"[sched-serving] step={self.step} items={b[3] if b else 0} "
                 f"R={self.cfg.resident} probes={self.probes_folded} uncert={u:.2f} "
+                f"hook_errors={self.hook_errors} "
                 f"mode={'observe' if self.cfg.observe_only else 'enforce'}")

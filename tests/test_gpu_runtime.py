@@ -199,6 +199,37 @@ def test_dynamic_loop_demo(lib):
     lib.sched_rt_disarm()
 
 
+def test_shed_quality_curve(lib):
+    """The shed quality contract (test/py/eval_quality.py:30-70) on the
+    dynamic-loop fixture: tau = 0 is full attention, every tau in (24, 16, 8,
+    4) matches its truncated reference, and the cosine to full attention
+    does not rise as the budget shrinks."""
+    f = Fixture(fixture_dynamic_loop)
+    assert lib.sched_rt_init()
+    lib.sched_rt_set_num_tasks(f.nseq)
+    full = np.asarray(f.reference(tau=0), np.float64).ravel()
+    last = None
+    try:
+        for tau in (0, 24, 16, 8, 4):
+            for i in range(f.nseq):
+                lib.sched_rt_set_tau(i, tau)
+            lib.sched_rt_push_ctrl()
+            o = f.launch(lib).cpu().double().numpy()
+            assert close(o, f.reference(tau=tau)), f"tau {tau}"
+            o = o.ravel()
+            cos = float(o @ full / (np.linalg.norm(o) * np.linalg.norm(full)))
+            if tau == 0:
+                assert cos > 1 - 1e-9
+            if last is not None:
+                assert cos <= last + 1e-6, f"tau {tau}: cosine {cos} > {last}"
+            last = cos
+    finally:
+        for i in range(f.nseq):
+            lib.sched_rt_set_tau(i, 0)
+        lib.sched_rt_push_ctrl()
+        lib.sched_rt_disarm()
+
+
 def test_runtime_work_queue_through_rt_tables(lib):
     """Ticket queue armed through the C runtime (flags RT_TABLES)."""
     import sched_pd

@@ -169,3 +169,19 @@ def test_off_cadence_rebuilds_tiles_and_disarms_a_mismatched_queue():
     grown = h.on_batch_begin([0, 1, 2], [33, 32, 32])           # 3 chunks for r0
     assert grown["tiles"].shape[0] == 7 and grown["workers"] == 0
     assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 0
+
+
+def test_oversized_batch_raises_and_begin_degrades_to_stock(capsys):
+    p = plane(8)
+    h = ServingHooks(p, 2, HookConfig(plan_every=1, timer_every=1), event_factory=Ev)
+    import pytest
+    with pytest.raises(RuntimeError, match="max_tasks"):
+        h.on_batch_begin([0, 1, 2, 3, 4], [16] * 5)          # 10 tasks > 8 rows
+    launch = h.begin([0, 1, 2, 3, 4], [16] * 5)
+    assert launch == ServingHooks.STOCK and h.hook_errors == 1
+    h.begin([0, 1, 2, 3, 4], [16] * 5)
+    assert h.hook_errors == 2
+    out = capsys.readouterr().out
+    assert out.count("begin hook error") == 1                 # first per site only
+    assert "hook_errors=2" in h.stats()
+    assert h.begin([0, 1], [16, 32])["plane"] is p            # recovers on a valid batch
