@@ -49,10 +49,12 @@ template <bool FP8> struct PageRegs;
 template <> struct PageRegs<false> {
   u32x4_t k[4]; // 4 x 8 bf16 K
   u32x4_t v[4]; // V row halves, see bf16_v_operands
+  float lw[4];  // linear mode: the lane's token weights, loaded with the page
 };
 template <> struct PageRegs<true> {
   u32x4_t k[2]; // 2 x 16 fp8 K
   u32x4_t v[2]; // V rows lane and lane + 64 (16 fp8 tokens each), see fp8_v_operands
+  float lw[4];   // linear mode: the lane's token weights, loaded with the page
   float ks, vs;  // the page's K / V scales, loaded with its KV so that no
                  // load is consumed right after issue (which would drain the
                  // whole prefetch ring with s_waitcnt vmcnt(0))
@@ -191,7 +193,18 @@ struct MfmaState {
 
 template <bool FP8, bool NT, bool LINEAR>
 __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, int32_t page,
-                                           PageRegs<FP8> &B) {
+                                           uint32_t pidx, PageRegs<FP8> &B) {
+  if constexpr (LINEAR) {
+    // weights of tokens 4*g4..+3 of the page, for the lanes of MFMA column 0;
+    // positions past the context are masked later and not read
+    const uint32_t lane = threadIdx.x & 63u, g4 = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t t = pidx * 16u + 4u * g4 + v;
+      B.lw[v] = ((lane & 15u) == 0u && t < T.n)
+                    ? P.lin_w[P.lin_w_period ? t % P.lin_w_period : t] : 0.f;
+    }
+  }
   const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes;
   const uint8_t *vp = T.vbase + (int64_t)page * T.vpage_bytes + T.vhead_bytes;
   if constexpr (!FP8) {
@@ -325,7 +338,7 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
   for (int v = 0; v < 4; ++v) {
     const uint32_t i = 4u * g4 + v, t = pos0 + i;
     const bool keep = c16 == 0u && t < T.n && (prefix ? t : i) < T.budget;
-    wv[v] = keep ? P.lin_w[P.lin_w_period ? t % P.lin_w_period : t] * vs : 0.f;
+    wv[v] = keep ? B.lw[v] * vs : 0.f;
   }
   u32x2_t hi, lo;
   hi.x = pack_bf16_rne(wv[0], wv[1]);
@@ -395,12 +408,13 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   // Unconditional prologue: a wave with fewer than DEPTH pages re-reads its
   // last page into the unused slots (same lines, L2 hits) so that the loop is
   // entered with the same DEPTH pages outstanding as on every back edge.
+  auto pidx_of = [&](int j) { return T.p0 + T.w + NW * (uint32_t)j; };
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s)
-    issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
+    issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
 
   auto compute = [&](int s, int j) {
-    const uint32_t pidx = T.p0 + T.w + NW * (uint32_t)j;
+    const uint32_t pidx = pidx_of(j);
     if constexpr (LINEAR)
       linear_page<FP8>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
     else
@@ -412,7 +426,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     for (int s = 0; s < DEPTH; ++s) {
       compute(s, j + s);
       pid[s] = idn[s];
-      issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
+      issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
       idn[s] = page_id<NW>(P, T, min(j + 2 * DEPTH + s, last));
     }
   }
@@ -423,7 +437,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
         compute(s, j + s);
         if (j + DEPTH + s < npg) {
           pid[s] = idn[s];
-          issue_page<FP8, NT, LINEAR>(P, T, pid[s], buf[s]);
+          issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
         }
       }
     }
