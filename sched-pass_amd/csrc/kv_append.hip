@@ -42,6 +42,7 @@ struct AParams {
   float *k_scale, *v_scale;
   uint32_t *errors;
   uint32_t hpw; // kv-heads per workgroup, divides Hkv
+  uint32_t w8;  // one-round path reads and writes 8-element chunks
 };
 
 template <bool SRC_F32>
@@ -69,6 +70,38 @@ __device__ __forceinline__ void load_src4(const void *src, int64_t idx, float x[
     x[0] = __uint_as_float(v.x << 16), x[1] = __uint_as_float(v.x & 0xffff0000u);
     x[2] = __uint_as_float(v.y << 16), x[3] = __uint_as_float(v.y & 0xffff0000u);
   }
+}
+
+// Eight consecutive source elements (16 bytes of bf16, 32 of fp32).
+template <bool SRC_F32>
+__device__ __forceinline__ void load_src8(const void *src, int64_t idx, float x[8]) {
+  if (SRC_F32) {
+    const u32x4_t a = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx));
+    const u32x4_t b = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx + 4));
+    x[0] = __uint_as_float(a.x), x[1] = __uint_as_float(a.y);
+    x[2] = __uint_as_float(a.z), x[3] = __uint_as_float(a.w);
+    x[4] = __uint_as_float(b.x), x[5] = __uint_as_float(b.y);
+    x[6] = __uint_as_float(b.z), x[7] = __uint_as_float(b.w);
+  } else {
+    const u32x4_t v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(src) + idx));
+    const unsigned w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+}
+
+template <bool SRC_F32, int W>
+__device__ __forceinline__ void load_chunk(const void *src, int64_t idx, float x[W]) {
+  if constexpr (W == 8)
+    load_src8<SRC_F32>(src, idx, x);
+  else
+    load_src4<SRC_F32>(src, idx, x);
 }
 
 // Least 2^k (k >= -126) with a <= 448 * 2^k; 0 for a == 0. With
@@ -419,6 +452,27 @@ __device__ void write_tensor(const AParams &P, const PageScales &S, int x, const
   }
 }
 
+// A W-element chunk of token-row dims, encoded and stored (one 4/8/16-byte
+// store for W = 4; W = 8 stores 8/16/32 bytes as one or two stores).
+template <int KVD, int W>
+__device__ __forceinline__ void store_chunk(PoolElem<KVD> *p, const float x[W], float inv) {
+  typedef Codec<KVD> C;
+  typedef typename C::Vec Vec;
+  if constexpr (W == 4) {
+    *reinterpret_cast<Vec *>(p) = C::enc(x, inv);
+  } else {
+    const Vec a = C::enc(x, inv), b = C::enc(x + 4, inv);
+    if constexpr (KVD == SCHED_PD_BF16)
+      *reinterpret_cast<uint4 *>(p) = make_uint4(a.x, a.y, b.x, b.y);
+    else if constexpr (KVD == SCHED_PD_FP8_E4M3)
+      *reinterpret_cast<uint2 *>(p) = make_uint2(a, b);
+    else {
+      reinterpret_cast<Vec *>(p)[0] = a;
+      reinterpret_cast<Vec *>(p)[1] = b;
+    }
+  }
+}
+
 // Chunks one lane holds in the one-round path, and the LDS stage that
 // transposes a d-major V: rows (head, appended slot) of d floats, padded by
 // one float so the four slot rows a chunk reads fall in different banks.
@@ -449,18 +503,21 @@ __device__ void regrow_rows(const AParams &P, const PageScales &S, int x, PoolEl
   }
 }
 
-// One page of a head group whose appended chunks (per tensor) fit one round:
-// every lane loads its K and V chunks once, keeps them in registers through
-// the fp8 amax, and stores them; a d-major V goes through the LDS stage so
-// that the source is read in rows and the pool written in slot groups.
-template <bool SRC_F32, int KVD>
+// One page of a head group whose appended elements (per tensor) fit one
+// round: every lane loads its K and V chunks of W elements once (16 values
+// per lane and tensor), keeps them in registers through the fp8 amax, and
+// stores them; a d-major V goes through the LDS stage so that the source is
+// read in rows and the pool written in slot groups.
+template <bool SRC_F32, int KVD, int W>
 __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, int64_t page,
                                uint32_t h0, uint32_t hpw, uint32_t o0, uint32_t o1,
                                int64_t row0) {
   typedef Codec<KVD> C;
   typedef typename C::Vec Vec;
   constexpr bool FP8 = KVD == SCHED_PD_FP8_E4M3;
-  const uint32_t d = P.d, q = d / 4, nn = o1 - o0, per_head = nn * q, total = hpw * per_head;
+  static_assert(W == 4 || (W == 8 && kBatch % 2 == 0), "chunk width");
+  constexpr uint32_t NB = kBatch * 4 / W; // chunks per lane and tensor
+  const uint32_t d = P.d, q = d / W, nn = o1 - o0, per_head = nn * q, total = hpw * per_head;
   const bool vdm = P.vds != 1;
   const uint32_t row_len = d + 1;
   // fp8: lanes [0, hpw) own the K scales of the group, [hpw, 2 hpw) the V
@@ -470,24 +527,24 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     slot = (threadIdx.x < hpw ? P.k_scale : P.v_scale) + page * P.Hkv + h0 + threadIdx.x % hpw;
     s_old = *slot;
   }
-  float xk[kBatch][4], xv[kBatch][4];
-  uint32_t hh[kBatch], t[kBatch], j[kBatch];
+  float xk[NB][W], xv[NB][W];
+  uint32_t hh[NB], t[NB], j[NB];
 #pragma unroll
-  for (uint32_t u = 0; u < kBatch; ++u) {
+  for (uint32_t u = 0; u < NB; ++u) {
     const uint32_t c = u * kBlock + threadIdx.x;
     hh[u] = hpw - 1; // lanes past the end add 0 to the last head
     t[u] = j[u] = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < W; ++i)
       xk[u][i] = xv[u][i] = 0.f;
     if (c < total) {
       hh[u] = c / per_head;
       const uint32_t rem = c - hh[u] * per_head;
       t[u] = rem / q;
-      j[u] = (rem - t[u] * q) * 4;
+      j[u] = (rem - t[u] * q) * W;
       const int64_t s = (row0 + t[u]) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j[u];
-      load_src4<SRC_F32>(P.k_src, s, xk[u]);
-      load_src4<SRC_F32>(P.v_src, s, xv[u]);
+      load_chunk<SRC_F32, W>(P.k_src, s, xk[u]);
+      load_chunk<SRC_F32, W>(P.v_src, s, xv[u]);
     }
   }
   __syncthreads(); // the stage and S are free: the previous page is written
@@ -496,11 +553,11 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
   if (vdm) {
     // d-major V: stage the appended rows for the slot-group writes below
 #pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
+    for (uint32_t u = 0; u < NB; ++u) {
       if (u * kBlock + threadIdx.x < total) {
         float *row = stage + (hh[u] * nn + t[u]) * row_len + j[u];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < W; ++i)
           row[i] = xv[u][i];
       }
     }
@@ -512,7 +569,7 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     float mk = 0.f, mv = 0.f;
     uint32_t h_run = hh[0];
 #pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
+    for (uint32_t u = 0; u < NB; ++u) {
       if (u > 0 && __builtin_amdgcn_ballot_w64(hh[u] != h_run) != 0) {
         lds_max(S.amax[0], h_run, mk, wide);
         lds_max(S.amax[1], h_run, mv, wide);
@@ -520,7 +577,7 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
         h_run = hh[u];
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < W; ++i) {
         mk = fmaxf(mk, fabsf(xk[u][i]));
         mv = fmaxf(mv, fabsf(xv[u][i]));
       }
@@ -538,12 +595,11 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
   // K: token rows
   PoolElem<KVD> *kpool = static_cast<PoolElem<KVD> *>(P.k_pool) + page * P.kps;
 #pragma unroll
-  for (uint32_t u = 0; u < kBatch; ++u) {
-    if (u * kBlock + threadIdx.x < total) {
-      Vec *dst = reinterpret_cast<Vec *>(kpool + (int64_t)(h0 + hh[u]) * P.khs +
-                                         (int64_t)(o0 + t[u]) * P.kts + j[u]);
-      *dst = C::enc(xk[u], FP8 ? S.inv[0][hh[u]] : 0.f);
-    }
+  for (uint32_t u = 0; u < NB; ++u) {
+    if (u * kBlock + threadIdx.x < total)
+      store_chunk<KVD, W>(kpool + (int64_t)(h0 + hh[u]) * P.khs + (int64_t)(o0 + t[u]) * P.kts +
+                              j[u],
+                          xk[u], FP8 ? S.inv[0][hh[u]] : 0.f);
   }
   if (FP8 && S.any_regrow[0])
     regrow_rows<KVD>(P, S, 0, kpool, P.khs, P.kts, h0, hpw, o0);
@@ -552,12 +608,11 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
   if (!vdm) {
     // token-major V: as K
 #pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
-      if (u * kBlock + threadIdx.x < total) {
-        Vec *dst = reinterpret_cast<Vec *>(vpool + (int64_t)(h0 + hh[u]) * P.vhs +
-                                           (int64_t)(o0 + t[u]) * P.vts + j[u]);
-        *dst = C::enc(xv[u], FP8 ? S.inv[1][hh[u]] : 0.f);
-      }
+    for (uint32_t u = 0; u < NB; ++u) {
+      if (u * kBlock + threadIdx.x < total)
+        store_chunk<KVD, W>(vpool + (int64_t)(h0 + hh[u]) * P.vhs + (int64_t)(o0 + t[u]) * P.vts +
+                                j[u],
+                            xv[u], FP8 ? S.inv[1][hh[u]] : 0.f);
     }
     if (FP8 && S.any_regrow[1])
       regrow_rows<KVD>(P, S, 1, vpool, P.vhs, P.vts, h0, hpw, o0);
@@ -634,7 +689,11 @@ __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
     }
     const int64_t row0 = a0 + (pbase + o0 - pos0);
     if ((uint64_t)hpw * (o1 - o0) * (P.d / 4) <= kFastChunks) {
-      page_one_round<SRC_F32, KVD>(P, S, stage, page, h0, hpw, o0, o1, row0);
+      if (kBatch % 2 == 0 && P.w8)
+        page_one_round<SRC_F32, KVD, (kBatch % 2 == 0 ? 8 : 4)>(P, S, stage, page, h0, hpw, o0,
+                                                                o1, row0);
+      else
+        page_one_round<SRC_F32, KVD, 4>(P, S, stage, page, h0, hpw, o0, o1, row0);
       continue;
     }
     if (KVD == SCHED_PD_FP8_E4M3)
@@ -661,6 +720,8 @@ uint32_t esize(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF
 bool aligned(const void *p, uint32_t bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 bool mult4(int64_t s) { return s % 4 == 0; }
+
+bool mult8(int64_t s) { return s % 8 == 0; }
 
 } // namespace
 
@@ -756,6 +817,13 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
                          "and be <= %u", hpw, a->num_kv_heads, kMaxGroup);
   }
   P.hpw = hpw;
+  // 8-element chunks (16-byte bf16 source loads) when every row the
+  // one-round path touches starts on an 8-element boundary
+  P.w8 = a->head_dim % 8 == 0 && mult8(a->src_tok_stride) && mult8(a->src_head_stride) &&
+         mult8(a->k_page_stride) && mult8(a->k_head_stride) && mult8(a->k_tok_stride) &&
+         mult8(a->v_page_stride) && mult8(a->v_head_stride) && (vdm || mult8(a->v_tok_stride)) &&
+         aligned(a->k_src, 8 * se) && aligned(a->v_src, 8 * se) && aligned(a->k_pool, 8 * ke) &&
+         aligned(a->v_pool, 8 * ke);
   uint64_t gy = (uint64_t)(max_app + a->page_size - 1) / a->page_size + 1;
   if (gy > 65535)
     gy = 65535;

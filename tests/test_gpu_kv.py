@@ -64,7 +64,9 @@ def assert_same(got, ref):
 @pytest.mark.parametrize("csr", [False, True])
 @pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
 def test_append_is_bit_exact_with_the_oracle(kv, v_layout, csr, src):
-    for seed, (hkv, d) in enumerate([(8, 128), (4, 64), (2, 32)]):
+    # d = 20 (a multiple of 4, not of 8) runs the 4-element chunk path, the
+    # others the 8-element one
+    for seed, (hkv, d) in enumerate([(8, 128), (4, 64), (2, 32), (3, 20)]):
         print(f"case kv={kv} v={v_layout} csr={csr} src={src} hkv={hkv} d={d}", flush=True)
         c = append_case(100 + seed, kv, v_layout, csr, hkv=hkv, d=d, src_dtype=src)
         assert_same(run_gpu(c), c["out"])
