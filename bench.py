@@ -241,15 +241,26 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     sched_pd.launch(A["wq_tiles"], stream)
     torch.cuda.synchronize()
     cyc = p_tile.read_timer()[:ntask].numpy()
-    # closed loop: pi over tiles by the measured per-task cost, longest first
-    p_tile.install_order(sched_pd.tile_order_by_task_key(tiles, cyc.astype(np.float64)), nt)
-    p_tile.push()
-    res["wq_tiles_lpt_timer"] = round(_makespan_us(torch, sched_pd, A["wq_tiles"], stream), 2)
+    # closed loop: pi over tiles by the measured per-task cost, longest first,
+    # on tiles of twice the size (with the heaviest work first the tail is
+    # short items anyway, and fewer items cost less start-up)
+    tp2 = 2 * tile_pages
+    tiles2 = sched_pd.plan_tiles(b["ctx_lens"], 16, tp2, 8)
+    nt2 = tiles2.shape[0]
+    p_lpt = SchedPlane(max_tasks=max(nt2, ntask))
+    p_lpt.install_order(sched_pd.tile_order_by_task_key(tiles2, cyc.astype(np.float64)), nt2)
+    p_lpt.set_num_tasks(nt2)
+    p_lpt.push()
+    p_lpt.reset_queue(W)
+    a_lpt = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                plane=p_lpt, workers=W, tiles=tiles2, tile_pages=tp2, **common)
+    res["wq_tiles_lpt_timer"] = round(_makespan_us(torch, sched_pd, a_lpt, stream), 2)
     kv = b["kv_bytes"]
     return {
         "static_us": res["static_task"], "ticket_wq_us": res["wq_tiles"],
         "cut_pct": round(100.0 * (res["static_task"] - res["wq_tiles"]) / res["static_task"], 2),
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
+        "lpt_tile_pages": tp2,
         "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
         "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                              "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())},
@@ -261,7 +272,10 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     armed (q ~ U(0,1), lambda_bw 0.5, H 0.1: urgent tasks stream 4 pages
     ahead). Online softmax (score -> -inf) and linear contraction (value -> 0)
     variants; pages past the budget skipped (default) or loaded and masked
-    (the reference weave's behaviour). Work queue over split tiles."""
+    (the reference weave's behaviour). Work queue over split tiles, pi by
+    urgency; then the skip variants with pi = longest-first over tiles of
+    twice the size by the pages each reads (known on the host from ctx and
+    tau)."""
     import numpy as np
     import sched_abi as abi
     b = workloads.workload("llama3_8b_shed", seed=0)
@@ -296,6 +310,26 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
         loaded = (full if "loads" in name else kept) * vb
         res[name] = {"us": round(us, 2), "gbs_loaded": round(loaded / us / 1e3, 1),
                      "gbs_ctx_equiv": round(full * vb / us / 1e3, 1)}
+    tp2 = 2 * tile_pages
+    tiles2 = sched_pd.plan_tiles(ctx, 16, tp2, 8)
+    nt2 = tiles2.shape[0]
+    plane2 = SchedPlane(max_tasks=max(nt2, ntask))
+    plane2.set_lambda(0.5)
+    plane2.set_rows(q=b["urgency"], tau=b["tau"], n=ntask)
+    pages = sched_pd.tile_pages_loaded(tiles2, ctx, 16, tp2, 8, tau=b["tau"])
+    plane2.install_order(sched_pd.tile_order_lpt(pages), nt2)
+    plane2.set_num_tasks(nt2)
+    plane2.push()
+    plane2.reset_queue(W)
+    res["lpt_tile_pages"] = tp2
+    for name, kw, o, vb in (("softmax_skip_lpt", {}, out, 1.0),
+                            ("linear_skip_lpt", {"mode": abi.LINEAR, "lin_w": w}, lout, 0.5)):
+        a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                out=o, plane=plane2, workers=W, tiles=tiles2, tile_pages=tp2,
+                                policy=(1.0, 1.0, 0.1), **kw)
+        us = _makespan_us(torch, sched_pd, a, stream)
+        res[name] = {"us": round(us, 2), "gbs_loaded": round(kept * vb / us / 1e3, 1),
+                     "gbs_ctx_equiv": round(full * vb / us / 1e3, 1)}
     return res
 
 
@@ -303,7 +337,8 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
     """Qwen2-7B shape (Hq 28 / Hkv 4), fp8-e4m3fn KV with per-(page, head)
     scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
     max 16384); ticket work queue over split tiles, timer on; then the same
-    queue with pi over tiles by the timer's per-task cycles, longest first."""
+    queue with pi over tiles (twice the size) by the timer's per-task cycles,
+    longest first."""
     import numpy as np
     b = workloads.workload("qwen2_7b_fp8", seed=0)
     R, ntask = 512, 512 * 4
@@ -329,15 +364,25 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
     sched_pd.launch(a_wq, stream)
     torch.cuda.synchronize()
     cyc = plane.read_timer()[:ntask].numpy()
-    # closed loop: pi over tiles by the measured per-task cost, longest first
-    plane.install_order(sched_pd.tile_order_by_task_key(tiles, cyc.astype(np.float64)), nt)
-    plane.push()
-    us_lpt = _makespan_us(torch, sched_pd, a_wq, stream)
+    # closed loop: pi over tiles (twice the size) by the measured per-task
+    # cost, longest first
+    tp2 = 2 * tile_pages
+    tiles2 = sched_pd.plan_tiles(ctx, 16, tp2, 4)
+    nt2 = tiles2.shape[0]
+    plane3 = SchedPlane(max_tasks=max(nt2, ntask))
+    plane3.install_order(sched_pd.tile_order_by_task_key(tiles2, cyc.astype(np.float64)), nt2)
+    plane3.set_num_tasks(nt2)
+    plane3.push()
+    plane3.reset_queue(W)
+    a_lpt = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane3,
+                                workers=W, tiles=tiles2, tile_pages=tp2)
+    us_lpt = _makespan_us(torch, sched_pd, a_lpt, stream)
     kv = b["kv_bytes"]
     return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
             "wq_tiles_lpt_timer_us": round(us_lpt, 2),
             "gbs": round(kv / us_wq / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
-            "tiles": nt, "tile_pages": tile_pages, "workers": W,
+            "tiles": nt, "tile_pages": tile_pages, "lpt_tile_pages": tp2, "workers": W,
             "max_ctx": int(ctx.max()),
             "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                                  "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())}}

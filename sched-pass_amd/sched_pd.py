@@ -217,6 +217,31 @@ def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.T
     return torch.tensor(order, dtype=torch.int32)
 
 
+def tile_pages_loaded(tiles: torch.Tensor, ctx_lens, page_size: int, tile_pages: int,
+                      num_kv_heads: int, tau=None, tau_scope: int = abi.TAU_PREFIX) -> np.ndarray:
+    """Pages each work item of a plan_tiles() plan reads when shed pages are
+    skipped: task t reads ceil(n_t / page_size) pages, n_t = ctx, or
+    min(ctx, tau_t) under a prefix budget (tau_t = 0: no cap; the per-page
+    scope reads every page). Chunk c holds the pages of [c*tile_pages,
+    (c+1)*tile_pages) among them (0 for a chunk wholly past the budget)."""
+    t = tiles.cpu().numpy() if isinstance(tiles, torch.Tensor) else np.asarray(tiles)
+    ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
+                     dtype=np.int64)
+    n = np.repeat(ctx, num_kv_heads)
+    if tau is not None and tau_scope == abi.TAU_PREFIX:
+        tau = np.asarray(tau, dtype=np.int64)[:n.size]
+        n = np.where(tau > 0, np.minimum(n, tau), n)
+    pages = (n + page_size - 1) // page_size
+    return np.clip(pages[t[:, 0]] - t[:, 1].astype(np.int64) * tile_pages, 0, tile_pages)
+
+
+def tile_order_lpt(cost) -> torch.Tensor:
+    """pi over work items, heaviest first (ties keep index order): the
+    longest-processing-time list order for the ticket queue."""
+    c = np.asarray(cost, dtype=np.float64)
+    return torch.tensor(np.argsort(-c, kind="stable"), dtype=torch.int32)
+
+
 def launch(args: abi.SchedDecodeArgs, stream=None) -> None:
     """Launch one decode step described by `args` on `stream` (default: the
     current torch stream). Raises RuntimeError with the library's message."""

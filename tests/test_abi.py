@@ -182,6 +182,28 @@ def test_plan_tiles_is_task_major():
     assert o[:4].tolist() == [10, 11, 12, 13] and o[-1] == 0
 
 
+def test_tile_pages_loaded_and_lpt_order():
+    import numpy as np
+    import sched_abi as abi
+    import sched_pd
+    t = sched_pd.plan_tiles([0, 16, 17, 100], 16, 2, 2, device="cpu").numpy()
+    # without a budget: 0, 1, 2, 7 pages per request -> chunks of at most 2
+    got = sched_pd.tile_pages_loaded(t, [0, 16, 17, 100], 16, 2, 2)
+    assert got.tolist() == [0, 0, 1, 1, 2, 2, 2, 2, 2, 1, 2, 2, 2, 1]
+    # prefix budget on request 3's tasks (6 and 7): 33 tokens -> 3 pages,
+    # 0 (no cap) and 5 tokens -> 1 page; per-page scope reads every page
+    tau = np.array([0, 0, 0, 0, 0, 0, 33, 5])
+    got = sched_pd.tile_pages_loaded(t, [0, 16, 17, 100], 16, 2, 2, tau=tau)
+    assert got[6:].tolist() == [2, 1, 0, 0, 1, 0, 0, 0]
+    per_page = sched_pd.tile_pages_loaded(t, [0, 16, 17, 100], 16, 2, 2, tau=tau,
+                                          tau_scope=abi.TAU_PER_PAGE)
+    assert per_page[6:].tolist() == [2, 2, 2, 1, 2, 2, 2, 1]
+    o = sched_pd.tile_order_lpt(got).numpy()
+    assert sorted(o.tolist()) == list(range(14))
+    assert all(got[o[i]] >= got[o[i + 1]] for i in range(13))
+    assert o[:3].tolist() == [4, 5, 6]   # ties keep index order
+
+
 def torch_tiles(t):
     import torch
     return torch.from_numpy(t)
