@@ -95,6 +95,18 @@ def test_page_size_32_and_64():
         assert_same(run_gpu(c), c["out"])
 
 
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8])
+def test_small_and_odd_page_sizes(kv):
+    """Page sizes 8, 12 and 20 (multiples of 4, not of 16) with a d-major V:
+    appends of 1 to 3 pages + 1 tokens on top of prior tokens, so first and
+    last pages are partial and the 4-slot groups straddle o0 and o1."""
+    for seed, ps in enumerate((8, 12, 20)):
+        print(f"case kv={kv} ps={ps}", flush=True)
+        c = append_case(60 + seed, kv, "dmajor", hkv=4, d=64, ps=ps,
+                        prior=[0, 3, ps - 1, 2 * ps + 5, 7], n=[ps, 1, 2, 3 * ps + 1, 29])
+        assert_same(run_gpu(c), c["out"])
+
+
 def test_errors_are_counted_and_nothing_else_is_written():
     rng = np.random.default_rng(9)
     hkv, d, ps = 2, 8, 8
