@@ -5,13 +5,18 @@
 // One workgroup serves one request and a group of its kv-heads (all of them
 // unless a small append needs more workgroups), over a strided subset of the
 // pages the append touches (grid.y covers the pages of the longest append,
-// so a bulk append runs one page per workgroup). Per page:
+// so a bulk append runs one page per workgroup). A page whose appended
+// elements fit one round (16 per lane and tensor) is written by
+// page_one_round: each lane loads its K and V chunks once (8 or 4 elements
+// each), keeps them in registers through the fp8 amax and stores them, a
+// d-major V going through an LDS stage. Larger pages take two passes:
 //   1. fp8: max |x| of each head's appended K and V slots (LDS atomics, one
 //      per wave when its lanes share a head) -> the new scales;
 //   2. K, then V: one pass over the group's slots in storage order, four
 //      elements per lane along the contiguous dimension (one 4/8/16-byte
-//      store): earlier slots are re-encoded when their head's scale grew
-//      (fp8) or skipped, appended slots are converted from the source.
+//      store).
+// Either way earlier slots are re-encoded when their head's scale grew (fp8)
+// or left as they are, and appended slots are converted from the source.
 // Every address is bounds-checked against the pool, the page table and the
 // source rows; a slot that cannot be written is counted in `errors`.
 #include <hip/hip_runtime.h>
