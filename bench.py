@@ -459,28 +459,47 @@ def profiled_traffic():
 
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
-    2 of the 64 requests of the uniform workload, timed on this host."""
+    the uniform workload's shape (64 requests x 2048 tokens, a pool of just
+    the batch's pages), on all host threads, min of 3 (~10 CPU-seconds);
+    plus one thread on 2 of the requests."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    b = workloads.make_batch(np.full(2, 2048), num_q_heads=32, num_kv_heads=8, seed=3,
-                             device="cuda")
-    host = {k: b[k].cpu() for k in ("q", "k_pool", "v_pool", "block_table", "ctx_lens")}
+
+    def timed(n_req, threads, reps=3):
+        b = workloads.make_batch(np.full(n_req, 2048), num_q_heads=32, num_kv_heads=8, seed=3,
+                                 device="cuda")
+        host = {k: b[k].cpu() for k in ("q", "k_pool", "v_pool", "block_table", "ctx_lens")}
+        del b["k_pool"], b["v_pool"]
+        run = lambda: oracle.decode(host["q"], host["k_pool"], host["v_pool"],  # noqa: E731
+                                    host["block_table"], host["ctx_lens"],
+                                    precision=oracle.F32, threads=threads)
+        run()  # warm
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            run()
+            best = min(best, time.perf_counter() - t0)
+        return b["kv_bytes"], best
+
     threads = len(os.sched_getaffinity(0))
-    oracle.decode(host["q"], host["k_pool"], host["v_pool"], host["block_table"],
-                  host["ctx_lens"], precision=oracle.F32, threads=threads)  # warm
-    best = float("inf")
-    for _ in range(3):
-        t0 = time.perf_counter()
-        oracle.decode(host["q"], host["k_pool"], host["v_pool"], host["block_table"],
-                      host["ctx_lens"], precision=oracle.F32, threads=threads)
-        best = min(best, time.perf_counter() - t0)
-    kv = b["kv_bytes"]
+    kv, best = timed(64, threads)
+    kv1, best1 = timed(2, 1)
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(kv / best / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"2 of 64 requests x 2048 tokens (KV {kv >> 20} MiB), fp32 oracle port "
-                      f"of the reference CPU loop, {threads} OpenMP threads, min of 3: "
-                      f"{best * 1e3:.1f} ms"}
+            "sample": f"the whole 64 x 2048-token step (KV {kv >> 20} MiB), fp32 oracle port of "
+                      f"the reference CPU loop, {threads} OpenMP threads, min of 3: "
+                      f"{best * 1e3:.1f} ms",
+            "single_thread_gbs": round(kv1 / best1 / 1e9, 3),
+            "single_thread_sample": f"2 of the requests (KV {kv1 >> 20} MiB), 1 thread: "
+                                    f"{best1 * 1e3:.1f} ms",
+            "cpu_model": cpu}
 
 
 def main():
