@@ -21,6 +21,12 @@
 //       whole rows (fp8) and trade these 4-token slices across lane rows
 //       with v_permlane16/32_swap (bf16_v_operands, fp8_v_operands).
 //
+// Token-major V (FlashInfer's NHD / HND caches, bf16): a lane loads dims
+// 8*(lane%16)..+7 of tokens 4*(lane/16)..+3 (four 16-byte row pieces), and
+// MFMA row lane%16 of dim block blk stands for dim 8*(lane%16) + blk, so each
+// block's A operand is two v_perm_b32 of the lane's own registers; the state
+// goes to LDS with that dim order undone (bf16_vt_operand, VT).
+//
 // A workgroup of NW waves runs one task = (request, kv-head); wave w streams
 // pages w, w+NW, ... with DEPTH pages of loads in flight (register ring), and
 // the wave states merge in LDS in fixed order. Nothing
@@ -175,6 +181,17 @@ __device__ __forceinline__ void bf16_v_operands(u32x4_t v[4]) {
   }
 }
 
+// Token-major bf16 V: r[v] holds dims 8*c16..+7 of token 4*g4 + v; the A
+// operand of block blk is dim 8*c16 + blk of the four tokens (low or high
+// halves of dword blk/2, paired by v_perm_b32).
+__device__ __forceinline__ s16x4_t bf16_vt_operand(const u32x4_t r[4], int blk) {
+  const unsigned sel = (blk & 1) ? 0x07060302u : 0x05040100u;
+  const int dw = blk >> 1;
+  const unsigned lo = __builtin_amdgcn_perm(r[1][dw], r[0][dw], sel);
+  const unsigned hi = __builtin_amdgcn_perm(r[3][dw], r[2][dw], sel);
+  return __builtin_bit_cast(s16x4_t, u32x2_t{lo, hi});
+}
+
 struct MfmaTask {
   uint32_t r, h, n, budget;
   int64_t row; // block-table index of the request's first page
@@ -183,6 +200,8 @@ struct MfmaTask {
   const uint8_t *kbase; // K pool bytes + per-lane offset
   const uint8_t *vbase;
   int64_t kpage_bytes, khead_bytes, vpage_bytes, vhead_bytes;
+  int64_t vrow_bytes; // token-major V: bytes between token rows
+  uint32_t vlane;     // token-major V: this lane's byte offset in a page
 };
 
 struct MfmaState {
@@ -191,7 +210,7 @@ struct MfmaState {
   bf16x8_t qop[4];
 };
 
-template <bool FP8, bool NT, bool LINEAR>
+template <bool FP8, bool NT, bool LINEAR, bool VT>
 __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, int32_t page,
                                            uint32_t pidx, PageRegs<FP8> &B) {
   if constexpr (LINEAR) {
@@ -212,9 +231,18 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
+    if constexpr (VT) {
+      // uniform row base + the lane's 32-bit offset: one address VGPR
+      const uint8_t *pb = static_cast<const uint8_t *>(P.v_pool) +
+                          (int64_t)page * T.vpage_bytes + T.vhead_bytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      B.v[i] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 1024 * i));
+      for (int i = 0; i < 4; ++i)
+        B.v[i] = gload<NT>(reinterpret_cast<const u32x4_t *>(pb + i * T.vrow_bytes + T.vlane));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        B.v[i] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 1024 * i));
+    }
   } else {
     if constexpr (!LINEAR)
 #pragma unroll
@@ -228,7 +256,7 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
   }
 }
 
-template <bool FP8>
+template <bool FP8, bool VT>
 __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                              uint32_t g4) {
@@ -307,12 +335,15 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       vb[i] = B.v[i];
-    bf16_v_operands(vb);
+    if constexpr (!VT)
+      bf16_v_operands(vb);
   }
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
-    if constexpr (!FP8)
+    if constexpr (VT)
+      a = bf16_vt_operand(vb, blk);
+    else if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
                                                 : u32x2_t{vb[blk >> 1].x, vb[blk >> 1].y});
     else
@@ -324,7 +355,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 // Linear contraction of one page: acc[:, 0] += V^T . w over the page's kept
 // tokens. w enters PV as column 0 of the B operand, split into bf16 hi + lo
 // halves (two MFMAs) so the weights keep ~16 mantissa bits; V is exact.
-template <bool FP8>
+template <bool FP8, bool VT>
 __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T, MfmaState &S,
                                             const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                             uint32_t c16, uint32_t g4) {
@@ -356,12 +387,15 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       vb[i] = B.v[i];
-    bf16_v_operands(vb);
+    if constexpr (!VT)
+      bf16_v_operands(vb);
   }
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
-    if constexpr (!FP8)
+    if constexpr (VT)
+      a = bf16_vt_operand(vb, blk);
+    else if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
                                                 : u32x2_t{vb[blk >> 1].x, vb[blk >> 1].y});
     else
@@ -390,7 +424,7 @@ __device__ __forceinline__ int32_t page_id(const KParams &P, const MfmaTask &T, 
 // waves round-robin, so the assignment (and with it every summation order)
 // depends only on the page index, not on how many pages are read: a task whose
 // shed pages are loaded and masked gives the same bits as one that skips them.
-template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR>
+template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR, bool VT>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
   const uint32_t span = T.p1 - T.p0;
@@ -411,14 +445,14 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   auto pidx_of = [&](int j) { return T.p0 + T.w + NW * (uint32_t)j; };
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s)
-    issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
+    issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
 
   auto compute = [&](int s, int j) {
     const uint32_t pidx = pidx_of(j);
     if constexpr (LINEAR)
-      linear_page<FP8>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
+      linear_page<FP8, VT>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
     else
-      compute_page<FP8>(P, T, S, buf[s], pid[s], pidx, g4);
+      compute_page<FP8, VT>(P, T, S, buf[s], pid[s], pidx, g4);
   };
   int j = 0;
   for (; j + 2 * DEPTH <= npg; j += DEPTH) {
@@ -426,7 +460,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     for (int s = 0; s < DEPTH; ++s) {
       compute(s, j + s);
       pid[s] = idn[s];
-      issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
+      issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
       idn[s] = page_id<NW>(P, T, min(j + 2 * DEPTH + s, last));
     }
   }
@@ -437,15 +471,17 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
         compute(s, j + s);
         if (j + DEPTH + s < npg) {
           pid[s] = idn[s];
-          issue_page<FP8, NT, LINEAR>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
+          issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
         }
       }
     }
   }
 }
 
-template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false>
+template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false,
+          bool VT = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
+  static_assert(!(VT && FP8), "token-major V is bf16 only");
   __shared__ float s_acc[NW][GMAX][128];
   __shared__ float s_m[NW][GMAX];
   __shared__ float s_l[NW][GMAX];
@@ -479,10 +515,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.p1 = R.p1;
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
-    // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16
+    // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16;
+    // token-major bf16: dims 8*c16.. of token 4*g4 (then rows 4*g4 + 1..3)
     T.vbase = static_cast<const uint8_t *>(P.v_pool) +
-              (FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
-                   : (int64_t)(c16 + 16u * (g4 & 1u)) * P.vds * EB + 16u * (g4 >> 1));
+              (VT ? (int64_t)(4u * g4) * P.vts * EB + 16u * c16
+               : FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
+                     : (int64_t)(c16 + 16u * (g4 & 1u)) * P.vds * EB + 16u * (g4 >> 1));
+    T.vrow_bytes = P.vts * EB;
+    T.vlane = (uint32_t)(4u * g4 * (uint32_t)T.vrow_bytes + 16u * c16);
     T.kpage_bytes = P.kps * EB;
     T.khead_bytes = P.khs * EB * T.h;
     T.vpage_bytes = P.vps * EB;
@@ -513,13 +553,13 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
 
     if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
-      stream_pages<FP8, NW, DEPTH_U, false, LINEAR>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT>(P, T, S, lane, g4);
     else if (pol.urgent)
-      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT>(P, T, S, lane, g4);
     else if (pol.polite)
-      stream_pages<FP8, NW, DEPTH_S, true, LINEAR>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT>(P, T, S, lane, g4);
     else
-      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR, VT>(P, T, S, lane, g4);
 
     // Wave states to LDS (l summed over the 4 lane rows first), then the
     // work item's result: output, or partial + fixed-order task merge.
@@ -529,9 +569,18 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
         s_m[w][c16] = S.m;
         s_l[w][c16] = lt;
       }
+      if constexpr (VT) {
+        // row 4*g4 + i of block blk is dim 8*(4*g4 + i) + blk
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk)
-        *reinterpret_cast<f32x4_t *>(&s_acc[w][c16][16 * blk + 4 * g4]) = S.acc[blk];
+        for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            s_acc[w][c16][8 * (4 * g4 + i) + blk] = S.acc[blk][i];
+      } else {
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk)
+          *reinterpret_cast<f32x4_t *>(&s_acc[w][c16][16 * blk + 4 * g4]) = S.acc[blk];
+      }
     }
     __syncthreads();
     finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, chunk, R.nchunks, T.r, T.h, G, s_acc,

@@ -53,17 +53,25 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
 #define SCHED_PD_MFMA_DEPTH_FP8_URGENT 6
 #endif
 
-template <bool FP8> KernelFn mfma_kernel(uint32_t G, bool linear) {
+// Token-major V keeps its row pieces for the in-lane operand build: an urgent
+// ring of 4 pages would need 270 VGPRs (one wave per SIMD); 3 fits in 229.
+#ifndef SCHED_PD_MFMA_DEPTH_VT_URGENT
+#define SCHED_PD_MFMA_DEPTH_VT_URGENT 3
+#endif
+
+template <bool FP8, bool VT = false> KernelFn mfma_kernel(uint32_t G, bool linear) {
   constexpr int NW = SCHED_PD_MFMA_NW;
   constexpr int DS = FP8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH;
-  constexpr int DU = FP8 ? SCHED_PD_MFMA_DEPTH_FP8_URGENT : SCHED_PD_MFMA_DEPTH_URGENT;
+  constexpr int DU = FP8  ? SCHED_PD_MFMA_DEPTH_FP8_URGENT
+                     : VT ? SCHED_PD_MFMA_DEPTH_VT_URGENT
+                          : SCHED_PD_MFMA_DEPTH_URGENT;
   if (linear)
-    return decode_mfma<FP8, NW, 4, DS, DU, true>;
+    return decode_mfma<FP8, NW, 4, DS, DU, true, VT>;
   if (G <= 4)
-    return decode_mfma<FP8, NW, 4, DS, DU>;
+    return decode_mfma<FP8, NW, 4, DS, DU, false, VT>;
   if (G <= 8)
-    return decode_mfma<FP8, NW, 8, DS, DU>;
-  return decode_mfma<FP8, NW, 16, DS, DU>;
+    return decode_mfma<FP8, NW, 8, DS, DU, false, VT>;
+  return decode_mfma<FP8, NW, 16, DS, DU, false, VT>;
 }
 
 uint32_t elem_bytes(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u; }
@@ -91,8 +99,14 @@ WsLayout ws_layout(const SchedDecodeArgs *a) {
   return L;
 }
 
+// V token-major (dims contiguous, 16-byte aligned token rows): bf16 only.
+bool v_token_major(const SchedDecodeArgs *a) {
+  return a->v_dim_stride == 1 && a->v_tok_stride != 1;
+}
+
 // The MFMA kernel's shape: bf16/fp8 KV, d 128, page 16, K rows dims-contiguous,
-// V d-major 16-token rows, bf16 Q, G <= 16, 16-byte aligned pools.
+// V d-major 16-token rows (or, bf16, token-major rows), bf16 Q, G <= 16,
+// 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
     return false;
@@ -105,8 +119,12 @@ bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->head_dim != 128 || a->page_size != 16 || G > 16)
     return false;
   const int64_t eb = elem_bytes(a->kv_dtype);
-  if (a->v_tok_stride != 1 || a->v_dim_stride != 16)
+  if (v_token_major(a)) {
+    if (a->kv_dtype != SCHED_PD_BF16 || (a->v_tok_stride * eb) % 16)
+      return false;
+  } else if (a->v_tok_stride != 1 || a->v_dim_stride != 16) {
     return false;
+  }
   if ((a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 || (a->k_head_stride * eb) % 16)
     return false;
   if ((a->v_page_stride * eb) % 16 || (a->v_head_stride * eb) % 16)
@@ -236,8 +254,9 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->scale_log2 = scale * 1.4426950408889634f;
 
   if (mfma) {
-    sel->fn = a->kv_dtype == SCHED_PD_BF16 ? mfma_kernel<false>(G, linear)
-                                           : mfma_kernel<true>(G, linear);
+    sel->fn = a->kv_dtype != SCHED_PD_BF16 ? mfma_kernel<true>(G, linear)
+              : v_token_major(a)          ? mfma_kernel<false, true>(G, linear)
+                                          : mfma_kernel<false>(G, linear);
     sel->block = SCHED_PD_MFMA_NW * 64;
     sel->mfma = 1;
   } else {

@@ -4,7 +4,8 @@
 Pool layout (HND pages; the MFMA kernel's layout):
     k_pool [num_pages, Hkv, page_size, d]    token rows, dims contiguous
     v_pool [num_pages, Hkv, d, page_size]    d-major ("dmajor", default)
-        or [num_pages, Hkv, page_size, d]    token-major ("tokmajor", VALU only)
+        or [num_pages, Hkv, page_size, d]    token-major ("tokmajor"; MFMA for
+                                             bf16, VALU for fp8)
 Any strides are accepted as long as the innermost listed dim is contiguous;
 they are passed to the kernel in elements.
 

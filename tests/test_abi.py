@@ -111,7 +111,11 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(flags=abi.FLAG_FORCE_VALU)) == 0
     assert kind(schedlib, fake_args(q_dtype=abi.F32)) == 0                # fp32 Q keeps fp32 scores
     assert kind(schedlib, fake_args(kv_dtype=abi.F32, q_dtype=abi.F32)) == 0
-    assert kind(schedlib, fake_args(v_tok_stride=128, v_dim_stride=1)) == 0  # token-major V
+    assert kind(schedlib, fake_args(v_tok_stride=128, v_dim_stride=1)) == 1  # token-major V
+    assert kind(schedlib, fake_args(v_tok_stride=1024, v_dim_stride=1)) == 1  # NHD rows, Hkv 8
+    assert kind(schedlib, fake_args(v_tok_stride=132, v_dim_stride=1)) == 0  # rows not 16-B aligned
+    assert kind(schedlib, fake_args(kv_dtype=abi.FP8_E4M3, v_tok_stride=128,
+                                    v_dim_stride=1)) == 0                    # fp8 token-major V
     assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32)) == 0
     assert kind(schedlib, fake_args(num_q_heads=28, num_kv_heads=4)) == 1   # G = 7
 

@@ -25,8 +25,9 @@ def mixed_err(a, r):
 
 def run(b, plane=None, out_dtype=torch.float32, **kw):
     torch.cuda.synchronize()
+    d = b["v_pool"].shape[3 if kw.get("v_layout", "dmajor") == "tokmajor" else 2]
     out = torch.full((b["ctx_lens"].numel(), b["q"].shape[1] if kw.get("mode", 0) == 0
-                      else b["v_pool"].shape[1], b["v_pool"].shape[2]), float("nan"),
+                      else b["v_pool"].shape[1], d), float("nan"),
                      dtype=out_dtype, device="cuda")
     sched_pd.paged_decode(b["q"], b["k_pool"], b["v_pool"], kw.pop("bt", b["block_table"]),
                           b["ctx_lens"], out=out, k_scale=b["k_scale"], v_scale=b["v_scale"],
@@ -100,6 +101,63 @@ def test_bf16_gqa_parity(ctx, force_valu):
     assert e <= TOL_BF16
     o16 = run(b, flags=flags, out_dtype=torch.bfloat16)
     assert mixed_err(o16.float().cpu(), ref(b)) <= TOL_BF16
+
+
+def token_major(b):
+    """The batch with V stored token-major ([P, Hkv, page, d]), same values."""
+    c = dict(b)
+    c["v_pool"] = b["v_pool"].permute(0, 1, 3, 2).contiguous()
+    return c
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4), (64, 4)])
+def test_token_major_v_matches_dmajor_bitwise(hq, hkv):
+    """bf16 V stored token-major (FlashInfer's HND / NHD rows) takes the MFMA
+    kernel with an in-lane operand build and a permuted dim order in its
+    accumulators; every output element sums the same products in the same
+    order as the d-major kernel, so the bits agree. Then the oracle, the
+    VALU kernel on the same layout, and split tiles under the queue with pi
+    reversed against the static grid."""
+    b = batch([1, 15, 16, 17, 300, 2048, 5000], hq=hq, hkv=hkv, seed=hq + hkv)
+    t = token_major(b)
+    d_out = run(b)
+    t_out = run(t, v_layout="tokmajor")
+    args = sched_pd.build_args(t["q"], t["k_pool"], t["v_pool"], t["block_table"],
+                               t["ctx_lens"], out=t_out, v_layout="tokmajor")
+    assert sched_pd.kernel_kind(args) == "mfma"
+    assert torch.equal(d_out, t_out)
+    e = mixed_err(t_out.cpu(), ref(t, v_layout="tokmajor"))
+    print(f"token-major mfma G={hq // hkv} err {e:.3g}")
+    assert e <= TOL_BF16
+    v = run(t, v_layout="tokmajor", flags=abi.FLAG_FORCE_VALU)
+    assert mixed_err(v.cpu(), ref(t, v_layout="tokmajor")) <= TOL_BF16
+    ctx = t["ctx_lens"].cpu().numpy()
+    tiles = sched_pd.plan_tiles(ctx, 16, 32, hkv)
+    nt = tiles.shape[0]
+    plane = SchedPlane(max_tasks=max(nt, ctx.size * hkv))
+    plane.set_num_tasks(0)
+    plane.push()
+    st = run(t, plane=plane, v_layout="tokmajor", tiles=tiles, tile_pages=32)
+    plane.set_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32))
+    plane.set_num_tasks(nt)
+    plane.push()
+    plane.reset_queue(2 * sched_pd.cu_count())
+    wq = run(t, plane=plane, v_layout="tokmajor", tiles=tiles, tile_pages=32,
+             workers=2 * sched_pd.cu_count())
+    assert torch.equal(st, wq)
+    assert mixed_err(st.cpu(), ref(t, v_layout="tokmajor")) <= TOL_BF16
+
+
+def test_token_major_v_linear_matches_dmajor_bitwise():
+    b = batch([16, 700, 2048, 3], seed=9)
+    t = token_major(b)
+    w = torch.randn(4096, device="cuda")
+    d_out = run(b, mode=abi.LINEAR, lin_w=w)
+    t_out = run(t, mode=abi.LINEAR, lin_w=w, v_layout="tokmajor")
+    assert torch.equal(d_out, t_out)
+    e = mixed_err(t_out.cpu(), ref(t, mode=abi.LINEAR, lin_w=w.cpu().numpy(),
+                                   v_layout="tokmajor"))
+    assert e <= TOL_BF16
 
 
 def test_bf16_output_is_rne_of_fp32_output():

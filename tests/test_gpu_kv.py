@@ -273,8 +273,10 @@ def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
     q = (torch.randn(R, hq, d, device="cuda") / d ** 0.5).bfloat16()
     kview, vview = kv_cache.nhd_views(kv)
     out = torch.empty(R, hq, d, dtype=torch.float32, device="cuda")
-    sched_pd.paged_decode(q, kview, vview, indices, ctx, out=out, page_indptr=indptr,
-                          v_layout="tokmajor")
+    args = sched_pd.build_args(q, kview, vview, indices, ctx, out=out, page_indptr=indptr,
+                               v_layout="tokmajor")
+    assert sched_pd.kernel_kind(args) == "mfma"
+    sched_pd.launch(args)
     torch.cuda.synchronize()
     ref = np.asarray(oracle.decode(q, kview, vview, indices, ctx, page_indptr=indptr,
                                    v_layout="tokmajor"), np.float64)
@@ -296,3 +298,6 @@ def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
     cache.decode(q, list(range(R)), out=out2)
     torch.cuda.synchronize()
     assert err(out2) <= TOL_BF16
+    # same values, same page order per request: the token-major and d-major
+    # MFMA paths give the same bits
+    assert torch.equal(out, out2)
