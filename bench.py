@@ -1,7 +1,7 @@
 """Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
-                    [--sections hetero,shed,fp8,kv]
+                    [--sections hetero,shed,fp8,kv,layouts]
 
 One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
 Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
@@ -41,8 +41,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
-    p.add_argument("--sections", default="hetero,shed,fp8,kv",
-                   help="comma list of the extra measurements: hetero, shed, fp8, kv")
+    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts",
+                   help="comma list of the extra measurements: hetero, shed, fp8, kv, layouts")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--tables", type=int, default=8)
     return p.parse_args()
@@ -457,6 +457,52 @@ def profiled_traffic():
         return None
 
 
+def bench_layouts(torch, sched_pd, workloads, tables=4):
+    """The uniform step's batch (64 x 2048, bf16, Hq 32 / Hkv 8) with V stored
+    token-major: HND pages [P, Hkv, 16, 128] and FlashInfer's NHD cache
+    [P, 2, 16, Hkv, 128] read in place; the same values as the d-major
+    layout, rotating `tables` block tables."""
+    import numpy as np
+    import kv_cache
+    R, T, hkv, hq, d, ps = 64, 2048, 8, 32, 128, 16
+    npg = R * T // ps * tables
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = (torch.randn(R, hq, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    ctx = torch.full((R,), T, dtype=torch.int32, device="cuda")
+    out = torch.empty(R, hq, d, dtype=torch.bfloat16, device="cuda")
+    perm = torch.randperm(npg, device="cuda", generator=g).int()
+    bts = [perm[i * (npg // tables):(i + 1) * (npg // tables)].view(R, T // ps).contiguous()
+           for i in range(tables)]
+    kv_bytes = R * T * hkv * d * 2 * 2
+    stream = torch.cuda.current_stream()
+
+    def measure(k_pool, v_pool, layout):
+        args = [sched_pd.build_args(q, k_pool, v_pool, bt, ctx, out=out, v_layout=layout)
+                for bt in bts]
+        f = lambda i: sched_pd.launch(args[i % tables], stream)  # noqa: E731
+        for i in range(2 * tables):
+            f(i)
+        torch.cuda.synchronize()
+        ms = min(time_region(f, 20, stream) for _ in range(3))
+        return {"us": round(ms * 1e3, 2), "gbs": round(kv_bytes / ms / 1e6, 1),
+                "kernel": sched_pd.kernel_kind(args[0])}
+
+    res = {}
+    kp = (torch.randn(npg, hkv, ps, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    vp = (torch.randn(npg, hkv, ps, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    res["hnd_token_major_v"] = measure(kp, vp, "tokmajor")
+    res["hnd_d_major_v"] = measure(kp, vp.view(npg, hkv, d, ps), "dmajor")
+    del kp, vp
+    torch.cuda.empty_cache()
+    nhd = (torch.randn(npg, 2, ps, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    kview, vview = kv_cache.nhd_views(nhd)
+    res["flashinfer_nhd_in_place"] = measure(kview, vview, "tokmajor")
+    del nhd, kview, vview
+    torch.cuda.empty_cache()
+    res["kv_bytes"] = kv_bytes
+    return res
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
     the uniform workload's shape (64 requests x 2048 tokens, a pool of just
@@ -559,6 +605,8 @@ def main():
         line["shed_policy"] = bench_shed(torch, sched_pd, workloads, SchedPlane, cu)
     if "fp8" in sections:
         line["fp8_qwen2_7b"] = bench_fp8(torch, sched_pd, workloads, SchedPlane, cu)
+    if "layouts" in sections:
+        line["kv_layouts"] = bench_layouts(torch, sched_pd, workloads)
     if "kv" in sections:
         line["kv_append"] = bench_kv_append(torch)
     if not args.no_cpu:
