@@ -27,6 +27,13 @@
 // block's A operand is two v_perm_b32 of the lane's own registers; the state
 // goes to LDS with that dim order undone (bf16_vt_operand, VT).
 //
+// Pages of 32..256 tokens (PG): the kernel streams 16-token blocks; block b
+// is sub-block b % m of table entry b / m (m = page / 16). A d-major V row
+// then holds several blocks, which neighbouring waves read at about the same
+// time: those loads are temporal, so the line one wave fetched is still in
+// L2 for the next. The shed's per-page scope counts the token's offset in its
+// whole page.
+//
 // A workgroup of NW waves runs one task = (request, kv-head); wave w streams
 // pages w, w+NW, ... with DEPTH pages of loads in flight (register ring), and
 // the wave states merge in LDS in fixed order. Nothing
@@ -201,8 +208,20 @@ struct MfmaTask {
   const uint8_t *vbase;
   int64_t kpage_bytes, khead_bytes, vpage_bytes, vhead_bytes;
   int64_t vrow_bytes; // token-major V: bytes between token rows
-  uint32_t vlane;     // token-major V: this lane's byte offset in a page
+  uint32_t vlane;     // token-major V / PG: this lane's V byte offset in a block
+  uint32_t bshift, bmask; // PG: 16-token blocks per page = 1 << bshift
+  int64_t ksub, vsub;     // PG: bytes from one block of a page to the next
+  int64_t vblk;           // PG, d-major V: bytes between the lane's dim blocks
 };
+
+// Offset of pidx's first token within its page (PG), else 0.
+template <bool PG>
+__device__ __forceinline__ uint32_t block_in_page(const MfmaTask &T, uint32_t pidx) {
+  if constexpr (PG)
+    return (pidx & T.bmask) * 16u;
+  else
+    return 0u;
+}
 
 struct MfmaState {
   float m, lsum;
@@ -210,7 +229,7 @@ struct MfmaState {
   bf16x8_t qop[4];
 };
 
-template <bool FP8, bool NT, bool LINEAR, bool VT>
+template <bool FP8, bool NT, bool LINEAR, bool VT, bool PG>
 __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, int32_t page,
                                            uint32_t pidx, PageRegs<FP8> &B) {
   if constexpr (LINEAR) {
@@ -224,20 +243,26 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
                     ? P.lin_w[P.lin_w_period ? t % P.lin_w_period : t] : 0.f;
     }
   }
-  const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes;
+  const uint32_t sub = PG ? (pidx & T.bmask) : 0u;
+  const uint8_t *kp = T.kbase + (int64_t)page * T.kpage_bytes + T.khead_bytes +
+                      (PG ? (int64_t)sub * T.ksub : 0);
   const uint8_t *vp = T.vbase + (int64_t)page * T.vpage_bytes + T.vhead_bytes;
+  // PG and token-major V: a uniform block base + the lane's 32-bit offset
+  const uint8_t *pb = static_cast<const uint8_t *>(P.v_pool) + (int64_t)page * T.vpage_bytes +
+                      T.vhead_bytes + (PG ? (int64_t)sub * T.vsub : 0);
   if constexpr (!FP8) {
     if constexpr (!LINEAR)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         B.k[kb] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * kb));
     if constexpr (VT) {
-      // uniform row base + the lane's 32-bit offset: one address VGPR
-      const uint8_t *pb = static_cast<const uint8_t *>(P.v_pool) +
-                          (int64_t)page * T.vpage_bytes + T.vhead_bytes;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         B.v[i] = gload<NT>(reinterpret_cast<const u32x4_t *>(pb + i * T.vrow_bytes + T.vlane));
+    } else if constexpr (PG) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        B.v[i] = gload<false>(reinterpret_cast<const u32x4_t *>(pb + i * T.vblk + T.vlane));
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -251,12 +276,17 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
     const int64_t si = (int64_t)page * P.Hkv + T.h;
     B.ks = (!LINEAR && P.k_scale) ? P.k_scale[si] : 1.f;
     B.vs = P.v_scale ? P.v_scale[si] : 1.f;
-    B.v[0] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp));
-    B.v[1] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 64 * 16));
+    if constexpr (PG) {
+      B.v[0] = gload<false>(reinterpret_cast<const u32x4_t *>(pb + T.vlane));
+      B.v[1] = gload<false>(reinterpret_cast<const u32x4_t *>(pb + T.vblk + T.vlane));
+    } else {
+      B.v[0] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp));
+      B.v[1] = gload<NT>(reinterpret_cast<const u32x4_t *>(vp + 64 * 16));
+    }
   }
 }
 
-template <bool FP8, bool VT>
+template <bool FP8, bool VT, bool PG>
 __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                              uint32_t g4) {
@@ -284,10 +314,10 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   }
 
   // Online softmax over this page (exp2 domain).
-  const uint32_t pos0 = pidx * 16u;
+  const uint32_t pos0 = pidx * 16u, so = block_in_page<PG>(T, pidx);
   const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
-  const bool full = pos0 + 16u <= T.n &&
-                    (T.budget == 0xFFFFFFFFu || (prefix ? pos0 + 16u <= T.budget : T.budget >= 16u));
+  const bool full = pos0 + 16u <= T.n && (T.budget == 0xFFFFFFFFu ||
+                                          (prefix ? pos0 + 16u <= T.budget : so + 16u <= T.budget));
   float s[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v)
@@ -297,7 +327,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
     for (int v = 0; v < 4; ++v) {
       const uint32_t i = 4u * g4 + v; // token in page (page size 16)
       const uint32_t t = pos0 + i;
-      if (!(t < T.n && (prefix ? t : i) < T.budget))
+      if (!(t < T.n && (prefix ? t : so + i) < T.budget))
         s[v] = kNegInf;
     }
   }
@@ -355,20 +385,20 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 // Linear contraction of one page: acc[:, 0] += V^T . w over the page's kept
 // tokens. w enters PV as column 0 of the B operand, split into bf16 hi + lo
 // halves (two MFMAs) so the weights keep ~16 mantissa bits; V is exact.
-template <bool FP8, bool VT>
+template <bool FP8, bool VT, bool PG>
 __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T, MfmaState &S,
                                             const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                             uint32_t c16, uint32_t g4) {
   float vs = 1.f;
   if constexpr (FP8)
     vs = B.vs;
-  const uint32_t pos0 = pidx * 16u;
+  const uint32_t pos0 = pidx * 16u, so = block_in_page<PG>(T, pidx);
   const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
   float wv[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const uint32_t i = 4u * g4 + v, t = pos0 + i;
-    const bool keep = c16 == 0u && t < T.n && (prefix ? t : i) < T.budget;
+    const bool keep = c16 == 0u && t < T.n && (prefix ? t : so + i) < T.budget;
     wv[v] = keep ? B.lw[v] * vs : 0.f;
   }
   u32x2_t hi, lo;
@@ -408,11 +438,14 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
 // Page id of the wave's i-th page (task page p0 + w + NW*i), read through the
 // constant address space so it is a scalar load: it is counted by lgkmcnt, not
 // by the vmcnt of the KV ring, and the ring's waits stay exact.
-template <int NW>
+template <int NW, bool PG>
 __device__ __forceinline__ int32_t page_id(const KParams &P, const MfmaTask &T, int i) {
   typedef const __attribute__((address_space(4))) int32_t cint32;
   const cint32 *bt = (const cint32 *)P.bt;
-  return bt[T.row + T.p0 + T.w + (int64_t)NW * i];
+  if constexpr (PG) // block T.p0 + T.w + NW*i is in table entry block >> bshift
+    return bt[T.row + ((T.p0 + T.w + NW * (uint32_t)i) >> T.bshift)];
+  else
+    return bt[T.row + T.p0 + T.w + (int64_t)NW * i];
 }
 
 // Stream the wave's pages with DEPTH pages of loads in flight. The steady
@@ -424,7 +457,7 @@ __device__ __forceinline__ int32_t page_id(const KParams &P, const MfmaTask &T, 
 // waves round-robin, so the assignment (and with it every summation order)
 // depends only on the page index, not on how many pages are read: a task whose
 // shed pages are loaded and masked gives the same bits as one that skips them.
-template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR, bool VT>
+template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR, bool VT, bool PG>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
   const uint32_t span = T.p1 - T.p0;
@@ -436,8 +469,8 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   int32_t pid[DEPTH], idn[DEPTH];
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s) {
-    pid[s] = page_id<NW>(P, T, min(s, last));
-    idn[s] = page_id<NW>(P, T, min(DEPTH + s, last));
+    pid[s] = page_id<NW, PG>(P, T, min(s, last));
+    idn[s] = page_id<NW, PG>(P, T, min(DEPTH + s, last));
   }
   // Unconditional prologue: a wave with fewer than DEPTH pages re-reads its
   // last page into the unused slots (same lines, L2 hits) so that the loop is
@@ -445,14 +478,14 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   auto pidx_of = [&](int j) { return T.p0 + T.w + NW * (uint32_t)j; };
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s)
-    issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
+    issue_page<FP8, NT, LINEAR, VT, PG>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
 
   auto compute = [&](int s, int j) {
     const uint32_t pidx = pidx_of(j);
     if constexpr (LINEAR)
-      linear_page<FP8, VT>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
+      linear_page<FP8, VT, PG>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
     else
-      compute_page<FP8, VT>(P, T, S, buf[s], pid[s], pidx, g4);
+      compute_page<FP8, VT, PG>(P, T, S, buf[s], pid[s], pidx, g4);
   };
   int j = 0;
   for (; j + 2 * DEPTH <= npg; j += DEPTH) {
@@ -460,8 +493,8 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     for (int s = 0; s < DEPTH; ++s) {
       compute(s, j + s);
       pid[s] = idn[s];
-      issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
-      idn[s] = page_id<NW>(P, T, min(j + 2 * DEPTH + s, last));
+      issue_page<FP8, NT, LINEAR, VT, PG>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
+      idn[s] = page_id<NW, PG>(P, T, min(j + 2 * DEPTH + s, last));
     }
   }
   for (; j < npg; j += DEPTH) {
@@ -471,7 +504,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
         compute(s, j + s);
         if (j + DEPTH + s < npg) {
           pid[s] = idn[s];
-          issue_page<FP8, NT, LINEAR, VT>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
+          issue_page<FP8, NT, LINEAR, VT, PG>(P, T, pid[s], pidx_of(j + DEPTH + s), buf[s]);
         }
       }
     }
@@ -479,7 +512,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
 }
 
 template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false,
-          bool VT = false>
+          bool VT = false, bool PG = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
   static_assert(!(VT && FP8), "token-major V is bf16 only");
   __shared__ float s_acc[NW][GMAX][128];
@@ -508,11 +541,20 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     const TaskPolicy pol = task_policy(P.L, task);
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;
-    const ItemRange R = item_range(P, chunk, T.n, (load_extent(P, T.n, pol.budget) + 15u) / 16u);
+    const uint32_t ext = load_extent(P, T.n, pol.budget);
+    const ItemRange R = item_range(P, chunk, T.n, PG ? (ext + P.ps - 1u) / P.ps : (ext + 15u) / 16u);
     if (!item_ok(P, wi, chunk, R))
       return;
-    T.p0 = R.p0;
-    T.p1 = R.p1;
+    if constexpr (PG) {
+      // pages [p0, p1) of the item as 16-token blocks, up to the last read
+      T.bshift = 31u - __builtin_clz(P.ps >> 4);
+      T.bmask = (1u << T.bshift) - 1u;
+      T.p0 = R.p0 << T.bshift;
+      T.p1 = min(R.p1 << T.bshift, (ext + 15u) / 16u);
+    } else {
+      T.p0 = R.p0;
+      T.p1 = R.p1;
+    }
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
     // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16;
@@ -522,7 +564,13 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
                : FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
                      : (int64_t)(c16 + 16u * (g4 & 1u)) * P.vds * EB + 16u * (g4 >> 1));
     T.vrow_bytes = P.vts * EB;
-    T.vlane = (uint32_t)(4u * g4 * (uint32_t)T.vrow_bytes + 16u * c16);
+    if constexpr (VT)
+      T.vlane = (uint32_t)(4u * g4 * (uint32_t)T.vrow_bytes + 16u * c16);
+    else
+      T.vlane = (uint32_t)(T.vbase - static_cast<const uint8_t *>(P.v_pool));
+    T.ksub = 16 * P.kts * EB;
+    T.vsub = VT ? 16 * P.vts * EB : 16 * (int64_t)EB;
+    T.vblk = FP8 ? 64 * P.vds : 32 * P.vds * EB;
     T.kpage_bytes = P.kps * EB;
     T.khead_bytes = P.khs * EB * T.h;
     T.vpage_bytes = P.vps * EB;
@@ -553,13 +601,13 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
 
     if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
-      stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG>(P, T, S, lane, g4);
     else if (pol.urgent)
-      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT, PG>(P, T, S, lane, g4);
     else if (pol.polite)
-      stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT, PG>(P, T, S, lane, g4);
     else
-      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR, VT>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR, VT, PG>(P, T, S, lane, g4);
 
     // Wave states to LDS (l summed over the 4 lane rows first), then the
     // work item's result: output, or partial + fixed-order task merge.

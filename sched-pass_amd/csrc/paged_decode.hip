@@ -59,19 +59,20 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
 #define SCHED_PD_MFMA_DEPTH_VT_URGENT 3
 #endif
 
-template <bool FP8, bool VT = false> KernelFn mfma_kernel(uint32_t G, bool linear) {
+template <bool FP8, bool VT = false, bool PG = false>
+KernelFn mfma_kernel(uint32_t G, bool linear) {
   constexpr int NW = SCHED_PD_MFMA_NW;
   constexpr int DS = FP8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH;
   constexpr int DU = FP8  ? SCHED_PD_MFMA_DEPTH_FP8_URGENT
                      : VT ? SCHED_PD_MFMA_DEPTH_VT_URGENT
                           : SCHED_PD_MFMA_DEPTH_URGENT;
   if (linear)
-    return decode_mfma<FP8, NW, 4, DS, DU, true, VT>;
+    return decode_mfma<FP8, NW, 4, DS, DU, true, VT, PG>;
   if (G <= 4)
-    return decode_mfma<FP8, NW, 4, DS, DU, false, VT>;
+    return decode_mfma<FP8, NW, 4, DS, DU, false, VT, PG>;
   if (G <= 8)
-    return decode_mfma<FP8, NW, 8, DS, DU, false, VT>;
-  return decode_mfma<FP8, NW, 16, DS, DU, false, VT>;
+    return decode_mfma<FP8, NW, 8, DS, DU, false, VT, PG>;
+  return decode_mfma<FP8, NW, 16, DS, DU, false, VT, PG>;
 }
 
 uint32_t elem_bytes(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u; }
@@ -104,9 +105,9 @@ bool v_token_major(const SchedDecodeArgs *a) {
   return a->v_dim_stride == 1 && a->v_tok_stride != 1;
 }
 
-// The MFMA kernel's shape: bf16/fp8 KV, d 128, page 16, K rows dims-contiguous,
-// V d-major 16-token rows (or, bf16, token-major rows), bf16 Q, G <= 16,
-// 16-byte aligned pools.
+// The MFMA kernel's shape: bf16/fp8 KV, d 128, pages of 16..256 tokens (a power
+// of two), K rows dims-contiguous, V d-major rows of one page (or, bf16,
+// token-major rows), bf16 Q, G <= 16, 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
     return false;
@@ -116,13 +117,14 @@ bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_FP8_E4M3)
     return false;
   const uint32_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
-  if (a->head_dim != 128 || a->page_size != 16 || G > 16)
+  const uint32_t ps = a->page_size;
+  if (a->head_dim != 128 || ps < 16 || ps > 256 || (ps & (ps - 1)) || G > 16)
     return false;
   const int64_t eb = elem_bytes(a->kv_dtype);
   if (v_token_major(a)) {
     if (a->kv_dtype != SCHED_PD_BF16 || (a->v_tok_stride * eb) % 16)
       return false;
-  } else if (a->v_tok_stride != 1 || a->v_dim_stride != 16) {
+  } else if (a->v_tok_stride != 1 || a->v_dim_stride != (int64_t)ps) {
     return false;
   }
   if ((a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 || (a->k_head_stride * eb) % 16)
@@ -254,9 +256,14 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->scale_log2 = scale * 1.4426950408889634f;
 
   if (mfma) {
-    sel->fn = a->kv_dtype != SCHED_PD_BF16 ? mfma_kernel<true>(G, linear)
-              : v_token_major(a)          ? mfma_kernel<false, true>(G, linear)
-                                          : mfma_kernel<false>(G, linear);
+    const bool pg = a->page_size > 16;
+    if (a->kv_dtype != SCHED_PD_BF16)
+      sel->fn = pg ? mfma_kernel<true, false, true>(G, linear) : mfma_kernel<true>(G, linear);
+    else if (v_token_major(a))
+      sel->fn = pg ? mfma_kernel<false, true, true>(G, linear)
+                   : mfma_kernel<false, true>(G, linear);
+    else
+      sel->fn = pg ? mfma_kernel<false, false, true>(G, linear) : mfma_kernel<false>(G, linear);
     sel->block = SCHED_PD_MFMA_NW * 64;
     sel->mfma = 1;
   } else {

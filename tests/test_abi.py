@@ -116,7 +116,10 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(v_tok_stride=132, v_dim_stride=1)) == 0  # rows not 16-B aligned
     assert kind(schedlib, fake_args(kv_dtype=abi.FP8_E4M3, v_tok_stride=128,
                                     v_dim_stride=1)) == 0                    # fp8 token-major V
-    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32)) == 0
+    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32)) == 1  # 2 blocks per page
+    assert kind(schedlib, fake_args(page_size=256, v_dim_stride=256)) == 1
+    assert kind(schedlib, fake_args(page_size=48, v_dim_stride=48)) == 0  # not a power of two
+    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=16)) == 0  # V rows not one page
     assert kind(schedlib, fake_args(num_q_heads=28, num_kv_heads=4)) == 1   # G = 7
 
 

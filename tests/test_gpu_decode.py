@@ -160,6 +160,78 @@ def test_token_major_v_linear_matches_dmajor_bitwise():
     assert e <= TOL_BF16
 
 
+PG_CTX = [1, 15, 16, 17, 33, 100, 511, 5000]
+
+
+@pytest.mark.parametrize("ps", [32, 64, 256])
+@pytest.mark.parametrize("kvt,layout", [(torch.bfloat16, "dmajor"),
+                                        (torch.float8_e4m3fn, "dmajor"),
+                                        (torch.bfloat16, "tokmajor")])
+def test_pages_of_more_than_16_tokens(ps, kvt, layout):
+    """Pages of 32..256 tokens run on the MFMA kernel as 16-token blocks
+    (block b is sub-block b % m of table entry b / m): oracle parity for
+    GQA 4 and 7, and pi reversed under the queue over split tiles (in pages)
+    against the static grid over the same tiles."""
+    for hq, hkv in ((32, 8), (28, 4)):
+        b = workloads.make_batch(np.asarray(PG_CTX), num_q_heads=hq, num_kv_heads=hkv,
+                                 page_size=ps, kv_dtype=kvt, seed=ps + hq, device="cuda")
+        if layout == "tokmajor":
+            b = token_major(b)
+        out = run(b, v_layout=layout)
+        args = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                   b["ctx_lens"], out=out, v_layout=layout,
+                                   k_scale=b["k_scale"], v_scale=b["v_scale"])
+        assert sched_pd.kernel_kind(args) == "mfma"
+        e = mixed_err(out.cpu(), ref(b, v_layout=layout))
+        print(f"page {ps} {kvt} {layout} G={hq // hkv} err {e:.3g}", flush=True)
+        assert e <= TOL_BF16
+    ctx = b["ctx_lens"].cpu().numpy()
+    tp = 2
+    tiles = sched_pd.plan_tiles(ctx, ps, tp, hkv)
+    nt = tiles.shape[0]
+    plane = SchedPlane(max_tasks=max(nt, ctx.size * hkv))
+    plane.set_num_tasks(0)
+    plane.push()
+    st = run(b, plane=plane, v_layout=layout, tiles=tiles, tile_pages=tp)
+    plane.set_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32))
+    plane.set_num_tasks(nt)
+    plane.push()
+    plane.reset_queue(2 * sched_pd.cu_count())
+    wq = run(b, plane=plane, v_layout=layout, tiles=tiles, tile_pages=tp,
+             workers=2 * sched_pd.cu_count())
+    assert torch.equal(st, wq)
+    assert mixed_err(st.cpu(), ref(b, v_layout=layout)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("scope", [abi.TAU_PREFIX, abi.TAU_PER_PAGE])
+def test_pages_of_32_tokens_shed_and_linear(scope):
+    """Shed on 32-token pages: the per-page scope counts the offset in the
+    whole page (not the 16-token block); skipping and load + mask agree
+    bitwise; the linear contraction over the same pages."""
+    rng = np.random.default_rng(8)
+    ctx = rng.integers(300, 3000, size=5)
+    b = workloads.make_batch(ctx, num_q_heads=32, num_kv_heads=8, page_size=32, seed=12,
+                             device="cuda")
+    n = ctx.size * 8
+    plane = SchedPlane(max_tasks=n)
+    if scope == abi.TAU_PREFIX:
+        tau = np.repeat([rng.integers(-(-c // 4), c + 1) for c in ctx], 8)
+    else:
+        tau = rng.integers(1, 33, size=n)   # in-page budgets, both blocks of a page
+    plane.set_rows(tau=tau, n=n)
+    plane.push()
+    s = run(b, plane=plane, tau_scope=scope)
+    e = mixed_err(s.cpu(), ref(b, plane, tau_scope=scope))
+    print(f"page 32 shed scope {scope} err {e:.3g}", flush=True)
+    assert e <= TOL_BF16
+    assert torch.equal(run(b, plane=plane, tau_scope=scope, flags=abi.FLAG_SHED_LOADS), s)
+    w = torch.randn(4096, device="cuda")
+    lo = run(b, plane=plane, mode=abi.LINEAR, lin_w=w, tau_scope=scope)
+    e = mixed_err(lo.cpu(), ref(b, plane, mode=abi.LINEAR, lin_w=w.cpu().numpy(),
+                                tau_scope=scope))
+    assert e <= TOL_BF16
+
+
 def test_bf16_output_is_rne_of_fp32_output():
     b = batch([300, 2048, 17], seed=3)
     f = run(b)
