@@ -457,6 +457,18 @@ def profiled_traffic():
         return None
 
 
+def profiled_mfma_busy():
+    """MFMA busy % of the C2 decode kernel from the committed counter summary
+    (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "decode_mfma_busy.md")
+    try:
+        m = re.search(r"^mfma_busy_pct_c2: ([0-9.]+)$", open(path).read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def bench_layouts(torch, sched_pd, workloads, tables=4):
     """The uniform step's batch (64 x 2048, bf16, Hq 32 / Hkv 8) with V stored
     token-major: HND pages [P, Hkv, 16, 128] and FlashInfer's NHD cache
@@ -598,6 +610,7 @@ def main():
                      "frac_of_random_page_ceiling": round(kern_gbs / u["random_page_ceiling_gbs"], 4)},
     }
     line["roofline"]["traffic"] = profiled_traffic()
+    line["roofline"]["mfma_busy_pct"] = profiled_mfma_busy()
     sections = set() if args.no_hetero else set(x for x in args.sections.split(",") if x)
     if "hetero" in sections:
         line["hetero_makespan"] = bench_hetero(torch, sched_pd, workloads, SchedPlane, cu)
