@@ -136,6 +136,7 @@ bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
 #define SCHED_PD_F32 0u
 #define SCHED_PD_BF16 1u
 #define SCHED_PD_FP8_E4M3 2u /* OCP e4m3fn, per-(page, kv-head) fp32 scales */
+#define SCHED_PD_F16 3u      /* IEEE binary16 (FlashInfer's fp16 caches, Q, output) */
 
 /* tau scope: prefix = the first tau tokens of the request; per_page = the first
  * tau tokens of every page, the counter of the reference fixtures' woven
@@ -161,9 +162,9 @@ bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
 typedef struct SchedDecodeArgs {
   uint32_t abi_version; /* SCHED_PD_ABI_VERSION */
   uint32_t mode;
-  uint32_t kv_dtype;
-  uint32_t q_dtype;     /* F32 or BF16 (softmax mode) */
-  uint32_t o_dtype;     /* F32 or BF16 */
+  uint32_t kv_dtype;    /* F32, BF16, F16 or FP8_E4M3 */
+  uint32_t q_dtype;     /* F32, BF16 or F16 (softmax mode) */
+  uint32_t o_dtype;     /* F32, BF16 or F16 */
   uint32_t num_requests;
   uint32_t num_q_heads;  /* softmax: multiple of num_kv_heads */
   uint32_t num_kv_heads;

@@ -18,9 +18,9 @@
  *     (lib/SchedWeave.cpp:585-614); keep = counter < budget where the counter
  *     is the token position in the request (prefix scope) or within its page
  *     (per-page scope, the reference fixtures' innermost loop IV).
- *   - dequantisation: bf16 (upper half of an IEEE float) and OCP fp8 e4m3fn
- *     (1 sign, 4 exponent bits bias 7, 3 mantissa bits, no inf, S.1111.111 =
- *     NaN) times a per-(page, kv-head) fp32 scale.
+ *   - dequantisation: bf16 (upper half of an IEEE float), IEEE binary16, and
+ *     OCP fp8 e4m3fn (1 sign, 4 exponent bits bias 7, 3 mantissa bits, no
+ *     inf, S.1111.111 = NaN) times a per-(page, kv-head) fp32 scale.
  *
  * Two precisions:
  *   ORACLE_F64: every product and sum in double -- the checker;
@@ -47,6 +47,20 @@ float oracle_bf16_to_float(uint16_t h) {
   return f;
 }
 
+/* IEEE binary16 decode, from the format definition (1 sign, 5 exponent bits
+ * bias 15, 10 mantissa bits; exponent 0 subnormal, 31 inf / NaN). */
+float oracle_f16_to_float(uint16_t h) {
+  int s = (h >> 15) & 1, e = (h >> 10) & 31, m = h & 1023;
+  float v;
+  if (e == 31)
+    v = m ? NAN : INFINITY;
+  else if (e == 0)
+    v = ldexpf((float)m, -24); /* m/1024 * 2^-14 */
+  else
+    v = ldexpf((float)(1024 + m), e - 25); /* (1+m/1024) * 2^(e-15) */
+  return s ? -v : v;
+}
+
 /* OCP e4m3fn decode, from the format definition. */
 float oracle_fp8_e4m3_to_float(uint8_t b) {
   int s = (b >> 7) & 1, e = (b >> 3) & 15, m = b & 7;
@@ -66,6 +80,8 @@ static double load_elem(const void *base, int64_t idx, uint32_t dtype) {
     return ((const float *)base)[idx];
   case SCHED_PD_BF16:
     return oracle_bf16_to_float(((const uint16_t *)base)[idx]);
+  case SCHED_PD_F16:
+    return oracle_f16_to_float(((const uint16_t *)base)[idx]);
   default:
     return oracle_fp8_e4m3_to_float(((const uint8_t *)base)[idx]);
   }

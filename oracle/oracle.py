@@ -55,6 +55,8 @@ def load():
                                       ctypes.c_int]
         lib.oracle_bf16_to_float.restype = ctypes.c_float
         lib.oracle_bf16_to_float.argtypes = [ctypes.c_uint16]
+        lib.oracle_f16_to_float.restype = ctypes.c_float
+        lib.oracle_f16_to_float.argtypes = [ctypes.c_uint16]
         lib.oracle_fp8_e4m3_to_float.restype = ctypes.c_float
         lib.oracle_fp8_e4m3_to_float.argtypes = [ctypes.c_uint8]
         lib.oracle_max_threads.restype = ctypes.c_int
@@ -88,6 +90,8 @@ def _host(x, dtype=None):
             t = x.detach().cpu().contiguous()
             if t.dtype == torch.bfloat16:
                 return t.view(torch.int16).numpy().view(np.uint16), abi.BF16
+            if t.dtype == torch.float16:
+                return t.view(torch.int16).numpy().view(np.uint16), abi.F16
             if hasattr(torch, "float8_e4m3fn") and t.dtype == torch.float8_e4m3fn:
                 return t.view(torch.uint8).numpy(), abi.FP8_E4M3
             x = t.numpy()
@@ -193,6 +197,8 @@ def _dequant(x):
     a, code = _host(x)
     if code == abi.BF16:
         return bf16_to_float(a).astype(np.float64)
+    if code == abi.F16:
+        return a.view(np.float16).astype(np.float64)
     if code == abi.FP8_E4M3:
         return fp8_e4m3_table()[a].astype(np.float64)
     return a.astype(np.float64)

@@ -27,6 +27,7 @@ struct KParams {
   uint32_t R, Hq, Hkv, G;
   uint32_t ps, bt_stride, tau_scope;
   uint32_t q_f32, o_f32, ctx_in_pages, shed_loads, lin_w_period;
+  uint32_t q_f16, o_f16; // IEEE binary16 Q / output (else bf16 unless *_f32)
   float scale_log2; // softmax scale * log2(e): scores live in the exp2 domain
   // split-KV work items (tiles == nullptr: one work item per task)
   const int32_t *tiles;
@@ -94,13 +95,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 __device__ __forceinline__ void store_out(const KParams &P, int64_t idx, float v) {
   if (P.o_f32)
     static_cast<float *>(P.out)[idx] = v;
+  else if (P.o_f16)
+    static_cast<_Float16 *>(P.out)[idx] = (_Float16)v; // round to nearest even
   else
     static_cast<uint16_t *>(P.out)[idx] = f32_to_bf16_rne(v);
 }
 
 __device__ __forceinline__ float load_q(const KParams &P, int64_t idx) {
-  return P.q_f32 ? static_cast<const float *>(P.q)[idx]
-                 : bf16_bits_to_f32(static_cast<const uint16_t *>(P.q)[idx]);
+  return P.q_f32   ? static_cast<const float *>(P.q)[idx]
+         : P.q_f16 ? (float)static_cast<const _Float16 *>(P.q)[idx]
+                   : bf16_bits_to_f32(static_cast<const uint16_t *>(P.q)[idx]);
 }
 
 } // namespace schedpd

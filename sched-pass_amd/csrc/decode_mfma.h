@@ -113,6 +113,34 @@ __device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
   return __builtin_bit_cast(unsigned, v);
 }
 
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+// Round-to-nearest-even pair conversion to IEEE binary16.
+__device__ __forceinline__ unsigned pack_f16_rne(float lo, float hi) {
+  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(unsigned, v);
+}
+
+// QK and PV MFMAs on 16-bit operands held as raw bits: bf16, or (F16) IEEE
+// binary16 for fp16 caches with fp16 Q.
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma_qk(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma_pv(s16x4_t a, s16x4_t b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                 __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
 // Reductions across the four 16-lane rows with the gfx950 row swaps (VALU,
 // no LDS traffic). v_permlane16_swap(x, x) leaves {x[row], x[row ^ 1]} in its
 // two results on every lane, v_permlane32_swap(x, x) {x[half], x[half ^ 1]};
@@ -286,7 +314,7 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
   }
 }
 
-template <bool FP8, bool VT, bool PG>
+template <bool FP8, bool VT, bool PG, bool F16>
 __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              const PageRegs<FP8> &B, int32_t page, uint32_t pidx,
                                              uint32_t g4) {
@@ -304,7 +332,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
       const u32x4_t packed = {lo.x, lo.y, hi.x, hi.y};
       a = __builtin_bit_cast(bf16x8_t, packed);
     }
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, S.qop[kb], sc, 0, 0, 0);
+    sc = mfma_qk<F16>(a, S.qop[kb], sc);
   }
 
   float kscale = P.scale_log2, vs = 1.f;
@@ -350,6 +378,9 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   if constexpr (FP8) {
     pk.x = pack_bf16_rne(p[0] * vs, p[1] * vs);
     pk.y = pack_bf16_rne(p[2] * vs, p[3] * vs);
+  } else if constexpr (F16) {
+    pk.x = pack_f16_rne(p[0], p[1]);
+    pk.y = pack_f16_rne(p[2], p[3]);
   } else {
     pk.x = pack_bf16_rne(p[0], p[1]);
     pk.y = pack_bf16_rne(p[2], p[3]);
@@ -378,7 +409,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
                                                 : u32x2_t{vb[blk >> 1].x, vb[blk >> 1].y});
     else
       a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
-    S.acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop, S.acc[blk], 0, 0, 0);
+    S.acc[blk] = mfma_pv<F16>(a, pop, S.acc[blk]);
   }
 }
 
@@ -457,7 +488,7 @@ __device__ __forceinline__ int32_t page_id(const KParams &P, const MfmaTask &T, 
 // waves round-robin, so the assignment (and with it every summation order)
 // depends only on the page index, not on how many pages are read: a task whose
 // shed pages are loaded and masked gives the same bits as one that skips them.
-template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR, bool VT, bool PG>
+template <bool FP8, int NW, int DEPTH, bool NT, bool LINEAR, bool VT, bool PG, bool F16>
 __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T, MfmaState &S,
                                              uint32_t lane, uint32_t g4) {
   const uint32_t span = T.p1 - T.p0;
@@ -485,7 +516,7 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
     if constexpr (LINEAR)
       linear_page<FP8, VT, PG>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
     else
-      compute_page<FP8, VT, PG>(P, T, S, buf[s], pid[s], pidx, g4);
+      compute_page<FP8, VT, PG, F16>(P, T, S, buf[s], pid[s], pidx, g4);
   };
   int j = 0;
   for (; j + 2 * DEPTH <= npg; j += DEPTH) {
@@ -512,9 +543,10 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
 }
 
 template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false,
-          bool VT = false, bool PG = false>
+          bool VT = false, bool PG = false, bool F16 = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
-  static_assert(!(VT && FP8), "token-major V is bf16 only");
+  static_assert(!(VT && FP8), "token-major V is 16-bit only");
+  static_assert(!(F16 && (FP8 || LINEAR)), "fp16: softmax over an fp16 cache");
   __shared__ float s_acc[NW][GMAX][128];
   __shared__ float s_m[NW][GMAX];
   __shared__ float s_l[NW][GMAX];
@@ -591,8 +623,12 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
         const uint32_t d0 = qk_dim(FP8, kb, g4);
         if (P.q_f32) {
           const float *qf = static_cast<const float *>(P.q) + qrow + d0;
-          qv = u32x4_t{pack_bf16_rne(qf[0], qf[1]), pack_bf16_rne(qf[2], qf[3]),
-                       pack_bf16_rne(qf[4], qf[5]), pack_bf16_rne(qf[6], qf[7])};
+          if constexpr (F16)
+            qv = u32x4_t{pack_f16_rne(qf[0], qf[1]), pack_f16_rne(qf[2], qf[3]),
+                         pack_f16_rne(qf[4], qf[5]), pack_f16_rne(qf[6], qf[7])};
+          else
+            qv = u32x4_t{pack_bf16_rne(qf[0], qf[1]), pack_bf16_rne(qf[2], qf[3]),
+                         pack_bf16_rne(qf[4], qf[5]), pack_bf16_rne(qf[6], qf[7])};
         } else {
           qv = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(P.q) + qrow + d0);
         }
@@ -601,13 +637,13 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
 
     if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
-      stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.urgent)
-      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT, PG>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.polite)
-      stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT, PG>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else
-      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR, VT, PG>(P, T, S, lane, g4);
+      stream_pages<FP8, NW, DEPTH_S, kStockNT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
 
     // Wave states to LDS (l summed over the 4 lane rows first), then the
     // work item's result: output, or partial + fixed-order task merge.

@@ -1,5 +1,5 @@
 // decode_valu.h -- the general decode kernel on the VALU: any kv dtype
-// (fp32 / bf16 / fp8 e4m3fn), head dim 32/64/128, any page size that is a
+// (fp32 / bf16 / fp16 / fp8 e4m3fn), head dim 32/64/128, any page size that is a
 // multiple of 16, general K/V strides, up to 16 q-heads per kv-head, and the
 // linear-contraction mode. It serves the fp32 configurations (where the
 // score must stay in fp32), the reference's fixture layouts (interleaved
@@ -31,6 +31,7 @@ template <typename KVT> struct Vec16;
 template <> struct Vec16<float> { static constexpr int N = 4; };
 template <> struct Vec16<uint16_t> { static constexpr int N = 8; };
 template <> struct Vec16<uint8_t> { static constexpr int N = 16; };
+template <> struct Vec16<_Float16> { static constexpr int N = 8; };
 
 __device__ __forceinline__ void cvt16(const uint4 &raw, float *f, float) {
   f[0] = __uint_as_float(raw.x);
@@ -46,6 +47,16 @@ __device__ __forceinline__ void cvt16(const uint4 &raw, float *f, uint16_t) {
     f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
   }
 }
+__device__ __forceinline__ void cvt16(const uint4 &raw, float *f, _Float16) {
+  typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const h2 v = __builtin_bit_cast(h2, w[k]);
+    f[2 * k] = (float)v.x;
+    f[2 * k + 1] = (float)v.y;
+  }
+}
 __device__ __forceinline__ void cvt16(const uint4 &raw, float *f, uint8_t) {
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -58,6 +69,7 @@ __device__ __forceinline__ void cvt16(const uint4 &raw, float *f, uint8_t) {
 __device__ __forceinline__ float ldv(const float *p) { return *p; }
 __device__ __forceinline__ float ldv(const uint16_t *p) { return bf16_bits_to_f32(*p); }
 __device__ __forceinline__ float ldv(const uint8_t *p) { return fp8e4m3_to_f32(*p); }
+__device__ __forceinline__ float ldv(const _Float16 *p) { return (float)*p; }
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));

@@ -1,0 +1,98 @@
+// kernel_set.h -- every decode kernel the launcher can select, and the tuning
+// constants of the MFMA ones. paged_decode.hip declares them (extern
+// template); the kernels_*.hip files instantiate them, one group per
+// translation unit so that the library compiles in parallel.
+#pragma once
+
+#include "decode_mfma.h"
+#include "decode_valu.h"
+
+// MFMA kernel shape: waves per workgroup, pages in flight per wave (stock,
+// urgent). Overridable at build time for tuning sweeps.
+#ifndef SCHED_PD_MFMA_NW
+#define SCHED_PD_MFMA_NW 4
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH
+#define SCHED_PD_MFMA_DEPTH 2
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH_URGENT
+#define SCHED_PD_MFMA_DEPTH_URGENT 4
+#endif
+// fp8 pages are half the bytes: twice the pages in flight for the same bytes.
+#ifndef SCHED_PD_MFMA_DEPTH_FP8
+#define SCHED_PD_MFMA_DEPTH_FP8 4
+#endif
+#ifndef SCHED_PD_MFMA_DEPTH_FP8_URGENT
+#define SCHED_PD_MFMA_DEPTH_FP8_URGENT 6
+#endif
+// Token-major V keeps its row pieces for the in-lane operand build: an urgent
+// ring of 4 pages would need 270 VGPRs (one wave per SIMD); 3 fits in 229.
+#ifndef SCHED_PD_MFMA_DEPTH_VT_URGENT
+#define SCHED_PD_MFMA_DEPTH_VT_URGENT 3
+#endif
+
+namespace schedpd {
+
+constexpr int mfma_ds(bool fp8) { return fp8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH; }
+constexpr int mfma_du(bool fp8, bool vt) {
+  return fp8 ? SCHED_PD_MFMA_DEPTH_FP8_URGENT
+         : vt ? SCHED_PD_MFMA_DEPTH_VT_URGENT
+              : SCHED_PD_MFMA_DEPTH_URGENT;
+}
+
+} // namespace schedpd
+
+// One MFMA variant (kv format, V layout, page blocks, fp16): the softmax
+// kernels for up to 4 / 8 / 16 q-heads per kv-head, and (LIN) the linear one.
+#define SCHED_PD_MFMA_ONE(PRE, FP8, GMAX, LIN, VT, PG, F16)                                      \
+  PRE template __global__ void schedpd::decode_mfma<FP8, SCHED_PD_MFMA_NW, GMAX,                 \
+                                                    schedpd::mfma_ds(FP8),                       \
+                                                    schedpd::mfma_du(FP8, VT), LIN, VT, PG, F16>( \
+      schedpd::KParams);
+#define SCHED_PD_MFMA_SOFTMAX(PRE, FP8, VT, PG, F16)                                             \
+  SCHED_PD_MFMA_ONE(PRE, FP8, 4, false, VT, PG, F16)                                             \
+  SCHED_PD_MFMA_ONE(PRE, FP8, 8, false, VT, PG, F16)                                             \
+  SCHED_PD_MFMA_ONE(PRE, FP8, 16, false, VT, PG, F16)
+#define SCHED_PD_MFMA_WITH_LINEAR(PRE, FP8, VT, PG)                                              \
+  SCHED_PD_MFMA_SOFTMAX(PRE, FP8, VT, PG, false)                                                 \
+  SCHED_PD_MFMA_ONE(PRE, FP8, 4, true, VT, PG, false)
+
+// The groups, one per translation unit.
+#define SCHED_PD_MFMA_BF16_PAGE16(PRE)                                                           \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, false, false, false)                                            \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, false, true, false)
+#define SCHED_PD_MFMA_BF16_PAGEBLOCKS(PRE)                                                       \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, false, false, true)                                             \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, false, true, true)
+#define SCHED_PD_MFMA_FP8(PRE)                                                                   \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, true, false, false)                                             \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, true, false, true)
+#define SCHED_PD_MFMA_F16(PRE)                                                                   \
+  SCHED_PD_MFMA_SOFTMAX(PRE, false, false, false, true)                                          \
+  SCHED_PD_MFMA_SOFTMAX(PRE, false, true, false, true)
+
+// VALU kernels: kv element type x head dim, each for 1 / 4 / 16 q-heads per
+// kv-head and the linear mode.
+#define SCHED_PD_VALU_ONE(PRE, KVT, D)                                                           \
+  PRE template __global__ void schedpd::decode_valu<KVT, D, 1, true>(schedpd::KParams);          \
+  PRE template __global__ void schedpd::decode_valu<KVT, D, 1, false>(schedpd::KParams);         \
+  PRE template __global__ void schedpd::decode_valu<KVT, D, 4, false>(schedpd::KParams);         \
+  PRE template __global__ void schedpd::decode_valu<KVT, D, 16, false>(schedpd::KParams);
+#define SCHED_PD_VALU_ALL(PRE)                                                                   \
+  SCHED_PD_VALU_ONE(PRE, float, 32)                                                              \
+  SCHED_PD_VALU_ONE(PRE, float, 64)                                                              \
+  SCHED_PD_VALU_ONE(PRE, float, 128)                                                             \
+  SCHED_PD_VALU_ONE(PRE, uint16_t, 64)                                                           \
+  SCHED_PD_VALU_ONE(PRE, uint16_t, 128)                                                          \
+  SCHED_PD_VALU_ONE(PRE, _Float16, 64)                                                           \
+  SCHED_PD_VALU_ONE(PRE, _Float16, 128)                                                          \
+  SCHED_PD_VALU_ONE(PRE, uint8_t, 64)                                                            \
+  SCHED_PD_VALU_ONE(PRE, uint8_t, 128)
+
+// Declarations for the launcher (paged_decode.hip).
+#define SCHED_PD_DECLARE_ALL_KERNELS                                                             \
+  SCHED_PD_MFMA_BF16_PAGE16(extern)                                                              \
+  SCHED_PD_MFMA_BF16_PAGEBLOCKS(extern)                                                          \
+  SCHED_PD_MFMA_FP8(extern)                                                                      \
+  SCHED_PD_MFMA_F16(extern)                                                                      \
+  SCHED_PD_VALU_ALL(extern)

@@ -1,16 +1,18 @@
-// paged_decode.hip -- kernel instantiations and the C-ABI launchers:
-// sched_paged_decode (one decode step over a paged batch with the levers),
-// its occupancy query, and the reference's launch_paged_softmax /
-// paged_softmax_occupancy (python/kernels/paged_softmax.cu:47-67).
+// paged_decode.hip -- the C-ABI launchers: sched_paged_decode (one decode
+// step over a paged batch with the levers), its occupancy query, and the
+// reference's launch_paged_softmax / paged_softmax_occupancy
+// (python/kernels/paged_softmax.cu:47-67). The kernels are instantiated in
+// kernels_*.hip (kernel_set.h lists them).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdint>
 #include <cstring>
 
-#include "decode_mfma.h"
-#include "decode_valu.h"
+#include "kernel_set.h"
 #include "rt_internal.h"
+
+SCHED_PD_DECLARE_ALL_KERNELS
 
 using namespace schedpd;
 
@@ -34,48 +36,31 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
   return decode_valu<KVT, D, 16, false>;
 }
 
-// MFMA kernel shape: waves per workgroup, pages in flight per wave (stock,
-// urgent). Overridable at build time for tuning sweeps.
-#ifndef SCHED_PD_MFMA_NW
-#define SCHED_PD_MFMA_NW 4
-#endif
-#ifndef SCHED_PD_MFMA_DEPTH
-#define SCHED_PD_MFMA_DEPTH 2
-#endif
-#ifndef SCHED_PD_MFMA_DEPTH_URGENT
-#define SCHED_PD_MFMA_DEPTH_URGENT 4
-#endif
-// fp8 pages are half the bytes: twice the pages in flight for the same bytes.
-#ifndef SCHED_PD_MFMA_DEPTH_FP8
-#define SCHED_PD_MFMA_DEPTH_FP8 4
-#endif
-#ifndef SCHED_PD_MFMA_DEPTH_FP8_URGENT
-#define SCHED_PD_MFMA_DEPTH_FP8_URGENT 6
-#endif
-
-// Token-major V keeps its row pieces for the in-lane operand build: an urgent
-// ring of 4 pages would need 270 VGPRs (one wave per SIMD); 3 fits in 229.
-#ifndef SCHED_PD_MFMA_DEPTH_VT_URGENT
-#define SCHED_PD_MFMA_DEPTH_VT_URGENT 3
-#endif
-
 template <bool FP8, bool VT = false, bool PG = false>
 KernelFn mfma_kernel(uint32_t G, bool linear) {
-  constexpr int NW = SCHED_PD_MFMA_NW;
-  constexpr int DS = FP8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH;
-  constexpr int DU = FP8  ? SCHED_PD_MFMA_DEPTH_FP8_URGENT
-                     : VT ? SCHED_PD_MFMA_DEPTH_VT_URGENT
-                          : SCHED_PD_MFMA_DEPTH_URGENT;
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(FP8), DU = mfma_du(FP8, VT);
   if (linear)
-    return decode_mfma<FP8, NW, 4, DS, DU, true, VT, PG>;
+    return decode_mfma<FP8, NW, 4, DS, DU, true, VT, PG, false>;
   if (G <= 4)
-    return decode_mfma<FP8, NW, 4, DS, DU, false, VT, PG>;
+    return decode_mfma<FP8, NW, 4, DS, DU, false, VT, PG, false>;
   if (G <= 8)
-    return decode_mfma<FP8, NW, 8, DS, DU, false, VT, PG>;
-  return decode_mfma<FP8, NW, 16, DS, DU, false, VT, PG>;
+    return decode_mfma<FP8, NW, 8, DS, DU, false, VT, PG, false>;
+  return decode_mfma<FP8, NW, 16, DS, DU, false, VT, PG, false>;
 }
 
-uint32_t elem_bytes(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u; }
+uint32_t elem_bytes(uint32_t dt) {
+  return dt == SCHED_PD_F32 ? 4u : (dt == SCHED_PD_BF16 || dt == SCHED_PD_F16) ? 2u : 1u;
+}
+
+// fp16 cache with fp16 Q: 16-byte page-16 layouts, softmax mode.
+template <bool VT> KernelFn mfma_kernel_f16(uint32_t G) {
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT);
+  if (G <= 4)
+    return decode_mfma<false, NW, 4, DS, DU, false, VT, false, true>;
+  if (G <= 8)
+    return decode_mfma<false, NW, 8, DS, DU, false, VT, false, true>;
+  return decode_mfma<false, NW, 16, DS, DU, false, VT, false, true>;
+}
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -105,24 +90,30 @@ bool v_token_major(const SchedDecodeArgs *a) {
   return a->v_dim_stride == 1 && a->v_tok_stride != 1;
 }
 
-// The MFMA kernel's shape: bf16/fp8 KV, d 128, pages of 16..256 tokens (a power
-// of two), K rows dims-contiguous, V d-major rows of one page (or, bf16,
-// token-major rows), bf16 Q, G <= 16, 16-byte aligned pools.
+// The MFMA kernel's shape: bf16/fp8 KV with bf16 Q (or fp16 KV with fp16 Q,
+// softmax, page 16), d 128, pages of 16..256 tokens (a power of two), K rows
+// dims-contiguous, V d-major rows of one page (or, 16-bit, token-major rows),
+// G <= 16, 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
     return false;
   const bool linear = a->mode == SCHED_PD_LINEAR;
-  if (!linear && a->q_dtype != SCHED_PD_BF16)
-    return false;
-  if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_FP8_E4M3)
-    return false;
+  if (a->kv_dtype == SCHED_PD_F16) {
+    if (linear || a->q_dtype != SCHED_PD_F16 || a->page_size != 16)
+      return false;
+  } else {
+    if (!linear && a->q_dtype != SCHED_PD_BF16)
+      return false;
+    if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_FP8_E4M3)
+      return false;
+  }
   const uint32_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
   const uint32_t ps = a->page_size;
   if (a->head_dim != 128 || ps < 16 || ps > 256 || (ps & (ps - 1)) || G > 16)
     return false;
   const int64_t eb = elem_bytes(a->kv_dtype);
   if (v_token_major(a)) {
-    if (a->kv_dtype != SCHED_PD_BF16 || (a->v_tok_stride * eb) % 16)
+    if (a->kv_dtype == SCHED_PD_FP8_E4M3 || (a->v_tok_stride * eb) % 16)
       return false;
   } else if (a->v_tok_stride != 1 || a->v_dim_stride != (int64_t)ps) {
     return false;
@@ -145,7 +136,10 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
                      SCHED_PD_ABI_VERSION);
   if (a->mode > SCHED_PD_LINEAR)
     return set_error(hipErrorInvalidValue, "unknown mode %u", a->mode);
-  if (a->kv_dtype > SCHED_PD_FP8_E4M3 || a->q_dtype > SCHED_PD_BF16 || a->o_dtype > SCHED_PD_BF16)
+  auto qo_ok = [](uint32_t dt) {
+    return dt == SCHED_PD_F32 || dt == SCHED_PD_BF16 || dt == SCHED_PD_F16;
+  };
+  if (a->kv_dtype > SCHED_PD_F16 || !qo_ok(a->q_dtype) || !qo_ok(a->o_dtype))
     return set_error(hipErrorInvalidValue, "unsupported dtype (kv %u, q %u, out %u)", a->kv_dtype,
                      a->q_dtype, a->o_dtype);
   if (a->num_kv_heads == 0)
@@ -249,6 +243,8 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->tau_scope = a->tau_scope;
   kp->q_f32 = a->q_dtype == SCHED_PD_F32;
   kp->o_f32 = a->o_dtype == SCHED_PD_F32;
+  kp->q_f16 = a->q_dtype == SCHED_PD_F16;
+  kp->o_f16 = a->o_dtype == SCHED_PD_F16;
   kp->ctx_in_pages = (a->flags & SCHED_PD_FLAG_CTX_IN_PAGES) ? 1u : 0u;
   kp->shed_loads = (a->flags & SCHED_PD_FLAG_SHED_LOADS) ? 1u : 0u;
   kp->lin_w_period = a->lin_w_period;
@@ -257,7 +253,9 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
 
   if (mfma) {
     const bool pg = a->page_size > 16;
-    if (a->kv_dtype != SCHED_PD_BF16)
+    if (a->kv_dtype == SCHED_PD_F16)
+      sel->fn = v_token_major(a) ? mfma_kernel_f16<true>(G) : mfma_kernel_f16<false>(G);
+    else if (a->kv_dtype != SCHED_PD_BF16)
       sel->fn = pg ? mfma_kernel<true, false, true>(G, linear) : mfma_kernel<true>(G, linear);
     else if (v_token_major(a))
       sel->fn = pg ? mfma_kernel<false, true, true>(G, linear)
@@ -277,6 +275,10 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     case SCHED_PD_BF16:
       fn = a->head_dim == 64 ? valu_kernel<uint16_t, 64>(linear, G)
                              : valu_kernel<uint16_t, 128>(linear, G);
+      break;
+    case SCHED_PD_F16:
+      fn = a->head_dim == 64 ? valu_kernel<_Float16, 64>(linear, G)
+                             : valu_kernel<_Float16, 128>(linear, G);
       break;
     default:
       fn = a->head_dim == 64 ? valu_kernel<uint8_t, 64>(linear, G)

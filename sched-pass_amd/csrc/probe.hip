@@ -88,8 +88,9 @@ extern "C" int sched_pd_read_probe_blocks(const void *buf, uint64_t bytes, const
   if (nblocks == 0)
     return 0;
   int dev = 0, cus = 0;
-  hipGetDevice(&dev);
-  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0; // grid from the default below
   const unsigned grid = (unsigned)(cus > 0 ? cus : 256) * 16u;
   hipLaunchKernelGGL(read_probe_blocks, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      static_cast<const u32x4 *>(buf), bytes / 16u, block_ids, nblocks,
@@ -103,8 +104,9 @@ extern "C" int sched_pd_read_probe(const void *buf, uint64_t bytes, void *sink, 
   if (!buf || (bytes & 15u) || ((uintptr_t)buf & 15u))
     return schedpd::set_error(hipErrorInvalidValue, "read probe needs a 16-byte aligned buffer");
   int dev = 0, cus = 0;
-  hipGetDevice(&dev);
-  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0; // grid from the default below
   const unsigned grid = (unsigned)(cus > 0 ? cus : 256) * kProbeWgPerCu;
   hipLaunchKernelGGL(read_probe, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      static_cast<const u32x4 *>(buf), bytes / 16u, static_cast<unsigned *>(sink));

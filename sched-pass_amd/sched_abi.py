@@ -30,7 +30,7 @@ HINT_AUTO, HINT_URGENT, HINT_POLITE = 0, 1, 2
 # --- decode launcher ---------------------------------------------------------
 ABI_VERSION = 1
 SOFTMAX, LINEAR = 0, 1
-F32, BF16, FP8_E4M3 = 0, 1, 2
+F32, BF16, FP8_E4M3, F16 = 0, 1, 2, 3
 TAU_PREFIX, TAU_PER_PAGE = 0, 1
 FLAG_RT_TABLES = 0x1
 FLAG_WALLCLOCK = 0x2

@@ -23,7 +23,7 @@ import torch
 
 import sched_abi as abi
 
-_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16}
+_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16, torch.float16: abi.F16}
 if hasattr(torch, "float8_e4m3fn"):
     _DT[torch.float8_e4m3fn] = abi.FP8_E4M3
 

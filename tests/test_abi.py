@@ -121,6 +121,12 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(page_size=48, v_dim_stride=48)) == 0  # not a power of two
     assert kind(schedlib, fake_args(page_size=32, v_dim_stride=16)) == 0  # V rows not one page
     assert kind(schedlib, fake_args(num_q_heads=28, num_kv_heads=4)) == 1   # G = 7
+    f16 = dict(kv_dtype=abi.F16, q_dtype=abi.F16, o_dtype=abi.F16)
+    assert kind(schedlib, fake_args(**f16)) == 1                            # fp16 cache + Q
+    assert kind(schedlib, fake_args(v_tok_stride=1024, v_dim_stride=1, **f16)) == 1  # NHD
+    assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.BF16)) == 0
+    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32, **f16)) == 0
+    assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.FP8_E4M3)) == -1
 
 
 @pytest.mark.parametrize("field,value,msg", [

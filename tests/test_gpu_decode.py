@@ -232,6 +232,52 @@ def test_pages_of_32_tokens_shed_and_linear(scope):
     assert e <= TOL_BF16
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4), (16, 2), (64, 4)])
+def test_fp16_cache_parity(hq, hkv):
+    """An fp16 cache with fp16 Q (FlashInfer's dtype in the reference's
+    serving tests) runs on the MFMA kernel's fp16 operands: oracle parity,
+    fp16 output the RNE of the fp32 one, the VALU kernel on the same inputs,
+    and pi reversed under the queue bitwise against the static grid."""
+    b = batch([1, 15, 16, 17, 300, 2048, 5000], hq=hq, hkv=hkv, kv=torch.float16,
+              qd=torch.float16, seed=hq * hkv)
+    out = run(b)
+    args = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                               b["ctx_lens"], out=out)
+    assert sched_pd.kernel_kind(args) == "mfma"
+    r = ref(b)
+    e = mixed_err(out.cpu(), r)
+    print(f"fp16 mfma G={hq // hkv} err {e:.3g}", flush=True)
+    assert e <= TOL_BF16
+    o16 = run(b, out_dtype=torch.float16)
+    assert torch.equal(out.to(torch.float16), o16)
+    v = run(b, flags=abi.FLAG_FORCE_VALU)
+    assert mixed_err(v.cpu(), r) <= TOL_BF16
+    n = b["ctx_lens"].numel() * hkv
+    plane = SchedPlane(max_tasks=n)
+    plane.set_order(torch.arange(n - 1, -1, -1, dtype=torch.int32))
+    plane.set_num_tasks(n)
+    plane.push()
+    plane.reset_queue(2 * sched_pd.cu_count())
+    assert torch.equal(run(b, plane=plane, workers=2 * sched_pd.cu_count()), out)
+    t = token_major(b)
+    assert torch.equal(run(t, v_layout="tokmajor"), out)
+
+
+def test_fp16_shapes_off_the_mfma_path():
+    """fp16 caches the MFMA kernel does not take (32-token pages, fp32 Q,
+    the linear mode) run on the VALU kernel against the oracle."""
+    b = workloads.make_batch(np.asarray([100, 700, 33]), num_q_heads=32, num_kv_heads=8,
+                             page_size=32, kv_dtype=torch.float16, q_dtype=torch.float16,
+                             seed=5, device="cuda")
+    out = run(b)
+    assert mixed_err(out.cpu(), ref(b)) <= TOL_BF16
+    b = batch([100, 700, 33], kv=torch.float16, qd=torch.float32, seed=6)
+    assert mixed_err(run(b).cpu(), ref(b)) <= TOL_BF16
+    w = torch.randn(4096, device="cuda")
+    lo = run(b, mode=abi.LINEAR, lin_w=w)
+    assert mixed_err(lo.cpu(), ref(b, mode=abi.LINEAR, lin_w=w.cpu().numpy())) <= TOL_BF16
+
+
 def test_bf16_output_is_rne_of_fp32_output():
     b = batch([300, 2048, 17], seed=3)
     f = run(b)

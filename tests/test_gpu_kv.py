@@ -255,6 +255,32 @@ def test_full_size_fp8_append_scales_and_error_bound():
         assert torch.all((deq - x).abs() <= bound)
 
 
+def test_flashinfer_fp16_nhd_cache_in_place():
+    """The reference's FlashInfer serving shape (test/py/eval_pi_makespan.py:
+    31-60: fp16 Q and NHD cache, page 16, Hq 16 / Hkv 2, d 128, full last
+    pages) decoded in place on the MFMA kernel against the oracle."""
+    rng = np.random.default_rng(33)
+    P, ps, hkv, hq, d, R = 96, 16, 2, 16, 128, 8
+    pages = rng.integers(1, 12, R).astype(np.int32)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)).cuda()
+    indices = torch.from_numpy(rng.permutation(P)[:pages.sum()].astype(np.int32)).cuda()
+    last = torch.full((R,), ps, dtype=torch.int32, device="cuda")
+    ctx = kv_cache.ctx_lens_from_last_page_len(indptr, last, ps)
+    kv = torch.randn(P, 2, ps, hkv, d, device="cuda").half()
+    q = torch.randn(R, hq, d, device="cuda").half()
+    kview, vview = kv_cache.nhd_views(kv)
+    out = torch.empty(R, hq, d, dtype=torch.float16, device="cuda")
+    args = sched_pd.build_args(q, kview, vview, indices, ctx, out=out, page_indptr=indptr,
+                               v_layout="tokmajor")
+    assert sched_pd.kernel_kind(args) == "mfma"
+    sched_pd.launch(args)
+    torch.cuda.synchronize()
+    ref = np.asarray(oracle.decode(q, kview, vview, indices, ctx, page_indptr=indptr,
+                                   v_layout="tokmajor"), np.float64)
+    got = out.float().cpu().double().numpy()
+    assert float(np.max(np.abs(got - ref) / (1 + np.abs(ref)))) <= TOL_BF16
+
+
 def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
     """A FlashInfer NHD cache [P, 2, page, Hkv, d] with its CSR table
     (indptr, indices, last_page_len; test/py/eval_pi_makespan.py:46-60) is

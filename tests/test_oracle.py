@@ -71,6 +71,20 @@ def test_fp8_e4m3fn_table_matches_torch_all_256_codes():
     assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
 
 
+def test_f16_decode_matches_torch_on_every_code():
+    """The oracle's binary16 decode (from the format definition) against
+    torch's on all 65536 codes: subnormals, infinities, every exponent."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    ref = torch.from_numpy(bits.view(np.int16)).view(torch.float16).float().numpy()
+    lib = oracle.load()
+    ours = np.array([lib.oracle_f16_to_float(int(x)) for x in bits], np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # the closed forms the decode follows: smallest subnormal, largest finite
+    assert ours[1] == 2.0 ** -24 and ours[0x7bff] == 65504.0 and ours[0x3c00] == 1.0
+
+
 def test_bf16_decode_matches_torch():
     bits = np.random.default_rng(0).integers(0, 1 << 16, 4096, dtype=np.uint32).astype(np.uint16)
     bits = bits[(bits & 0x7f80) != 0x7f80]  # finite values
