@@ -1,7 +1,7 @@
 """Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
-                    [--sections hetero,shed,fp8,kv,layouts]
+                    [--sections hetero,shed,fp8,kv,layouts,pi]
 
 One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
 Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
@@ -41,8 +41,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
-    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts",
-                   help="comma list of the extra measurements: hetero, shed, fp8, kv, layouts")
+    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi",
+                   help="comma list of the extra measurements: hetero, shed, fp8, kv, "
+                        "layouts, pi")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--tables", type=int, default=8)
     return p.parse_args()
@@ -515,6 +516,62 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
     return res
 
 
+def bench_pi_makespan(torch, sched_pd, batch_sizes=(256, 1024, 4096, 8192)):
+    """The reference's isolated pi-makespan evaluation (test/py/
+    eval_pi_makespan.py:31-130) through FlashInfer's wrapper calls: Qwen-3B
+    GQA decode (Hq 16 / Hkv 2, d 128, page 16), fp16 Q and NHD cache, pages
+    per request ~ exp(N(2.6, 1.1)) clipped to [1, 512], static grid; pi
+    identity, longest-first and shortest-first by pages (over (request,
+    kv-head) tasks). Min over 5 repeats of the mean of 10 launches."""
+    import numpy as np
+    from flashinfer_compat import BatchDecodeWithPagedKVCacheWrapper
+    from sched_rt import SchedPlane
+    page, hd, nqo, nkv = 16, 128, 16, 2
+    gen = torch.Generator().manual_seed(1)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for bs in batch_sizes:
+        pages = torch.exp(torch.normal(2.6, 1.1, (bs,), generator=gen)).clamp(1, 512).to(
+            torch.int32)
+        npages = int(pages.sum())
+        indptr = torch.zeros(bs + 1, dtype=torch.int32)
+        indptr[1:] = torch.cumsum(pages, 0)
+        indptr = indptr.cuda()
+        indices = torch.arange(npages, dtype=torch.int32, device="cuda")
+        last = torch.full((bs,), page, dtype=torch.int32, device="cuda")
+        q = torch.randn(bs, nqo, hd, dtype=torch.float16, device="cuda")
+        kv = torch.randn(npages, 2, page, nkv, hd, dtype=torch.float16, device="cuda")
+        ntask = bs * nkv
+        plane = SchedPlane(max_tasks=ntask)
+        w = BatchDecodeWithPagedKVCacheWrapper(None, "NHD", plane=plane)
+        w.plan(indptr, indices, last, nqo, nkv, hd, page, data_type=torch.float16,
+               q_data_type=torch.float16)
+        out = torch.empty(bs, nqo, hd, dtype=torch.float16, device="cuda")
+        args = sched_pd.build_args(q, *w._views(kv), indices, w._plan["ctx"], out=out,
+                                   page_indptr=indptr, v_layout="tokmajor", plane=plane)
+        cost = np.repeat(pages.numpy().astype(np.float64), nkv)
+        orders = {"identity": None,
+                  "lpt": np.argsort(-cost, kind="stable").astype(np.int32),
+                  "spt": np.argsort(cost, kind="stable").astype(np.int32)}
+        row = {}
+        for name, order in orders.items():
+            if order is None:
+                plane.reset_order()
+                plane.set_order_size(0)
+            else:
+                plane.install_order(order, ntask)
+            plane.push()
+            row[name] = round(_makespan_us(torch, sched_pd, args, stream), 2)
+        row["lpt_vs_identity_pct"] = round(100 * (row["lpt"] - row["identity"]) / row["identity"], 2)
+        row["spt_vs_identity_pct"] = round(100 * (row["spt"] - row["identity"]) / row["identity"], 2)
+        row["kv_bytes"] = npages * page * nkv * hd * 2 * 2
+        row["gbs_lpt"] = round(row["kv_bytes"] / row["lpt"] / 1e3, 1)
+        res[str(bs)] = row
+        del q, kv, out, plane, w, args
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
     the uniform workload's shape (64 requests x 2048 tokens, a pool of just
@@ -618,6 +675,8 @@ def main():
         line["shed_policy"] = bench_shed(torch, sched_pd, workloads, SchedPlane, cu)
     if "fp8" in sections:
         line["fp8_qwen2_7b"] = bench_fp8(torch, sched_pd, workloads, SchedPlane, cu)
+    if "pi" in sections:
+        line["pi_makespan_flashinfer_shape"] = bench_pi_makespan(torch, sched_pd)
     if "layouts" in sections:
         line["kv_layouts"] = bench_layouts(torch, sched_pd, workloads)
     if "kv" in sections:
