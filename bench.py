@@ -562,6 +562,17 @@ def bench_pi_makespan(torch, sched_pd, batch_sizes=(256, 1024, 4096, 8192)):
                 plane.install_order(order, ntask)
             plane.push()
             row[name] = round(_makespan_us(torch, sched_pd, args, stream), 2)
+        if bs == batch_sizes[-1]:
+            # the residency timer's cost (reference ROADMAP.md:1481-1488):
+            # identity order, timer rows off against on (device rows)
+            plane.reset_order()
+            plane.set_order_size(0)
+            for name, on in (("timer_off", False), ("timer_on", True)):
+                plane.set_timer_enabled(on)
+                plane.push()
+                row[name] = round(_makespan_us(torch, sched_pd, args, stream), 2)
+            row["timer_cost_pct"] = round(
+                100 * (row["timer_on"] - row["timer_off"]) / row["timer_off"], 2)
         row["lpt_vs_identity_pct"] = round(100 * (row["lpt"] - row["identity"]) / row["identity"], 2)
         row["spt_vs_identity_pct"] = round(100 * (row["spt"] - row["identity"]) / row["identity"], 2)
         row["kv_bytes"] = npages * page * nkv * hd * 2 * 2
