@@ -391,9 +391,10 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
 
 def bench_kv_append(torch, steps=20):
     """The cache writer (sched_kv_append) on the Llama-3-8B decode shape
-    (Hkv 8, d 128, page 16, d-major V), bf16 K/V rows in:
+    (Hkv 8, d 128, page 16, d-major V), bf16 K/V rows into a bf16 and an fp8
+    cache, fp16 rows into an fp16 cache:
       decode_step: one token for each of 64 requests at ragged positions
-        (ctx after the append ~ U[1024, 2048]), into a bf16 and an fp8 cache;
+        (ctx after the append ~ U[1024, 2048]);
       bulk: the whole 64 x 2048-token KV of the uniform batch in one call.
     Bytes per call = source rows read + cache bytes written (+ fp8 scales);
     the d-major V's read-merge of a partial 4-slot group is not counted."""
@@ -414,7 +415,10 @@ def bench_kv_append(torch, steps=20):
     app_step = torch.arange(R + 1, dtype=torch.int32, device="cuda")
     app_bulk = torch.arange(0, R * T + 1, T, dtype=torch.int32, device="cuda")
     ctx_bulk = torch.full((R,), T, dtype=torch.int32, device="cuda")
-    for name, dt in (("bf16", torch.bfloat16), ("fp8", fp8)):
+    for name, dt in (("bf16", torch.bfloat16), ("fp8", fp8), ("fp16", torch.float16)):
+        if dt == torch.float16:
+            k_big, v_big = k_big.half(), v_big.half()
+            k1, v1 = k_big[:R].contiguous(), v_big[:R].contiguous()
         kp = torch.zeros(npg, hkv, ps, d, dtype=dt, device="cuda")
         vp = torch.zeros(npg, hkv, d, ps, dtype=dt, device="cuda")
         ks = vs = None

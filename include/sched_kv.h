@@ -53,8 +53,8 @@ extern "C" {
  *   k_src[i*src_tok_stride + h*src_head_stride + j] (v_src alike). */
 typedef struct SchedKvAppendArgs {
   uint32_t abi_version;   /* SCHED_KV_ABI_VERSION */
-  uint32_t src_dtype;     /* SCHED_PD_F32 or SCHED_PD_BF16 */
-  uint32_t kv_dtype;      /* SCHED_PD_F32, SCHED_PD_BF16 or SCHED_PD_FP8_E4M3 */
+  uint32_t src_dtype;     /* SCHED_PD_F32, SCHED_PD_BF16 or SCHED_PD_F16 */
+  uint32_t kv_dtype;      /* SCHED_PD_F32, SCHED_PD_BF16, SCHED_PD_F16 or SCHED_PD_FP8_E4M3 */
   uint32_t num_requests;
   uint32_t num_kv_heads;
   uint32_t head_dim;      /* multiple of 4, <= 256 */

@@ -11,6 +11,10 @@
  *     table the reference's tests build (test/py/eval_pi_makespan.py:46-60)
  *     or a 2-D block table;
  *   - fp32 -> bf16 round-to-nearest-even;
+ *   - fp32 -> IEEE binary16 round-to-nearest-even, written from the format
+ *     definition (5 exponent bits bias 15, 10 mantissa bits, subnormals
+ *     m * 2^-24, overflow to infinity from 65520 up); NaN payloads are not
+ *     restated (any NaN becomes the quiet NaN 0x7e00 with its sign);
  *   - OCP e4m3fn encoding with round-to-nearest-even and saturation to 448,
  *     written from the format definition (sign, 4 exponent bits bias 7, 3
  *     mantissa bits, subnormals m * 2^-9, no infinity);
@@ -27,6 +31,7 @@
 
 float oracle_bf16_to_float(uint16_t h);
 float oracle_fp8_e4m3_to_float(uint8_t b);
+float oracle_f16_to_float(uint16_t h);
 
 uint16_t oracle_float_to_bf16(float f) {
   uint32_t u;
@@ -35,6 +40,29 @@ uint16_t oracle_float_to_bf16(float f) {
     return (uint16_t)((u >> 16) | 0x40u);
   uint32_t lsb = (u >> 16) & 1u;
   return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+
+/* Round-to-nearest-even to binary16. */
+uint16_t oracle_float_to_f16(float x) {
+  uint16_t sign = signbit(x) ? 0x8000 : 0x0000;
+  float a = fabsf(x);
+  if (isnan(x))
+    return sign | 0x7e00;
+  if (a >= 65520.0f) /* the midpoint between 65504 and 2^16 rounds to even: up */
+    return sign | 0x7c00;
+  if (a < 6.103515625e-05f) { /* below 2^-14: subnormal grid m * 2^-24 */
+    float m = nearbyintf(a * 16777216.0f); /* exact scaling, then RNE */
+    return sign | (uint16_t)m;             /* m == 1024 is the first normal */
+  }
+  int e;
+  float f = frexpf(a, &e);                         /* a = f * 2^e, f in [0.5, 1) */
+  float q = nearbyintf((f * 2.0f - 1.0f) * 1024.0f); /* 10 mantissa bits, RNE */
+  int exp = e - 1;
+  if (q == 1024.0f) {
+    q = 0.0f;
+    exp += 1;
+  }
+  return sign | (uint16_t)(((exp + 15) << 10) | (int)q);
 }
 
 /* Round-to-nearest-even to e4m3fn, saturating finite values at +-448. */
@@ -73,7 +101,7 @@ float oracle_pow2_scale(float a) {
 }
 
 static uint32_t esize(uint32_t dt) {
-  return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u;
+  return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_FP8_E4M3 ? 1u : 2u;
 }
 
 static float src_at(const SchedKvAppendArgs *a, const void *src, int64_t row, uint32_t h,
@@ -81,6 +109,8 @@ static float src_at(const SchedKvAppendArgs *a, const void *src, int64_t row, ui
   int64_t i = row * a->src_tok_stride + (int64_t)h * a->src_head_stride + j;
   if (a->src_dtype == SCHED_PD_F32)
     return ((const float *)src)[i];
+  if (a->src_dtype == SCHED_PD_F16)
+    return oracle_f16_to_float(((const uint16_t *)src)[i]);
   return oracle_bf16_to_float(((const uint16_t *)src)[i]);
 }
 
@@ -89,6 +119,8 @@ static float code_value(const void *pool, int64_t i, uint32_t dt) {
     return ((const float *)pool)[i];
   if (dt == SCHED_PD_BF16)
     return oracle_bf16_to_float(((const uint16_t *)pool)[i]);
+  if (dt == SCHED_PD_F16)
+    return oracle_f16_to_float(((const uint16_t *)pool)[i]);
   return oracle_fp8_e4m3_to_float(((const uint8_t *)pool)[i]);
 }
 
@@ -97,6 +129,8 @@ static void put(void *pool, int64_t i, uint32_t dt, float x, float inv) {
     ((float *)pool)[i] = x;
   } else if (dt == SCHED_PD_BF16) {
     ((uint16_t *)pool)[i] = oracle_float_to_bf16(x);
+  } else if (dt == SCHED_PD_F16) {
+    ((uint16_t *)pool)[i] = oracle_float_to_f16(x);
   } else {
     float q = fminf(fmaxf(x * inv, -448.0f), 448.0f);
     ((uint8_t *)pool)[i] = oracle_fp8_e4m3_from_float(q);

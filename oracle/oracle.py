@@ -70,6 +70,8 @@ def load():
         lib.oracle_fp8_e4m3_from_float.argtypes = [ctypes.c_float]
         lib.oracle_float_to_bf16.restype = ctypes.c_uint16
         lib.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+        lib.oracle_float_to_f16.restype = ctypes.c_uint16
+        lib.oracle_float_to_f16.argtypes = [ctypes.c_float]
         lib.oracle_pow2_scale.restype = ctypes.c_float
         lib.oracle_pow2_scale.argtypes = [ctypes.c_float]
         _lib = lib
@@ -263,6 +265,13 @@ def fp8_e4m3_encode(x) -> np.ndarray:
     return np.array([lib.oracle_fp8_e4m3_from_float(float(v)) for v in x], np.uint8)
 
 
+def f16_encode(x) -> np.ndarray:
+    """The oracle's binary16 encoder (RNE) over an array, as raw bits."""
+    lib = load()
+    x = np.asarray(x, np.float32).ravel()
+    return np.array([lib.oracle_float_to_f16(float(v)) for v in x], np.uint16)
+
+
 def pow2_scale(a: float) -> float:
     return load().oracle_pow2_scale(float(a))
 
@@ -273,7 +282,7 @@ def kv_append(k_src, v_src, append_indptr, ctx_lens, k_pool, v_pool, block_table
     """Restated sched_kv_append on host copies. Pools: k [P, Hkv, ps, d];
     v [P, Hkv, d, ps] (dmajor) or [P, Hkv, ps, d] (tokmajor); sources
     [T, Hkv, d]. Returns (k_pool, v_pool, k_scale, v_scale, errors) as numpy
-    arrays of the pools' raw element bits (uint16 for bf16, uint8 for fp8)
+    arrays of the pools' raw element bits (uint16 for bf16/fp16, uint8 for fp8)
     and float32 scales (None without scales)."""
     lib = load()
     ks, src_code = _host(k_src)

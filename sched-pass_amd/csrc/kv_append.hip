@@ -1,6 +1,6 @@
 // kv_append.hip -- the paged KV-cache writer (sched_kv_append): appends
-// source token rows into the decode pools, converting to bf16 / fp32 or
-// quantising to fp8 e4m3fn with per-(page, kv-head) power-of-two scales.
+// source token rows (fp32, bf16 or fp16) into the decode pools, converting to
+// fp32 / bf16 / fp16 (round to nearest even) or quantising to fp8 e4m3fn with per-(page, kv-head) power-of-two scales.
 //
 // One workgroup serves one request and a group of its kv-heads (all of them
 // unless a small append needs more workgroups), over a strided subset of the
@@ -50,11 +50,24 @@ struct AParams {
   uint32_t w8;  // one-round path reads and writes 8-element chunks
 };
 
-template <bool SRC_F32>
+// Source rows are fp32, bf16 or fp16 (SRC is the SCHED_PD_* code).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int SRC> __device__ __forceinline__ float half_to_f32(uint32_t h) {
+  if constexpr (SRC == SCHED_PD_BF16)
+    return bf16_bits_to_f32(h);
+  else
+    return f16_bits_to_f32(h);
+}
+
+template <int SRC>
 __device__ __forceinline__ float load_src(const void *src, int64_t idx) {
-  if (SRC_F32)
+  if constexpr (SRC == SCHED_PD_F32)
     return static_cast<const float *>(src)[idx];
-  return bf16_bits_to_f32(static_cast<const uint16_t *>(src)[idx]);
+  else
+    return half_to_f32<SRC>(static_cast<const uint16_t *>(src)[idx]);
 }
 
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
@@ -62,9 +75,9 @@ typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
 
 // Source rows are read once: non-temporal loads (bulk bf16 append measured
 // 280 -> 252 us).
-template <bool SRC_F32>
+template <int SRC>
 __device__ __forceinline__ void load_src4(const void *src, int64_t idx, float x[4]) {
-  if (SRC_F32) {
+  if constexpr (SRC == SCHED_PD_F32) {
     const u32x4_t v = __builtin_nontemporal_load(
         reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx));
     x[0] = __uint_as_float(v.x), x[1] = __uint_as_float(v.y);
@@ -72,15 +85,15 @@ __device__ __forceinline__ void load_src4(const void *src, int64_t idx, float x[
   } else {
     const u32x2_t v = __builtin_nontemporal_load(
         reinterpret_cast<const u32x2_t *>(static_cast<const uint16_t *>(src) + idx));
-    x[0] = __uint_as_float(v.x << 16), x[1] = __uint_as_float(v.x & 0xffff0000u);
-    x[2] = __uint_as_float(v.y << 16), x[3] = __uint_as_float(v.y & 0xffff0000u);
+    x[0] = half_to_f32<SRC>(v.x & 0xffffu), x[1] = half_to_f32<SRC>(v.x >> 16);
+    x[2] = half_to_f32<SRC>(v.y & 0xffffu), x[3] = half_to_f32<SRC>(v.y >> 16);
   }
 }
 
-// Eight consecutive source elements (16 bytes of bf16, 32 of fp32).
-template <bool SRC_F32>
+// Eight consecutive source elements (16 bytes of bf16/fp16, 32 of fp32).
+template <int SRC>
 __device__ __forceinline__ void load_src8(const void *src, int64_t idx, float x[8]) {
-  if (SRC_F32) {
+  if constexpr (SRC == SCHED_PD_F32) {
     const u32x4_t a = __builtin_nontemporal_load(
         reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx));
     const u32x4_t b = __builtin_nontemporal_load(
@@ -95,18 +108,18 @@ __device__ __forceinline__ void load_src8(const void *src, int64_t idx, float x[
     const unsigned w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[2 * i] = __uint_as_float(w[i] << 16);
-      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      x[2 * i] = half_to_f32<SRC>(w[i] & 0xffffu);
+      x[2 * i + 1] = half_to_f32<SRC>(w[i] >> 16);
     }
   }
 }
 
-template <bool SRC_F32, int W>
+template <int SRC, int W>
 __device__ __forceinline__ void load_chunk(const void *src, int64_t idx, float x[W]) {
   if constexpr (W == 8)
-    load_src8<SRC_F32>(src, idx, x);
+    load_src8<SRC>(src, idx, x);
   else
-    load_src4<SRC_F32>(src, idx, x);
+    load_src4<SRC>(src, idx, x);
 }
 
 // Least 2^k (k >= -126) with a <= 448 * 2^k; 0 for a == 0. With
@@ -173,6 +186,25 @@ template <> struct Codec<SCHED_PD_BF16> {
   }
 };
 
+// IEEE binary16, round to nearest even (v_cvt_f16_f32 under the default
+// rounding mode; magnitudes past 65520 become infinity, as a cast does).
+template <> struct Codec<SCHED_PD_F16> {
+  typedef uint2 Vec;
+  __device__ static uint32_t h(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static Vec enc(const float x[4], float) {
+    return make_uint2(h(x[0]) | (h(x[1]) << 16), h(x[2]) | (h(x[3]) << 16));
+  }
+  __device__ static float dec(const Vec &v, int i) {
+    uint32_t w = i < 2 ? v.x : v.y;
+    return f16_bits_to_f32((i & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+  __device__ static Vec keep(Vec v, const Vec &old, uint32_t keep) {
+    return Codec<SCHED_PD_BF16>::keep(v, old, keep);
+  }
+};
+
 template <> struct Codec<SCHED_PD_FP8_E4M3> {
   typedef uint32_t Vec;
   __device__ static Vec enc(const float x[4], float inv) {
@@ -207,7 +239,8 @@ struct PageScales {
 template <int KVD>
 using PoolElem = typename std::conditional<
     KVD == SCHED_PD_F32, float,
-    typename std::conditional<KVD == SCHED_PD_BF16, uint16_t, uint8_t>::type>::type;
+    typename std::conditional<KVD == SCHED_PD_BF16 || KVD == SCHED_PD_F16, uint16_t,
+                              uint8_t>::type>::type;
 
 // Max over the 64 lanes of a wave (all lanes active), in VALU cross-lane
 // moves: quad permutes and row rotations (DPP) within each row of 16, then
@@ -298,7 +331,7 @@ __device__ void scales_from_amax(const AParams &P, PageScales &S, int64_t page, 
   __syncthreads();
 }
 
-template <bool SRC_F32>
+template <int SRC>
 __device__ void page_scales(const AParams &P, PageScales &S, int64_t page, uint32_t h0,
                             uint32_t hpw, uint32_t o0, uint32_t o1, int64_t row0) {
   const uint32_t q = P.d / 4, per_head = (o1 - o0) * q, total = hpw * per_head;
@@ -318,8 +351,8 @@ __device__ void page_scales(const AParams &P, PageScales &S, int64_t page, uint3
         const uint32_t rem = c - hh[u] * per_head;
         const uint32_t t = rem / q, j = (rem - t * q) * 4;
         const int64_t s = (row0 + t) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j;
-        load_src4<SRC_F32>(P.k_src, s, xk[u]);
-        load_src4<SRC_F32>(P.v_src, s, xv[u]);
+        load_src4<SRC>(P.k_src, s, xk[u]);
+        load_src4<SRC>(P.v_src, s, xv[u]);
       }
     }
 #pragma unroll
@@ -340,7 +373,7 @@ __device__ void page_scales(const AParams &P, PageScales &S, int64_t page, uint3
 // One tensor (K: x = 0, V: x = 1) of heads [h0, h0 + hpw) of one page:
 // slots [o0, o1) appended from source rows row0 + (t - o0); with fp8, the
 // earlier slots of heads whose scale grew are re-encoded.
-template <bool SRC_F32, int KVD>
+template <int SRC, int KVD>
 __device__ void write_tensor(const AParams &P, const PageScales &S, int x, const void *src,
                              void *pool_v, int64_t base, int64_t head_stride, int64_t tok_stride,
                              int64_t dim_stride, uint32_t h0, uint32_t hpw, uint32_t o0,
@@ -374,7 +407,7 @@ __device__ void write_tensor(const AParams &P, const PageScales &S, int x, const
                                            (int64_t)t * tok_stride + j);
           if (t >= o0) {
             state[u] = 1;
-            load_src4<SRC_F32>(
+            load_src4<SRC>(
                 src, (row0 + (t - o0)) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j, v[u]);
           } else if (FP8 && S.regrow[x][hh[u]]) {
             state[u] = 2;
@@ -431,7 +464,7 @@ __device__ void write_tensor(const AParams &P, const PageScales &S, int x, const
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const uint32_t t = o[u] + i;
-              v[u][i] = (t >= o0 && t < o1) ? load_src<SRC_F32>(src, (row0 + (t - o0)) * P.s_tok + s)
+              v[u][i] = (t >= o0 && t < o1) ? load_src<SRC>(src, (row0 + (t - o0)) * P.s_tok + s)
                                             : 0.f;
             }
           }
@@ -467,7 +500,7 @@ __device__ __forceinline__ void store_chunk(PoolElem<KVD> *p, const float x[W], 
     *reinterpret_cast<Vec *>(p) = C::enc(x, inv);
   } else {
     const Vec a = C::enc(x, inv), b = C::enc(x + 4, inv);
-    if constexpr (KVD == SCHED_PD_BF16)
+    if constexpr (KVD == SCHED_PD_BF16 || KVD == SCHED_PD_F16)
       *reinterpret_cast<uint4 *>(p) = make_uint4(a.x, a.y, b.x, b.y);
     else if constexpr (KVD == SCHED_PD_FP8_E4M3)
       *reinterpret_cast<uint2 *>(p) = make_uint2(a, b);
@@ -513,7 +546,7 @@ __device__ void regrow_rows(const AParams &P, const PageScales &S, int x, PoolEl
 // per lane and tensor), keeps them in registers through the fp8 amax, and
 // stores them; a d-major V goes through the LDS stage so that the source is
 // read in rows and the pool written in slot groups.
-template <bool SRC_F32, int KVD, int W>
+template <int SRC, int KVD, int W>
 __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, int64_t page,
                                uint32_t h0, uint32_t hpw, uint32_t o0, uint32_t o1,
                                int64_t row0) {
@@ -548,8 +581,8 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
       t[u] = rem / q;
       j[u] = (rem - t[u] * q) * W;
       const int64_t s = (row0 + t[u]) * P.s_tok + (int64_t)(h0 + hh[u]) * P.s_head + j[u];
-      load_chunk<SRC_F32, W>(P.k_src, s, xk[u]);
-      load_chunk<SRC_F32, W>(P.v_src, s, xv[u]);
+      load_chunk<SRC, W>(P.k_src, s, xk[u]);
+      load_chunk<SRC, W>(P.v_src, s, xv[u]);
     }
   }
   __syncthreads(); // the stage and S are free: the previous page is written
@@ -658,7 +691,7 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
 
 // grid.x = requests x head groups, grid.y strides over the pages of the
 // longest append.
-template <bool SRC_F32, int KVD>
+template <int SRC, int KVD>
 __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
   __shared__ PageScales S;
   __shared__ float stage[kStageFloats];
@@ -695,32 +728,33 @@ __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
     const int64_t row0 = a0 + (pbase + o0 - pos0);
     if ((uint64_t)hpw * (o1 - o0) * (P.d / 4) <= kFastChunks) {
       if (kBatch % 2 == 0 && P.w8)
-        page_one_round<SRC_F32, KVD, (kBatch % 2 == 0 ? 8 : 4)>(P, S, stage, page, h0, hpw, o0,
+        page_one_round<SRC, KVD, (kBatch % 2 == 0 ? 8 : 4)>(P, S, stage, page, h0, hpw, o0,
                                                                 o1, row0);
       else
-        page_one_round<SRC_F32, KVD, 4>(P, S, stage, page, h0, hpw, o0, o1, row0);
+        page_one_round<SRC, KVD, 4>(P, S, stage, page, h0, hpw, o0, o1, row0);
       continue;
     }
     if (KVD == SCHED_PD_FP8_E4M3)
-      page_scales<SRC_F32>(P, S, page, h0, hpw, o0, o1, row0);
-    write_tensor<SRC_F32, KVD>(P, S, 0, P.k_src, P.k_pool, page * P.kps, P.khs, P.kts, 1, h0, hpw,
+      page_scales<SRC>(P, S, page, h0, hpw, o0, o1, row0);
+    write_tensor<SRC, KVD>(P, S, 0, P.k_src, P.k_pool, page * P.kps, P.khs, P.kts, 1, h0, hpw,
                                o0, o1, row0);
-    write_tensor<SRC_F32, KVD>(P, S, 1, P.v_src, P.v_pool, page * P.vps, P.vhs, P.vts, P.vds, h0,
+    write_tensor<SRC, KVD>(P, S, 1, P.v_src, P.v_pool, page * P.vps, P.vhs, P.vts, P.vds, h0,
                                hpw, o0, o1, row0);
   }
 }
 
 typedef void (*AppendFn)(AParams);
 
-template <bool SRC_F32> AppendFn pick(uint32_t kvd) {
+template <int SRC> AppendFn pick(uint32_t kvd) {
   switch (kvd) {
-  case SCHED_PD_F32: return kv_append_kernel<SRC_F32, SCHED_PD_F32>;
-  case SCHED_PD_BF16: return kv_append_kernel<SRC_F32, SCHED_PD_BF16>;
-  default: return kv_append_kernel<SRC_F32, SCHED_PD_FP8_E4M3>;
+  case SCHED_PD_F32: return kv_append_kernel<SRC, SCHED_PD_F32>;
+  case SCHED_PD_BF16: return kv_append_kernel<SRC, SCHED_PD_BF16>;
+  case SCHED_PD_F16: return kv_append_kernel<SRC, SCHED_PD_F16>;
+  default: return kv_append_kernel<SRC, SCHED_PD_FP8_E4M3>;
   }
 }
 
-uint32_t esize(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_BF16 ? 2u : 1u; }
+uint32_t esize(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_FP8_E4M3 ? 1u : 2u; }
 
 bool aligned(const void *p, uint32_t bytes) { return ((uintptr_t)p % bytes) == 0; }
 
@@ -747,9 +781,10 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   if (a->abi_version != SCHED_KV_ABI_VERSION)
     return set_error(-1, "sched_kv_append: abi_version %u, library has %u", a->abi_version,
                      SCHED_KV_ABI_VERSION);
-  if (a->src_dtype != SCHED_PD_F32 && a->src_dtype != SCHED_PD_BF16)
-    return set_error(-1, "sched_kv_append: src dtype %u (F32 or BF16)", a->src_dtype);
-  if (a->kv_dtype > SCHED_PD_FP8_E4M3)
+  if (a->src_dtype != SCHED_PD_F32 && a->src_dtype != SCHED_PD_BF16 &&
+      a->src_dtype != SCHED_PD_F16)
+    return set_error(-1, "sched_kv_append: src dtype %u (F32, BF16 or F16)", a->src_dtype);
+  if (a->kv_dtype > SCHED_PD_F16)
     return set_error(-1, "sched_kv_append: kv dtype %u", a->kv_dtype);
   if (a->num_requests == 0)
     return 0;
@@ -833,7 +868,9 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   if (gy > 65535)
     gy = 65535;
   const dim3 grid(a->num_requests * (a->num_kv_heads / hpw), (uint32_t)gy);
-  AppendFn fn = a->src_dtype == SCHED_PD_F32 ? pick<true>(a->kv_dtype) : pick<false>(a->kv_dtype);
+  AppendFn fn = a->src_dtype == SCHED_PD_F32    ? pick<SCHED_PD_F32>(a->kv_dtype)
+                : a->src_dtype == SCHED_PD_BF16 ? pick<SCHED_PD_BF16>(a->kv_dtype)
+                                                : pick<SCHED_PD_F16>(a->kv_dtype);
   hipLaunchKernelGGL(fn, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), P);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)

@@ -24,7 +24,8 @@ import torch
 import sched_abi as abi
 import sched_pd
 
-_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16}
+_DT = {torch.float32: abi.F32, torch.bfloat16: abi.BF16, torch.float16: abi.F16}
+_SRC_DT = (torch.float32, torch.bfloat16, torch.float16)
 if hasattr(torch, "float8_e4m3fn"):
     _DT[torch.float8_e4m3fn] = abi.FP8_E4M3
 
@@ -40,8 +41,8 @@ def _ptr(t):
 def append(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, block_table, *,
            page_indptr=None, v_layout="dmajor", k_scale=None, v_scale=None,
            max_append=0, errors=None, heads_per_group=0, stream=None) -> None:
-    """Write source rows k_new/v_new [T, Hkv, d] (bf16 or fp32, dims
-    contiguous) into the pools: request r's rows append_indptr[r] ..
+    """Write source rows k_new/v_new [T, Hkv, d] (fp32, bf16 or fp16, dims
+    contiguous) into the pools (fp32, bf16, fp16 or fp8 e4m3fn): request r's rows append_indptr[r] ..
     append_indptr[r+1]-1 go to positions ctx_lens[r] - n_r .. ctx_lens[r]-1
     (ctx_lens counts tokens after the append). An fp8 pool needs k_scale /
     v_scale [P * Hkv] float32 (read and written). `errors` (int32/uint32 [1],
@@ -66,9 +67,9 @@ def build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, blo
                       max_append=0, errors=None, heads_per_group=0) -> abi.SchedKvAppendArgs:
     """Validate and fill a SchedKvAppendArgs (no launch); see append()."""
     a = abi.default_kv_args()
-    if k_new.dtype not in (torch.float32, torch.bfloat16) or v_new.dtype != k_new.dtype:
-        raise TypeError(f"sources must both be float32 or bfloat16, got {k_new.dtype}, "
-                        f"{v_new.dtype}")
+    if k_new.dtype not in _SRC_DT or v_new.dtype != k_new.dtype:
+        raise TypeError(f"sources must both be float32, bfloat16 or float16, got "
+                        f"{k_new.dtype}, {v_new.dtype}")
     if k_pool.dtype not in _DT or v_pool.dtype != k_pool.dtype:
         raise TypeError(f"pool dtypes {k_pool.dtype}, {v_pool.dtype}")
     if k_new.dim() != 3 or k_new.shape != v_new.shape or k_new.stride() != v_new.stride():

@@ -20,6 +20,8 @@ def random_pool(shape, dtype, rng):
     bits = rng.integers(0, 1 << 16, size=shape, dtype=np.uint16)
     if dtype == torch.bfloat16:
         return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    if dtype == torch.float16:
+        return torch.from_numpy(bits.view(np.int16)).view(torch.float16)
     return torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
 
 
@@ -76,6 +78,8 @@ def as_float(bits, dtype):
         return fp8_values()[bits].astype(np.float64)
     if dtype == torch.bfloat16:
         return oracle.bf16_to_float(bits).astype(np.float64)
+    if dtype == torch.float16:
+        return bits.view(np.float16).astype(np.float64)
     return bits.astype(np.float64)
 
 

@@ -24,7 +24,7 @@ def lib(schedlib):
 
 def raw(t):
     t = t.detach().cpu().contiguous()
-    if t.dtype == torch.bfloat16:
+    if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16)
     if t.dtype == FP8:
         return t.view(torch.uint8).numpy()
@@ -59,10 +59,10 @@ def assert_same(got, ref):
             assert np.array_equal(g, r), (what, int(np.sum(g != r)))
 
 
-@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8])
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8, torch.float16])
 @pytest.mark.parametrize("v_layout", ["dmajor", "tokmajor"])
 @pytest.mark.parametrize("csr", [False, True])
-@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32, torch.float16])
 def test_append_is_bit_exact_with_the_oracle(kv, v_layout, csr, src):
     # d = 20 (a multiple of 4, not of 8) runs the 4-element chunk path, the
     # others the 8-element one
@@ -95,7 +95,7 @@ def test_page_size_32_and_64():
         assert_same(run_gpu(c), c["out"])
 
 
-@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8])
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32, FP8, torch.float16])
 def test_small_and_odd_page_sizes(kv):
     """Page sizes 8, 12 and 20 (multiples of 4, not of 16) with a d-major V:
     appends of 1 to 3 pages + 1 tokens on top of prior tokens, so first and
@@ -154,11 +154,14 @@ def test_hardware_fp8_encoder_on_every_tie_and_neighbour():
     assert np.array_equal(got, ref), int(np.sum(got != ref))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8, torch.float16])
 def test_cache_prefill_then_decode_loop(dtype):
     """PagedKvCache: a prefill append, then 20 one-token appends per request
     (page boundaries crossed), mirrored on the oracle; then a decode step over
-    the cache against the oracle decode on the same pools."""
+    the cache against the oracle decode on the same pools. An fp16 cache is
+    fed fp16 rows and decoded with fp16 Q (the reference's FlashInfer serving
+    dtype), the others bf16."""
+    half = torch.float16 if dtype == torch.float16 else torch.bfloat16
     rng = np.random.default_rng(21)
     hkv, hq, d, ps, R = 8, 32, 128, 16, 6
     cache = kv_cache.PagedKvCache(64, hkv, d, ps, dtype=dtype)
@@ -171,13 +174,13 @@ def test_cache_prefill_then_decode_loop(dtype):
 
     def step(counts):
         T = int(sum(counts))
-        k = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).bfloat16()
-        v = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).bfloat16()
+        k = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).to(half)
+        v = torch.from_numpy(rng.standard_normal((T, hkv, d)).astype(np.float32)).to(half)
         cache.append(rids, k.cuda(), v.cuda(), counts)
         bt, ctx = cache.block_table(rids)
         app = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
         as_t = (lambda a: torch.from_numpy(a).view(FP8)) if dtype == FP8 else \
-               (lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16))
+               (lambda a: torch.from_numpy(a.view(np.int16)).view(dtype))
         kp, vp, ks, vs, err = oracle.kv_append(k, v, app, ctx.cpu().numpy(), as_t(host[0]),
                                                as_t(host[1]), bt.cpu().numpy(),
                                                k_scale=host[2], v_scale=host[3])
@@ -193,7 +196,7 @@ def test_cache_prefill_then_decode_loop(dtype):
     if dtype == FP8:
         assert np.array_equal(cache.k_scale.cpu().numpy(), host[2])
         assert np.array_equal(cache.v_scale.cpu().numpy(), host[3])
-    q = torch.randn(R, hq, d, dtype=torch.bfloat16, device="cuda")
+    q = torch.randn(R, hq, d, dtype=half, device="cuda")
     out = torch.empty(R, hq, d, dtype=torch.float32, device="cuda")
     cache.decode(q, rids, out=out)
     bt, ctx = cache.block_table(rids)
@@ -209,11 +212,13 @@ def test_cache_prefill_then_decode_loop(dtype):
 
 def _full_size(dtype):
     """Llama-3-8B decode KV (64 requests x 2048 tokens, Hkv 8, d 128, page 16)
-    written by one bulk append into a shuffled pool."""
+    written by one bulk append into a shuffled pool (fp16 rows into an fp16
+    cache, bf16 rows otherwise)."""
     R, T, hkv, d, ps = 64, 2048, 8, 128, 16
     g = torch.Generator(device="cuda").manual_seed(3)
-    k = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
-    v = torch.randn(R * T, hkv, d, device="cuda", generator=g).bfloat16()
+    src = torch.float16 if dtype == torch.float16 else torch.bfloat16
+    k = torch.randn(R * T, hkv, d, device="cuda", generator=g).to(src)
+    v = torch.randn(R * T, hkv, d, device="cuda", generator=g).to(src)
     npg = R * T // ps
     pages = torch.randperm(npg + 512, device="cuda", generator=g)[:npg].int().view(R, T // ps)
     kp = torch.zeros(npg + 512, hkv, ps, d, dtype=dtype, device="cuda")
@@ -236,8 +241,9 @@ def _full_size(dtype):
     return k, v, kb, vb, flat, ks, vs, hkv, ps
 
 
-def test_full_size_bf16_append_reads_back_identically():
-    k, v, kb, vb, *_ = _full_size(torch.bfloat16)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_full_size_append_reads_back_identically(dtype):
+    k, v, kb, vb, *_ = _full_size(dtype)
     assert torch.equal(kb, k) and torch.equal(vb, v)
 
 

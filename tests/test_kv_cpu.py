@@ -51,6 +51,30 @@ def test_bf16_rne_matches_torch():
     assert np.array_equal(ours, ref)
 
 
+def test_f16_rne_matches_numpy_and_torch():
+    """binary16 encoding against numpy's and torch's IEEE conversions: every
+    representable value, the exact midpoints between neighbours (ties to
+    even), one ulp either side of them, the overflow boundary and random
+    values across the subnormal and normal range."""
+    vals = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mids = (vals[:-1].astype(np.float64) + vals[1:]) / 2        # exact in fp32
+    mids = np.append(mids, 65520.0).astype(np.float32)            # 65504 | inf
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)),
+                           np.nextafter(mids, np.float32(-np.inf))])
+    rng = np.random.default_rng(2)
+    rnd = rng.standard_normal(40000).astype(np.float32) * np.exp2(rng.integers(-28, 17, 40000))
+    x = np.concatenate([vals, mids, near, rnd, [7e4, 1e30, np.inf, 1e-30, 0.0]]).astype(np.float32)
+    x = np.concatenate([x, -x])
+    ours = oracle.f16_encode(x)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(ours, x.astype(np.float16).view(np.uint16))
+    assert np.array_equal(ours, torch.from_numpy(x).half().view(torch.int16).numpy().view(np.uint16))
+    # every finite code re-encodes to itself; overflow and NaN
+    assert np.array_equal(oracle.f16_encode(vals), np.arange(0, 0x7c00, dtype=np.uint16))
+    assert list(oracle.f16_encode([65519.99, 65520.0, -65520.0])) == [0x7bff, 0x7c00, 0xfc00]
+    assert oracle.f16_encode([np.nan])[0] & 0x7e00 == 0x7e00
+
+
 @pytest.mark.parametrize("a", [448.0, 448.0 * 2 ** -20, 449.0, 224.0, 224.5, 1.0, 3e38,
                                1e-40, 2 ** -130, 0.875, 0.8751])
 def test_pow2_scale_closed_form(a):
@@ -66,9 +90,10 @@ def test_pow2_scale_closed_form(a):
 
 @pytest.mark.parametrize("v_layout", ["dmajor", "tokmajor"])
 @pytest.mark.parametrize("csr", [False, True])
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
 def test_oracle_append_reads_back_exactly(v_layout, csr, dt):
-    c = append_case(3, dt, v_layout, csr)
+    c = append_case(3, dt, v_layout, csr,
+                    src_dtype=torch.float16 if dt == torch.float16 else torch.bfloat16)
     assert c["out"][4] == 0
     for r in range(5):
         for i in range(c["n"][r]):
