@@ -92,6 +92,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+// Round-to-nearest-even pair conversions (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32; fp32 denormals are preserved, NaN stays NaN).
+__device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ unsigned pack_f16_rne(float lo, float hi) {
+  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(unsigned, v);
+}
+
 __device__ __forceinline__ void store_out(const KParams &P, int64_t idx, float v) {
   if (P.o_f32)
     static_cast<float *>(P.out)[idx] = v;

@@ -106,21 +106,8 @@ __device__ __forceinline__ uint32_t qk_dim(bool fp8, uint32_t kb, uint32_t g4) {
   return fp8 ? 64u * (kb >> 1) + 16u * g4 + 8u * (kb & 1u) : 32u * kb + 8u * g4;
 }
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-// Round-to-nearest-even pair conversion (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
-  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(unsigned, v);
-}
-
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
-typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
-// Round-to-nearest-even pair conversion to IEEE binary16.
-__device__ __forceinline__ unsigned pack_f16_rne(float lo, float hi) {
-  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
-  return __builtin_bit_cast(unsigned, v);
-}
 
 // QK and PV MFMAs on 16-bit operands held as raw bits: bf16, or (F16) IEEE
 // binary16 for fp16 caches with fp16 Q.

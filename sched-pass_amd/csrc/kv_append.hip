@@ -170,8 +170,7 @@ template <> struct Codec<SCHED_PD_F32> {
 template <> struct Codec<SCHED_PD_BF16> {
   typedef uint2 Vec;
   __device__ static Vec enc(const float x[4], float) {
-    return make_uint2((uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16),
-                      (uint32_t)f32_to_bf16_rne(x[2]) | ((uint32_t)f32_to_bf16_rne(x[3]) << 16));
+    return make_uint2(pack_bf16_rne(x[0], x[1]), pack_bf16_rne(x[2], x[3]));
   }
   __device__ static float dec(const Vec &v, int i) {
     uint32_t w = i < 2 ? v.x : v.y;
@@ -186,15 +185,12 @@ template <> struct Codec<SCHED_PD_BF16> {
   }
 };
 
-// IEEE binary16, round to nearest even (v_cvt_f16_f32 under the default
-// rounding mode; magnitudes past 65520 become infinity, as a cast does).
+// IEEE binary16, round to nearest even (magnitudes from 65520 up become
+// infinity, as a cast does).
 template <> struct Codec<SCHED_PD_F16> {
   typedef uint2 Vec;
-  __device__ static uint32_t h(float x) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
-  }
   __device__ static Vec enc(const float x[4], float) {
-    return make_uint2(h(x[0]) | (h(x[1]) << 16), h(x[2]) | (h(x[3]) << 16));
+    return make_uint2(pack_f16_rne(x[0], x[1]), pack_f16_rne(x[2], x[3]));
   }
   __device__ static float dec(const Vec &v, int i) {
     uint32_t w = i < 2 ? v.x : v.y;

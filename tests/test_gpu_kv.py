@@ -154,6 +154,58 @@ def test_hardware_fp8_encoder_on_every_tie_and_neighbour():
     assert np.array_equal(got, ref), int(np.sum(got != ref))
 
 
+def _rounding_cases(dtype):
+    """fp32 values that pin a round-to-nearest-even conversion: for fp16 every
+    finite value, every midpoint between neighbours and the floats either
+    side of it, the overflow boundary and fp32 denormals; for bf16 random
+    fp32 bit patterns over the whole exponent range (denormals and the
+    largest finite values included) whose low 16 bits are an exact tie,
+    either side of one, zero or random. Both signs, infinities, no NaN."""
+    rng = np.random.default_rng(9)
+    if dtype == torch.float16:
+        vals = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float32)
+        mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+        mids = np.append(mids, np.float32(65520.0))
+        x = np.concatenate([vals, mids, np.nextafter(mids, np.float32(np.inf)),
+                            np.nextafter(mids, np.float32(-np.inf)), [7e4, 1e30, 1e-40, 1e-45]])
+    else:
+        hi = rng.integers(0, 1 << 16, 40000, dtype=np.uint32) << 16
+        lo = rng.choice(np.array([0x8000, 0x7fff, 0x8001, 0, 0xffff], np.uint32), 40000)
+        lo = np.where(rng.random(40000) < 0.2, rng.integers(0, 1 << 16, 40000, dtype=np.uint32), lo)
+        x = (hi | lo).astype(np.uint32).view(np.float32)
+        x = x[np.isfinite(x)]
+        x = np.concatenate([x, np.array([0x7f7f8000, 0x7f7fffff, 0x7f7f7fff, 0x00008000, 0x00018000],
+                                        np.uint32).view(np.float32)])
+    x = np.concatenate([x, [np.inf, 0.0]]).astype(np.float32)
+    return np.concatenate([x, -x])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_hardware_16bit_rounding_on_ties_neighbours_and_extremes(dtype):
+    """fp32 rows appended into a bf16 / fp16 cache (K token-major, V d-major,
+    16-token pages in order): every stored code equals torch's RNE cast of
+    its source value."""
+    x = _rounding_cases(dtype)
+    d, ps = 128, 16
+    T = ps * -(-x.size // (d * ps))
+    padded = np.zeros(T * d, np.float32)
+    padded[:x.size] = x
+    npg = T // ps
+    src = torch.from_numpy(padded.reshape(T, 1, d)).cuda()
+    k_pool = torch.zeros(npg, 1, ps, d, dtype=dtype, device="cuda")
+    v_pool = torch.zeros(npg, 1, d, ps, dtype=dtype, device="cuda")
+    table = torch.arange(npg, dtype=torch.int32, device="cuda").view(1, npg)
+    print(f"case dtype={dtype} values={x.size} rows={T}", flush=True)
+    kv_cache.append(src, src, torch.tensor([0, T], dtype=torch.int32, device="cuda"),
+                    torch.tensor([T], dtype=torch.int32, device="cuda"), k_pool, v_pool, table)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(padded).to(dtype).view(torch.int16).numpy().view(np.uint16)
+    got_k = raw(k_pool).reshape(-1)
+    got_v = raw(v_pool.permute(0, 1, 3, 2)).reshape(-1)
+    assert np.array_equal(got_k, ref), int(np.sum(got_k != ref))
+    assert np.array_equal(got_v, ref), int(np.sum(got_v != ref))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, FP8, torch.float16])
 def test_cache_prefill_then_decode_loop(dtype):
     """PagedKvCache: a prefill append, then 20 one-token appends per request
