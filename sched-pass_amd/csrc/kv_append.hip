@@ -90,36 +90,52 @@ __device__ __forceinline__ void load_src4(const void *src, int64_t idx, float x[
   }
 }
 
-// Eight consecutive source elements (16 bytes of bf16/fp16, 32 of fp32).
-template <int SRC>
-__device__ __forceinline__ void load_src8(const void *src, int64_t idx, float x[8]) {
-  if constexpr (SRC == SCHED_PD_F32) {
-    const u32x4_t a = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx));
-    const u32x4_t b = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t *>(static_cast<const float *>(src) + idx + 4));
-    x[0] = __uint_as_float(a.x), x[1] = __uint_as_float(a.y);
-    x[2] = __uint_as_float(a.z), x[3] = __uint_as_float(a.w);
-    x[4] = __uint_as_float(b.x), x[5] = __uint_as_float(b.y);
-    x[6] = __uint_as_float(b.z), x[7] = __uint_as_float(b.w);
-  } else {
-    const u32x4_t v = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(src) + idx));
-    const unsigned w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[2 * i] = half_to_f32<SRC>(w[i] & 0xffffu);
-      x[2 * i + 1] = half_to_f32<SRC>(w[i] >> 16);
-    }
+// W consecutive source elements as loaded: fp32 words, or 16-bit codes in
+// pairs, which hold a chunk in half the registers while it waits for its
+// page's fp8 scale. Elements convert to float where they are used.
+template <int SRC, int W> struct Chunk {
+  static constexpr int N = SRC == SCHED_PD_F32 ? W : W / 2;
+  uint32_t w[N];
+  __device__ __forceinline__ float operator[](int i) const {
+    if constexpr (SRC == SCHED_PD_F32)
+      return __uint_as_float(w[i]);
+    else
+      return half_to_f32<SRC>((i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu));
   }
-}
+  __device__ __forceinline__ void to_float(float x[W]) const {
+#pragma unroll
+    for (int i = 0; i < W; ++i)
+      x[i] = (*this)[i];
+  }
+  // Conversions made before this point are not reused after it (the
+  // compiler would otherwise keep the converted floats live instead of the
+  // packed codes). No instruction is emitted.
+  __device__ __forceinline__ void reload() {
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      asm volatile("" : "+v"(w[k]));
+  }
+};
 
 template <int SRC, int W>
-__device__ __forceinline__ void load_chunk(const void *src, int64_t idx, float x[W]) {
-  if constexpr (W == 8)
-    load_src8<SRC>(src, idx, x);
-  else
-    load_src4<SRC>(src, idx, x);
+__device__ __forceinline__ void load_chunk(const void *src, int64_t idx, Chunk<SRC, W> &c) {
+  typedef Chunk<SRC, W> C;
+  if constexpr (C::N == 8) {
+    const float *p = static_cast<const float *>(src) + idx;
+    const u32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    const u32x4_t b = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p + 4));
+    c.w[0] = a.x, c.w[1] = a.y, c.w[2] = a.z, c.w[3] = a.w;
+    c.w[4] = b.x, c.w[5] = b.y, c.w[6] = b.z, c.w[7] = b.w;
+  } else if constexpr (C::N == 4) {
+    const u32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(
+        static_cast<const char *>(src) + idx * (SRC == SCHED_PD_F32 ? 4 : 2)));
+    c.w[0] = a.x, c.w[1] = a.y, c.w[2] = a.z, c.w[3] = a.w;
+  } else {
+    static_assert(C::N == 2, "chunk width");
+    const u32x2_t a = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2_t *>(static_cast<const uint16_t *>(src) + idx));
+    c.w[0] = a.x, c.w[1] = a.y;
+  }
 }
 
 // Least 2^k (k >= -126) with a <= 448 * 2^k; 0 for a == 0. With
@@ -561,7 +577,7 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     slot = (threadIdx.x < hpw ? P.k_scale : P.v_scale) + page * P.Hkv + h0 + threadIdx.x % hpw;
     s_old = *slot;
   }
-  float xk[NB][W], xv[NB][W];
+  Chunk<SRC, W> xk[NB], xv[NB];
   uint32_t hh[NB], t[NB], j[NB];
 #pragma unroll
   for (uint32_t u = 0; u < NB; ++u) {
@@ -569,8 +585,8 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     hh[u] = hpw - 1; // lanes past the end add 0 to the last head
     t[u] = j[u] = 0;
 #pragma unroll
-    for (int i = 0; i < W; ++i)
-      xk[u][i] = xv[u][i] = 0.f;
+    for (int k = 0; k < Chunk<SRC, W>::N; ++k)
+      xk[u].w[k] = xv[u].w[k] = 0u;
     if (c < total) {
       hh[u] = c / per_head;
       const uint32_t rem = c - hh[u] * per_head;
@@ -627,13 +643,21 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
   }
 
   // K: token rows
+#pragma unroll
+  for (uint32_t u = 0; u < NB; ++u) {
+    xk[u].reload();
+    xv[u].reload();
+  }
   PoolElem<KVD> *kpool = static_cast<PoolElem<KVD> *>(P.k_pool) + page * P.kps;
 #pragma unroll
   for (uint32_t u = 0; u < NB; ++u) {
-    if (u * kBlock + threadIdx.x < total)
+    if (u * kBlock + threadIdx.x < total) {
+      float x[W];
+      xk[u].to_float(x);
       store_chunk<KVD, W>(kpool + (int64_t)(h0 + hh[u]) * P.khs + (int64_t)(o0 + t[u]) * P.kts +
                               j[u],
-                          xk[u], FP8 ? S.inv[0][hh[u]] : 0.f);
+                          x, FP8 ? S.inv[0][hh[u]] : 0.f);
+    }
   }
   if (FP8 && S.any_regrow[0])
     regrow_rows<KVD>(P, S, 0, kpool, P.khs, P.kts, h0, hpw, o0);
@@ -643,10 +667,13 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     // token-major V: as K
 #pragma unroll
     for (uint32_t u = 0; u < NB; ++u) {
-      if (u * kBlock + threadIdx.x < total)
-        store_chunk<KVD, W>(vpool + (int64_t)(h0 + hh[u]) * P.vhs + (int64_t)(o0 + t[u]) * P.vts +
-                                j[u],
-                            xv[u], FP8 ? S.inv[1][hh[u]] : 0.f);
+      if (u * kBlock + threadIdx.x < total) {
+        float x[W];
+        xv[u].to_float(x);
+        store_chunk<KVD, W>(vpool + (int64_t)(h0 + hh[u]) * P.vhs +
+                                (int64_t)(o0 + t[u]) * P.vts + j[u],
+                            x, FP8 ? S.inv[1][hh[u]] : 0.f);
+      }
     }
     if (FP8 && S.any_regrow[1])
       regrow_rows<KVD>(P, S, 1, vpool, P.vhs, P.vts, h0, hpw, o0);
@@ -686,8 +713,10 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
 }
 
 // grid.x = requests x head groups, grid.y strides over the pages of the
-// longest append.
-template <int SRC, int KVD>
+// longest append. ONE: the host has checked that a whole page of the group
+// fits one round, so the two-pass code is left out (it sets the register
+// count of the kernel: 90 -> 69 for fp8, 71 -> 52 for bf16).
+template <int SRC, int KVD, bool ONE>
 __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
   __shared__ PageScales S;
   __shared__ float stage[kStageFloats];
@@ -722,7 +751,7 @@ __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
       continue;
     }
     const int64_t row0 = a0 + (pbase + o0 - pos0);
-    if ((uint64_t)hpw * (o1 - o0) * (P.d / 4) <= kFastChunks) {
+    if (ONE || (uint64_t)hpw * (o1 - o0) * (P.d / 4) <= kFastChunks) {
       if (kBatch % 2 == 0 && P.w8)
         page_one_round<SRC, KVD, (kBatch % 2 == 0 ? 8 : 4)>(P, S, stage, page, h0, hpw, o0,
                                                                 o1, row0);
@@ -730,24 +759,32 @@ __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
         page_one_round<SRC, KVD, 4>(P, S, stage, page, h0, hpw, o0, o1, row0);
       continue;
     }
-    if (KVD == SCHED_PD_FP8_E4M3)
-      page_scales<SRC>(P, S, page, h0, hpw, o0, o1, row0);
-    write_tensor<SRC, KVD>(P, S, 0, P.k_src, P.k_pool, page * P.kps, P.khs, P.kts, 1, h0, hpw,
-                               o0, o1, row0);
-    write_tensor<SRC, KVD>(P, S, 1, P.v_src, P.v_pool, page * P.vps, P.vhs, P.vts, P.vds, h0,
-                               hpw, o0, o1, row0);
+    if constexpr (!ONE) {
+      if (KVD == SCHED_PD_FP8_E4M3)
+        page_scales<SRC>(P, S, page, h0, hpw, o0, o1, row0);
+      write_tensor<SRC, KVD>(P, S, 0, P.k_src, P.k_pool, page * P.kps, P.khs, P.kts, 1, h0,
+                             hpw, o0, o1, row0);
+      write_tensor<SRC, KVD>(P, S, 1, P.v_src, P.v_pool, page * P.vps, P.vhs, P.vts, P.vds, h0,
+                             hpw, o0, o1, row0);
+    }
   }
 }
 
 typedef void (*AppendFn)(AParams);
 
-template <int SRC> AppendFn pick(uint32_t kvd) {
+template <int SRC, bool ONE> AppendFn pick(uint32_t kvd) {
   switch (kvd) {
-  case SCHED_PD_F32: return kv_append_kernel<SRC, SCHED_PD_F32>;
-  case SCHED_PD_BF16: return kv_append_kernel<SRC, SCHED_PD_BF16>;
-  case SCHED_PD_F16: return kv_append_kernel<SRC, SCHED_PD_F16>;
-  default: return kv_append_kernel<SRC, SCHED_PD_FP8_E4M3>;
+  case SCHED_PD_F32: return kv_append_kernel<SRC, SCHED_PD_F32, ONE>;
+  case SCHED_PD_BF16: return kv_append_kernel<SRC, SCHED_PD_BF16, ONE>;
+  case SCHED_PD_F16: return kv_append_kernel<SRC, SCHED_PD_F16, ONE>;
+  default: return kv_append_kernel<SRC, SCHED_PD_FP8_E4M3, ONE>;
   }
+}
+
+template <bool ONE> AppendFn pick(uint32_t src, uint32_t kvd) {
+  return src == SCHED_PD_F32    ? pick<SCHED_PD_F32, ONE>(kvd)
+         : src == SCHED_PD_BF16 ? pick<SCHED_PD_BF16, ONE>(kvd)
+                                : pick<SCHED_PD_F16, ONE>(kvd);
 }
 
 uint32_t esize(uint32_t dt) { return dt == SCHED_PD_F32 ? 4u : dt == SCHED_PD_FP8_E4M3 ? 1u : 2u; }
@@ -864,9 +901,9 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   if (gy > 65535)
     gy = 65535;
   const dim3 grid(a->num_requests * (a->num_kv_heads / hpw), (uint32_t)gy);
-  AppendFn fn = a->src_dtype == SCHED_PD_F32    ? pick<SCHED_PD_F32>(a->kv_dtype)
-                : a->src_dtype == SCHED_PD_BF16 ? pick<SCHED_PD_BF16>(a->kv_dtype)
-                                                : pick<SCHED_PD_F16>(a->kv_dtype);
+  // every page of a group fits one round whatever the append sizes are
+  const bool one = (uint64_t)hpw * a->page_size * (a->head_dim / 4) <= kFastChunks;
+  AppendFn fn = one ? pick<true>(a->src_dtype, a->kv_dtype) : pick<false>(a->src_dtype, a->kv_dtype);
   hipLaunchKernelGGL(fn, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), P);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
