@@ -48,6 +48,7 @@ struct AParams {
   uint32_t *errors;
   uint32_t hpw; // kv-heads per workgroup, divides Hkv
   uint32_t w8;  // one-round path reads and writes 8-element chunks
+  uint32_t vrow16; // d-major V rows start 16-element aligned (16-slot row stores)
 };
 
 // Source rows are fp32, bf16 or fp16 (SRC is the SCHED_PD_* code).
@@ -523,6 +524,28 @@ __device__ __forceinline__ void store_chunk(PoolElem<KVD> *p, const float x[W], 
   }
 }
 
+// Slots [o, o + 16) of one d-major V dim row, encoded and stored as 16-byte
+// stores (the row start is 16-element aligned).
+template <int KVD>
+__device__ __forceinline__ void store_row16(PoolElem<KVD> *p, const float v[16], float inv) {
+  typedef Codec<KVD> C;
+  typename C::Vec e[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    e[q] = C::enc(v + 4 * q, inv);
+  uint4 *d = reinterpret_cast<uint4 *>(p);
+  if constexpr (KVD == SCHED_PD_FP8_E4M3) {
+    d[0] = make_uint4(e[0], e[1], e[2], e[3]);
+  } else if constexpr (KVD == SCHED_PD_F32) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      d[q] = e[q];
+  } else {
+    d[0] = make_uint4(e[0].x, e[0].y, e[1].x, e[1].y);
+    d[1] = make_uint4(e[2].x, e[2].y, e[3].x, e[3].y);
+  }
+}
+
 // Chunks one lane holds in the one-round path, and the LDS stage that
 // transposes a d-major V: rows (head, appended slot) of d floats, padded by
 // one float so the four slot rows a chunk reads fall in different banks.
@@ -677,6 +700,23 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
     }
     if (FP8 && S.any_regrow[1])
       regrow_rows<KVD>(P, S, 1, vpool, P.vhs, P.vts, h0, hpw, o0);
+    return;
+  }
+
+  if (o0 == 0 && o1 == P.ps && P.vrow16) {
+    // d-major V, the whole page (no earlier slot to keep or re-encode): one
+    // item is 16 slots of one dim row, read down a stage column
+    const uint32_t rows = P.ps / 16, vper_head = d * rows, vtotal = hpw * vper_head;
+    for (uint32_t c = threadIdx.x; c < vtotal; c += kBlock) {
+      const uint32_t g = c / vper_head, rem = c - g * vper_head, jj = rem / rows;
+      const uint32_t o = (rem - jj * rows) * 16;
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        v[i] = stage[(g * nn + o + i) * row_len + jj];
+      store_row16<KVD>(vpool + (int64_t)(h0 + g) * P.vhs + (int64_t)jj * P.vds + o, v,
+                       FP8 ? S.inv[1][g] : 0.f);
+    }
     return;
   }
 
@@ -892,6 +932,9 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   P.hpw = hpw;
   // 8-element chunks (16-byte bf16 source loads) when every row the
   // one-round path touches starts on an 8-element boundary
+  P.vrow16 = vdm && a->page_size % 16 == 0 && a->v_dim_stride % 16 == 0 &&
+             a->v_head_stride % 16 == 0 && a->v_page_stride % 16 == 0 &&
+             aligned(a->v_pool, 16 * ke);
   P.w8 = a->head_dim % 8 == 0 && mult8(a->src_tok_stride) && mult8(a->src_head_stride) &&
          mult8(a->k_page_stride) && mult8(a->k_head_stride) && mult8(a->k_tok_stride) &&
          mult8(a->v_page_stride) && mult8(a->v_head_stride) && (vdm || mult8(a->v_tok_stride)) &&
