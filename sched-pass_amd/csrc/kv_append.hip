@@ -755,7 +755,7 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
 // grid.x = requests x head groups, grid.y strides over the pages of the
 // longest append. ONE: the host has checked that a whole page of the group
 // fits one round, so the two-pass code is left out (it sets the register
-// count of the kernel: 90 -> 69 for fp8, 71 -> 52 for bf16).
+// count of the kernel: 93 -> 74 VGPRs for fp8, 73 -> 57 for bf16).
 template <int SRC, int KVD, bool ONE>
 __global__ __launch_bounds__(kBlock) void kv_append_kernel(AParams P) {
   __shared__ PageScales S;
