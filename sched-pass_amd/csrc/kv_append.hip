@@ -1,6 +1,7 @@
 // kv_append.hip -- the paged KV-cache writer (sched_kv_append): appends
 // source token rows (fp32, bf16 or fp16) into the decode pools, converting to
-// fp32 / bf16 / fp16 (round to nearest even) or quantising to fp8 e4m3fn with per-(page, kv-head) power-of-two scales.
+// fp32 / bf16 / fp16 (round to nearest even) or quantising to fp8 e4m3fn
+// with per-(page, kv-head) power-of-two scales.
 //
 // One workgroup serves one request and a group of its kv-heads (all of them
 // unless a small append needs more workgroups), over a strided subset of the
@@ -9,7 +10,8 @@
 // elements fit one round (16 per lane and tensor) is written by
 // page_one_round: each lane loads its K and V chunks once (8 or 4 elements
 // each), keeps them in registers through the fp8 amax and stores them, a
-// d-major V going through an LDS stage. Larger pages take two passes:
+// d-major V going through an LDS stage (a whole page leaves it as 16-slot
+// dim rows, a partial one as 4-slot groups). Larger pages take two passes:
 //   1. fp8: max |x| of each head's appended K and V slots (LDS atomics, one
 //      per wave when its lanes share a head) -> the new scales;
 //   2. K, then V: one pass over the group's slots in storage order, four
