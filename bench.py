@@ -635,8 +635,8 @@ def cpu_baseline(torch, workloads):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              f"the decode path shards by request / kv-head with no exchange, see DESIGN.md",
+        print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}); "
+              f"the decode path shards by request / kv-head with no exchange between GPUs",
               file=sys.stderr)
         sys.exit(2)
     import torch

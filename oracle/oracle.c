@@ -1,7 +1,7 @@
 /* oracle.c -- CPU restatement of the reference's truncated paged-attention
- * path. TEST INFRASTRUCTURE ONLY: this file is the checker that the HIP
- * kernels are compared against (tests/), and the CPU baseline that bench.py
- * times beside them. No product code links, loads or calls it.
+ * path. TEST INFRASTRUCTURE ONLY: this file gives the expected values the
+ * HIP kernels are compared against (tests/), and the CPU baseline that
+ * bench.py times beside them. No product code links, loads or calls it.
  *
  * What it restates (reference file:line):
  *   - softmax decode: the online-softmax CPU reference with the -1e30 running
@@ -23,7 +23,7 @@
  *     inf, S.1111.111 = NaN) times a per-(page, kv-head) fp32 scale.
  *
  * Two precisions:
- *   ORACLE_F64: every product and sum in double -- the checker;
+ *   ORACLE_F64: every product and sum in double -- the expected values;
  *   ORACLE_F32: the reference CPU loop as written, in float with expf -- the
  *               "port" CPU baseline, parallelised over tasks with OpenMP.
  */

@@ -1,7 +1,7 @@
 """Oracle for the paged-decode hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import
-this module, and only as the checker / the timed CPU baseline; no product code
+this module, and only for expected values / the timed CPU baseline; no product code
 path imports, loads or calls anything under oracle/.
 
 The KV-cache writer's restatement is kv_append() (kv_oracle.c), with the
@@ -10,7 +10,7 @@ fp8 encoder and scale rule it uses exposed for their own pins.
 Two independent CPU restatements of the reference's truncated attention:
   * decode(): liboracle.so (oracle.c), the reference's online-softmax loop
     (test/paged_decode.cu:124-153, test/py/test_dynamic_loop.py:77-100) in
-    fp64 (the checker) or fp32 (the CPU baseline), OpenMP over tasks;
+    fp64 (the expected values) or fp32 (the CPU baseline), OpenMP over tasks;
   * numpy_decode(): the closed form out = sum_{t in kept} e^{s_t - max} v_t /
     sum_{t in kept} e^{s_t - max} in float64 numpy, written from the layout
     semantics (no argument block), used on small inputs to pin decode().

@@ -39,7 +39,7 @@ MAX_TASKS_LIMIT = 16384
 
 # Lever manifest (reference include/sched/SchedManifest.h:76-105 and its
 # mirror python/sched_rt.py:72-79): name, effect type, what it reads, and how
-# this build arms it. Order = the order the kernels apply them in.
+# this library arms it. Order = the order the kernels apply them in.
 MANIFEST = [
     ("workqueue", "acquire", "ctrl,queue", "launch with workers=W and num_tasks>0"),
     ("pi", "E1/permute", "order,ctrl", "order table (identity by default)"),

@@ -211,7 +211,7 @@ def test_page_relocation_is_invisible():
     assert np.array_equal(a, c)
 
 
-def test_f32_port_matches_f64_checker():
+def test_f32_port_matches_f64_expected_values():
     b = small_batch([512, 300, 64], 8, 8, 64, torch.float32, seed=12)
     f64 = oracle.decode(b["q"], b["k"], b["v"], b["bt"], b["ctx"], precision=F64)
     f32 = oracle.decode(b["q"], b["k"], b["v"], b["bt"], b["ctx"], precision=F32)
