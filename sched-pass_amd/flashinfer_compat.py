@@ -28,6 +28,16 @@ import kv_cache
 import sched_pd
 
 
+def _dtype(x):
+    """A torch dtype, or its name as FlashInfer also accepts ("float16")."""
+    if x is None or isinstance(x, torch.dtype):
+        return x
+    t = getattr(torch, str(x).replace("torch.", ""), None)
+    if not isinstance(t, torch.dtype):
+        raise ValueError(f"unknown dtype {x!r}")
+    return t
+
+
 class BatchDecodeWithPagedKVCacheWrapper:
     """plan() once per batch shape, run() per step (FlashInfer's contract).
     `workspace` is accepted for signature compatibility; the split-KV
@@ -46,8 +56,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
     def plan(self, indptr, indices, last_page_len, num_qo_heads: int, num_kv_heads: int,
              head_dim: int, page_size: int, *, pos_encoding_mode: str = "NONE",
              window_left: int = -1, logits_soft_cap: float | None = None,
-             data_type=torch.float16, q_data_type=None, sm_scale: float | None = None,
-             **unused) -> None:
+             data_type=None, q_data_type=None, kv_data_type=None,
+             sm_scale: float | None = None, **unused) -> None:
         if pos_encoding_mode != "NONE" or window_left != -1 or logits_soft_cap not in (None, 0.0):
             raise ValueError("only plain softmax attention is supported (no positional "
                              "encoding, window or soft cap)")
@@ -58,6 +68,10 @@ class BatchDecodeWithPagedKVCacheWrapper:
                         (last_page_len, "last_page_len")):
             if not isinstance(t, torch.Tensor) or t.dtype != torch.int32:
                 raise ValueError(f"{what} must be an int32 tensor")
+        if data_type is not None and kv_data_type is not None and \
+                _dtype(data_type) != _dtype(kv_data_type):
+            raise ValueError(f"data_type {data_type} and kv_data_type {kv_data_type} differ")
+        kv_dt = _dtype(kv_data_type) or _dtype(data_type) or torch.float16
         dev = indices.device
         indptr = indptr.to(dev).contiguous()
         last = last_page_len.to(dev).contiguous()
@@ -65,8 +79,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
             "indptr": indptr, "indices": indices.contiguous(),
             "ctx": kv_cache.ctx_lens_from_last_page_len(indptr, last, page_size).contiguous(),
             "hq": int(num_qo_heads), "hkv": int(num_kv_heads), "d": int(head_dim),
-            "page": int(page_size), "kv_dtype": data_type,
-            "q_dtype": q_data_type or data_type, "sm_scale": sm_scale,
+            "page": int(page_size), "kv_dtype": kv_dt,
+            "q_dtype": _dtype(q_data_type) or kv_dt, "sm_scale": sm_scale,
         }
 
     def _views(self, kv):
