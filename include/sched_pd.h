@@ -157,7 +157,10 @@ bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
  *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
  *   V: v_pool + page*v_page_stride + h*v_head_stride + t*v_tok_stride + j*v_dim_stride
  * (strides in elements). Request r's page b is block_table[r*bt_stride + b],
- * or block_table[page_indptr[r] + b] when page_indptr is not NULL.
+ * or block_table[page_indptr[r] + b] when page_indptr is not NULL. Page
+ * ids are not bounds-checked on the device (as in the reference's kernels):
+ * every page a request's context reaches must lie in the pools (the Python
+ * layer's check_tables verifies this on the host).
  * Task id = r*num_kv_heads + h; the lever tables are indexed by task. */
 typedef struct SchedDecodeArgs {
   uint32_t abi_version; /* SCHED_PD_ABI_VERSION */

@@ -49,10 +49,12 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                tau_scope=abi.TAU_PREFIX, lin_w=None, lin_w_period=0,
                plane=None, rt_tables=False, workers=0, pf_dist=0, flags=0,
                policy=(1.0, 1.0, 0.25), tiles=None, tile_pages=0,
-               workspace=None) -> abi.SchedDecodeArgs:
+               workspace=None, check_tables=False) -> abi.SchedDecodeArgs:
     """Fill a SchedDecodeArgs from tensors (no launch). With `tiles` (from
     plan_tiles) long tasks run as several work items; the workspace is taken
-    from a per-device cache unless one is given."""
+    from a per-device cache unless one is given. The kernels trust the page
+    table (as the reference's do); check_tables=True verifies it on the host
+    first (check_page_table; this synchronises)."""
     a = abi.default_args()
     linear = mode == abi.LINEAR
     a.mode = mode
@@ -119,6 +121,13 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
             raise ValueError("block_table must be [num_requests, max_pages] without page_indptr")
         a.bt_stride = block_table.stride(0)
     a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
+    if check_tables:
+        check_page_table(block_table, ctx_lens, ps, num_pages, page_indptr=page_indptr,
+                         ctx_in_pages=bool(flags & abi.FLAG_CTX_IN_PAGES))
+        if a.kv_dtype == abi.FP8_E4M3:
+            for t, what in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+                if t is None or t.numel() < num_pages * hkv:
+                    raise ValueError(f"fp8 pools need {what} with {num_pages * hkv} entries")
     a.sm_scale = 0.0 if sm_scale is None else float(sm_scale)
     a.tau_scope = tau_scope
     a.pf_dist = pf_dist
@@ -168,6 +177,37 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
 
 
 _WS = {}
+
+
+def check_page_table(block_table, ctx_lens, page_size: int, num_pages: int, *,
+                     page_indptr=None, ctx_in_pages: bool = False) -> None:
+    """Raise ValueError unless every page a request's context reaches is in
+    its table row (2-D block table) or CSR segment, and is a pool page id in
+    [0, num_pages). Host-side check (copies the tables; synchronises)."""
+    ctx = ctx_lens.detach().cpu().numpy().astype(np.int64)
+    if (ctx < 0).any():
+        raise ValueError(f"negative context length for request {int(np.argmax(ctx < 0))}")
+    need = ctx if ctx_in_pages else -(-ctx // page_size)
+    bt = block_table.detach().cpu().numpy()
+    if page_indptr is None:
+        bt = bt.reshape(ctx.size, -1)
+        if ctx.size and need.max(initial=0) > bt.shape[1]:
+            r = int(np.argmax(need > bt.shape[1]))
+            raise ValueError(f"request {r} needs {need[r]} pages, its table row has {bt.shape[1]}")
+        rows = [bt[r, :need[r]] for r in range(ctx.size)]
+    else:
+        ind = page_indptr.detach().cpu().numpy().astype(np.int64)
+        if ind.size != ctx.size + 1 or (np.diff(ind) < 0).any() or ind[0] < 0 \
+                or ind[-1] > bt.size:
+            raise ValueError("page_indptr is not a CSR index over the page list")
+        have = np.diff(ind)
+        if (need > have).any():
+            r = int(np.argmax(need > have))
+            raise ValueError(f"request {r} needs {need[r]} pages, its segment has {have[r]}")
+        rows = [bt.reshape(-1)[ind[r]:ind[r] + need[r]] for r in range(ctx.size)]
+    for r, ids in enumerate(rows):
+        if ids.size and (ids.min() < 0 or ids.max() >= num_pages):
+            raise ValueError(f"request {r} has a page id outside [0, {num_pages})")
 
 
 def workspace_for(nbytes: int, device, count_bytes: int = 0) -> torch.Tensor:

@@ -229,3 +229,30 @@ def test_block_probe_validates_arguments_without_the_gpu(schedlib):
     assert "block probe" in abi.last_error()
     assert schedlib.sched_pd_read_probe_blocks(buf, 1 << 20, ids, 4, 4095, None, None) != 0
     assert schedlib.sched_pd_read_probe_blocks(buf, 1 << 20, ids, 0, 4096, None, None) == 0
+
+
+def test_check_page_table_accepts_reachable_ids_and_names_the_bad_request():
+    import torch
+    from sched_pd import check_page_table
+    bt = torch.tensor([[3, 1, -1], [0, 2, 4]], dtype=torch.int32)
+    ctx = torch.tensor([17, 33], dtype=torch.int32)     # 2 and 3 pages of 16
+    check_page_table(bt, ctx, 16, 5)                     # -1 past the reach is fine
+    with pytest.raises(ValueError, match="request 1 has a page id"):
+        check_page_table(bt, ctx, 16, 4)                 # page 4 of a 4-page pool
+    with pytest.raises(ValueError, match="request 0 has a page id"):
+        check_page_table(bt, torch.tensor([33, 1], dtype=torch.int32), 16, 5)  # reaches -1
+    with pytest.raises(ValueError, match="request 1 needs 4 pages"):
+        check_page_table(bt, torch.tensor([1, 49], dtype=torch.int32), 16, 5)
+    with pytest.raises(ValueError, match="negative"):
+        check_page_table(bt, torch.tensor([1, -1], dtype=torch.int32), 16, 5)
+    check_page_table(bt, torch.tensor([2, 3], dtype=torch.int32), 16, 5, ctx_in_pages=True)
+    # CSR
+    ind = torch.tensor([0, 2, 5], dtype=torch.int32)
+    flat = torch.tensor([3, 1, 0, 2, 4], dtype=torch.int32)
+    check_page_table(flat, ctx, 16, 5, page_indptr=ind)
+    with pytest.raises(ValueError, match="request 0 needs 3 pages, its segment has 2"):
+        check_page_table(flat, torch.tensor([40, 1], dtype=torch.int32), 16, 5, page_indptr=ind)
+    with pytest.raises(ValueError, match="CSR"):
+        check_page_table(flat, ctx, 16, 5, page_indptr=torch.tensor([0, 3, 2], dtype=torch.int32))
+    with pytest.raises(ValueError, match="CSR"):
+        check_page_table(flat, ctx, 16, 5, page_indptr=torch.tensor([0, 2, 6], dtype=torch.int32))

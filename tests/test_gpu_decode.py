@@ -364,8 +364,13 @@ def test_csr_page_table():
     flat = torch.tensor(np.concatenate([bt[r, :npg[r]] for r in range(3)]), dtype=torch.int32,
                         device="cuda")
     a = run(b)
-    c = run(b, bt=flat, page_indptr=indptr)
+    c = run(b, bt=flat, page_indptr=indptr, check_tables=True)
     assert torch.equal(a, c)
+    # the host check refuses a table whose reach leaves the pool, before launch
+    bad = flat.clone()
+    bad[-1] = b["k_pool"].shape[0]
+    with pytest.raises(ValueError, match="request 2 has a page id"):
+        run(b, bt=bad, page_indptr=indptr, check_tables=True)
 
 
 # --- levers that must not change a bit ---------------------------------------
