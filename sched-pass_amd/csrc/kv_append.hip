@@ -942,7 +942,11 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
          mult8(a->v_page_stride) && mult8(a->v_head_stride) && (vdm || mult8(a->v_tok_stride)) &&
          aligned(a->k_src, 8 * se) && aligned(a->v_src, 8 * se) && aligned(a->k_pool, 8 * ke) &&
          aligned(a->v_pool, 8 * ke);
-  uint64_t gy = (uint64_t)(max_app + a->page_size - 1) / a->page_size + 1;
+  // pages an append of max_app tokens can touch: a run of n >= 1 slots
+  // starting anywhere in a page spans at most (n + page - 2) / page + 1 pages
+  // (one page for a single token); the page loop strides by grid.y, so any
+  // grid.y >= 1 writes every page
+  uint64_t gy = max_app ? (uint64_t)(max_app + a->page_size - 2) / a->page_size + 1 : 1;
   if (gy > 65535)
     gy = 65535;
   const dim3 grid(a->num_requests * (a->num_kv_heads / hpw), (uint32_t)gy);
