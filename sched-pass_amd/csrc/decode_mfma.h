@@ -1,7 +1,8 @@
 // decode_mfma.h -- the GQA decode kernel on the CDNA4 matrix cores:
-// bf16 or fp8-e4m3fn KV, head dim 128, page size 16, up to 16 q-heads per
-// kv-head (one MFMA column block), bf16 Q; and the linear contraction over the
-// same V stream (LINEAR: no K, weights as MFMA column 0).
+// bf16 or fp8-e4m3fn KV with bf16 Q, or fp16 KV with fp16 Q (F16), head dim
+// 128, pages of 16..256 tokens, up to 16 q-heads per kv-head (one MFMA
+// column block); and the linear contraction over the same V stream (LINEAR:
+// no K, weights as MFMA column 0).
 //
 // Layout it reads (one (page, kv-head) chunk each for K and V):
 //   K: 16 token rows x 128 dims, dims contiguous (row stride k_tok_stride);
@@ -21,7 +22,7 @@
 //       whole rows (fp8) and trade these 4-token slices across lane rows
 //       with v_permlane16/32_swap (bf16_v_operands, fp8_v_operands).
 //
-// Token-major V (FlashInfer's NHD / HND caches, bf16): a lane loads dims
+// Token-major V (FlashInfer's NHD / HND caches, 16-bit): a lane loads dims
 // 8*(lane%16)..+7 of tokens 4*(lane/16)..+3 (four 16-byte row pieces), and
 // MFMA row lane%16 of dim block blk stands for dim 8*(lane%16) + blk, so each
 // block's A operand is two v_perm_b32 of the lane's own registers; the state

@@ -70,6 +70,9 @@ constexpr int mfma_du(bool fp8, bool vt) {
 #define SCHED_PD_MFMA_F16(PRE)                                                                   \
   SCHED_PD_MFMA_SOFTMAX(PRE, false, false, false, true)                                          \
   SCHED_PD_MFMA_SOFTMAX(PRE, false, true, false, true)
+#define SCHED_PD_MFMA_F16_PAGEBLOCKS(PRE)                                                        \
+  SCHED_PD_MFMA_SOFTMAX(PRE, false, false, true, true)                                           \
+  SCHED_PD_MFMA_SOFTMAX(PRE, false, true, true, true)
 
 // VALU kernels: kv element type x head dim, each for 1 / 4 / 16 q-heads per
 // kv-head and the linear mode.
@@ -95,4 +98,5 @@ constexpr int mfma_du(bool fp8, bool vt) {
   SCHED_PD_MFMA_BF16_PAGEBLOCKS(extern)                                                          \
   SCHED_PD_MFMA_FP8(extern)                                                                      \
   SCHED_PD_MFMA_F16(extern)                                                                      \
+  SCHED_PD_MFMA_F16_PAGEBLOCKS(extern)                                                           \
   SCHED_PD_VALU_ALL(extern)

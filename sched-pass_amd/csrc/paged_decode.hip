@@ -53,13 +53,13 @@ uint32_t elem_bytes(uint32_t dt) {
 }
 
 // fp16 cache with fp16 Q: 16-byte page-16 layouts, softmax mode.
-template <bool VT> KernelFn mfma_kernel_f16(uint32_t G) {
+template <bool VT, bool PG = false> KernelFn mfma_kernel_f16(uint32_t G) {
   constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT);
   if (G <= 4)
-    return decode_mfma<false, NW, 4, DS, DU, false, VT, false, true>;
+    return decode_mfma<false, NW, 4, DS, DU, false, VT, PG, true>;
   if (G <= 8)
-    return decode_mfma<false, NW, 8, DS, DU, false, VT, false, true>;
-  return decode_mfma<false, NW, 16, DS, DU, false, VT, false, true>;
+    return decode_mfma<false, NW, 8, DS, DU, false, VT, PG, true>;
+  return decode_mfma<false, NW, 16, DS, DU, false, VT, PG, true>;
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -85,13 +85,13 @@ WsLayout ws_layout(const SchedDecodeArgs *a) {
   return L;
 }
 
-// V token-major (dims contiguous, 16-byte aligned token rows): bf16 only.
+// V token-major (dims contiguous, 16-byte aligned token rows): 16-bit KV only.
 bool v_token_major(const SchedDecodeArgs *a) {
   return a->v_dim_stride == 1 && a->v_tok_stride != 1;
 }
 
 // The MFMA kernel's shape: bf16/fp8 KV with bf16 Q (or fp16 KV with fp16 Q,
-// softmax, page 16), d 128, pages of 16..256 tokens (a power of two), K rows
+// softmax), d 128, pages of 16..256 tokens (a power of two), K rows
 // dims-contiguous, V d-major rows of one page (or, 16-bit, token-major rows),
 // G <= 16, 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
@@ -99,7 +99,7 @@ bool mfma_applies(const SchedDecodeArgs *a) {
     return false;
   const bool linear = a->mode == SCHED_PD_LINEAR;
   if (a->kv_dtype == SCHED_PD_F16) {
-    if (linear || a->q_dtype != SCHED_PD_F16 || a->page_size != 16)
+    if (linear || a->q_dtype != SCHED_PD_F16)
       return false;
   } else {
     if (!linear && a->q_dtype != SCHED_PD_BF16)
@@ -254,7 +254,9 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   if (mfma) {
     const bool pg = a->page_size > 16;
     if (a->kv_dtype == SCHED_PD_F16)
-      sel->fn = v_token_major(a) ? mfma_kernel_f16<true>(G) : mfma_kernel_f16<false>(G);
+      sel->fn = v_token_major(a) ? (pg ? mfma_kernel_f16<true, true>(G) : mfma_kernel_f16<true>(G))
+                                 : (pg ? mfma_kernel_f16<false, true>(G)
+                                       : mfma_kernel_f16<false>(G));
     else if (a->kv_dtype != SCHED_PD_BF16)
       sel->fn = pg ? mfma_kernel<true, false, true>(G, linear) : mfma_kernel<true>(G, linear);
     else if (v_token_major(a))

@@ -125,7 +125,7 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(**f16)) == 1                            # fp16 cache + Q
     assert kind(schedlib, fake_args(v_tok_stride=1024, v_dim_stride=1, **f16)) == 1  # NHD
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.BF16)) == 0
-    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32, **f16)) == 0
+    assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32, **f16)) == 1   # fp16, 32-token pages
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.FP8_E4M3)) == -1
 
 

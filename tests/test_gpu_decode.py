@@ -166,15 +166,19 @@ PG_CTX = [1, 15, 16, 17, 33, 100, 511, 5000]
 @pytest.mark.parametrize("ps", [32, 64, 256])
 @pytest.mark.parametrize("kvt,layout", [(torch.bfloat16, "dmajor"),
                                         (torch.float8_e4m3fn, "dmajor"),
-                                        (torch.bfloat16, "tokmajor")])
+                                        (torch.bfloat16, "tokmajor"),
+                                        (torch.float16, "tokmajor"),
+                                        (torch.float16, "dmajor")])
 def test_pages_of_more_than_16_tokens(ps, kvt, layout):
     """Pages of 32..256 tokens run on the MFMA kernel as 16-token blocks
     (block b is sub-block b % m of table entry b / m): oracle parity for
     GQA 4 and 7, and pi reversed under the queue over split tiles (in pages)
-    against the static grid over the same tiles."""
+    against the static grid over the same tiles. fp16 caches take fp16 Q."""
     for hq, hkv in ((32, 8), (28, 4)):
         b = workloads.make_batch(np.asarray(PG_CTX), num_q_heads=hq, num_kv_heads=hkv,
-                                 page_size=ps, kv_dtype=kvt, seed=ps + hq, device="cuda")
+                                 page_size=ps, kv_dtype=kvt, seed=ps + hq, device="cuda",
+                                 q_dtype=torch.float16 if kvt == torch.float16 else
+                                 torch.bfloat16)
         if layout == "tokmajor":
             b = token_major(b)
         out = run(b, v_layout=layout)
@@ -264,12 +268,13 @@ def test_fp16_cache_parity(hq, hkv):
 
 
 def test_fp16_shapes_off_the_mfma_path():
-    """fp16 caches the MFMA kernel does not take (32-token pages, fp32 Q,
-    the linear mode) run on the VALU kernel against the oracle."""
+    """fp16 caches on the VALU kernel against the oracle: 32-token pages with
+    the MFMA kernel switched off, and what the MFMA kernel does not take
+    (fp32 Q, the linear mode)."""
     b = workloads.make_batch(np.asarray([100, 700, 33]), num_q_heads=32, num_kv_heads=8,
                              page_size=32, kv_dtype=torch.float16, q_dtype=torch.float16,
                              seed=5, device="cuda")
-    out = run(b)
+    out = run(b, flags=abi.FLAG_FORCE_VALU)
     assert mixed_err(out.cpu(), ref(b)) <= TOL_BF16
     b = batch([100, 700, 33], kv=torch.float16, qd=torch.float32, seed=6)
     assert mixed_err(run(b).cpu(), ref(b)) <= TOL_BF16

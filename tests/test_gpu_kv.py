@@ -206,17 +206,21 @@ def test_hardware_16bit_rounding_on_ties_neighbours_and_extremes(dtype):
     assert np.array_equal(got_v, ref), int(np.sum(got_v != ref))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8, torch.float16])
-def test_cache_prefill_then_decode_loop(dtype):
+@pytest.mark.parametrize("dtype,ps", [(torch.bfloat16, 16), (FP8, 16), (torch.float16, 16),
+                                      (torch.bfloat16, 32), (FP8, 32), (torch.float16, 32)])
+def test_cache_prefill_then_decode_loop(dtype, ps):
     """PagedKvCache: a prefill append, then 20 one-token appends per request
     (page boundaries crossed), mirrored on the oracle; then a decode step over
     the cache against the oracle decode on the same pools. An fp16 cache is
     fed fp16 rows and decoded with fp16 Q (the reference's FlashInfer serving
-    dtype), the others bf16."""
+    dtype), the others bf16. 32-token pages: a bf16 cache keeps V
+    token-major, an fp8 one d-major."""
     half = torch.float16 if dtype == torch.float16 else torch.bfloat16
     rng = np.random.default_rng(21)
-    hkv, hq, d, ps, R = 8, 32, 128, 16, 6
-    cache = kv_cache.PagedKvCache(64, hkv, d, ps, dtype=dtype)
+    hkv, hq, d, R = 8, 32, 128, 6
+    cache = kv_cache.PagedKvCache(64 if ps == 16 else 40, hkv, d, ps, dtype=dtype)
+    lay = cache.v_layout
+    assert lay == ("tokmajor" if ps > 16 and dtype != FP8 else "dmajor")
     rids = list(range(R))
     for r in rids:
         cache.add_request(r)
@@ -234,7 +238,7 @@ def test_cache_prefill_then_decode_loop(dtype):
         as_t = (lambda a: torch.from_numpy(a).view(FP8)) if dtype == FP8 else \
                (lambda a: torch.from_numpy(a.view(np.int16)).view(dtype))
         kp, vp, ks, vs, err = oracle.kv_append(k, v, app, ctx.cpu().numpy(), as_t(host[0]),
-                                               as_t(host[1]), bt.cpu().numpy(),
+                                               as_t(host[1]), bt.cpu().numpy(), v_layout=lay,
                                                k_scale=host[2], v_scale=host[3])
         assert err == 0
         host[:] = [kp, vp, ks, vs]
@@ -253,11 +257,11 @@ def test_cache_prefill_then_decode_loop(dtype):
     cache.decode(q, rids, out=out)
     bt, ctx = cache.block_table(rids)
     ref = oracle.decode(q, cache.k_pool, cache.v_pool, bt, ctx, k_scale=cache.k_scale,
-                        v_scale=cache.v_scale)
+                        v_scale=cache.v_scale, v_layout=lay)
     r = np.asarray(ref, np.float64)
     err = float(np.max(np.abs(out.cpu().double().numpy() - r) / (1 + np.abs(r))))
     assert err <= TOL_BF16
-    args = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out,
+    args = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out, v_layout=lay,
                                k_scale=cache.k_scale, v_scale=cache.v_scale)
     assert sched_pd.kernel_kind(args) == "mfma"
 

@@ -321,3 +321,19 @@ def test_cache_append_rolls_back_a_rejected_launch():
     assert c.allocator.num_free == 8
     with pytest.raises(ValueError):
         c.append(["a", "a"], rows, rows, [2, 3])
+
+
+def test_cache_v_layout_choice():
+    """token-major V for 16-bit caches with pages above 16 tokens, d-major
+    otherwise (fp8, or 16-token pages)."""
+    fp8 = torch.float8_e4m3fn
+    for dt, ps, lay in ((torch.bfloat16, 16, "dmajor"), (torch.bfloat16, 32, "tokmajor"),
+                        (torch.float16, 64, "tokmajor"), (fp8, 32, "dmajor"),
+                        (torch.float32, 32, "dmajor")):
+        c = PagedKvCache(4, 2, 8, page_size=ps, dtype=dt, device="cpu")
+        assert c.v_layout == lay
+        assert tuple(c.v_pool.shape) == ((4, 2, 8, ps) if lay == "dmajor" else (4, 2, ps, 8))
+    c = PagedKvCache(4, 2, 8, page_size=32, dtype=torch.bfloat16, device="cpu", v_layout="dmajor")
+    assert tuple(c.v_pool.shape) == (4, 2, 8, 32)
+    with pytest.raises(ValueError):
+        PagedKvCache(4, 2, 8, page_size=32, device="cpu", v_layout="hnd")
