@@ -1,7 +1,7 @@
 """Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
-                    [--sections hetero,shed,fp8,kv,layouts,pi]
+                    [--sections hetero,shed,fp8,kv,layouts,pi,trace]
 
 One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
 Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
-    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi",
+    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi,trace",
                    help="comma list of the extra measurements: hetero, shed, fp8, kv, "
                         "layouts, pi")
     p.add_argument("--no-cpu", action="store_true")
@@ -587,6 +587,117 @@ def bench_pi_makespan(torch, sched_pd, batch_sizes=(256, 1024, 4096, 8192)):
     return res
 
 
+def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
+    """The reference's serving-trace evaluation (test/py/eval_trace.py:36-160,
+    published at README.md:95-118): NSEQ requests of one fp32 head (d 32)
+    over 32-token [token][K | V] pages -- the JIT launcher's fixture format,
+    python/kernels/paged_softmax.cu -- 10% long with 24 pages, the rest 3,
+    pages packed in request order; one task per request, static grid.
+    Policies: stock (no lever tables), then with a SchedPlane armed:
+    identity, sorted ascending (longs last), LPT from the true lengths, and
+    LPT from the previous step's timer rows (closed loop: one identity step
+    fills the rows). Each policy runs `steps` steps, each timed alone with
+    events (as the reference does); mean and min per policy, outputs
+    bit-exact against identity. The regime map repeats identity against the
+    closed loop at every batch size."""
+    import numpy as np
+    import sched_abi as abi
+    from sched_rt import SchedPlane
+    SD, PT, NS, NL, PAD = 32, 32, 3, 24, 4096
+    stream = torch.cuda.current_stream()
+
+    def step_ms(a):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        sched_pd.launch(a, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    res = {"regime_lpt_timer_vs_identity_pct": {}}
+    for nseq in batch_sizes:
+        gen = torch.Generator().manual_seed(0)
+        is_long = torch.rand(nseq, generator=gen) < 0.1
+        nbl_h = torch.where(is_long, NL, NS).to(torch.int32)
+        npages = int(nbl_h.sum())
+        bt = torch.zeros(nseq, NL, dtype=torch.int32)
+        starts = torch.cumsum(nbl_h, 0) - nbl_h
+        for r in range(nseq):
+            bt[r, :nbl_h[r]] = torch.arange(int(starts[r]), int(starts[r]) + int(nbl_h[r]),
+                                            dtype=torch.int32)
+        bt, nbl = bt.cuda(), nbl_h.cuda()
+        kv = torch.randn(npages * PT * 2 * SD + PAD, device="cuda")
+        pages = kv[:npages * PT * 2 * SD].view(npages, 1, PT, 2 * SD)
+        q = torch.randn(nseq, 1, SD, device="cuda")
+        out = torch.zeros(nseq, 1, SD, device="cuda")
+        common = dict(out=out, v_layout="tokmajor", sm_scale=0.125, tau_scope=abi.TAU_PER_PAGE,
+                      flags=abi.FLAG_CTX_IN_PAGES)
+        k_view, v_view = pages[..., :SD], pages[..., SD:]
+        plane = SchedPlane(max_tasks=nseq)
+        plane.set_num_tasks(0)
+        plane.set_timer_enabled(True)
+        plane.push()
+        stock = sched_pd.build_args(q, k_view, v_view, bt, nbl, **common)
+        armed = sched_pd.build_args(q, k_view, v_view, bt, nbl, plane=plane, **common)
+        lengths = nbl_h.numpy()
+        orders = {"identity": None,
+                  "sorted_ascending": np.argsort(lengths, kind="stable").astype(np.int32),
+                  "lpt_oracle": np.argsort(-lengths, kind="stable").astype(np.int32),
+                  "lpt_timer": "timer"}
+        for _ in range(5):
+            sched_pd.launch(armed, stream)
+        row, golden, exact = {}, None, True
+        if nseq == batch_sizes[-1]:
+            t = [step_ms(stock) for _ in range(steps)]
+            row["stock"] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
+                            "min_us": round(1e3 * min(t), 2)}
+        for name, order in orders.items():
+            if nseq != batch_sizes[-1] and name not in ("identity", "lpt_timer"):
+                continue
+            if order is None:
+                plane.reset_order()
+            elif isinstance(order, str):
+                plane.reset_order()
+                plane.clear_timer()
+                sched_pd.launch(armed, stream)
+                torch.cuda.synchronize()
+                cyc = plane.read_timer()[:nseq].cpu().numpy()
+                order = np.argsort(-cyc, kind="stable").astype(np.int32)
+                nlong = int(is_long.sum())
+                row["timer_top_are_long_pct"] = round(
+                    100.0 * float(is_long.numpy()[order[:nlong]].mean()), 1)
+                plane.install_order(order, nseq)
+            else:
+                plane.install_order(order, nseq)
+            plane.push()
+            t = [step_ms(armed) for _ in range(steps)]
+            o = out.clone()
+            if golden is None:
+                golden = o
+            else:
+                exact = exact and bool(torch.equal(o, golden))
+            row[name] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
+                         "min_us": round(1e3 * min(t), 2)}
+        base = row["identity"]["mean_us"]
+        gain = round(100 * (row["lpt_timer"]["mean_us"] - base) / base, 2)
+        res["regime_lpt_timer_vs_identity_pct"][str(nseq)] = gain
+        if nseq == batch_sizes[-1]:
+            for name in ("sorted_ascending", "lpt_oracle", "lpt_timer"):
+                row[name]["vs_identity_pct"] = round(
+                    100 * (row[name]["mean_us"] - base) / base, 2)
+            st = row["stock"]["mean_us"]
+            for name in ("identity", "sorted_ascending", "lpt_oracle", "lpt_timer"):
+                row[name]["vs_stock_pct"] = round(100 * (row[name]["mean_us"] - st) / st, 2)
+            row["kv_bytes"] = npages * PT * 2 * SD * 4
+            res[str(nseq)] = row
+        res.setdefault("bit_exact_vs_identity", True)
+        res["bit_exact_vs_identity"] = res["bit_exact_vs_identity"] and exact
+        del kv, pages, q, out, plane, stock, armed
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
     the uniform workload's shape (64 requests x 2048 tokens, a pool of just
@@ -696,6 +807,8 @@ def main():
         line["kv_layouts"] = bench_layouts(torch, sched_pd, workloads)
     if "kv" in sections:
         line["kv_append"] = bench_kv_append(torch)
+    if "trace" in sections:
+        line["trace_eval"] = bench_trace_eval(torch, sched_pd)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, workloads)
     print(json.dumps(line), flush=True)
