@@ -1,7 +1,7 @@
 """Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
-                    [--sections hetero,shed,fp8,kv,layouts,pi,trace]
+                    [--sections hetero,shed,fp8,kv,layouts,pi,trace,fixture]
 
 One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
 Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
-    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi,trace",
+    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi,trace,fixture",
                    help="comma list of the extra measurements: hetero, shed, fp8, kv, "
                         "layouts, pi")
     p.add_argument("--no-cpu", action="store_true")
@@ -698,6 +698,142 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
     return res
 
 
+def _lcg_uniform(n, seed):
+    """n draws of the reference fixtures' generator (s = s*1664525 +
+    1013904223 mod 2^32, value ((s >> 8) & 0xffff) / 65536 - 0.5; test/
+    hetero_batch.cu:104-108), vectorised: within a block of B steps,
+    s_(k+j) = A_j s_k + C_j mod 2^32 with A_j, C_j the j-step affine map."""
+    import numpy as np
+    a, c, m, B = 1664525, 1013904223, (1 << 32) - 1, 4096
+    A = np.empty(B, np.uint64)
+    C = np.empty(B, np.uint64)
+    x, y = 1, 0
+    for j in range(B):           # the (j + 1)-step map
+        x, y = (x * a) & m, (y * a + c) & m
+        A[j], C[j] = x, y
+    out = np.empty(n, np.float32)
+    s = seed
+    for k in range(0, n, B):
+        st = (A * np.uint64(s) + C) & np.uint64(m)
+        w = min(B, n - k)
+        out[k:k + w] = ((st[:w] >> np.uint64(8)) & np.uint64(0xFFFF)).astype(np.float32) \
+            / 65536.0 - 0.5
+        s = int(st[B - 1])
+    return out
+
+
+def bench_fixture_hetero(torch, sched_pd, iters=100):
+    """The reference's heterogeneous-batch fixture (test/hetero_batch.cu:
+    34-330, published at README.md:135-138): the linear contraction over
+    fp32 pages of 64 tokens x d 128 (weights indexed by token-in-page), 64
+    tasks -- every 8th long with 32 pages, the rest 4 -- on the fixture's own
+    LCG inputs (seed 777) and page map. Levers come from the C runtime's
+    slots (sched_rt_*), as the fixture arms them: static grid unarmed, then
+    the ticket queue with W = 16 workers under identity, longs last, LPT from
+    one profiling step's timer rows, LPT + cache hints (longs polite, shorts
+    urgent) and longs last + hints; and the LPT order on the static grid
+    (claim loop off). Mean of `iters` back-to-back launches each; every
+    schedule bit-exact against the static grid."""
+    import ctypes
+    import numpy as np
+    import sched_abi as abi
+    lib = abi.load_library()
+    NSEQ, D, PT, LONGB, SHORTB, W, PAD = 64, 128, 64, 32, 4, 16, 8192
+    npages = NSEQ * LONGB
+    n = npages * PT * D + PAD + PT
+    vals = _lcg_uniform(n, 777)   # the fixture's generator: kv first, then w
+    kv = torch.from_numpy(vals[:npages * PT * D + PAD]).cuda()
+    w = torch.from_numpy(vals[npages * PT * D + PAD:]).cuda()
+    is_long = np.arange(NSEQ) % 8 == 0
+    nbl = torch.from_numpy(np.where(is_long, LONGB, SHORTB).astype(np.int32)).cuda()
+    bt = torch.tensor([[(t * LONGB + b * 17 + 5) % npages for b in range(LONGB)]
+                       for t in range(NSEQ)], dtype=torch.int32).cuda()
+    v_pool = kv[:npages * PT * D].view(npages, 1, PT, D)
+    out = torch.zeros(NSEQ, 1, D, device="cuda")
+    common = dict(out=out, mode=abi.LINEAR, v_layout="tokmajor", lin_w=w, lin_w_period=PT,
+                  flags=abi.FLAG_CTX_IN_PAGES)
+    stream = torch.cuda.current_stream()
+    static = sched_pd.build_args(None, None, v_pool, bt, nbl, **common)
+    queue = sched_pd.build_args(None, None, v_pool, bt, nbl, rt_tables=True, workers=W, **common)
+    static_pi = sched_pd.build_args(None, None, v_pool, bt, nbl, rt_tables=True, **common)
+
+    def mean_us(a):
+        for _ in range(3):
+            sched_pd.launch(a, stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
+            sched_pd.launch(a, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return round(1e3 * e0.elapsed_time(e1) / iters, 2)
+
+    def set_order(tasks):
+        order = np.arange(abi.SCHED_MAX_TASKS, dtype=np.int32)
+        order[:len(tasks)] = tasks
+        assert lib.sched_rt_set_order(order.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                      order.size)
+
+    lib.sched_rt_disarm()
+    sched_pd.launch(static, stream)
+    torch.cuda.synchronize()
+    golden = out.clone()
+    res = {"static_us": mean_us(static)}
+    assert lib.sched_rt_init()
+    lib.sched_rt_set_num_tasks(NSEQ)
+    assert lib.sched_rt_push_ctrl() and lib.sched_rt_queue_reset(W)
+    segregated = np.concatenate([np.flatnonzero(~is_long), np.flatnonzero(is_long)])
+    exact = True
+
+    def run(name):
+        nonlocal exact
+        out.zero_()
+        sched_pd.launch(queue, stream)
+        torch.cuda.synchronize()
+        exact = exact and bool(torch.equal(out, golden))
+        res[name + "_us"] = mean_us(queue)
+
+    set_order(np.arange(NSEQ))
+    run("identity")
+    set_order(segregated)
+    run("longs_last")
+    lib.sched_rt_timer_clear()
+    set_order(np.arange(NSEQ))
+    sched_pd.launch(queue, stream)
+    torch.cuda.synchronize()
+    cyc = np.array([lib.sched_rt_timer(t) for t in range(NSEQ)], np.float64)
+    lpt = np.argsort(-cyc, kind="stable").astype(np.int32)
+    res["timer_ranks_longs_first"] = bool(is_long[lpt[:8]].all())
+    set_order(lpt)
+    run("lpt_timer")
+    # the same order on the static grid (claim loop off: num_tasks 0)
+    lib.sched_rt_set_num_tasks(0)
+    assert lib.sched_rt_push_ctrl()
+    out.zero_()
+    sched_pd.launch(static_pi, stream)
+    torch.cuda.synchronize()
+    exact = exact and bool(torch.equal(out, golden))
+    res["static_lpt_timer_us"] = mean_us(static_pi)
+    lib.sched_rt_set_num_tasks(NSEQ)
+    assert lib.sched_rt_push_ctrl()
+    for t in range(NSEQ):
+        lib.sched_rt_set_task(t, 0.0, 0, abi.HINT_POLITE if is_long[t] else abi.HINT_URGENT)
+    assert lib.sched_rt_push_ctrl()
+    run("lpt_timer_hints")
+    set_order(segregated)
+    run("longs_last_hints")
+    lib.sched_rt_disarm()
+    res["bit_exact_vs_static"] = exact
+    res["lpt_timer_vs_identity_pct"] = round(
+        100 * (res["lpt_timer_us"] - res["identity_us"]) / res["identity_us"], 2)
+    res["queue_best_vs_static_pct"] = round(
+        100 * (min(res["identity_us"], res["lpt_timer_us"], res["longs_last_us"])
+               - res["static_us"]) / res["static_us"], 2)
+    res["kv_bytes"] = int(nbl.sum().item()) * PT * D * 4
+    return res
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
     the uniform workload's shape (64 requests x 2048 tokens, a pool of just
@@ -809,6 +945,8 @@ def main():
         line["kv_append"] = bench_kv_append(torch)
     if "trace" in sections:
         line["trace_eval"] = bench_trace_eval(torch, sched_pd)
+    if "fixture" in sections:
+        line["fixture_hetero"] = bench_fixture_hetero(torch, sched_pd)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, workloads)
     print(json.dumps(line), flush=True)
