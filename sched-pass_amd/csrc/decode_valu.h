@@ -89,6 +89,11 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
   __shared__ Acc s_acc[NW][GH][D];
   __shared__ float s_m[NW][GH];
   __shared__ float s_l[NW][GH];
+  // Page ids of the item's first kPageCache pages, read once per item: a
+  // chunk's K/V loads then wait on an LDS read instead of a dependent global
+  // load of the page table (which set the pace of single long tasks).
+  constexpr uint32_t kPageCache = 256;
+  __shared__ int32_t s_page[kPageCache];
 
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // scalar wave index
@@ -118,6 +123,13 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
         uint32_t g = idx / D, j = idx % D;
         s_q[g][j] = load_q(P, ((int64_t)r * P.Hq + h * G + g) * D + j);
       }
+    // pages [p0, p_end) hold the chunks below; the first kPageCache of them
+    // go to LDS (the previous item's reads ended before its merge barrier)
+    const uint32_t tok_end = min(R.p1 * P.ps, nload);
+    const uint32_t p_end = (tok_end + P.ps - 1) / P.ps;
+    const uint32_t ncache = p_end > R.p0 ? min(p_end - R.p0, kPageCache) : 0u;
+    for (uint32_t i = threadIdx.x; i < ncache; i += 256)
+      s_page[i] = page_of(P, r, R.p0 + i);
     __syncthreads();
 
     float m[NP], lsum[NP];
@@ -135,13 +147,14 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
 
     // 16-token chunks of this work item's pages [p0, p1), round-robin over waves
     const uint32_t cpp = P.ps / 16u;
-    const uint32_t c_end = (min(R.p1 * P.ps, nload) + 15u) / 16u;
+    const uint32_t c_end = (tok_end + 15u) / 16u;
     for (uint32_t c = R.p0 * cpp + w; c < c_end; c += NW) {
       const uint32_t pos0 = c * 16u, b = pos0 / P.ps, o = pos0 % P.ps;
-      const int64_t page = page_of(P, r, b);
+      const int64_t page = b - R.p0 < ncache ? s_page[b - R.p0] : page_of(P, r, b);
       const float ks = (fp8 && P.k_scale) ? P.k_scale[page * P.Hkv + h] : 1.f;
       const float vs = (fp8 && P.v_scale) ? P.v_scale[page * P.Hkv + h] : 1.f;
       float p_hp[NP], c_hp[NP];
+
 
       if (!LINEAR) {
         const uint32_t t = pos0 + i16;
@@ -185,6 +198,11 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
       }
 
       // PV (or the linear contraction): V for the 16 tokens at my elements.
+      // Every slot of a page this loop visits is addressable, so the loads
+      // are unconditional (issued together, not one branch each) and masked
+      // tokens are selected to 0 afterwards; a lane past D reads element D-1
+      // and drops it. (Issuing them before the score, or loading K for
+      // masked lanes too, measured slower: more VGPRs, fewer waves.)
       float v[16][EPL];
       const KVT *vbase = static_cast<const KVT *>(P.v_pool) + page * P.vps + (int64_t)h * P.vhs;
 #pragma unroll
@@ -194,8 +212,9 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
           const uint32_t d = lane + 64u * e;
-          v[i][e] = (ki && d < D) ? ldv(vbase + (int64_t)(o + i) * P.vts + (int64_t)d * P.vds) * vs
-                                  : 0.f;
+          const uint32_t dc = d < (uint32_t)D ? d : (uint32_t)D - 1u;
+          const float x = ldv(vbase + (int64_t)(o + i) * P.vts + (int64_t)dc * P.vds);
+          v[i][e] = (ki && d < D) ? x * vs : 0.f;
         }
       }
       if (LINEAR) {
@@ -203,7 +222,10 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
         for (int i = 0; i < 16; ++i) {
           const uint32_t ti = pos0 + i;
           const bool ki = ti < n && keep_pos(P, pol.budget, ti);
-          const float wi = ki ? P.lin_w[P.lin_w_period ? ti % P.lin_w_period : ti] : 0.f;
+          // weight index clamped into [0, n) (the weights cover the context)
+          const uint32_t wix = P.lin_w_period ? ti % P.lin_w_period : min(ti, n - 1u);
+          const float wv = P.lin_w[wix];
+          const float wi = ki ? wv : 0.f;
 #pragma unroll
           for (int e = 0; e < EPL; ++e)
             acc[0][e] += (double)wi * (double)v[i][e];
