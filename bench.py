@@ -18,7 +18,10 @@ makespan of the static grid and the ticket work queue (W = 2 x CU), two
 measured read ceilings (contiguous streaming, and random whole pages -- the
 decode's own access pattern -- for one step's bytes), and the CPU
 baseline (the oracle's fp32 port of the reference CPU loop, OpenMP, on a
-bounded sample, timed on this host).
+bounded sample, timed on this host). Further sections: the shed/policy and
+fp8 configurations, the cache writer, V layouts, and the reference's own
+evaluations re-run here (pi makespan through the FlashInfer wrapper, the
+serving-trace eval, the heterogeneous-batch fixture).
 """
 from __future__ import annotations
 
