@@ -22,11 +22,13 @@
 //       whole rows (fp8) and trade these 4-token slices across lane rows
 //       with v_permlane16/32_swap (bf16_v_operands, fp8_v_operands).
 //
-// Token-major V (FlashInfer's NHD / HND caches, 16-bit): a lane loads dims
-// 8*(lane%16)..+7 of tokens 4*(lane/16)..+3 (four 16-byte row pieces), and
+// Token-major V (FlashInfer's NHD / HND caches): a lane loads dims
+// 8*(lane%16)..+7 of tokens 4*(lane/16)..+3 (four 16-byte row pieces, or
+// 8-byte ones for fp8), and
 // MFMA row lane%16 of dim block blk stands for dim 8*(lane%16) + blk, so each
 // block's A operand is two v_perm_b32 of the lane's own registers; the state
-// goes to LDS with that dim order undone (bf16_vt_operand, VT).
+// goes to LDS with that dim order undone (bf16_vt_operand, fp8_vt_operands,
+// VT).
 //
 // Pages of 32..256 tokens (PG): the kernel streams 16-token blocks; block b
 // is sub-block b % m of table entry b / m (m = page / 16). A d-major V row
@@ -215,6 +217,27 @@ __device__ __forceinline__ s16x4_t bf16_vt_operand(const u32x4_t r[4], int blk) 
   return __builtin_bit_cast(s16x4_t, u32x2_t{lo, hi});
 }
 
+// Token-major fp8 V: lane (c16, g4) holds dims 8*c16..+7 of tokens 4*g4 + t
+// (t = 0..3) as 8 bytes each, v[t >> 1] dwords 2*(t & 1) (dims 0..3) and
+// 2*(t & 1) + 1 (dims 4..7). The A operand of block blk is byte blk of those
+// tokens, one token per byte: a 4 x 4 byte transpose of the low dwords
+// (blocks 0..3) and of the high ones (4..7), two v_perm_b32 per operand.
+__device__ __forceinline__ void fp8_vt_transpose(unsigned w0, unsigned w1, unsigned w2,
+                                                 unsigned w3, unsigned out[4]) {
+  const unsigned t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u); // w0.0 w1.0 w0.1 w1.1
+  const unsigned t1 = __builtin_amdgcn_perm(w3, w2, 0x05010400u); // w2.0 w3.0 w2.1 w3.1
+  const unsigned t2 = __builtin_amdgcn_perm(w1, w0, 0x07030602u); // w0.2 w1.2 w0.3 w1.3
+  const unsigned t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u); // w2.2 w3.2 w2.3 w3.3
+  out[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+__device__ __forceinline__ void fp8_vt_operands(const u32x4_t v[2], unsigned out[8]) {
+  fp8_vt_transpose(v[0].x, v[0].z, v[1].x, v[1].z, out);
+  fp8_vt_transpose(v[0].y, v[0].w, v[1].y, v[1].w, out + 4);
+}
+
 struct MfmaTask {
   uint32_t r, h, n, budget;
   int64_t row; // block-table index of the request's first page
@@ -292,7 +315,16 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
     const int64_t si = (int64_t)page * P.Hkv + T.h;
     B.ks = (!LINEAR && P.k_scale) ? P.k_scale[si] : 1.f;
     B.vs = P.v_scale ? P.v_scale[si] : 1.f;
-    if constexpr (PG) {
+    if constexpr (VT) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const u32x2_t a =
+            gload<NT>(reinterpret_cast<const u32x2_t *>(pb + (2 * t) * T.vrow_bytes + T.vlane));
+        const u32x2_t b = gload<NT>(
+            reinterpret_cast<const u32x2_t *>(pb + (2 * t + 1) * T.vrow_bytes + T.vlane));
+        B.v[t] = u32x4_t{a.x, a.y, b.x, b.y};
+      }
+    } else if constexpr (PG) {
       B.v[0] = gload<false>(reinterpret_cast<const u32x4_t *>(pb + T.vlane));
       B.v[1] = gload<false>(reinterpret_cast<const u32x4_t *>(pb + T.vblk + T.vlane));
     } else {
@@ -378,7 +410,9 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   // PV
   unsigned v8[8];
   u32x4_t vb[4];
-  if constexpr (FP8) {
+  if constexpr (FP8 && VT) {
+    fp8_vt_operands(B.v, v8);
+  } else if constexpr (FP8) {
     fp8_v_operands(B.v, v8);
   } else {
 #pragma unroll
@@ -390,7 +424,7 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
-    if constexpr (VT)
+    if constexpr (VT && !FP8)
       a = bf16_vt_operand(vb, blk);
     else if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
@@ -430,7 +464,9 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
   const s16x4_t bhi = __builtin_bit_cast(s16x4_t, hi), blo = __builtin_bit_cast(s16x4_t, lo);
   unsigned v8[8];
   u32x4_t vb[4];
-  if constexpr (FP8) {
+  if constexpr (FP8 && VT) {
+    fp8_vt_operands(B.v, v8);
+  } else if constexpr (FP8) {
     fp8_v_operands(B.v, v8);
   } else {
 #pragma unroll
@@ -442,7 +478,7 @@ __device__ __forceinline__ void linear_page(const KParams &P, const MfmaTask &T,
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     s16x4_t a;
-    if constexpr (VT)
+    if constexpr (VT && !FP8)
       a = bf16_vt_operand(vb, blk);
     else if constexpr (!FP8)
       a = __builtin_bit_cast(s16x4_t, (blk & 1) ? u32x2_t{vb[blk >> 1].z, vb[blk >> 1].w}
@@ -533,7 +569,6 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
 template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false,
           bool VT = false, bool PG = false, bool F16 = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
-  static_assert(!(VT && FP8), "token-major V is 16-bit only");
   static_assert(!(F16 && (FP8 || LINEAR)), "fp16: softmax over an fp16 cache");
   __shared__ float s_acc[NW][GMAX][128];
   __shared__ float s_m[NW][GMAX];
@@ -578,14 +613,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.w = w;
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
     // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16;
-    // token-major bf16: dims 8*c16.. of token 4*g4 (then rows 4*g4 + 1..3)
+    // token-major: dims 8*c16.. of token 4*g4 (then rows 4*g4 + 1..3)
     T.vbase = static_cast<const uint8_t *>(P.v_pool) +
-              (VT ? (int64_t)(4u * g4) * P.vts * EB + 16u * c16
+              (VT ? (int64_t)(4u * g4) * P.vts * EB + 8u * EB * c16
                : FP8 ? (int64_t)(c16 + 16u * g4) * P.vds
                      : (int64_t)(c16 + 16u * (g4 & 1u)) * P.vds * EB + 16u * (g4 >> 1));
     T.vrow_bytes = P.vts * EB;
     if constexpr (VT)
-      T.vlane = (uint32_t)(4u * g4 * (uint32_t)T.vrow_bytes + 16u * c16);
+      T.vlane = (uint32_t)(4u * g4 * (uint32_t)T.vrow_bytes + 8u * EB * c16);
     else
       T.vlane = (uint32_t)(T.vbase - static_cast<const uint8_t *>(P.v_pool));
     T.ksub = 16 * P.kts * EB;

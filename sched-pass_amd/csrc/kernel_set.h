@@ -30,12 +30,17 @@
 #ifndef SCHED_PD_MFMA_DEPTH_VT_URGENT
 #define SCHED_PD_MFMA_DEPTH_VT_URGENT 3
 #endif
+// fp8 token-major V: at the fp8 urgent depth of 6 the kernel needs 274
+// VGPRs (and spills with page blocks); 4 keeps it in the register file.
+#ifndef SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT
+#define SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT 4
+#endif
 
 namespace schedpd {
 
 constexpr int mfma_ds(bool fp8) { return fp8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH; }
 constexpr int mfma_du(bool fp8, bool vt) {
-  return fp8 ? SCHED_PD_MFMA_DEPTH_FP8_URGENT
+  return fp8 ? (vt ? SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT : SCHED_PD_MFMA_DEPTH_FP8_URGENT)
          : vt ? SCHED_PD_MFMA_DEPTH_VT_URGENT
               : SCHED_PD_MFMA_DEPTH_URGENT;
 }
@@ -67,6 +72,9 @@ constexpr int mfma_du(bool fp8, bool vt) {
 #define SCHED_PD_MFMA_FP8(PRE)                                                                   \
   SCHED_PD_MFMA_WITH_LINEAR(PRE, true, false, false)                                             \
   SCHED_PD_MFMA_WITH_LINEAR(PRE, true, false, true)
+#define SCHED_PD_MFMA_FP8_TOKMAJOR(PRE)                                                          \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, true, true, false)                                              \
+  SCHED_PD_MFMA_WITH_LINEAR(PRE, true, true, true)
 #define SCHED_PD_MFMA_F16(PRE)                                                                   \
   SCHED_PD_MFMA_SOFTMAX(PRE, false, false, false, true)                                          \
   SCHED_PD_MFMA_SOFTMAX(PRE, false, true, false, true)
@@ -97,6 +105,7 @@ constexpr int mfma_du(bool fp8, bool vt) {
   SCHED_PD_MFMA_BF16_PAGE16(extern)                                                              \
   SCHED_PD_MFMA_BF16_PAGEBLOCKS(extern)                                                          \
   SCHED_PD_MFMA_FP8(extern)                                                                      \
+  SCHED_PD_MFMA_FP8_TOKMAJOR(extern)                                                             \
   SCHED_PD_MFMA_F16(extern)                                                                      \
   SCHED_PD_MFMA_F16_PAGEBLOCKS(extern)                                                           \
   SCHED_PD_VALU_ALL(extern)

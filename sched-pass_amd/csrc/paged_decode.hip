@@ -85,14 +85,14 @@ WsLayout ws_layout(const SchedDecodeArgs *a) {
   return L;
 }
 
-// V token-major (dims contiguous, 16-byte aligned token rows): 16-bit KV only.
+// V token-major (dims contiguous, aligned token rows).
 bool v_token_major(const SchedDecodeArgs *a) {
   return a->v_dim_stride == 1 && a->v_tok_stride != 1;
 }
 
 // The MFMA kernel's shape: bf16/fp8 KV with bf16 Q (or fp16 KV with fp16 Q,
 // softmax), d 128, pages of 16..256 tokens (a power of two), K rows
-// dims-contiguous, V d-major rows of one page (or, 16-bit, token-major rows),
+// dims-contiguous, V d-major rows of one page (or token-major rows),
 // G <= 16, 16-byte aligned pools.
 bool mfma_applies(const SchedDecodeArgs *a) {
   if (a->flags & SCHED_PD_FLAG_FORCE_VALU)
@@ -113,7 +113,8 @@ bool mfma_applies(const SchedDecodeArgs *a) {
     return false;
   const int64_t eb = elem_bytes(a->kv_dtype);
   if (v_token_major(a)) {
-    if (a->kv_dtype == SCHED_PD_FP8_E4M3 || (a->v_tok_stride * eb) % 16)
+    // token rows start 16-byte (16-bit V) or 8-byte (fp8 V) aligned
+    if ((a->v_tok_stride * eb) % (a->kv_dtype == SCHED_PD_FP8_E4M3 ? 8 : 16))
       return false;
   } else if (a->v_tok_stride != 1 || a->v_dim_stride != (int64_t)ps) {
     return false;
@@ -258,7 +259,10 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
                                  : (pg ? mfma_kernel_f16<false, true>(G)
                                        : mfma_kernel_f16<false>(G));
     else if (a->kv_dtype != SCHED_PD_BF16)
-      sel->fn = pg ? mfma_kernel<true, false, true>(G, linear) : mfma_kernel<true>(G, linear);
+      sel->fn = v_token_major(a) ? (pg ? mfma_kernel<true, true, true>(G, linear)
+                                       : mfma_kernel<true, true>(G, linear))
+                : pg ? mfma_kernel<true, false, true>(G, linear)
+                     : mfma_kernel<true>(G, linear);
     else if (v_token_major(a))
       sel->fn = pg ? mfma_kernel<false, true, true>(G, linear)
                    : mfma_kernel<false, true>(G, linear);

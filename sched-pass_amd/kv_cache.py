@@ -201,12 +201,12 @@ class PagedKvCache:
     [P, Hkv, page, d] (token-major); for an fp8 cache k_scale / v_scale
     [P * Hkv] (index page * Hkv + head).
 
-    v_layout "auto" picks d-major for 16-token pages and fp8 caches, and
-    token-major for bf16/fp16 caches with larger pages: there a 16-token block
-    of a d-major V row is a partial row, and the decode measured 98 / 109 /
-    109 us for 32- / 64- / 128-token pages against 87 / 86 / 86 us
-    token-major (Llama-3-8B decode batch, 64 x 2048 tokens; 83 us either
-    way at 16)."""
+    v_layout "auto" picks d-major for 16-token pages and token-major for
+    larger ones (bf16, fp16 and fp8 caches): there a 16-token block of a
+    d-major V row is a partial row, and the decode measured 98 / 109 / 109 us
+    for 32- / 64- / 128-token bf16 pages against 87 / 86 / 86 us token-major,
+    fp8 54 / 62 us against 48 / 48 (Llama-3-8B decode batch, 64 x 2048
+    tokens; the same either way at 16)."""
 
     def __init__(self, num_pages: int, num_kv_heads: int, head_dim: int, page_size: int = 16,
                  dtype=torch.bfloat16, device="cuda", v_layout: str = "auto"):
@@ -214,8 +214,9 @@ class PagedKvCache:
         self.dtype = dtype
         self.device = torch.device(device)
         if v_layout == "auto":
-            v_layout = "tokmajor" if page_size > 16 and dtype in (torch.bfloat16,
-                                                                   torch.float16) else "dmajor"
+            v_layout = "tokmajor" if page_size > 16 and dtype in (
+                torch.bfloat16, torch.float16, getattr(torch, "float8_e4m3fn", None)) \
+                else "dmajor"
         if v_layout not in ("dmajor", "tokmajor"):
             raise ValueError(f"v_layout {v_layout!r}")
         self.v_layout = v_layout

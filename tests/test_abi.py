@@ -115,7 +115,9 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(v_tok_stride=1024, v_dim_stride=1)) == 1  # NHD rows, Hkv 8
     assert kind(schedlib, fake_args(v_tok_stride=132, v_dim_stride=1)) == 0  # rows not 16-B aligned
     assert kind(schedlib, fake_args(kv_dtype=abi.FP8_E4M3, v_tok_stride=128,
-                                    v_dim_stride=1)) == 0                    # fp8 token-major V
+                                    v_dim_stride=1)) == 1                    # fp8 token-major V
+    assert kind(schedlib, fake_args(kv_dtype=abi.FP8_E4M3, v_tok_stride=132,
+                                    v_dim_stride=1)) == 0                    # rows not 8-B aligned
     assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32)) == 1  # 2 blocks per page
     assert kind(schedlib, fake_args(page_size=256, v_dim_stride=256)) == 1
     assert kind(schedlib, fake_args(page_size=48, v_dim_stride=48)) == 0  # not a power of two

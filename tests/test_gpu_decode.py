@@ -110,15 +110,16 @@ def token_major(b):
     return c
 
 
+@pytest.mark.parametrize("kvt", [torch.bfloat16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4), (64, 4)])
-def test_token_major_v_matches_dmajor_bitwise(hq, hkv):
-    """bf16 V stored token-major (FlashInfer's HND / NHD rows) takes the MFMA
-    kernel with an in-lane operand build and a permuted dim order in its
-    accumulators; every output element sums the same products in the same
-    order as the d-major kernel, so the bits agree. Then the oracle, the
+def test_token_major_v_matches_dmajor_bitwise(hq, hkv, kvt):
+    """bf16 or fp8 V stored token-major (FlashInfer's HND / NHD rows) takes
+    the MFMA kernel with an in-lane operand build and a permuted dim order in
+    its accumulators; every output element sums the same products in the
+    same order as the d-major kernel, so the bits agree. Then the oracle, the
     VALU kernel on the same layout, and split tiles under the queue with pi
     reversed against the static grid."""
-    b = batch([1, 15, 16, 17, 300, 2048, 5000], hq=hq, hkv=hkv, seed=hq + hkv)
+    b = batch([1, 15, 16, 17, 300, 2048, 5000], hq=hq, hkv=hkv, kv=kvt, seed=hq + hkv)
     t = token_major(b)
     d_out = run(b)
     t_out = run(t, v_layout="tokmajor")
@@ -148,8 +149,9 @@ def test_token_major_v_matches_dmajor_bitwise(hq, hkv):
     assert mixed_err(st.cpu(), ref(t, v_layout="tokmajor")) <= TOL_BF16
 
 
-def test_token_major_v_linear_matches_dmajor_bitwise():
-    b = batch([16, 700, 2048, 3], seed=9)
+@pytest.mark.parametrize("kvt", [torch.bfloat16, torch.float8_e4m3fn])
+def test_token_major_v_linear_matches_dmajor_bitwise(kvt):
+    b = batch([16, 700, 2048, 3], kv=kvt, seed=9)
     t = token_major(b)
     w = torch.randn(4096, device="cuda")
     d_out = run(b, mode=abi.LINEAR, lin_w=w)
@@ -166,6 +168,7 @@ PG_CTX = [1, 15, 16, 17, 33, 100, 511, 5000]
 @pytest.mark.parametrize("ps", [32, 64, 256])
 @pytest.mark.parametrize("kvt,layout", [(torch.bfloat16, "dmajor"),
                                         (torch.float8_e4m3fn, "dmajor"),
+                                        (torch.float8_e4m3fn, "tokmajor"),
                                         (torch.bfloat16, "tokmajor"),
                                         (torch.float16, "tokmajor"),
                                         (torch.float16, "dmajor")])

@@ -213,14 +213,13 @@ def test_cache_prefill_then_decode_loop(dtype, ps):
     (page boundaries crossed), mirrored on the oracle; then a decode step over
     the cache against the oracle decode on the same pools. An fp16 cache is
     fed fp16 rows and decoded with fp16 Q (the reference's FlashInfer serving
-    dtype), the others bf16. 32-token pages: a bf16 cache keeps V
-    token-major, an fp8 one d-major."""
+    dtype), the others bf16. 32-token pages keep V token-major."""
     half = torch.float16 if dtype == torch.float16 else torch.bfloat16
     rng = np.random.default_rng(21)
     hkv, hq, d, R = 8, 32, 128, 6
     cache = kv_cache.PagedKvCache(64 if ps == 16 else 40, hkv, d, ps, dtype=dtype)
     lay = cache.v_layout
-    assert lay == ("tokmajor" if ps > 16 and dtype != FP8 else "dmajor")
+    assert lay == ("tokmajor" if ps > 16 else "dmajor")
     rids = list(range(R))
     for r in rids:
         cache.add_request(r)
