@@ -96,8 +96,27 @@ class BatchDecodeWithPagedKVCacheWrapper:
             return kv_cache.nhd_views(kv)
         return kv[:, 0], kv[:, 1]                 # HND: [P, Hkv, page, d]
 
+    def _scales(self, kv_pool, k_scale, v_scale):
+        """FlashInfer's fp8 scales are one float per tensor (default 1); the
+        kernels read one per (page, kv-head): expand (kept per value)."""
+        n = kv_pool.shape[0] * self._plan["hkv"]
+        out = []
+        for x in (k_scale, v_scale):
+            if isinstance(x, torch.Tensor) and x.numel() == n:
+                out.append(x.to(torch.float32).contiguous())
+                continue
+            val = 1.0 if x is None else float(x)
+            key = (n, val, str(kv_pool.device))
+            cache = self.__dict__.setdefault("_scale_cache", {})
+            if key not in cache:
+                cache[key] = torch.full((n,), val, dtype=torch.float32, device=kv_pool.device)
+            out.append(cache[key])
+        return out
+
     def run(self, q: torch.Tensor, paged_kv_cache, *, out: torch.Tensor | None = None,
-            **kw) -> torch.Tensor:
+            k_scale=None, v_scale=None, **kw) -> torch.Tensor:
+        """k_scale / v_scale (fp8 caches): a float per tensor as FlashInfer
+        takes them, or [P * Hkv] per-(page, kv-head) scales."""
         p = self._plan
         if p is None:
             raise RuntimeError("plan() must be called before run()")
@@ -110,6 +129,10 @@ class BatchDecodeWithPagedKVCacheWrapper:
                              f"(q {p['q_dtype']}, kv {p['kv_dtype']})")
         if out is None:
             out = torch.empty(q.shape[0], p["hq"], p["d"], dtype=q.dtype, device=q.device)
+        if k.dtype == getattr(torch, "float8_e4m3fn", None):
+            kw["k_scale"], kw["v_scale"] = self._scales(k, k_scale, v_scale)
+        elif k_scale is not None or v_scale is not None:
+            raise ValueError("k_scale / v_scale apply to fp8 caches only")
         return sched_pd.paged_decode(q.contiguous(), k, v, p["indices"], p["ctx"], out=out,
                                      page_indptr=p["indptr"], v_layout="tokmajor",
                                      sm_scale=p["sm_scale"], plane=self.plane,

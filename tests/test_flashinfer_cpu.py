@@ -74,3 +74,5 @@ def test_run_checks_the_plan_before_launching():
         w.run(q.bfloat16(), kv)
     with pytest.raises(ValueError, match="paged cache"):
         w.run(q, kv[:, 0])
+    with pytest.raises(ValueError, match="fp8 caches only"):
+        w.run(q, kv, k_scale=0.5)

@@ -111,3 +111,39 @@ def test_plan_and_run_reject_what_they_cannot_honour():
     w.plan(indptr, indices, last, 8, 8, 128, 16, data_type=torch.bfloat16)
     with pytest.raises(ValueError):
         w.run(q, kv)      # fp16 cache against a bf16 plan
+
+
+def test_fp8_nhd_cache_with_flashinfer_scales():
+    """An fp8 e4m3fn NHD cache with bf16 Q, FlashInfer's per-tensor k_scale /
+    v_scale floats: the MFMA kernel on the cache in place (token-major fp8 V)
+    against the oracle on the same codes and scales."""
+    import kv_cache
+    torch.manual_seed(5)
+    bs, max_pages, page, nqo, nkv, hd = 6, 9, 16, 16, 4, 128
+    pages = torch.tensor([1, 9, 4, 7, 2, 5], dtype=torch.int32)
+    indptr = torch.zeros(bs + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(pages, 0)
+    npg = int(indptr[-1])
+    indptr = indptr.cuda()
+    indices = torch.randperm(npg + 3)[:npg].to(torch.int32).cuda()
+    last = torch.tensor([16, 3, 9, 16, 1, 12], dtype=torch.int32).cuda()
+    kv = torch.randn(npg + 3, 2, page, nkv, hd, device="cuda").to(torch.float8_e4m3fn)
+    q = (torch.randn(bs, nqo, hd, device="cuda") / hd ** 0.5).bfloat16()
+    w = BatchDecodeWithPagedKVCacheWrapper(None, "NHD")
+    w.plan(indptr, indices, last, nqo, nkv, hd, page, data_type=torch.float8_e4m3fn,
+           q_data_type=torch.bfloat16)
+    out = w.run(q, kv, k_scale=0.0625, v_scale=0.125)
+    torch.cuda.synchronize()
+    kview, vview = kv_cache.nhd_views(kv)
+    args = sched_pd.build_args(q, kview, vview, indices, w._plan["ctx"],
+                               out=torch.empty_like(out), page_indptr=indptr,
+                               v_layout="tokmajor", k_scale=w._scales(kview, 0.0625, 0.125)[0],
+                               v_scale=w._scales(kview, 0.0625, 0.125)[1])
+    assert sched_pd.kernel_kind(args) == "mfma"
+    n = (npg + 3) * nkv
+    ref = np.asarray(oracle.decode(q, kview, vview, indices, w._plan["ctx"],
+                                   page_indptr=indptr, v_layout="tokmajor",
+                                   k_scale=torch.full((n,), 0.0625),
+                                   v_scale=torch.full((n,), 0.125)), np.float64)
+    got = out.float().cpu().double().numpy()
+    assert float(np.max(np.abs(got - ref) / (1 + np.abs(ref)))) <= 2e-3
