@@ -82,6 +82,9 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
   constexpr int NP = (GH + 3) / 4;       // score passes (4 heads per pass)
   constexpr int EPL = D >= 64 ? D / 64 : 1;
   constexpr int VN = Vec16<KVT>::N;
+  // K loads unrolled in the score: fp8 converts 16 values per load, so 2
+  // (not 4) in flight keep it in the register file (4 spilled to AGPRs)
+  constexpr int kScoreUnroll = VN == 16 ? 2 : 4;
   __shared__ float s_q[GH][D];
   // Linear mode accumulates in double: an unnormalised sum of thousands of
   // products loses the fp32 tolerance in float; the mode is bandwidth-bound.
@@ -168,7 +171,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
           float dot = 0.f;
           if (act) {
             const float *qh = s_q[head];
-#pragma unroll 4
+#pragma unroll kScoreUnroll
             for (int j0 = 0; j0 < D; j0 += VN) {
               uint4 raw = *reinterpret_cast<const uint4 *>(krow + j0);
               float f[VN];

@@ -1,0 +1,42 @@
+"""The built library's gfx950 code objects, read from their metadata notes:
+every kernel runs without scratch memory (no register spills to private
+memory) and spills no VGPRs. Skipped when the library is not built or the
+ROCm LLVM tools are absent."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "sched-pass_amd", "libschedpd.so")
+LLVM = "/opt/rocm/llvm/bin"
+
+
+def notes(tmp_path):
+    objdump, readelf = os.path.join(LLVM, "llvm-objdump"), os.path.join(LLVM, "llvm-readelf")
+    if not (os.path.exists(LIB) and os.path.exists(objdump) and os.path.exists(readelf)):
+        pytest.skip("library or ROCm LLVM tools not available")
+    lib = tmp_path / "lib.so"
+    shutil.copy(LIB, lib)
+    subprocess.run([objdump, "--offloading", str(lib)], cwd=tmp_path, check=True,
+                   capture_output=True, timeout=120)
+    objs = sorted(p for p in tmp_path.iterdir() if p.name.endswith("gfx950"))
+    assert objs, "no gfx950 code object in the library"
+    out = subprocess.run([readelf, "--notes", *map(str, objs)], check=True,
+                         capture_output=True, text=True, timeout=120).stdout
+    return out
+
+
+def test_every_kernel_runs_without_scratch_or_spills(tmp_path):
+    out = notes(tmp_path)
+    names = re.findall(r"^\s+\.name:\s+(\S+)$", out, re.M)
+    kernels = [n for n in names if "decode_" in n or "kv_append" in n or "probe" in n]
+    assert len(kernels) >= 100
+    scratch = [int(x) for x in re.findall(r"\.private_segment_fixed_size:\s+(\d+)", out)]
+    assert scratch and all(x == 0 for x in scratch), scratch
+    # VGPR spills would go to AGPRs or scratch; SGPR spills land in VGPR
+    # lanes (v_writelane), not in memory, and are not checked
+    counts = [int(x) for x in re.findall(r"\.vgpr_spill_count:\s+(\d+)", out)]
+    assert counts and all(x == 0 for x in counts), counts
