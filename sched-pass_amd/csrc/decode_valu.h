@@ -75,9 +75,16 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Waves per workgroup (one workgroup per work item). Overridable at build
+// time for tuning sweeps.
+#ifndef SCHED_PD_VALU_NW
+#define SCHED_PD_VALU_NW 4
+#endif
+
 template <typename KVT, int D, int GMAX, bool LINEAR>
-__global__ void __launch_bounds__(256) decode_valu(KParams P) {
-  constexpr int NW = 4;
+__global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) {
+  constexpr int NW = SCHED_PD_VALU_NW;
+  constexpr uint32_t NT = NW * 64;
   constexpr int GH = LINEAR ? 1 : GMAX;  // head rows of state
   constexpr int NP = (GH + 3) / 4;       // score passes (4 heads per pass)
   constexpr int EPL = D >= 64 ? D / 64 : 1;
@@ -122,7 +129,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
     const bool fp8 = sizeof(KVT) == 1;
 
     if (!LINEAR)
-      for (uint32_t idx = threadIdx.x; idx < G * D; idx += 256) {
+      for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
         uint32_t g = idx / D, j = idx % D;
         s_q[g][j] = load_q(P, ((int64_t)r * P.Hq + h * G + g) * D + j);
       }
@@ -131,7 +138,7 @@ __global__ void __launch_bounds__(256) decode_valu(KParams P) {
     const uint32_t tok_end = min(R.p1 * P.ps, nload);
     const uint32_t p_end = (tok_end + P.ps - 1) / P.ps;
     const uint32_t ncache = p_end > R.p0 ? min(p_end - R.p0, kPageCache) : 0u;
-    for (uint32_t i = threadIdx.x; i < ncache; i += 256)
+    for (uint32_t i = threadIdx.x; i < ncache; i += NT)
       s_page[i] = page_of(P, r, R.p0 + i);
     __syncthreads();
 

@@ -292,7 +292,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
       break;
     }
     sel->fn = fn;
-    sel->block = 256;
+    sel->block = SCHED_PD_VALU_NW * 64;
     sel->mfma = 0;
   }
   return 0;
