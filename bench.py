@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
