@@ -75,8 +75,10 @@ typedef struct SchedCtrl {
 
 /* Hints (reference lib/SchedUtil.h:119-122). */
 #define SCHED_HINT_AUTO 0   /* urgent iff q*dT - lambda_bw*dR - H > 0 */
-#define SCHED_HINT_URGENT 1 /* deep KV prefetch (pf_dist pages in flight) */
-#define SCHED_HINT_POLITE 2 /* streaming (non-temporal) KV loads */
+#define SCHED_HINT_URGENT 1 /* deeper KV prefetch ring (pf_dist pages in flight) */
+#define SCHED_HINT_POLITE 2 /* non-temporal KV loads always; stock tasks load the
+                               same way except items longer than 256 pages, which
+                               stream with ordinary loads on the deepest ring */
 
 #ifdef __cplusplus
 static_assert(offsetof(SchedCtrl, num_tasks) == SCHED_CTRL_NUM_TASKS_OFF, "sched ABI: num_tasks");
@@ -176,7 +178,10 @@ typedef struct SchedDecodeArgs {
   uint32_t bt_stride;
   uint32_t tau_scope;
   uint32_t workers;      /* 0 = static grid (one workgroup per task); W = ticket queue */
-  uint32_t pf_dist;      /* urgent tasks keep this many pages in flight (0 = default 4) */
+  uint32_t pf_dist;      /* pages of loads an urgent task's waves keep in flight: 0 = the
+                            selected kernel's deepest ring, else a depth it serves
+                            (sched_paged_decode_prefetch_range; other values are
+                            rejected with hipErrorInvalidValue) */
   uint32_t flags;
   uint32_t max_tasks;    /* rows of order/ctrl/timer; task ids >= max_tasks get no levers */
   float sm_scale;        /* 0 = 1/sqrt(head_dim) */
@@ -234,6 +239,16 @@ int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a);
 /* Workgroups per CU of the kernel `a` selects (0 = unknown). Counterpart of
  * reference paged_softmax_occupancy (python/kernels/paged_softmax.cu:61-67). */
 int sched_paged_decode_occupancy(const SchedDecodeArgs *a);
+
+/* Policy lever depths of the kernel `a` selects (a->pf_dist ignored): *stock =
+ * pages of loads in flight per wave for stock and polite tasks, *deepest = the
+ * deepest ring an urgent task may use (its default); pf_dist may be 0 or any
+ * value in [*stock, *deepest]. Both 0 for the VALU kernel, which has no ring
+ * (pf_dist must be 0 there). The counterpart of the reference's SCHED_PF_DIST
+ * (lib/SchedUtil.cpp:48), a per-build constant there and a per-launch choice
+ * among compiled depths here. Returns 0 or a hipError_t code. */
+int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
+                                      uint32_t *deepest);
 
 /* Which kernel `a` selects: 0 = VALU, 1 = MFMA, -1 = invalid args. */
 int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);

@@ -28,6 +28,7 @@ struct KParams {
   uint32_t ps, bt_stride, tau_scope;
   uint32_t q_f32, o_f32, ctx_in_pages, shed_loads, lin_w_period;
   uint32_t q_f16, o_f16; // IEEE binary16 Q / output (else bf16 unless *_f32)
+  uint32_t pf_depth;     // MFMA kernel: urgent ring depth in pages (0 = the deepest)
   float scale_log2; // softmax scale * log2(e): scores live in the exp2 domain
   // split-KV work items (tiles == nullptr: one work item per task)
   const int32_t *tiles;

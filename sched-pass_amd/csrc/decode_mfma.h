@@ -43,10 +43,13 @@
 // in the arithmetic depends on scheduling, so pi, the work queue and the
 // prefetch depth leave every output bit unchanged.
 //
-// Policy lever: urgent tasks stream with DEPTH_U pages in flight instead of
-// DEPTH_S (deeper KV prefetch); polite tasks use non-temporal loads, as every
-// task does by default (KV is read once per step) except work items longer
-// than kLongItemPages, which take the deep pipeline with ordinary loads.
+// Policy lever: urgent tasks stream with a deeper ring than stock (DEPTH_S
+// pages in flight per wave): the launch's pf_dist, any depth in
+// [DEPTH_S, DEPTH_U], DEPTH_U by default (deeper KV prefetch). Polite tasks
+// always stream with non-temporal loads (the reference's "do not keep this
+// task's lines"). Stock tasks do too (KV is read once per step), except work
+// items longer than kLongItemPages, which take the deep ring with ordinary
+// loads; so polite and stock differ only on those long items.
 // fp8: values convert exactly to bf16; the per-(page, head) K scale multiplies
 // the score and the V scale multiplies p before PV, so no element is scaled.
 #pragma once
@@ -78,8 +81,8 @@ template <> struct PageRegs<true> {
 
 // KV pages are read once per step, so every task streams them with
 // non-temporal loads (measured on the 64 x 2048 bf16 step: 93 -> 83 us).
-// Polite tasks therefore load exactly as stock ones do; urgent ones keep a
-// deeper pipeline. Overridable at build time for tuning.
+// Polite tasks therefore load as stock ones do, except on long items (below);
+// urgent ones keep a deeper ring. Overridable at build time for tuning.
 #ifndef SCHED_PD_MFMA_STOCK_NT
 #define SCHED_PD_MFMA_STOCK_NT 1
 #endif
@@ -394,16 +397,26 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
   for (int v = 0; v < 4; ++v)
     p[v] = __builtin_amdgcn_exp2f(s[v] - mnew);
   S.lsum += (p[0] + p[1]) + (p[2] + p[3]);
-  u32x2_t pk;
-  if constexpr (FP8) {
-    pk.x = pack_bf16_rne(p[0] * vs, p[1] * vs);
-    pk.y = pack_bf16_rne(p[2] * vs, p[3] * vs);
-  } else if constexpr (F16) {
+  // P as PV's B operand. bf16 keeps 8 significant bits, which alone would
+  // leave ~1.2e-3 relative error in the output (p is close to 1 for nearly
+  // flat scores), so bf16 / fp8 carry p as hi + lo bf16 halves through two
+  // MFMAs (~16 bits, the linear mode's split). fp16's 11 bits (~3e-4) are
+  // kept single.
+  u32x2_t pk, pl;
+  if constexpr (F16) {
     pk.x = pack_f16_rne(p[0], p[1]);
     pk.y = pack_f16_rne(p[2], p[3]);
   } else {
-    pk.x = pack_bf16_rne(p[0], p[1]);
-    pk.y = pack_bf16_rne(p[2], p[3]);
+    float pv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      pv[v] = FP8 ? p[v] * vs : p[v];
+    pk.x = pack_bf16_rne(pv[0], pv[1]);
+    pk.y = pack_bf16_rne(pv[2], pv[3]);
+    pl.x = pack_bf16_rne(pv[0] - __uint_as_float(pk.x << 16),
+                         pv[1] - __uint_as_float(pk.x & 0xffff0000u));
+    pl.y = pack_bf16_rne(pv[2] - __uint_as_float(pk.y << 16),
+                         pv[3] - __uint_as_float(pk.y & 0xffff0000u));
   }
   const s16x4_t pop = __builtin_bit_cast(s16x4_t, pk);
 
@@ -432,6 +445,8 @@ __device__ __forceinline__ void compute_page(const KParams &P, const MfmaTask &T
     else
       a = __builtin_bit_cast(s16x4_t, fp8x4_to_bf16x4(v8[blk]));
     S.acc[blk] = mfma_pv<F16>(a, pop, S.acc[blk]);
+    if constexpr (!F16)
+      S.acc[blk] = mfma_pv<false>(a, __builtin_bit_cast(s16x4_t, pl), S.acc[blk]);
   }
 }
 
@@ -530,12 +545,12 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   // Unconditional prologue: a wave with fewer than DEPTH pages re-reads its
   // last page into the unused slots (same lines, L2 hits) so that the loop is
   // entered with the same DEPTH pages outstanding as on every back edge.
-  auto pidx_of = [&](int j) { return T.p0 + T.w + NW * (uint32_t)j; };
+  auto pidx_of = [&](int j) __attribute__((always_inline)) { return T.p0 + T.w + NW * (uint32_t)j; };
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s)
     issue_page<FP8, NT, LINEAR, VT, PG>(P, T, pid[s], pidx_of(min(s, last)), buf[s]);
 
-  auto compute = [&](int s, int j) {
+  auto compute = [&](int s, int j) __attribute__((always_inline)) {
     const uint32_t pidx = pidx_of(j);
     if constexpr (LINEAR)
       linear_page<FP8, VT, PG>(P, T, S, buf[s], pid[s], pidx, lane & 15u, g4);
@@ -566,6 +581,23 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   }
 }
 
+// An urgent task's stream at the launch's ring depth: any depth in
+// [DLO, DHI] the host accepted (SchedDecodeArgs.pf_dist); 0 = DHI. Every
+// depth computes the same pages in the same order, so the bits do not change.
+template <bool FP8, int NW, int DLO, int DHI, bool NT, bool LINEAR, bool VT, bool PG, bool F16>
+__device__ __forceinline__ void stream_urgent(const KParams &P, const MfmaTask &T, MfmaState &S,
+                                              uint32_t lane, uint32_t g4) {
+  if constexpr (DLO < DHI) {
+    if (P.pf_depth == (uint32_t)DLO) {
+      stream_pages<FP8, NW, DLO, NT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
+      return;
+    }
+    stream_urgent<FP8, NW, DLO + 1, DHI, NT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
+  } else {
+    stream_pages<FP8, NW, DHI, NT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
+  }
+}
+
 template <bool FP8, int NW, int GMAX, int DEPTH_S, int DEPTH_U, bool LINEAR = false,
           bool VT = false, bool PG = false, bool F16 = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
@@ -581,7 +613,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
   const bool toff = timer_off_latched(P.L);
   constexpr uint32_t EB = FP8 ? 1u : 2u; // bytes per KV element
 
-  run_tasks(P.L, [&](uint32_t wi) {
+  run_tasks(P.L, [&](uint32_t wi) __attribute__((always_inline)) {
     if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
@@ -662,7 +694,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
       stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.urgent)
-      stream_pages<FP8, NW, DEPTH_U, kStockNT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
+      stream_urgent<FP8, NW, DEPTH_S, DEPTH_U, kStockNT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.polite)
       stream_pages<FP8, NW, DEPTH_S, true, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else

@@ -35,12 +35,21 @@
 #ifndef SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT
 #define SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT 4
 #endif
+// fp8 d-major V on pages of 32..256 tokens: depth 6 needs 258 VGPRs (one wave
+// per SIMD instead of two); 5 fits in the register file.
+#ifndef SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT
+#define SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT 5
+#endif
 
 namespace schedpd {
 
 constexpr int mfma_ds(bool fp8) { return fp8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH; }
-constexpr int mfma_du(bool fp8, bool vt) {
-  return fp8 ? (vt ? SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT : SCHED_PD_MFMA_DEPTH_FP8_URGENT)
+// Deepest ring (the urgent default). An urgent task's ring depth is any of
+// mfma_ds .. mfma_du (SchedDecodeArgs.pf_dist).
+constexpr int mfma_du(bool fp8, bool vt, bool pg) {
+  return fp8 ? (vt ? SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT
+                : pg ? SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT
+                     : SCHED_PD_MFMA_DEPTH_FP8_URGENT)
          : vt ? SCHED_PD_MFMA_DEPTH_VT_URGENT
               : SCHED_PD_MFMA_DEPTH_URGENT;
 }
@@ -52,7 +61,7 @@ constexpr int mfma_du(bool fp8, bool vt) {
 #define SCHED_PD_MFMA_ONE(PRE, FP8, GMAX, LIN, VT, PG, F16)                                      \
   PRE template __global__ void schedpd::decode_mfma<FP8, SCHED_PD_MFMA_NW, GMAX,                 \
                                                     schedpd::mfma_ds(FP8),                       \
-                                                    schedpd::mfma_du(FP8, VT), LIN, VT, PG, F16>( \
+                                                    schedpd::mfma_du(FP8, VT, PG), LIN, VT, PG, F16>( \
       schedpd::KParams);
 #define SCHED_PD_MFMA_SOFTMAX(PRE, FP8, VT, PG, F16)                                             \
   SCHED_PD_MFMA_ONE(PRE, FP8, 4, false, VT, PG, F16)                                             \

@@ -128,24 +128,24 @@ __device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uin
 template <class Body>
 __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
   const uint32_t pid = blockIdx.x;
-  if (!L.wq) {
-    body(remap_static(L, pid, gridDim.x));
-    return;
+  uint32_t ntasks = 0u;
+  if (L.wq) {
+    const bool grid1d = gridDim.y == 1 && gridDim.z == 1;
+    const bool armed = L.queue != nullptr && L.ctrl != nullptr && grid1d;
+    ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
   }
-  const bool grid1d = gridDim.y == 1 && gridDim.z == 1;
-  const bool armed = L.queue != nullptr && L.ctrl != nullptr && grid1d;
-  const uint32_t ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
-  if (ntasks == 0u) {
-    body(remap_static(L, pid, gridDim.x));
+  const bool queue = ntasks != 0u;
+  if (queue && pid >= ntasks)
     return;
-  }
   __shared__ uint32_t s_next;
-  uint32_t raw = pid;
-  if (raw >= ntasks)
-    return;
   const uint32_t last_ticket = gridDim.x + ntasks - 1u;
+  uint32_t raw = pid;
+  // One call site of the body (it is large: inlining it once keeps the
+  // kernel's code and register allocation that of a single task body).
   while (true) {
-    body(remap_wq(L, raw, ntasks));
+    body(queue ? remap_wq(L, raw, ntasks) : remap_static(L, pid, gridDim.x));
+    if (!queue)
+      return;
     __syncthreads();
     if (threadIdx.x == 0) {
       uint32_t t = __hip_atomic_fetch_add(L.queue, 1u, __ATOMIC_RELAXED,
@@ -157,7 +157,7 @@ __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
     __syncthreads();
     raw = s_next;
     if (raw >= ntasks)
-      break;
+      return;
   }
 }
 

@@ -38,7 +38,7 @@ template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
 
 template <bool FP8, bool VT = false, bool PG = false>
 KernelFn mfma_kernel(uint32_t G, bool linear) {
-  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(FP8), DU = mfma_du(FP8, VT);
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(FP8), DU = mfma_du(FP8, VT, PG);
   if (linear)
     return decode_mfma<FP8, NW, 4, DS, DU, true, VT, PG, false>;
   if (G <= 4)
@@ -54,7 +54,7 @@ uint32_t elem_bytes(uint32_t dt) {
 
 // fp16 cache with fp16 Q: 16-byte page-16 layouts, softmax mode.
 template <bool VT, bool PG = false> KernelFn mfma_kernel_f16(uint32_t G) {
-  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT);
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT, PG);
   if (G <= 4)
     return decode_mfma<false, NW, 4, DS, DU, false, VT, PG, true>;
   if (G <= 8)
@@ -126,6 +126,19 @@ bool mfma_applies(const SchedDecodeArgs *a) {
   if (linear)
     return aligned16(a->v_pool);
   return aligned16(a->k_pool) && aligned16(a->v_pool) && aligned16(a->q);
+}
+
+// Ring depths (pages in flight per wave) of the MFMA kernel `a` selects:
+// stock, and the deepest an urgent task may use (its default). 0, 0 for the
+// VALU kernel, which has no ring.
+void ring_depths(const SchedDecodeArgs *a, bool mfma, uint32_t *ds, uint32_t *du) {
+  if (!mfma) {
+    *ds = *du = 0;
+    return;
+  }
+  const bool fp8 = a->kv_dtype == SCHED_PD_FP8_E4M3;
+  *ds = (uint32_t)mfma_ds(fp8);
+  *du = (uint32_t)mfma_du(fp8, v_token_major(a), a->page_size > 16);
 }
 
 // Validate `a`; on success fill *kp (tables resolved) and *sel.
@@ -295,6 +308,17 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     sel->block = SCHED_PD_VALU_NW * 64;
     sel->mfma = 0;
   }
+  uint32_t ds = 0, du = 0;
+  ring_depths(a, mfma, &ds, &du);
+  if (a->pf_dist != 0 && !mfma)
+    return set_error(hipErrorInvalidValue,
+                     "pf_dist %u: these arguments select the VALU kernel, which has no prefetch "
+                     "ring (pass 0)", a->pf_dist);
+  if (a->pf_dist != 0 && (a->pf_dist < ds || a->pf_dist > du))
+    return set_error(hipErrorInvalidValue,
+                     "pf_dist %u: the kernel these arguments select keeps %u..%u pages in flight",
+                     a->pf_dist, ds, du);
+  kp->pf_depth = a->pf_dist;
   return 0;
 }
 
@@ -362,6 +386,27 @@ int sched_paged_decode_occupancy(const SchedDecodeArgs *a) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, sel.fn, sel.block, 0) != hipSuccess)
     return 0;
   return blocks;
+}
+
+int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
+                                      uint32_t *deepest) {
+  KParams kp;
+  Selected sel;
+  SchedDecodeArgs b;
+  if (a == nullptr)
+    return set_error(hipErrorInvalidValue, "args is NULL");
+  b = *a;
+  b.pf_dist = 0;
+  int rc = prepare(&b, &kp, &sel);
+  if (rc)
+    return rc;
+  uint32_t ds = 0, du = 0;
+  ring_depths(&b, sel.mfma != 0, &ds, &du);
+  if (stock)
+    *stock = ds;
+  if (deepest)
+    *deepest = du;
+  return 0;
 }
 
 int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a) {

@@ -134,6 +134,9 @@ SIGNATURES = {
     "sched_paged_decode_occupancy": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_kernel_kind": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
+    "sched_paged_decode_prefetch_range": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs),
+                                                         ctypes.POINTER(_u32),
+                                                         ctypes.POINTER(_u32)]),
     "sched_pd_cu_count": (ctypes.c_int, []),
     "sched_pd_read_probe": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _p]),
     "sched_pd_read_probe_blocks": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _u32, _u32, _p, _p]),

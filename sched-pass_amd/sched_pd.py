@@ -315,6 +315,18 @@ def kernel_kind(args: abi.SchedDecodeArgs) -> str:
     return "mfma" if k == 1 else "valu"
 
 
+def prefetch_range(args: abi.SchedDecodeArgs) -> tuple:
+    """(stock, deepest): pages in flight per wave of the kernel `args`
+    selects, for stock tasks and at most for urgent ones; pf_dist may be 0 (the
+    deepest) or any depth in between. (0, 0) for the VALU kernel."""
+    lo, hi = abi._u32(), abi._u32()
+    rc = abi.load_library().sched_paged_decode_prefetch_range(ctypes.byref(args),
+                                                              ctypes.byref(lo), ctypes.byref(hi))
+    if rc != 0:
+        raise RuntimeError(abi.last_error())
+    return lo.value, hi.value
+
+
 def occupancy(args: abi.SchedDecodeArgs) -> int:
     return abi.load_library().sched_paged_decode_occupancy(ctypes.byref(args))
 

@@ -131,6 +131,38 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.FP8_E4M3)) == -1
 
 
+def prefetch_range(lib, a):
+    lo, hi = ctypes.c_uint32(), ctypes.c_uint32()
+    rc = lib.sched_paged_decode_prefetch_range(ctypes.byref(a), ctypes.byref(lo), ctypes.byref(hi))
+    return rc, lo.value, hi.value
+
+
+def test_prefetch_range_and_pf_dist_validation(schedlib):
+    """pf_dist picks an urgent ring depth the selected kernel compiles, or
+    0 for its deepest; anything else is refused before any launch."""
+    fp8 = dict(kv_dtype=abi.FP8_E4M3)
+    tok = dict(v_tok_stride=128, v_dim_stride=1)
+    cases = [(fake_args(), (2, 4)),                                   # bf16 d-major page 16
+             (fake_args(**fp8), (4, 6)),                              # fp8 d-major
+             (fake_args(page_size=32, v_dim_stride=32, **fp8), (4, 5)),  # fp8 d-major, 32-token pages
+             (fake_args(**tok), (2, 3)),                              # bf16 token-major
+             (fake_args(**tok, **fp8), (4, 4)),                       # fp8 token-major
+             (fake_args(flags=abi.FLAG_FORCE_VALU), (0, 0))]          # VALU: no ring
+    for a, want in cases:
+        rc, lo, hi = prefetch_range(schedlib, a)
+        assert rc == 0 and (lo, hi) == want, (want, lo, hi)
+        for pf in range(0, 9):
+            a.pf_dist = pf
+            ok = pf == 0 or lo <= pf <= hi
+            rc = schedlib.sched_paged_decode_kernel_kind(ctypes.byref(a))
+            assert (rc >= 0) == ok, (want, pf)
+            if not ok:
+                assert "pf_dist" in abi.last_error()
+        # the range query ignores the block's own pf_dist
+        a.pf_dist = 99
+        assert prefetch_range(schedlib, a) == (0, lo, hi)
+
+
 @pytest.mark.parametrize("field,value,msg", [
     ("abi_version", 7, "abi_version"),
     ("num_q_heads", 33, "multiple"),

@@ -14,11 +14,12 @@ import oracle
 import sched_abi as abi
 import sched_pd
 import workloads
+from parity import TOL_BF16, par_err
 from sched_rt import SchedPlane
 
 pytestmark = pytest.mark.gpu
 
-TOL_BF16 = 2e-3  # mixed form |a-r| <= tol (1 + |r|), bf16 / fp8 KV
+# par_err <= TOL_BF16: mixed form and per-row norm-relative error (tests/parity.py)
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -27,10 +28,6 @@ def lib(schedlib):
     return schedlib
 
 
-def mixed_err(a, r):
-    a = np.asarray(a, np.float64)
-    r = np.asarray(r, np.float64)
-    return float(np.max(np.abs(a - r) / (1 + np.abs(r))))
 
 
 def sample(ctx, k, seed):
@@ -73,32 +70,33 @@ def compact(b, idx):
 
 def decode(b, **kw):
     R = b["ctx_lens"].numel()
-    out = torch.full((R, b["q"].shape[1], 128), float("nan"), dtype=torch.float32, device="cuda")
+    rows = b["v_pool"].shape[1] if kw.get("mode", abi.SOFTMAX) == abi.LINEAR else b["q"].shape[1]
+    out = torch.full((R, rows, 128), float("nan"), dtype=torch.float32, device="cuda")
     sched_pd.paged_decode(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                           out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], **kw)
     torch.cuda.synchronize()
     return out
 
 
-def oracle_of(c, plane=None):
+def oracle_of(c, plane=None, **kw):
     ctrl = None
     if plane is not None:
         ctrl = bytes(plane._ctrl_host)
     return oracle.decode(c["q"], c["k_pool"], c["v_pool"], c["block_table"], c["ctx_lens"],
                          k_scale=c["k_scale"], v_scale=c["v_scale"], ctrl=ctrl,
-                         max_tasks=plane.N if plane is not None else 4096)
+                         max_tasks=plane.N if plane is not None else 4096, **kw)
 
 
-def check_sample(b, out, idx, hkv, tau=None):
+def check_sample(b, out, idx, hkv, tau=None, **kw):
     """Oracle parity of out[idx] on the compacted sample; tau per task of the
-    whole batch (prefix budget) or None."""
+    whole batch (prefix budget) or None; kw: the oracle's mode arguments."""
     c = compact(b, idx)
     plane = None
     if tau is not None:
         plane = SchedPlane(max_tasks=idx.size * hkv, device="cpu")
         plane.set_rows(tau=np.asarray(tau).reshape(-1, hkv)[idx].reshape(-1), n=idx.size * hkv)
-    r = oracle_of(c, plane)
-    e = mixed_err(out[torch.from_numpy(idx).cuda()].cpu(), r)
+    r = oracle_of(c, plane, **kw)
+    e = par_err(out[torch.from_numpy(idx).cuda()].cpu(), r)
     print(f"sample {idx.tolist()} ctx {c['ctx_lens'].cpu().tolist()} err {e:.3g}", flush=True)
     assert e <= TOL_BF16
 
@@ -148,16 +146,19 @@ def test_hetero_batch_full_size():
         assert torch.equal(decode(b, plane=plane, workers=W, tiles=tiles, tile_pages=tp),
                            static_tiles)
     unsplit = decode(b)
-    assert mixed_err(unsplit.cpu(), static_tiles.cpu()) <= TOL_BF16
+    assert par_err(unsplit.cpu(), static_tiles.cpu()) <= TOL_BF16
     check_sample(b, static_tiles, sample(ctx, 5, 2), 8)
 
 
-def test_shed_full_size():
-    """128 requests, tau ~ U[ctx/4, ctx] per task (prefix budget): skipping
-    the pages past tau gives the bits of loading and masking them, under the
-    queue with pi longest-first over 256-page tiles; sampled requests match
-    the truncated oracle."""
-    print("case llama3_8b_shed", flush=True)
+@pytest.mark.parametrize("mode", [abi.SOFTMAX, abi.LINEAR])
+def test_shed_full_size(mode):
+    """128 requests, tau ~ U[ctx/4, ctx] per task (prefix budget), policy
+    armed (q ~ U(0,1), lambda_bw 0.5, H 0.1, urgent ring 4 pages), both shed
+    variants: online softmax (masked score -inf) and the linear contraction
+    (masked value 0). Skipping the pages past tau gives the bits of loading and
+    masking them, under the queue with pi longest-first over 256-page tiles;
+    sampled requests (the longest included) match the truncated oracle."""
+    print(f"case llama3_8b_shed mode {mode}", flush=True)
     b = workloads.workload("llama3_8b_shed", seed=0)
     ctx = b["ctx_lens"].cpu().numpy()
     ntask, tp = 128 * 8, 256
@@ -172,11 +173,21 @@ def test_shed_full_size():
     plane.set_num_tasks(nt)
     plane.push()
     plane.reset_queue(W)
-    kw = dict(plane=plane, workers=W, tiles=tiles, tile_pages=tp, policy=(1.0, 1.0, 0.1))
+    kw = dict(plane=plane, workers=W, tiles=tiles, tile_pages=tp, policy=(1.0, 1.0, 0.1),
+              pf_dist=4)
+    okw = {}
+    if mode == abi.LINEAR:
+        w = torch.randn(8192, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
+        kw.update(mode=abi.LINEAR, lin_w=w)
+        okw = dict(mode=abi.LINEAR, lin_w=w.cpu().numpy())
     skip = decode(b, **kw)
     assert torch.isfinite(skip).all()
     assert torch.equal(decode(b, flags=abi.FLAG_SHED_LOADS, **kw), skip)
-    check_sample(b, skip, sample(ctx, 5, 3), 8, tau=b["tau"])
+    # the policy priced out (no task urgent) gives the same bits
+    plane.set_lambda(1000.0)
+    plane.push()
+    assert torch.equal(decode(b, **kw), skip)
+    check_sample(b, skip, sample(ctx, 5, 3), 8, tau=b["tau"], **okw)
 
 
 def test_qwen2_fp8_full_size():
@@ -201,5 +212,5 @@ def test_qwen2_fp8_full_size():
     cyc = plane.read_timer()[:ntask].numpy()
     assert np.all(cyc > 0)
     static = decode(b)
-    assert mixed_err(static.cpu(), wq.cpu()) <= TOL_BF16
+    assert par_err(static.cpu(), wq.cpu()) <= TOL_BF16
     check_sample(b, wq, sample(ctx, 6, 4), 4)

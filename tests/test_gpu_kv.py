@@ -9,11 +9,11 @@ import torch
 import kv_cache
 import oracle
 import sched_pd
+from parity import TOL_BF16, par_err
 from kv_cases import FP8, append_case, random_pool
 
 pytestmark = pytest.mark.gpu
 
-TOL_BF16 = 2e-3
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -258,8 +258,7 @@ def test_cache_prefill_then_decode_loop(dtype, ps):
     ref = oracle.decode(q, cache.k_pool, cache.v_pool, bt, ctx, k_scale=cache.k_scale,
                         v_scale=cache.v_scale, v_layout=lay)
     r = np.asarray(ref, np.float64)
-    err = float(np.max(np.abs(out.cpu().double().numpy() - r) / (1 + np.abs(r))))
-    assert err <= TOL_BF16
+    assert par_err(out.cpu(), r, f"cache loop {dtype} page {ps}") <= TOL_BF16
     args = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out, v_layout=lay,
                                k_scale=cache.k_scale, v_scale=cache.v_scale)
     assert sched_pd.kernel_kind(args) == "mfma"
@@ -339,7 +338,7 @@ def test_flashinfer_fp16_nhd_cache_in_place():
     ref = np.asarray(oracle.decode(q, kview, vview, indices, ctx, page_indptr=indptr,
                                    v_layout="tokmajor"), np.float64)
     got = out.float().cpu().double().numpy()
-    assert float(np.max(np.abs(got - ref) / (1 + np.abs(ref)))) <= TOL_BF16
+    assert par_err(got, ref) <= TOL_BF16
 
 
 def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
@@ -367,7 +366,7 @@ def test_flashinfer_nhd_cache_decodes_in_place_and_imports():
     torch.cuda.synchronize()
     ref = np.asarray(oracle.decode(q, kview, vview, indices, ctx, page_indptr=indptr,
                                    v_layout="tokmajor"), np.float64)
-    err = lambda o: float(np.max(np.abs(o.cpu().double().numpy() - ref) / (1 + np.abs(ref))))  # noqa: E731
+    err = lambda o: par_err(o.cpu(), ref, "nhd in place")  # noqa: E731
     assert err(out) <= TOL_BF16
     # import: gather each request's tokens in order and append them
     rows_k, rows_v = [], []

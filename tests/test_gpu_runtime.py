@@ -10,6 +10,7 @@ import torch
 
 import oracle
 import sched_abi as abi
+from parity import TOL_F32, par_err
 
 pytestmark = pytest.mark.gpu
 
@@ -81,9 +82,9 @@ class Fixture:
                              ctrl=ctrl, ctx_in_pages=True)
 
 
-def close(a, r, tol=1e-5):
-    a, r = np.asarray(a, np.float64), np.asarray(r, np.float64)
-    return bool(np.all(np.abs(a - r) <= tol * (1 + np.abs(r))))
+def close(a, r, tol=TOL_F32):
+    """fp32: the mixed form and the per-row norm-relative error within tol."""
+    return par_err(a, r) <= tol
 
 
 def timer_rows(lib, n):

@@ -9,6 +9,7 @@ import torch
 
 import kv_cache
 import sched_pd
+from parity import TOL_BF16, par_err
 from sched_rt import SchedPlane
 from serving import HookConfig, ServingHooks
 
@@ -59,9 +60,9 @@ def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages):
             whole = torch.empty_like(out)
             cache.decode(q, rids, out=whole)
             torch.cuda.synchronize()
-            # the MFMA kernel rounds softmax weights to bf16 against the running
-            # max, which a split changes: bf16 tolerance, as against the oracle
-            assert float(((out - whole).abs() / (1 + whole.abs())).max()) <= 2e-3
+            # a split changes the summation order (and the running max each
+            # partial is scaled against): the tolerance, as against the oracle
+            assert par_err(out.cpu(), whole.cpu()) <= TOL_BF16
     torch.cuda.synchronize()
     hooks.on_batch_begin(rids, [cache.lens[r] for r in rids])   # folds the last probe
     assert hooks.probes_folded >= 2
