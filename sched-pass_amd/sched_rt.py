@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import struct
 
+import numpy as np
 import torch
 
 from sched_abi import (CTRL_FLAGS_OFF, CTRL_LAMBDA_OFF, CTRL_NUM_TASKS_OFF,
@@ -214,37 +215,41 @@ class SchedPlane:
     # -- pi builders (python/sched_rt.py:557-609) --------------------------------
     @staticmethod
     def _grouped_lpt(c, block: int) -> torch.Tensor:
-        """Blocks of `block` adjacent tiles ordered by descending summed cost,
-        ascending index order kept inside a block; block <= 1 is plain LPT.
-        Ties keep ascending index order (stable sort)."""
-        c = torch.as_tensor(c).float().flatten()
-        n = c.numel()
+        """Tiles grouped `block` at a time by index (tile i in group i //
+        block); groups served in descending summed cost, tiles of a group in
+        ascending index. block <= 1, or a batch of at most one group, is plain
+        longest-first. Every sort is stable: ties keep ascending index."""
+        cost = np.asarray(torch.as_tensor(c).float().flatten(), np.float64)
+        n = cost.size
         if block <= 1 or n <= block:
-            return torch.sort(c, descending=True, stable=True).indices.to(torch.int32)
-        nb = -(-n // block)
-        pad = nb * block - n
-        cc = torch.cat([c, c.new_zeros(pad)]) if pad else c
-        bcost = cc.reshape(nb, block).sum(1)
-        border = torch.sort(bcost, descending=True, stable=True).indices
-        order = (border[:, None] * block + torch.arange(block)[None, :]).flatten()
-        return order[order < n].to(torch.int32)
+            return torch.from_numpy(np.argsort(-cost, kind="stable").astype(np.int32))
+        group = np.arange(n) // block
+        group_cost = np.bincount(group, weights=cost)
+        rank = np.empty(group_cost.size, np.int64)
+        rank[np.argsort(-group_cost, kind="stable")] = np.arange(group_cost.size)
+        # primary key: the group's rank; secondary: the tile index
+        order = np.lexsort((np.arange(n), rank[group]))
+        return torch.from_numpy(order.astype(np.int32))
 
     @staticmethod
     def region_order(cost, R: int, block: int | None = None) -> torch.Tensor:
-        """Region-aware pi: with n <= R every tile starts at once, so use
-        grouped LPT (block default 16). Otherwise the first R slots alternate
-        heaviest and lightest tiles and the rest follow heaviest first."""
-        c = torch.as_tensor(cost).float().flatten()
-        n = c.numel()
+        """pi for a launch of R resident workers over n tiles. n <= R: every
+        tile starts at once, so tiles are grouped for locality (grouped
+        longest-first, block 16 by default). n > R: the R tiles that start
+        first alternate the heaviest ceil(R/2) (heaviest first) with the
+        lightest floor(R/2) (lightest first), so heavy work starts early
+        and light work frees workers to claim more; the remaining tiles
+        follow heaviest first."""
+        c = np.asarray(torch.as_tensor(cost).float().flatten(), np.float64)
+        n = c.size
         if R <= 0 or n <= int(R):
-            return SchedPlane._grouped_lpt(c, 16 if block is None else block)
+            return SchedPlane._grouped_lpt(torch.from_numpy(c), 16 if block is None else block)
         R = int(R)
-        lpt = torch.sort(c, descending=True, stable=True).indices.to(torch.int32)
-        nh = (R + 1) // 2
-        nl = R - nh
-        pre = torch.empty(R, dtype=torch.int32)
-        pre[0::2] = lpt[:nh]
-        if nl:
-            pre[1::2] = lpt[n - nl:].flip(0)
-        suf = lpt[nh:n - nl] if nl else lpt[nh:]
-        return torch.cat([pre, suf])
+        by_cost = np.argsort(-c, kind="stable")
+        n_heavy = (R + 1) // 2
+        n_light = R - n_heavy
+        heavy, middle, light = np.split(by_cost, [n_heavy, n - n_light])
+        first = np.empty(R, np.int64)
+        first[0::2] = heavy
+        first[1::2] = light[::-1]
+        return torch.from_numpy(np.concatenate([first, middle]).astype(np.int32))

@@ -151,9 +151,7 @@ class ServingHooks:
                                f"the plane's max_tasks {p.N}")
         self._consume_probe()
 
-        alpha, beta = self.ctl._fit.coeffs()
-        resid = np.array([self.ctl._resid.get(r, 0.0) for r in rids], np.float64)
-        cost_req = np.maximum(alpha * np.asarray(kv_list, np.float64) + beta + resid, 0.0)
+        cost_req = self.ctl.predict(rids, kv_list)
         req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
         cost_item = torch.as_tensor(cost_req[item_req] * item_pages / req_pages[item_req],
                                     dtype=torch.float32)

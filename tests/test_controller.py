@@ -3,9 +3,10 @@
 dead-band, and the fold from per-task timer rows to per-request cost."""
 import random
 
+import numpy as np
 import pytest
 
-from sched_controller import (CostFit, SchedControlPlane, task_costs_per_request,
+from sched_controller import (CostModel, SchedControlPlane, task_costs_per_request,
                               task_order_from_requests)
 
 
@@ -33,7 +34,7 @@ def test_reference_smoke():
     for _ in range(20):
         cyc = [alpha_true * ln + beta_true + random.gauss(0, 5) for ln in lens]
         ctl.step(plane, rids, lens, cycles=cyc)
-    a, b = ctl._fit.coeffs()
+    a, b = ctl.coefficients()
     assert abs(a - alpha_true) / alpha_true < 0.05
     oracle = sorted(range(len(lens)), key=lambda i: -lens[i])
     got = ctl.order(rids, lens)
@@ -46,17 +47,56 @@ def test_reference_smoke():
 
 
 def test_fit_known_answers():
-    f = CostFit()
-    assert f.coeffs() == (1.0, 0.0)
-    f.add(2.0, 10.0)
-    assert f.coeffs() == (5.0, 0.0)           # one point: proportional
-    f.add(2.0, 14.0)
-    assert f.coeffs() == (6.0, 0.0)           # all x equal: proportional
-    g = CostFit()
+    f = CostModel()
+    assert f.coefficients() == (1.0, 0.0)
+    f.add([2.0], [10.0])
+    assert f.coefficients() == (5.0, 0.0)     # one point: proportional
+    f.add([2.0], [14.0])
+    assert f.coefficients() == (6.0, 0.0)     # all x equal: proportional
+    g = CostModel()
     for x in (1.0, 2.0, 3.0, 10.0):
-        g.add(x, 3.0 * x + 4.0)
-    a, b = g.coeffs()
+        g.add([x], [3.0 * x + 4.0])
+    a, b = g.coefficients()
     assert abs(a - 3.0) < 1e-12 and abs(b - 4.0) < 1e-12
+    # a whole step at once gives the same fit as one sample at a time
+    h = CostModel()
+    h.add([1.0, 2.0, 3.0, 10.0], [7.0, 10.0, 13.0, 34.0])
+    assert np.allclose(h.coefficients(), (3.0, 4.0), rtol=0, atol=1e-12)
+    # least squares on noisy data: numpy's lstsq on the same samples
+    rng = np.random.default_rng(0)
+    x = rng.uniform(16, 32768, 500)
+    y = 7.5 * x + 120 + rng.normal(0, 50, 500)
+    m = CostModel()
+    m.add(x, y)
+    want = np.linalg.lstsq(np.stack([x, np.ones_like(x)], 1), y, rcond=None)[0]
+    assert np.allclose(m.coefficients(), want, rtol=1e-9)
+
+
+def test_forgetting_tracks_a_drifting_cost():
+    # cost per token doubles half way: the forgetting fit follows, the plain
+    # least-squares fit averages the two regimes
+    plain, fading = CostModel(), CostModel(forget=0.5)
+    x = np.array([100.0, 1000.0, 5000.0])
+    for step in range(40):
+        slope = 2.0 if step < 20 else 4.0
+        for m in (plain, fading):
+            m.add(x, slope * x + 10.0)
+    assert abs(fading.coefficients()[0] - 4.0) < 1e-4   # old regime weighs 0.5**20
+    assert 2.5 < plain.coefficients()[0] < 3.5
+    with pytest.raises(ValueError):
+        CostModel(forget=0.0)
+
+
+def test_step_estimate_does_not_depend_on_listing_order():
+    rng = np.random.default_rng(1)
+    rids = list(range(32))
+    lens = rng.integers(16, 4096, 32)
+    cyc = 3.0 * lens + 50 + rng.normal(0, 20, 32)
+    a, b = SchedControlPlane(), SchedControlPlane()
+    a.observe(rids, lens, cyc)
+    perm = rng.permutation(32)
+    b.observe([rids[i] for i in perm], lens[perm], cyc[perm])
+    assert np.allclose(a.predict(rids, lens), b.predict(rids, lens), rtol=1e-12)
 
 
 def test_policies_and_errors():
@@ -65,10 +105,10 @@ def test_policies_and_errors():
         ctl.observe([0, 1, 2], [100, 10, 50], [1000, 100, 500])
     assert ctl.order([0, 1, 2], [100, 10, 50]) == [1, 2, 0]
     ctl.policy = "lpt"
-    ctl._last_order = []
+    ctl.clear_published()
     assert ctl.order([0, 1, 2], [100, 10, 50]) == [0, 2, 1]
     ctl.policy = "edf"
-    ctl._last_order = []
+    ctl.clear_published()
     # slack = deadline - elapsed - t_hat
     assert ctl.order([0, 1, 2], [100, 10, 50], deadlines=[5000, 150, 1000],
                      elapsed=[0, 0, 0]) == [1, 2, 0]

@@ -51,7 +51,7 @@ def test_timer_to_controller_to_plane_loop():
         assert (rows > 0).all()
         cost = task_costs_per_request(rows, R, hkv)
         order = ctl.step(view, rids, ctx.tolist(), cycles=cost)
-    alpha, _ = ctl._fit.coeffs()
+    alpha, _ = ctl.coefficients()
     assert alpha > 0
     assert order[0] == 3                 # the straggler goes first
     top = set(order[:R // 4])

@@ -66,5 +66,5 @@ def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages):
     torch.cuda.synchronize()
     hooks.on_batch_begin(rids, [cache.lens[r] for r in rids])   # folds the last probe
     assert hooks.probes_folded >= 2
-    alpha, _ = hooks.ctl._fit.coeffs()
+    alpha, _ = hooks.ctl.coefficients()
     assert alpha > 0
