@@ -210,14 +210,22 @@ typedef struct SchedDecodeArgs {
    * its pages [c*tile_pages, (c+1)*tile_pages). The list is task-major: the
    * ceil(ceil(ctx/page_size)/tile_pages) chunks of a task (at least 1) are
    * consecutive and in chunk order. pi, num_tasks, order_size and the ticket
-   * queue count work items; policy rows and timer rows stay per task. */
+   * queue count work items; policy rows and timer rows stay per task.
+   * Plan the list from the ctx_lens of the launch: chunks a shorter context
+   * does not reach are skipped (the result is unchanged), but a task whose
+   * context needs a chunk the list lacks is stale -- its output rows are
+   * written as NaN and it is counted in the workspace's stale counter. */
   const int32_t *tiles;
   uint32_t num_tiles;
   uint32_t _pad0;
-  /* Device scratch for split tasks (sched_paged_decode_workspace_bytes):
-   * per-task arrival counters, then per-work-item partial results. The
-   * counters must be zero before the first launch; each launch leaves them
-   * zero. Launches sharing one workspace must not overlap. */
+  /* Device scratch for split tasks (sched_paged_decode_workspace_bytes),
+   * 256-byte aligned: bytes [0, 4) a u32 stale-plan counter (tasks found
+   * stale, see tiles; the launcher only adds to it: read it after the launch
+   * and zero it to reset), then from byte 256 the per-task arrival counters,
+   * then per-work-item partial results. The arrival counters must be zero
+   * before the first launch; each launch leaves them zero (a stale task's
+   * counter is never touched). Launches sharing one workspace must not
+   * overlap (use one workspace per stream). */
   void *workspace;
   uint64_t workspace_bytes;
 } SchedDecodeArgs;

@@ -163,13 +163,54 @@ __device__ __forceinline__ ItemRange item_range(const KParams &P, uint32_t chunk
   return it;
 }
 
-// A work item whose chunk cannot belong to a task-major list (chunk past the
-// task's chunk count, before the start of the list, or a task whose chunks
-// would run past the end) is skipped: the merge only ever reads work items
-// [wi - chunk, wi - chunk + nchunks), which this keeps inside the list.
-__device__ __forceinline__ bool item_ok(const KParams &P, uint32_t wi, uint32_t chunk,
-                                        const ItemRange &R) {
-  return chunk < R.nchunks && chunk <= wi && (wi - chunk) + R.nchunks <= P.L.nitems;
+// What a work item does, decided from the plan and the launch's context
+// length. It runs (streams its pages and takes part in the task's merge)
+// unless
+//   - it is skipped: a chunk the context does not reach (the plan was built
+//     for a longer context; the task's other chunks cover it), or a chunk
+//     index that cannot be task-major;
+//   - its task is stale: the context needs chunk nchunks-1 and the plan does
+//     not hold it right after the task's chunk 0 (the plan was built for a
+//     shorter context). No item of such a task merges or touches its arrival
+//     counter: chunk 0 writes the task's output rows as NaN and counts the
+//     task in the workspace's stale counter.
+// Every item of a task reads the same rows and lengths, so they all decide
+// alike. The merge only ever reads items [wi - chunk, wi - chunk + nchunks),
+// which a running item keeps inside the list.
+// Skip: the chunk lies past what the context reaches, or cannot be
+// task-major. Decided without a load.
+__device__ __forceinline__ bool item_skip(const KParams &P, uint32_t wi, uint32_t chunk,
+                                         const ItemRange &R) {
+  return P.tiles != nullptr && (chunk > wi || chunk >= R.nchunks);
+}
+
+// Stale: the context needs more chunks than the plan holds for the task (the
+// row of its chunk nchunks-1 is missing). One tile-row load, issued when the
+// item starts and consumed at its merge.
+__device__ __forceinline__ bool item_stale(const KParams &P, uint32_t wi, uint32_t task,
+                                           uint32_t chunk, const ItemRange &R) {
+  if (P.tiles == nullptr || R.nchunks == 1u)
+    return false;
+  const uint32_t last = wi - chunk + R.nchunks - 1u;
+  if (last >= P.L.nitems)
+    return true;
+  const int32_t lt = P.tiles[2 * last], lc = P.tiles[2 * last + 1];
+  return !((uint32_t)lt == task && (uint32_t)lc == R.nchunks - 1u);
+}
+
+// A stale task's signal: output rows NaN (chunk 0's item writes them), one
+// count in the workspace's stale counter.
+template <int NW, int D, bool LINEAR>
+__device__ __forceinline__ void mark_stale(const KParams &P, uint32_t chunk, uint32_t r,
+                                           uint32_t h, uint32_t G) {
+  if (chunk != 0u)
+    return;
+  constexpr uint32_t NT = NW * 64;
+  const int64_t orow = LINEAR ? ((int64_t)r * P.Hkv + h) : ((int64_t)r * P.Hq + h * G);
+  for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT)
+    store_out(P, orow * D + idx, __builtin_nanf(""));
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(P.ws_stale, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 } // namespace schedpd

@@ -630,8 +630,9 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.budget = pol.budget;
     const uint32_t ext = load_extent(P, T.n, pol.budget);
     const ItemRange R = item_range(P, chunk, T.n, PG ? (ext + P.ps - 1u) / P.ps : (ext + 15u) / 16u);
-    if (!item_ok(P, wi, chunk, R))
+    if (item_skip(P, wi, chunk, R))
       return;
+    const bool stale = item_stale(P, wi, task, chunk, R);
     if constexpr (PG) {
       // pages [p0, p1) of the item as 16-token blocks, up to the last read
       T.bshift = 31u - __builtin_clz(P.ps >> 4);
@@ -722,8 +723,11 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       }
     }
     __syncthreads();
-    finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, chunk, R.nchunks, T.r, T.h, G, s_acc,
-                                              s_m, s_l);
+    if (stale)
+      mark_stale<NW, 128, LINEAR>(P, chunk, T.r, T.h, G);
+    else
+      finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, chunk, R.nchunks, T.r, T.h, G,
+                                                s_acc, s_m, s_l);
     timer_commit(P.L, toff, task, t0);
   });
 }

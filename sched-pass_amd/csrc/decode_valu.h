@@ -123,8 +123,9 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
     const uint32_t n = ctx_tokens(P, r);
     const uint32_t nload = load_extent(P, n, pol.budget);
     const ItemRange R = item_range(P, chunk, n, (nload + P.ps - 1) / P.ps);
-    if (!item_ok(P, wi, chunk, R))
+    if (item_skip(P, wi, chunk, R))
       return;
+    const bool stale = item_stale(P, wi, task, chunk, R);
     const uint32_t G = LINEAR ? 1u : P.G;
     const bool fp8 = sizeof(KVT) == 1;
 
@@ -275,7 +276,11 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
       }
     }
     __syncthreads();
-    finish_item<NW, GH, D, Acc, LINEAR>(P, wi, task, chunk, R.nchunks, r, h, G, s_acc, s_m, s_l);
+    if (stale)
+      mark_stale<NW, D, LINEAR>(P, chunk, r, h, G);
+    else
+      finish_item<NW, GH, D, Acc, LINEAR>(P, wi, task, chunk, R.nchunks, r, h, G, s_acc, s_m,
+                                          s_l);
     timer_commit(P.L, toff, task, t0);
   });
 }

@@ -66,11 +66,11 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 uint64_t round256(uint64_t x) { return (x + 255u) & ~uint64_t(255); }
 
-// Workspace layout for split tasks: [counters: ntasks u32][(m, l): items x G
-// x 2 f32][partials: items x G x d x (f32 softmax | f64 linear)], each region
-// 256-byte aligned.
+// Workspace layout for split tasks: [stale-plan counter: u32][counters:
+// ntasks u32][(m, l): items x G x 2 f32][partials: items x G x d x (f32
+// softmax | f64 linear)], each region 256-byte aligned.
 struct WsLayout {
-  uint64_t count_off, ml_off, acc_off, total;
+  uint64_t stale_off, count_off, ml_off, acc_off, total;
 };
 
 WsLayout ws_layout(const SchedDecodeArgs *a) {
@@ -78,8 +78,9 @@ WsLayout ws_layout(const SchedDecodeArgs *a) {
   const uint64_t G = linear ? 1u : a->num_q_heads / a->num_kv_heads;
   const uint64_t ntasks = (uint64_t)a->num_requests * a->num_kv_heads;
   WsLayout L;
-  L.count_off = 0;
-  L.ml_off = round256(ntasks * 4u);
+  L.stale_off = 0;
+  L.count_off = 256;
+  L.ml_off = L.count_off + round256(ntasks * 4u);
   L.acc_off = L.ml_off + round256((uint64_t)a->num_tiles * G * 8u);
   L.total = L.acc_off + (uint64_t)a->num_tiles * G * a->head_dim * (linear ? 8u : 4u);
   return L;
@@ -223,6 +224,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     kp->tiles = a->tiles;
     kp->tile_pages = a->tile_pages;
     kp->L.nitems = a->num_tiles;
+    kp->ws_stale = reinterpret_cast<uint32_t *>(ws + W.stale_off);
     kp->ws_count = reinterpret_cast<uint32_t *>(ws + W.count_off);
     kp->ws_ml = reinterpret_cast<float *>(ws + W.ml_off);
     kp->ws_acc = ws + W.acc_off;

@@ -49,12 +49,14 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                tau_scope=abi.TAU_PREFIX, lin_w=None, lin_w_period=0,
                plane=None, rt_tables=False, workers=0, pf_dist=0, flags=0,
                policy=(1.0, 1.0, 0.25), tiles=None, tile_pages=0,
-               workspace=None, check_tables=False) -> abi.SchedDecodeArgs:
+               workspace=None, check_tables=False, stream=None) -> abi.SchedDecodeArgs:
     """Fill a SchedDecodeArgs from tensors (no launch). With `tiles` (from
-    plan_tiles) long tasks run as several work items; the workspace is taken
-    from a per-device cache unless one is given. The kernels trust the page
-    table (as the reference's do); check_tables=True verifies it on the host
-    first (check_page_table; this synchronises)."""
+    plan_tiles, built from these ctx_lens) long tasks run as several work
+    items; the workspace is taken from a cache with one per (device, stream)
+    unless one is given (`stream`: the stream the launch will use, default the
+    current one). The kernels trust the page table (as the reference's do);
+    check_tables=True verifies it on the host first (check_page_table; this
+    synchronises)."""
     a = abi.default_args()
     linear = mode == abi.LINEAR
     a.mode = mode
@@ -146,7 +148,8 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
             raise RuntimeError(abi.last_error())
         if workspace is None:
             workspace = workspace_for(need, v_pool.device,
-                                      count_bytes=4 * a.num_requests * a.num_kv_heads)
+                                      count_bytes=WS_COUNTERS_OFF + 4 * a.num_requests *
+                                      a.num_kv_heads, stream=stream)
         elif workspace.numel() * workspace.element_size() < need:
             raise ValueError(f"workspace holds {workspace.numel()} bytes, needs {need}")
         a.workspace = _ptr(workspace)
@@ -210,14 +213,24 @@ def check_page_table(block_table, ctx_lens, page_size: int, num_pages: int, *,
             raise ValueError(f"request {r} has a page id outside [0, {num_pages})")
 
 
-def workspace_for(nbytes: int, device, count_bytes: int = 0) -> torch.Tensor:
+# Workspace layout (include/sched_pd.h): a u32 stale-plan counter at byte 0,
+# the per-task arrival counters from byte 256, then the partials.
+WS_COUNTERS_OFF = 256
+
+
+def workspace_for(nbytes: int, device, count_bytes: int = 0, stream=None) -> torch.Tensor:
     """A device workspace of at least `nbytes` whose first `count_bytes` (the
-    per-task arrival counters) are zero, cached per device. A launch leaves
-    its counters zero but writes partials right after them, so the zeroed
-    prefix is tracked and cleared again when a launch needs more counters.
-    Launches that share the workspace must not overlap."""
+    stale counter and the per-task arrival counters) are zero, cached per
+    (device, stream): launches on one stream are ordered, launches on two
+    streams get two workspaces. A launch leaves its counters zero but writes
+    partials right after them, so the zeroed prefix is tracked and cleared
+    again when a launch needs more counters (which also clears the stale
+    counter)."""
     dev = torch.device(device)
-    key = (dev.type, dev.index)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    key = (dev.type, dev.index, int(s.cuda_stream))
     ent = _WS.get(key)
     if ent is None or ent[0].numel() < nbytes:
         ent = [torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev), 0]
@@ -228,6 +241,25 @@ def workspace_for(nbytes: int, device, count_bytes: int = 0) -> torch.Tensor:
         ent[0][:need_zero].zero_()
     ent[1] = need_zero
     return ent[0]
+
+
+def stale_plan_count(workspace: torch.Tensor, reset: bool = False) -> int:
+    """Tasks the launches on `workspace` found with a stale plan (a context
+    needing more chunks than the tile list held; their output rows are NaN).
+    Synchronises; reset=True zeroes the counter (stream-ordered)."""
+    n = int(workspace[:4].view(torch.int32).item())
+    if reset:
+        workspace[:4].zero_()
+    return n
+
+
+def workspace_of(args: abi.SchedDecodeArgs) -> torch.Tensor | None:
+    """The cached workspace tensor `args` points at (None without tiles or
+    for a caller-owned workspace)."""
+    for ent in _WS.values():
+        if args.workspace and ent[0].data_ptr() == args.workspace:
+            return ent[0]
+    return None
 
 
 def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
@@ -302,7 +334,8 @@ def paged_decode(q, k_pool, v_pool, block_table, ctx_lens, *, out=None,
         rows = q.shape[1] if mode == abi.SOFTMAX else v_pool.shape[1]
         dt = out_dtype or (q.dtype if q is not None else torch.float32)
         out = torch.empty(ctx_lens.numel(), rows, d, dtype=dt, device=v_pool.device)
-    args = build_args(q, k_pool, v_pool, block_table, ctx_lens, out=out, mode=mode, **kw)
+    args = build_args(q, k_pool, v_pool, block_table, ctx_lens, out=out, mode=mode,
+                      stream=stream, **kw)
     launch(args, stream)
     return out
 

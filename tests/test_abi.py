@@ -207,8 +207,9 @@ def test_missing_library_is_an_error(tmp_path):
 def test_split_arguments_validated(schedlib):
     a = fake_args(tiles=ctypes.c_void_p(0x90000), num_tiles=8, tile_pages=4)
     need = schedlib.sched_paged_decode_workspace_bytes(ctypes.byref(a))
-    # counters (32 tasks) + (m, l) for 8 items x 4 heads + partials 8 x 4 x 128 f32
-    assert need == 256 + 256 + 8 * 4 * 128 * 4
+    # stale counter + counters (32 tasks) + (m, l) for 8 items x 4 heads +
+    # partials 8 x 4 x 128 f32, regions 256-byte aligned
+    assert need == 256 + 256 + 256 + 8 * 4 * 128 * 4
     assert schedlib.sched_paged_decode(ctypes.byref(a), None) != 0
     assert "workspace" in abi.last_error()
     a.workspace, a.workspace_bytes = ctypes.c_void_p(0xA0000), need - 1

@@ -591,8 +591,44 @@ def test_split_kv_parity_and_schedule_invariance(tp, kvt):
     plane._queue_w = n + 9
     assert _same(run(b, plane=plane, tiles=tiles, tile_pages=tp, workers=n + 9), out)
     assert int(plane._queue.item()) == n + 9
-    ws = sched_pd._WS[("cuda", torch.cuda.current_device())][0]
-    assert int(ws[:4 * ntask].view(torch.int32).abs().sum()) == 0
+    ws = sched_pd.workspace_for(0, "cuda")
+    assert int(ws[:sched_pd.WS_COUNTERS_OFF + 4 * ntask].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("flags,workers", [(0, 0), (abi.FLAG_FORCE_VALU, 0), (0, 37)])
+def test_stale_split_plan_is_flagged_and_leaves_counters_clean(flags, workers):
+    """A plan built for older lengths: request 1 grew past two tile
+    boundaries (its tasks are stale: output rows NaN, counted, arrival
+    counters untouched), request 2 shrank below one (its extra chunk is
+    skipped, the output is right). A fresh plan on the same workspace then
+    gives the oracle's result everywhere and leaves every counter zero."""
+    old_ctx, new_ctx = [100, 3000, 1000], [100, 3600, 400]
+    b = batch(new_ctx, seed=41)
+    hkv, tp = 8, 32
+    stale_plan = sched_pd.plan_tiles(old_ctx, 16, tp, hkv)
+    fresh_plan = sched_pd.plan_tiles(new_ctx, 16, tp, hkv)
+    n = max(stale_plan.shape[0], fresh_plan.shape[0], len(new_ctx) * hkv)
+    plane = SchedPlane(max_tasks=n)
+    r = ref(b)
+    ws = sched_pd.workspace_for(0, "cuda")
+    sched_pd.stale_plan_count(ws, reset=True)
+    for plan in (stale_plan, fresh_plan):
+        nt = plan.shape[0]
+        plane.set_num_tasks(nt if workers else 0)
+        plane.push()
+        if workers:
+            plane.reset_queue(workers)
+        o = run(b, plane=plane, tiles=plan, tile_pages=tp, flags=flags, workers=workers)
+        got = o.cpu().numpy()
+        if plan is stale_plan:
+            assert np.isnan(got[1]).all()
+            assert par_err(got[[0, 2]], r[[0, 2]]) <= TOL_BF16
+            assert sched_pd.stale_plan_count(ws, reset=True) == hkv
+        else:
+            assert par_err(got, r) <= TOL_BF16
+            assert sched_pd.stale_plan_count(ws) == 0
+        counters = ws[sched_pd.WS_COUNTERS_OFF:sched_pd.WS_COUNTERS_OFF + 4 * len(new_ctx) * hkv]
+        assert int(counters.view(torch.int32).abs().sum()) == 0
 
 
 def _same(a, b):
