@@ -240,6 +240,20 @@ void sched_pd_default_args(SchedDecodeArgs *a);
  * python/kernels/paged_softmax.cu:47-54). */
 int sched_paged_decode(const SchedDecodeArgs *a, void *stream);
 
+/* sched_paged_decode without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc); it has no counterpart in the reference. Same
+ * arguments, except that a->workspace must be NULL and workspace_bytes 0: a
+ * split launch (tiles != NULL) uses the library's own scratch, a 16 MiB
+ * device array per GPU held until the process ends, and is rejected with
+ * hipErrorInvalidValue when it needs more (sched_paged_decode_workspace_bytes
+ * above 16 MiB). Before each split launch one small kernel on `stream` zeroes
+ * the scratch's stale counter and this launch's arrival counters. Calls on one
+ * GPU share its scratch: calls that overlap on one GPU (two streams, two
+ * threads) race. Without tiles it is sched_paged_decode. Returns 0 or a
+ * hipError_t code. */
+int sched_paged_decode_noalloc(const SchedDecodeArgs *a, void *stream);
+
 /* Bytes of workspace a launch with these arguments needs (0 without tiles,
  * or -1 on invalid arguments). */
 int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a);

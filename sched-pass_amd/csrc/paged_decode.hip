@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "kernel_set.h"
 #include "rt_internal.h"
@@ -324,9 +325,99 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   return 0;
 }
 
+// ---- scratch of the no-allocation entry point ------------------------------
+// The split-KV workspace of sched_paged_decode_noalloc: a file-scope device
+// array, one copy per GPU, held until the process ends. Host code never
+// passes the array's name to a kernel or copy: it uses the device address
+// hipGetSymbolAddress returns for the current device (kept per device).
+constexpr uint64_t kScratchBytes = 16ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device (nullptr on error).
+void *scratch_address(int *dev_out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(e, "hipGetDevice failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error(hipErrorInvalidDevice, "device %d is beyond the %d the library tracks", dev,
+              kMaxDevices);
+    return nullptr;
+  }
+  *dev_out = dev;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// Zero n words at p (stream-ordered; a kernel, so a captured graph records no
+// memset node).
+__global__ void zero_words(uint32_t *p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
 } // namespace
 
 extern "C" {
+
+int sched_paged_decode_noalloc(const SchedDecodeArgs *a, void *stream) {
+  if (a == nullptr)
+    return set_error(hipErrorInvalidValue, "args is NULL");
+  if (a->workspace != nullptr || a->workspace_bytes != 0)
+    return set_error(hipErrorInvalidValue,
+                     "sched_paged_decode_noalloc takes no workspace (it uses the library's "
+                     "%llu-byte scratch)", (unsigned long long)kScratchBytes);
+  if (a->tiles == nullptr)
+    return sched_paged_decode(a, stream);
+  KParams kp;
+  Selected sel;
+  SchedDecodeArgs b = *a;
+  // validate first with a stand-in workspace address (nothing is launched)
+  b.workspace = reinterpret_cast<void *>(uintptr_t(256));
+  b.workspace_bytes = kScratchBytes;
+  const WsLayout W = ws_layout(a);
+  if (W.total > kScratchBytes)
+    return set_error(hipErrorInvalidValue,
+                     "this launch needs %llu bytes of split workspace; the no-allocation entry "
+                     "point holds %llu (use sched_paged_decode with a workspace)",
+                     (unsigned long long)W.total, (unsigned long long)kScratchBytes);
+  int rc = prepare(&b, &kp, &sel);
+  if (rc)
+    return rc;
+  int dev = 0;
+  void *ptr = scratch_address(&dev);
+  if (ptr == nullptr)
+    return hipErrorInvalidSymbol;
+  // the stale counter and this launch's arrival counters start at zero
+  const uint32_t words = (uint32_t)(W.ml_off / 4u);
+  const uint32_t blocks = (words + 255u) / 256u;
+  hipLaunchKernelGGL(zero_words, dim3(blocks < 1024u ? blocks : 1024u), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<uint32_t *>(ptr), words);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(e, "scratch clear failed: %s", hipGetErrorString(e));
+  b.workspace = ptr;
+  b.workspace_bytes = kScratchBytes;
+  return sched_paged_decode(&b, stream);
+}
+
 
 void sched_pd_default_args(SchedDecodeArgs *a) {
   if (!a)

@@ -131,6 +131,7 @@ SIGNATURES = {
     "sched_rt_timer_read": (_c_bool, [ctypes.POINTER(ctypes.c_ulonglong), ctypes.c_uint]),
     "sched_pd_default_args": (None, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),
+    "sched_paged_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),
     "sched_paged_decode_occupancy": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode_kernel_kind": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs)]),

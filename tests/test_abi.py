@@ -204,6 +204,18 @@ def test_missing_library_is_an_error(tmp_path):
         abi._LIB = saved
 
 
+def test_noalloc_refuses_a_workspace_and_oversized_plans_without_the_gpu(schedlib):
+    a = fake_args(tiles=ctypes.c_void_p(0x90000), num_tiles=8, tile_pages=4,
+                  workspace=ctypes.c_void_p(0xA0000), workspace_bytes=1 << 20)
+    assert schedlib.sched_paged_decode_noalloc(ctypes.byref(a), None) != 0
+    assert "no workspace" in abi.last_error()
+    a.workspace, a.workspace_bytes = None, 0
+    a.num_tiles = 1 << 22          # 4M items x 4 heads x 512 B of partials
+    assert schedlib.sched_paged_decode_noalloc(ctypes.byref(a), None) != 0
+    assert "holds 16777216" in abi.last_error()
+    assert schedlib.sched_paged_decode_noalloc(None, None) != 0
+
+
 def test_split_arguments_validated(schedlib):
     a = fake_args(tiles=ctypes.c_void_p(0x90000), num_tiles=8, tile_pages=4)
     need = schedlib.sched_paged_decode_workspace_bytes(ctypes.byref(a))
