@@ -265,9 +265,19 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
                                 plane=p_lpt, workers=W, tiles=tiles2, tile_pages=tp2, **common)
     res["wq_tiles_lpt_timer"] = round(_makespan_us(torch, sched_pd, a_lpt, stream), 2)
     kv = b["kv_bytes"]
+
+    def cut(a, b_):
+        return round(100.0 * (res[a] - res[b_]) / res[a], 2)
+
     return {
         "static_us": res["static_task"], "ticket_wq_us": res["wq_tiles"],
-        "cut_pct": round(100.0 * (res["static_task"] - res["wq_tiles"]) / res["static_task"], 2),
+        # the config's comparison (queue over split tiles vs one workgroup per
+        # task), then its two parts on one decomposition each
+        "queue_plus_split_cut_pct": cut("static_task", "wq_tiles"),
+        "split_cut_pct": cut("static_task", "static_tiles"),
+        "queue_cut_pct": cut("static_tiles", "wq_tiles"),
+        "queue_over_tasks_cut_pct": cut("static_task", "wq_task"),
+        "queue_plus_split_plus_lpt_timer_cut_pct": cut("static_task", "wq_tiles_lpt_timer"),
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
         "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
@@ -278,8 +288,9 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
 
 def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES):
     """128 requests, ctx ~ U{1024..8192}, per-task tau ~ U{ctx/4..ctx}; policy
-    armed (q ~ U(0,1), lambda_bw 0.5, H 0.1: urgent tasks stream 4 pages
-    ahead). Online softmax (score -> -inf) and linear contraction (value -> 0)
+    armed (q ~ U(0,1), lambda_bw 0.5, H 0.1: urgent tasks keep pf_dist = 4
+    pages in flight per wave); the lever's A/B (firing, priced out, all
+    urgent, all polite) on the softmax skip launch. Online softmax (score -> -inf) and linear contraction (value -> 0)
     variants; pages past the budget skipped (default) or loaded and masked
     (the reference weave's behaviour). Work queue over split tiles, pi by
     urgency; then the skip variants with pi = longest-first over tiles of
@@ -314,11 +325,41 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
             ("linear_skip", {"mode": abi.LINEAR, "lin_w": w}, lout, 0.5)):
         a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                 out=o, plane=plane, workers=W, tiles=tiles, tile_pages=tile_pages,
-                                policy=(1.0, 1.0, 0.1), **kw)
+                                policy=(1.0, 1.0, 0.1), pf_dist=4, **kw)
         us = _makespan_us(torch, sched_pd, a, stream)
         loaded = (full if "loads" in name else kept) * vb
         res[name] = {"us": round(us, 2), "gbs_loaded": round(loaded / us / 1e3, 1),
                      "gbs_ctx_equiv": round(full * vb / us / 1e3, 1)}
+    # the policy lever on the softmax skip launch: the config's pricing fires
+    # it (q > lambda_bw + H: urgent tasks keep pf_dist = 4 pages in flight per
+    # wave instead of 2), against priced out (lambda_bw = 1000: no task
+    # urgent), every task urgent and every task polite. Same bits every time.
+    ab = {}
+    base = None
+    for name, lam, hint in (("firing", 0.5, None), ("priced_out", 1000.0, None),
+                            ("all_urgent", 0.5, abi.HINT_URGENT),
+                            ("all_polite", 0.5, abi.HINT_POLITE)):
+        plane.set_lambda(lam)
+        plane.set_rows(q=b["urgency"], tau=b["tau"], hint=np.full(ntask, 0 if hint is None else hint),
+                       n=ntask)
+        plane.push()
+        a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                b["ctx_lens"], out=out, plane=plane, workers=W, tiles=tiles,
+                                tile_pages=tile_pages, policy=(1.0, 1.0, 0.1), pf_dist=4)
+        ab[name + "_us"] = round(_makespan_us(torch, sched_pd, a, stream), 2)
+        sched_pd.launch(a, stream)
+        torch.cuda.synchronize()
+        if base is None:
+            base = out.clone()
+        elif not torch.equal(out, base):
+            raise AssertionError(f"policy {name} changed the output bits")
+    plane.set_lambda(0.5)
+    plane.set_rows(q=b["urgency"], tau=b["tau"], n=ntask)
+    plane.push()
+    ab["bit_exact"] = True
+    ab["firing_vs_priced_out_pct"] = round(
+        100.0 * (ab["firing_us"] - ab["priced_out_us"]) / ab["priced_out_us"], 2)
+    res["policy_ab"] = ab
     tp2 = 2 * tile_pages
     tiles2 = sched_pd.plan_tiles(ctx, 16, tp2, 8)
     nt2 = tiles2.shape[0]
@@ -335,7 +376,7 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
                             ("linear_skip_lpt", {"mode": abi.LINEAR, "lin_w": w}, lout, 0.5)):
         a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                 out=o, plane=plane2, workers=W, tiles=tiles2, tile_pages=tp2,
-                                policy=(1.0, 1.0, 0.1), **kw)
+                                policy=(1.0, 1.0, 0.1), pf_dist=4, **kw)
         us = _makespan_us(torch, sched_pd, a, stream)
         res[name] = {"us": round(us, 2), "gbs_loaded": round(kept * vb / us / 1e3, 1),
                      "gbs_ctx_equiv": round(full * vb / us / 1e3, 1)}
@@ -486,9 +527,12 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
     """The uniform step's batch (64 x 2048, bf16, Hq 32 / Hkv 8) with V stored
     token-major: HND pages [P, Hkv, 16, 128] and FlashInfer's NHD cache
     [P, 2, 16, Hkv, 128] read in place; the same values as the d-major
-    layout, rotating `tables` block tables."""
-    import numpy as np
+    layout, rotating `tables` block tables. Then a serving step (the writer
+    appends one token per request, then the decode) on each 16-token-page V
+    layout, and the MFMA against the VALU kernel at 1, 2 and 4 q-heads per
+    kv-head."""
     import kv_cache
+    import sched_abi as abi
     R, T, hkv, hq, d, ps = 64, 2048, 8, 32, 128, 16
     npg = R * T // ps * tables
     g = torch.Generator(device="cuda").manual_seed(11)
@@ -512,11 +556,71 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
         return {"us": round(ms * 1e3, 2), "gbs": round(kv_bytes / ms / 1e6, 1),
                 "kernel": sched_pd.kernel_kind(args[0])}
 
+    def serving_step(k_pool, v_pool, layout):
+        # one decode step of a server: append each request's new token
+        # (position 2047, the cache writer), then decode all 2048 tokens
+        k1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+        v1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+        app = torch.arange(R + 1, dtype=torch.int32, device="cuda")
+        ins = [kv_cache.build_append_args(k1, v1, app, ctx, k_pool, v_pool, bt, v_layout=layout,
+                                          max_append=1) for bt in bts]
+        dec = [sched_pd.build_args(q, k_pool, v_pool, bt, ctx, out=out, v_layout=layout)
+               for bt in bts]
+        fa = lambda i: kv_cache.launch_append(ins[i % tables], stream)  # noqa: E731
+        fd = lambda i: sched_pd.launch(dec[i % tables], stream)  # noqa: E731
+
+        def both(i):
+            fa(i)
+            fd(i)
+        for i in range(2 * tables):
+            both(i)
+        torch.cuda.synchronize()
+        out_ = {}
+        for name, f in (("append", fa), ("decode", fd), ("step", both)):
+            out_[name + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+        return out_
+
     res = {}
     kp = (torch.randn(npg, hkv, ps, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
     vp = (torch.randn(npg, hkv, ps, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
     res["hnd_token_major_v"] = measure(kp, vp, "tokmajor")
     res["hnd_d_major_v"] = measure(kp, vp.view(npg, hkv, d, ps), "dmajor")
+    # 16-token pages: the layout a serving step (append + decode) runs faster on
+    st = {"token_major_v": serving_step(kp, vp, "tokmajor"),
+          "d_major_v": serving_step(kp, vp.view(npg, hkv, d, ps), "dmajor")}
+    st["faster"] = min(("token_major_v", "d_major_v"), key=lambda k: st[k]["step_us"])
+    st["paged_kv_cache_default"] = kv_cache.PagedKvCache(1, hkv, d, 16, dtype=torch.bfloat16,
+                                                         device="cuda").v_layout
+    res["serving_step_page16"] = st
+    # MFMA vs VALU kernel below 4 q-heads per kv-head (same KV bytes: Hkv 8)
+    grp = {}
+    for G in (1, 2, 4):
+        qg = (torch.randn(R, 8 * G, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+        og = torch.empty(R, 8 * G, d, dtype=torch.bfloat16, device="cuda")
+        row = {}
+        for kern, flags in (("mfma", 0), ("valu", abi.FLAG_FORCE_VALU)):
+            args = [sched_pd.build_args(qg, kp, vp.view(npg, hkv, d, ps), bt, ctx, out=og,
+                                        flags=flags) for bt in bts]
+            f = lambda i: sched_pd.launch(args[i % tables], stream)  # noqa: E731
+            for i in range(2 * tables):
+                f(i)
+            torch.cuda.synchronize()
+            row[kern + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+            row["default"] = sched_pd.kernel_kind(sched_pd.build_args(
+                qg, kp, vp.view(npg, hkv, d, ps), bts[0], ctx, out=og))
+        if G == 1:
+            # one wave per task, over token-major V (fp32 Q: the MFMA kernel,
+            # which takes bf16 Q, would be chosen otherwise)
+            args = [sched_pd.build_args(qg.float(), kp, vp, bt, ctx, out=og, v_layout="tokmajor")
+                    for bt in bts]
+            assert sched_pd.kernel_kind(args[0]) == "wave"
+            f = lambda i: sched_pd.launch(args[i % tables], stream)  # noqa: E731
+            for i in range(2 * tables):
+                f(i)
+            torch.cuda.synchronize()
+            row["wave_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+        grp[f"G{G}"] = row
+    res["kernel_by_group"] = grp
     del kp, vp
     torch.cuda.empty_cache()
     nhd = (torch.randn(npg, 2, ps, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
@@ -659,7 +763,15 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         if nseq == batch_sizes[-1]:
             t = [step_ms(stock) for _ in range(steps)]
             row["stock"] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
-                            "min_us": round(1e3 * min(t), 2)}
+                            "min_us": round(1e3 * min(t), 2), "kernel": sched_pd.kernel_kind(stock)}
+            # the same step on the general VALU kernel (one workgroup per task)
+            gen = sched_pd.build_args(q, k_view, v_view, bt, nbl,
+                                      **dict(common, flags=common["flags"] | abi.FLAG_NO_WAVE))
+            for _ in range(3):
+                sched_pd.launch(gen, stream)
+            t = [step_ms(gen) for _ in range(steps)]
+            row["stock_general_kernel"] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
+                                           "min_us": round(1e3 * min(t), 2)}
         for name, order in orders.items():
             if nseq != batch_sizes[-1] and name not in ("identity", "lpt_timer"):
                 continue
@@ -698,6 +810,10 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
             for name in ("identity", "sorted_ascending", "lpt_oracle", "lpt_timer"):
                 row[name]["vs_stock_pct"] = round(100 * (row[name]["mean_us"] - st) / st, 2)
             row["kv_bytes"] = npages * PT * 2 * SD * 4
+            for name in ("stock", "stock_general_kernel", "lpt_timer"):
+                gbs = row["kv_bytes"] / row[name]["mean_us"] / 1e3
+                row[name]["gbs"] = round(gbs, 1)
+                row[name]["frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 4)
             res[str(nseq)] = row
         res.setdefault("bit_exact_vs_identity", True)
         res["bit_exact_vs_identity"] = res["bit_exact_vs_identity"] and exact

@@ -149,11 +149,14 @@ bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
 /* flags */
 #define SCHED_PD_FLAG_RT_TABLES 0x1u    /* take order/ctrl/timer/queue from the C runtime's slots */
 #define SCHED_PD_FLAG_WALLCLOCK 0x2u    /* timer counts s_memrealtime (100 MHz) instead of s_memtime */
-#define SCHED_PD_FLAG_FORCE_VALU 0x4u   /* use the VALU kernel even where the MFMA kernel applies */
+#define SCHED_PD_FLAG_FORCE_VALU 0x4u   /* use the general VALU kernel (one workgroup per
+                                           work item) even where another kernel applies */
 #define SCHED_PD_FLAG_CTX_IN_PAGES 0x8u /* ctx_lens counts full pages, not tokens */
 #define SCHED_PD_FLAG_SHED_LOADS 0x10u  /* load shed tokens and mask them (reference weave,
                                            lib/SchedWeave.cpp:646-651) instead of skipping
                                            the pages past a prefix budget; same output */
+#define SCHED_PD_FLAG_NO_WAVE 0x20u     /* do not use the one-wave-per-task kernel (G = 1):
+                                           take the general VALU kernel instead */
 
 /* One decode step. Element (page, kv-head h, token t, dim j) of the pools:
  *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
@@ -258,8 +261,10 @@ int sched_paged_decode_noalloc(const SchedDecodeArgs *a, void *stream);
  * or -1 on invalid arguments). */
 int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a);
 
-/* Workgroups per CU of the kernel `a` selects (0 = unknown). Counterpart of
- * reference paged_softmax_occupancy (python/kernels/paged_softmax.cu:61-67). */
+/* Work items resident per CU for the kernel `a` selects (workgroups per CU,
+ * times the tasks a workgroup of the one-wave-per-task kernel runs; 0 =
+ * unknown). Counterpart of reference paged_softmax_occupancy
+ * (python/kernels/paged_softmax.cu:61-67), whose CTAs are tasks. */
 int sched_paged_decode_occupancy(const SchedDecodeArgs *a);
 
 /* Policy lever depths of the kernel `a` selects (a->pf_dist ignored): *stock =
@@ -272,7 +277,9 @@ int sched_paged_decode_occupancy(const SchedDecodeArgs *a);
 int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
                                       uint32_t *deepest);
 
-/* Which kernel `a` selects: 0 = VALU, 1 = MFMA, -1 = invalid args. */
+/* Which kernel `a` selects: 0 = the general VALU kernel (one workgroup per
+ * work item), 1 = MFMA, 2 = one wave per task (G = 1 softmax over token-major
+ * rows, no split tiles), -1 = invalid args. */
 int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
 
 /* Compute-unit count of the current device (0 on error). */

@@ -1,0 +1,362 @@
+// decode_wave.h -- one wave per task for one q-head per kv-head (G = 1): the
+// shape of the reference's JIT kernel (python/kernels/paged_softmax.cu:14-45,
+// fp32, head dim 32, [token][K|V] pages) and of MHA caches with token-major
+// rows, fp32 / bf16 / fp16 KV, head dim 32 (fp32) / 64 / 128, softmax mode.
+//
+// With G = 1 a task is one (request, head) stream of K and V rows and little
+// arithmetic, so what bounds it is how many bytes are in flight and how long
+// the chain ctx -> page id -> KV takes, not compute. A workgroup of NWT waves
+// runs NWT independent tasks (no LDS, no barrier), so many tasks' chains
+// overlap and each wave keeps DEPTH 16-token chunks of loads in flight.
+//
+// Lane layout: a K or V row of D elements is LPR = D / VN lanes of 16-byte
+// loads (VN elements each); lane = ts * LPR + ds holds dims ds*VN..+VN-1 of
+// token slot ts, so one load instruction covers TPI = 64 / LPR tokens and a
+// 16-token chunk takes NI = 16 / TPI instructions per tensor. The score of
+// a token is the lane's partial dot product summed over its LPR lanes with
+// DPP (quad_perm, row_half_mirror, row_mirror; a row swap for 32 lanes), so
+// every lane of the slot holds the same bits. Each token slot keeps its own
+// online softmax state (m, l, acc) over the tokens it sees (token t of a
+// chunk goes to slot t % TPI), with no cross-slot reduction per chunk; the
+// TPI slot states merge once per task with lane shuffles. Which slot
+// sees a token depends only on the token's position, so the result bits do
+// not depend on pi, the work queue or which wave ran the task.
+//
+// Levers per wave: pi remaps the wave's virtual workgroup id (blockIdx * NWT
+// + wave) over the launch's work items; the ticket queue hands tasks to
+// waves; the timer row is added by lane 0 of the wave. The shed masks scores
+// to -inf (and skips chunks past a prefix budget, as the other kernels do).
+// The policy lever has no action here (no prefetch ring choice).
+#pragma once
+
+#include "common.h"
+
+namespace schedpd {
+
+// KV bytes each wave keeps in flight (a build-time tuning knob).
+#ifndef SCHED_PD_WAVE_BYTES
+#define SCHED_PD_WAVE_BYTES 16384
+#endif
+// Waves (tasks) per workgroup.
+#ifndef SCHED_PD_WAVE_NWT
+#define SCHED_PD_WAVE_NWT 4
+#endif
+
+typedef __attribute__((ext_vector_type(4))) unsigned wave_u4;
+
+template <typename KVT> struct WaveElem;
+template <> struct WaveElem<float> { static constexpr int VN = 4; };
+template <> struct WaveElem<uint16_t> { static constexpr int VN = 8; };  // bf16
+template <> struct WaveElem<_Float16> { static constexpr int VN = 8; };
+
+// 16 bytes of KV as VN floats.
+__device__ __forceinline__ void wave_cvt(const wave_u4 &r, float *f, float) {
+  f[0] = __uint_as_float(r.x);
+  f[1] = __uint_as_float(r.y);
+  f[2] = __uint_as_float(r.z);
+  f[3] = __uint_as_float(r.w);
+}
+__device__ __forceinline__ void wave_cvt(const wave_u4 &r, float *f, uint16_t) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void wave_cvt(const wave_u4 &r, float *f, _Float16) {
+  typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const h2 v = __builtin_bit_cast(h2, w[k]);
+    f[2 * k] = (float)v.x;
+    f[2 * k + 1] = (float)v.y;
+  }
+}
+
+// DPP controls (GFX9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror,
+// row_mirror, row_ror:8.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140,
+              kDppRor8 = 0x128;
+
+template <int CTRL> __device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the LPR consecutive lanes of a token slot; every lane of the slot
+// ends with the same bits (each step adds a value and its partner's, and
+// a + b == b + a).
+template <int LPR> __device__ __forceinline__ float slot_sum(float x) {
+  if constexpr (LPR >= 2)
+    x += dpp_f<kDppXor1>(x);
+  if constexpr (LPR >= 4)
+    x += dpp_f<kDppXor2>(x);
+  if constexpr (LPR >= 8)
+    x += dpp_f<kDppHalfMirror>(x);
+  if constexpr (LPR >= 16)
+    x += dpp_f<kDppMirror>(x);
+  if constexpr (LPR >= 32) {
+    const unsigned u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  return x;
+}
+
+// Online softmax state of one token slot (uniform over its LPR lanes) and
+// the lane's VN dims of the unnormalised output.
+template <int VN> struct WaveState {
+  float m, l;
+  float acc[VN];
+};
+
+// Merge the state of the slot S lanes away into this one (both partners end
+// with the same bits: max and the sum of two products commute). Once per
+// task, so the exchange is a plain lane shuffle.
+template <int S, int VN>
+__device__ __forceinline__ void merge_partner(WaveState<VN> &st) {
+  const float mo = __shfl_xor(st.m, S), lo = __shfl_xor(st.l, S);
+  float ao[VN];
+#pragma unroll
+  for (int e = 0; e < VN; ++e)
+    ao[e] = __shfl_xor(st.acc[e], S);
+  const float mn = fmaxf(st.m, mo);
+  const float cs = __builtin_amdgcn_exp2f(st.m - mn), co = __builtin_amdgcn_exp2f(mo - mn);
+  st.l = st.l * cs + lo * co;
+#pragma unroll
+  for (int e = 0; e < VN; ++e)
+    st.acc[e] = st.acc[e] * cs + ao[e] * co;
+  st.m = mn;
+}
+
+template <typename KVT, int D> struct WaveShape {
+  static constexpr int VN = WaveElem<KVT>::VN;
+  static constexpr int LPR = D / VN;        // lanes per K / V row
+  static constexpr int TPI = 64 / LPR;      // token slots (tokens per load instruction)
+  static constexpr int NI = 16 / TPI;       // load instructions per tensor per 16-token chunk
+  // chunks in flight per wave: SCHED_PD_WAVE_BYTES of KV, at least two
+  static constexpr int CHUNK_BYTES = 16 * D * (int)sizeof(KVT) * 2;
+  static constexpr int DEPTH =
+      SCHED_PD_WAVE_BYTES / CHUNK_BYTES >= 2 ? SCHED_PD_WAVE_BYTES / CHUNK_BYTES : 2;
+  static_assert(LPR >= 2 && LPR <= 32 && TPI * LPR == 64 && NI * TPI == 16, "wave shape");
+};
+
+template <typename KVT, int D> struct WaveChunk {
+  wave_u4 k[WaveShape<KVT, D>::NI];
+  wave_u4 v[WaveShape<KVT, D>::NI];
+};
+
+// Work items of one wave: the static grid (virtual workgroup id = blockIdx *
+// NWT + wave, remapped by pi over the launch's items) or the ticket queue
+// (W worker waves; claim after the body, lane 0's atomic, broadcast by
+// readfirstlane). Same decisions as run_tasks, per wave.
+template <int NWT, class Body>
+__device__ __forceinline__ void run_wave_tasks(const LeverTables &L, Body &&body) {
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t pid = blockIdx.x * NWT + w;
+  uint32_t ntasks = 0u;
+  if (L.wq) {
+    const bool armed = L.queue != nullptr && L.ctrl != nullptr && gridDim.y == 1 &&
+                       gridDim.z == 1;
+    ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
+  }
+  if (ntasks == 0u) {
+    if (pid < L.nitems)
+      body(remap_static(L, pid, L.nitems));
+    return;
+  }
+  const uint32_t W = L.workers;
+  if (pid >= W || pid >= ntasks)
+    return;
+  const uint32_t last_ticket = W + ntasks - 1u;
+  const uint32_t lane = threadIdx.x & 63u;
+  uint32_t raw = pid;
+  while (true) {
+    body(remap_wq(L, raw, ntasks));
+    uint32_t t = 0u;
+    if (lane == 0u) {
+      t = __hip_atomic_fetch_add(L.queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t == last_ticket)
+        __hip_atomic_store(L.queue, W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    raw = __builtin_amdgcn_readfirstlane(t);
+    if (raw >= ntasks)
+      return;
+  }
+}
+
+template <typename KVT, int D, int NWT>
+__global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
+  using S = WaveShape<KVT, D>;
+  constexpr int VN = S::VN, LPR = S::LPR, TPI = S::TPI, NI = S::NI, DEPTH = S::DEPTH;
+  constexpr uint32_t EB = sizeof(KVT);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t ts = lane / LPR, ds = lane % LPR;
+  const bool toff = timer_off_latched(P.L);
+
+  run_wave_tasks<NWT>(P.L, [&](uint32_t task) __attribute__((always_inline)) {
+    if (task >= P.ntasks)
+      return;
+    const unsigned long long t0 = read_clock(P.L.wallclock);
+    const uint32_t r = task / P.Hkv, h = task % P.Hkv;
+    const TaskPolicy pol = task_policy(P.L, task);
+    const uint32_t n = ctx_tokens(P, r);
+    const uint32_t nload = load_extent(P, n, pol.budget);
+    const uint32_t nchunks = (nload + 15u) / 16u;
+    const int64_t row = P.indptr ? (int64_t)P.indptr[r] : (int64_t)r * P.bt_stride;
+
+    // the lane's VN dims of q, pre-scaled into the exp2 domain
+    float q[VN];
+#pragma unroll
+    for (int e = 0; e < VN; ++e)
+      q[e] = load_q(P, ((int64_t)r * P.Hq + h) * D + ds * VN + e) * P.scale_log2;
+
+    WaveState<VN> st;
+    st.m = kMInit;
+    st.l = 0.f;
+#pragma unroll
+    for (int e = 0; e < VN; ++e)
+      st.acc[e] = 0.f;
+
+    // uniform (scalar) page bases; each lane adds a 32-bit offset (its token
+    // slot's row and its 16 bytes of the row), so the loads take the
+    // scalar-base + vector-offset form
+    const uint8_t *kb = static_cast<const uint8_t *>(P.k_pool) + (int64_t)h * P.khs * EB;
+    const uint8_t *vb = static_cast<const uint8_t *>(P.v_pool) + (int64_t)h * P.vhs * EB;
+    const int64_t kps = P.kps * EB, vps = P.vps * EB;
+    const int64_t kstep = (int64_t)TPI * P.kts * EB, vstep = (int64_t)TPI * P.vts * EB;
+    const int64_t krow = P.kts * EB, vrow = P.vts * EB;
+    const uint32_t klane = ts * (uint32_t)krow + ds * 16u, vlane = ts * (uint32_t)vrow + ds * 16u;
+    const uint32_t ps = P.ps, cpp = ps / 16u; // 16-token chunks per page
+    const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
+    const uint32_t budget = pol.budget;
+
+    // Page ids in windows of 64 pages: lane i holds the id of window page i
+    // (one vector load per window), read back per chunk with readlane, so a
+    // chunk's KV loads never wait on a page-table load.
+    int32_t win = 0;
+    uint32_t w0 = 0;
+    auto issue = [&](uint32_t c, WaveChunk<KVT, D> &B) __attribute__((always_inline)) {
+      const uint32_t b = c / cpp, o = (c % cpp) * 16u;
+      const int64_t page = __builtin_amdgcn_readlane(win, (int)(b - w0));
+      const uint8_t *kp = kb + page * kps + (int64_t)o * krow;
+      const uint8_t *vp = vb + page * vps + (int64_t)o * vrow;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        B.k[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const wave_u4 *>(kp + i * kstep + (uint64_t)klane));
+        B.v[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const wave_u4 *>(vp + i * vstep + (uint64_t)vlane));
+      }
+    };
+    auto compute = [&](uint32_t c, const WaveChunk<KVT, D> &B) __attribute__((always_inline)) {
+      const uint32_t pos0 = c * 16u, o = (c % cpp) * 16u; // o: chunk offset in its page
+      // a chunk wholly inside the context and the budget needs no mask
+      const bool full = pos0 + 16u <= n &&
+                        (budget == 0xFFFFFFFFu || (prefix ? pos0 : o) + 16u <= budget);
+      float s[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float f[VN];
+        wave_cvt(B.k[i], f, KVT());
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < VN; ++e)
+          dot = __builtin_fmaf(q[e], f[e], dot);
+        s[i] = slot_sum<LPR>(dot);
+      }
+      if (!full) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const uint32_t k = i * TPI + ts; // token in the chunk
+          if (!(pos0 + k < n && (prefix ? pos0 + k : o + k) < budget))
+            s[i] = kNegInf;
+        }
+      }
+      float mc = s[0];
+#pragma unroll
+      for (int i = 1; i < NI; ++i)
+        mc = fmaxf(mc, s[i]);
+      const float mn = fmaxf(st.m, mc);
+      const float cf = __builtin_amdgcn_exp2f(st.m - mn);
+      float p[NI];
+      float lsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
+        lsum += p[i];
+      }
+      st.l = st.l * cf + lsum;
+#pragma unroll
+      for (int e = 0; e < VN; ++e)
+        st.acc[e] *= cf;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float f[VN];
+        wave_cvt(B.v[i], f, KVT());
+#pragma unroll
+        for (int e = 0; e < VN; ++e)
+          st.acc[e] = __builtin_fmaf(p[i], f[e], st.acc[e]);
+      }
+      st.m = mn;
+    };
+
+    // Segments of up to 64 pages: load the window, then stream its chunks
+    // through a ring of DEPTH chunks -- an unconditional prologue (a segment
+    // with fewer chunks re-reads its last one into the spare slots) and a
+    // branch-free steady loop, so the compiler's vmcnt waits keep DEPTH-1
+    // chunks in flight; the tail computes what is left.
+    const uint32_t npages = (nload + ps - 1u) / ps;
+    for (w0 = 0; w0 < npages; w0 += 64u) {
+      const uint32_t wn = min(npages - w0, 64u);
+      win = lane < wn ? P.bt[row + w0 + lane] : 0;
+      const uint32_t c0 = w0 * cpp;
+      const uint32_t c1 = min((w0 + wn) * cpp, nchunks);
+      const uint32_t cnt = c1 - c0, last = c1 - 1u;
+      WaveChunk<KVT, D> buf[DEPTH];
+#pragma unroll
+      for (int sl = 0; sl < DEPTH; ++sl)
+        issue(min(c0 + sl, last), buf[sl]);
+      uint32_t j = 0;
+      for (; j + 2u * DEPTH <= cnt; j += DEPTH) {
+#pragma unroll
+        for (int sl = 0; sl < DEPTH; ++sl) {
+          compute(c0 + j + sl, buf[sl]);
+          issue(c0 + j + DEPTH + sl, buf[sl]);
+        }
+      }
+      for (; j < cnt; j += DEPTH) {
+#pragma unroll
+        for (int sl = 0; sl < DEPTH; ++sl) {
+          if (j + sl < cnt) {
+            compute(c0 + j + sl, buf[sl]);
+            if (j + DEPTH + sl < cnt)
+              issue(c0 + j + DEPTH + sl, buf[sl]);
+          }
+        }
+      }
+    }
+
+    // merge the TPI token slots (lanes LPR, 2 LPR, ... apart)
+    if constexpr (TPI >= 8)
+      merge_partner<8, VN>(st);
+    if constexpr (TPI >= 4)
+      merge_partner<16, VN>(st);
+    if constexpr (TPI >= 2)
+      merge_partner<32, VN>(st);
+    if (ts == 0u) {
+      const int64_t o = ((int64_t)r * P.Hq + h) * D + ds * VN;
+#pragma unroll
+      for (int e = 0; e < VN; ++e)
+        store_out(P, o + e, st.acc[e] / st.l);
+    }
+    if (lane == 0u && P.L.timer != nullptr && task < P.L.max_tasks && !toff) {
+      const unsigned long long dt = read_clock(P.L.wallclock) - t0;
+      __hip_atomic_fetch_add(P.L.timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  });
+}
+
+} // namespace schedpd

@@ -6,6 +6,7 @@
 
 #include "decode_mfma.h"
 #include "decode_valu.h"
+#include "decode_wave.h"
 
 // MFMA kernel shape: waves per workgroup, pages in flight per wave (stock,
 // urgent). Overridable at build time for tuning sweeps.
@@ -109,6 +110,23 @@ constexpr int mfma_du(bool fp8, bool vt, bool pg) {
   SCHED_PD_VALU_ONE(PRE, uint8_t, 64)                                                            \
   SCHED_PD_VALU_ONE(PRE, uint8_t, 128)
 
+// One wave per task (G = 1, softmax, token-major rows).
+#define SCHED_PD_WAVE_ALL(PRE)                                                                   \
+  PRE template __global__ void schedpd::decode_wave<float, 32, SCHED_PD_WAVE_NWT>(               \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<float, 64, SCHED_PD_WAVE_NWT>(               \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<float, 128, SCHED_PD_WAVE_NWT>(              \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<uint16_t, 64, SCHED_PD_WAVE_NWT>(            \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<uint16_t, 128, SCHED_PD_WAVE_NWT>(           \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<_Float16, 64, SCHED_PD_WAVE_NWT>(            \
+      schedpd::KParams);                                                                         \
+  PRE template __global__ void schedpd::decode_wave<_Float16, 128, SCHED_PD_WAVE_NWT>(           \
+      schedpd::KParams);
+
 // Declarations for the launcher (paged_decode.hip).
 #define SCHED_PD_DECLARE_ALL_KERNELS                                                             \
   SCHED_PD_MFMA_BF16_PAGE16(extern)                                                              \
@@ -117,4 +135,5 @@ constexpr int mfma_du(bool fp8, bool vt, bool pg) {
   SCHED_PD_MFMA_FP8_TOKMAJOR(extern)                                                             \
   SCHED_PD_MFMA_F16(extern)                                                                      \
   SCHED_PD_MFMA_F16_PAGEBLOCKS(extern)                                                           \
-  SCHED_PD_VALU_ALL(extern)
+  SCHED_PD_VALU_ALL(extern)                                                                      \
+  SCHED_PD_WAVE_ALL(extern)

@@ -22,6 +22,7 @@ struct LeverTables {
   uint32_t max_tasks;        // rows in order/ctrl/timer
   uint32_t nitems;           // work items of this launch (static grid size)
   uint32_t wq;               // 1 = launched as W persistent workers
+  uint32_t workers;          // W of a work-queue launch (per-wave kernels)
   uint32_t wallclock;        // timer source: 1 = s_memrealtime, 0 = s_memtime
   float dT, dR, H;           // policy marginal-exchange constants
 };

@@ -24,7 +24,8 @@ typedef void (*KernelFn)(KParams);
 struct Selected {
   KernelFn fn;
   int block;
-  int mfma;
+  int mfma;     // kernel kind: 0 general VALU, 1 MFMA, 2 one wave per task
+  int per_block; // work items a workgroup runs at once
 };
 
 template <typename KVT, int D> KernelFn valu_kernel(bool linear, uint32_t G) {
@@ -143,6 +144,45 @@ void ring_depths(const SchedDecodeArgs *a, bool mfma, uint32_t *ds, uint32_t *du
   *du = (uint32_t)mfma_du(fp8, v_token_major(a), a->page_size > 16);
 }
 
+// The one-wave-per-task kernel's shape: softmax, one q-head per kv-head, no
+// split tiles, fp32 KV (head dim 32/64/128) or bf16 / fp16 KV (64/128), K and
+// V token-major rows (dims contiguous), 16-byte aligned pools and strides.
+bool wave_applies(const SchedDecodeArgs *a) {
+  if (a->flags & (SCHED_PD_FLAG_FORCE_VALU | SCHED_PD_FLAG_NO_WAVE))
+    return false;
+  if (a->mode != SCHED_PD_SOFTMAX || a->num_q_heads != a->num_kv_heads || a->tiles)
+    return false;
+  const uint32_t d = a->head_dim;
+  if (a->kv_dtype == SCHED_PD_F32) {
+    if (d != 32 && d != 64 && d != 128)
+      return false;
+  } else if (a->kv_dtype == SCHED_PD_BF16 || a->kv_dtype == SCHED_PD_F16) {
+    if (d != 64 && d != 128)
+      return false;
+  } else {
+    return false;
+  }
+  if (a->v_dim_stride != 1)
+    return false;
+  const int64_t eb = elem_bytes(a->kv_dtype);
+  if ((a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 || (a->k_head_stride * eb) % 16)
+    return false;
+  if ((a->v_tok_stride * eb) % 16 || (a->v_page_stride * eb) % 16 || (a->v_head_stride * eb) % 16)
+    return false;
+  return aligned16(a->k_pool) && aligned16(a->v_pool);
+}
+
+KernelFn wave_kernel(const SchedDecodeArgs *a) {
+  constexpr int NWT = SCHED_PD_WAVE_NWT;
+  if (a->kv_dtype == SCHED_PD_F32)
+    return a->head_dim == 32   ? decode_wave<float, 32, NWT>
+           : a->head_dim == 64 ? decode_wave<float, 64, NWT>
+                               : decode_wave<float, 128, NWT>;
+  if (a->kv_dtype == SCHED_PD_BF16)
+    return a->head_dim == 64 ? decode_wave<uint16_t, 64, NWT> : decode_wave<uint16_t, 128, NWT>;
+  return a->head_dim == 64 ? decode_wave<_Float16, 64, NWT> : decode_wave<_Float16, 128, NWT>;
+}
+
 // Validate `a`; on success fill *kp (tables resolved) and *sel.
 int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   if (a == nullptr)
@@ -186,7 +226,10 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     return set_error(hipErrorInvalidValue, "bt_stride is 0 with a 2-D block table");
 
   const int64_t eb = elem_bytes(a->kv_dtype);
+  // MFMA first: at one q-head per kv-head it still streams bf16 faster than
+  // one wave per task (64 x 2048 x 8 heads: 80 vs 96 us)
   const bool mfma = mfma_applies(a);
+  const bool wave = !mfma && wave_applies(a);
   if (!mfma && !linear) {
     // VALU K rows are read with 16-byte vector loads.
     if (!aligned16(a->k_pool) || (a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 ||
@@ -268,7 +311,13 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   const float scale = a->sm_scale != 0.f ? a->sm_scale : 1.0f / std::sqrt((float)a->head_dim);
   kp->scale_log2 = scale * 1.4426950408889634f;
 
-  if (mfma) {
+  sel->per_block = 1;
+  if (wave) {
+    sel->fn = wave_kernel(a);
+    sel->block = SCHED_PD_WAVE_NWT * 64;
+    sel->mfma = 2;
+    sel->per_block = SCHED_PD_WAVE_NWT;
+  } else if (mfma) {
     const bool pg = a->page_size > 16;
     if (a->kv_dtype == SCHED_PD_F16)
       sel->fn = v_token_major(a) ? (pg ? mfma_kernel_f16<true, true>(G) : mfma_kernel_f16<true>(G))
@@ -315,7 +364,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   ring_depths(a, mfma, &ds, &du);
   if (a->pf_dist != 0 && !mfma)
     return set_error(hipErrorInvalidValue,
-                     "pf_dist %u: these arguments select the VALU kernel, which has no prefetch "
+                     "pf_dist %u: these arguments select a VALU kernel, which has no prefetch "
                      "ring (pass 0)", a->pf_dist);
   if (a->pf_dist != 0 && (a->pf_dist < ds || a->pf_dist > du))
     return set_error(hipErrorInvalidValue,
@@ -443,17 +492,17 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   const uint32_t nitems = kp.L.nitems;
   if (nitems == 0 || kp.ntasks == 0)
     return 0;
-  uint32_t grid = nitems;
   // A work-queue launch needs the queue and ctrl tables; without them the
-  // kernel's stock path serves one task per workgroup, so the grid must then
-  // cover every task. For the runtime's tables the pushed num_tasks is known
-  // here too (0 = the per-step disarm switch).
+  // kernel's stock path serves one task per workgroup (or wave), so the grid
+  // must then cover every task. For the runtime's tables the pushed num_tasks
+  // is known here too (0 = the per-step disarm switch).
   bool wq = a->workers > 0 && kp.L.queue != nullptr && kp.L.ctrl != nullptr;
   if (wq && (a->flags & SCHED_PD_FLAG_RT_TABLES) && rt_snapshot().num_tasks == 0)
     wq = false;
-  if (wq)
-    grid = a->workers;
+  const uint32_t slots = wq ? a->workers : nitems;
+  const uint32_t grid = (slots + sel.per_block - 1) / sel.per_block;
   kp.L.wq = wq ? 1u : 0u;
+  kp.L.workers = wq ? a->workers : 0u;
   hipLaunchKernelGGL(sel.fn, dim3(grid), dim3(sel.block), 0, (hipStream_t)stream, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -478,7 +527,7 @@ int sched_paged_decode_occupancy(const SchedDecodeArgs *a) {
   int blocks = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, sel.fn, sel.block, 0) != hipSuccess)
     return 0;
-  return blocks;
+  return blocks * sel.per_block;
 }
 
 int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
@@ -494,7 +543,7 @@ int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
   if (rc)
     return rc;
   uint32_t ds = 0, du = 0;
-  ring_depths(&b, sel.mfma != 0, &ds, &du);
+  ring_depths(&b, sel.mfma == 1, &ds, &du);
   if (stock)
     *stock = ds;
   if (deepest)

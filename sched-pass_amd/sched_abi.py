@@ -37,6 +37,7 @@ FLAG_WALLCLOCK = 0x2
 FLAG_FORCE_VALU = 0x4
 FLAG_CTX_IN_PAGES = 0x8
 FLAG_SHED_LOADS = 0x10
+FLAG_NO_WAVE = 0x20
 
 _u32, _f32, _i64, _p = ctypes.c_uint32, ctypes.c_float, ctypes.c_int64, ctypes.c_void_p
 

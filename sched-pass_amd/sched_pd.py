@@ -341,11 +341,12 @@ def paged_decode(q, k_pool, v_pool, block_table, ctx_lens, *, out=None,
 
 
 def kernel_kind(args: abi.SchedDecodeArgs) -> str:
-    """'mfma' or 'valu': which kernel the library picks for `args`."""
+    """'mfma', 'valu' (the general VALU kernel) or 'wave' (one wave per task,
+    G = 1): which kernel the library picks for `args`."""
     k = abi.load_library().sched_paged_decode_kernel_kind(ctypes.byref(args))
     if k < 0:
         raise RuntimeError(abi.last_error())
-    return "mfma" if k == 1 else "valu"
+    return {0: "valu", 1: "mfma", 2: "wave"}[k]
 
 
 def prefetch_range(args: abi.SchedDecodeArgs) -> tuple:

@@ -129,6 +129,23 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.BF16)) == 0
     assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32, **f16)) == 1   # fp16, 32-token pages
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.FP8_E4M3)) == -1
+    # one q-head per kv-head over token-major rows: one wave per task
+    mha = dict(num_q_heads=8, num_kv_heads=8, v_tok_stride=128, v_dim_stride=1)
+    assert kind(schedlib, fake_args(**mha)) == 1                             # bf16 d 128: MFMA
+    assert kind(schedlib, fake_args(**mha, head_dim=64)) == 2                # bf16 d 64
+    assert kind(schedlib, fake_args(**mha, q_dtype=abi.F32)) == 2            # fp32 Q
+    assert kind(schedlib, fake_args(**mha, page_size=48)) == 2               # page 48
+    assert kind(schedlib, fake_args(**mha, kv_dtype=abi.F32, q_dtype=abi.F32)) == 2
+    assert kind(schedlib, fake_args(**mha, head_dim=64, flags=abi.FLAG_NO_WAVE)) == 0
+    assert kind(schedlib, fake_args(**mha, kv_dtype=abi.F32, q_dtype=abi.F32,
+                                    flags=abi.FLAG_NO_WAVE)) == 0
+    assert kind(schedlib, fake_args(**mha, kv_dtype=abi.FP8_E4M3)) == 1      # no fp8 wave kernel
+    assert kind(schedlib, fake_args(num_q_heads=8, num_kv_heads=8)) == 1      # d-major V: MFMA
+    assert kind(schedlib, fake_args(**mha, mode=abi.LINEAR,
+                                    lin_w=ctypes.c_void_p(0x80000))) == 1     # linear: not wave
+    assert kind(schedlib, fake_args(**mha, tiles=ctypes.c_void_p(0x90000), num_tiles=8,
+                                    tile_pages=4, workspace=ctypes.c_void_p(0xA0000),
+                                    workspace_bytes=1 << 20)) == 1            # split: not wave
 
 
 def prefetch_range(lib, a):

@@ -1,0 +1,142 @@
+"""The one-wave-per-task kernel (G = 1, token-major rows) against the oracle,
+and its levers bitwise: pi, the ticket queue (W above and below the task
+count), the timer rows, both shed scopes with skip and load + mask, windows
+of 64 pages, page sizes that are not powers of two, the reference fixture's
+[token][K|V] pages, and the general VALU kernel on the same inputs."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sched_abi as abi
+import sched_pd
+import workloads
+from parity import TOL_BF16, TOL_F32, par_err
+from sched_rt import SchedPlane
+
+pytestmark = pytest.mark.gpu
+
+CTX = [1, 15, 16, 17, 33, 100, 511, 1025, 5000, 0]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib(schedlib):
+    torch.cuda.init()
+    return schedlib
+
+
+def batch(kv, d, ps, heads=4, ctx=CTX, seed=0, q_dtype=torch.float32):
+    # fp32 Q: the MFMA kernel (which takes 16-bit Q with d 128) does not apply
+    b = workloads.make_batch(np.asarray(ctx), num_q_heads=heads, num_kv_heads=heads,
+                             head_dim=d, page_size=ps, kv_dtype=kv, q_dtype=q_dtype, seed=seed,
+                             device="cuda")
+    b["v_pool"] = b["v_pool"].permute(0, 1, 3, 2).contiguous()   # token-major V
+    return b
+
+
+def run(b, plane=None, flags=0, **kw):
+    R, H, d = b["q"].shape
+    out = torch.full((R, H, d), float("nan"), device="cuda")
+    args = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                               out=out, v_layout="tokmajor", plane=plane, flags=flags, **kw)
+    sched_pd.launch(args)
+    torch.cuda.synchronize()
+    return out, sched_pd.kernel_kind(args)
+
+
+def ref(b, plane=None, **kw):
+    ctrl = bytes(plane._ctrl_host) if plane is not None else None
+    return oracle.decode(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                         v_layout="tokmajor", ctrl=ctrl,
+                         max_tasks=plane.N if plane is not None else 4096, **kw)
+
+
+def same(a, b):
+    return bool(torch.equal(torch.nan_to_num(a, nan=7.0), torch.nan_to_num(b, nan=7.0))) and \
+        bool(torch.equal(torch.isnan(a), torch.isnan(b)))
+
+
+@pytest.mark.parametrize("kv,d", [(torch.float32, 32), (torch.float32, 64), (torch.float32, 128),
+                                  (torch.bfloat16, 64), (torch.bfloat16, 128),
+                                  (torch.float16, 64), (torch.float16, 128)])
+@pytest.mark.parametrize("ps", [16, 32, 48])
+def test_wave_kernel_parity_and_levers(kv, d, ps):
+    b = batch(kv, d, ps, seed=d + ps)
+    tol = TOL_F32 if kv == torch.float32 else TOL_BF16
+    out, kind = run(b)
+    assert kind == "wave"
+    r = ref(b)
+    assert par_err(out.cpu(), r, f"wave {kv} d{d} p{ps}") <= tol
+    assert torch.isnan(out[-1]).all()          # an empty context gives the reference's 0/0
+    gen, _ = run(b, flags=abi.FLAG_NO_WAVE)
+    assert par_err(gen.cpu(), r) <= tol
+    n = len(CTX) * 4
+    plane = SchedPlane(max_tasks=n)
+    plane.set_order(torch.arange(n - 1, -1, -1, dtype=torch.int32))
+    plane.push()
+    plane.clear_timer()
+    o, _ = run(b, plane=plane)
+    assert same(o, out)
+    rows = plane.read_timer()[:n].numpy()
+    assert (rows > 0).all()
+    for W in (5, 2 * sched_pd.cu_count(), n + 3):
+        plane.set_num_tasks(n)
+        plane.push()
+        o, _ = run(b, plane=plane, workers=W)
+        assert same(o, out), W
+
+
+@pytest.mark.parametrize("scope", [abi.TAU_PREFIX, abi.TAU_PER_PAGE])
+@pytest.mark.parametrize("ps", [16, 32])
+def test_wave_kernel_shed(scope, ps):
+    b = batch(torch.float32, 64, ps, seed=3)
+    n = len(CTX) * 4
+    rng = np.random.default_rng(ps)
+    plane = SchedPlane(max_tasks=n)
+    ctx = np.repeat(np.asarray(CTX), 4)
+    tau = (rng.integers(1, np.maximum(ctx, 1) + 1) if scope == abi.TAU_PREFIX
+           else rng.integers(1, ps + 1, n))
+    tau[::5] = 0
+    plane.set_rows(tau=tau, n=n)
+    plane.push()
+    out, kind = run(b, plane=plane, tau_scope=scope)
+    assert kind == "wave"
+    assert par_err(out.cpu(), ref(b, plane, tau_scope=scope), f"shed {scope}") <= TOL_F32
+    o, _ = run(b, plane=plane, tau_scope=scope, flags=abi.FLAG_SHED_LOADS)
+    assert same(o, out)
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float16])
+def test_wave_kernel_16bit_q_at_d64(kv):
+    b = batch(kv, 64, 16, seed=11, q_dtype=kv)
+    out, kind = run(b)
+    assert kind == "wave"
+    assert par_err(out.cpu(), ref(b), f"wave {kv} q d64") <= TOL_BF16
+
+
+def test_wave_kernel_on_the_fixture_layout():
+    """The reference JIT kernel's layout: fp32 d 32, [token][K|V] pages of 32
+    tokens, one head, ctx counted in pages; pages packed per request."""
+    SD, PT = 32, 32
+    rng = np.random.default_rng(9)
+    nbl = rng.integers(1, 30, 300).astype(np.int32)
+    npages = int(nbl.sum())
+    bt = np.zeros((nbl.size, int(nbl.max())), np.int32)
+    at = 0
+    perm = rng.permutation(npages).astype(np.int32)
+    for r, k in enumerate(nbl):
+        bt[r, :k] = perm[at:at + k]
+        at += k
+    kv = torch.randn(npages, 1, PT, 2 * SD, device="cuda")
+    q = torch.randn(nbl.size, 1, SD, device="cuda")
+    out = torch.zeros(nbl.size, 1, SD, device="cuda")
+    bt_t, nbl_t = torch.from_numpy(bt).cuda(), torch.from_numpy(nbl).cuda()
+    args = sched_pd.build_args(q, kv[..., :SD], kv[..., SD:], bt_t, nbl_t, out=out,
+                               v_layout="tokmajor", sm_scale=0.125,
+                               tau_scope=abi.TAU_PER_PAGE, flags=abi.FLAG_CTX_IN_PAGES)
+    assert sched_pd.kernel_kind(args) == "wave"
+    sched_pd.launch(args)
+    torch.cuda.synchronize()
+    r = oracle.decode(q, kv[..., :SD], kv[..., SD:], bt_t, nbl_t, v_layout="tokmajor",
+                      sm_scale=0.125, tau_scope=abi.TAU_PER_PAGE, ctx_in_pages=True)
+    assert par_err(out.cpu(), r, "fixture layout") <= TOL_F32
