@@ -556,16 +556,17 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
         return {"us": round(ms * 1e3, 2), "gbs": round(kv_bytes / ms / 1e6, 1),
                 "kernel": sched_pd.kernel_kind(args[0])}
 
-    def serving_step(k_pool, v_pool, layout):
+    def serving_step(k_pool, v_pool, layout, k_scale=None, v_scale=None):
         # one decode step of a server: append each request's new token
         # (position 2047, the cache writer), then decode all 2048 tokens
         k1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
         v1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
         app = torch.arange(R + 1, dtype=torch.int32, device="cuda")
         ins = [kv_cache.build_append_args(k1, v1, app, ctx, k_pool, v_pool, bt, v_layout=layout,
-                                          max_append=1) for bt in bts]
-        dec = [sched_pd.build_args(q, k_pool, v_pool, bt, ctx, out=out, v_layout=layout)
+                                          k_scale=k_scale, v_scale=v_scale, max_append=1)
                for bt in bts]
+        dec = [sched_pd.build_args(q, k_pool, v_pool, bt, ctx, out=out, v_layout=layout,
+                                   k_scale=k_scale, v_scale=v_scale) for bt in bts]
         fa = lambda i: kv_cache.launch_append(ins[i % tables], stream)  # noqa: E731
         fd = lambda i: sched_pd.launch(dec[i % tables], stream)  # noqa: E731
 
@@ -622,6 +623,20 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
         grp[f"G{G}"] = row
     res["kernel_by_group"] = grp
     del kp, vp
+    torch.cuda.empty_cache()
+    # the same serving step over an fp8 cache (per-(page, head) scales)
+    f8 = torch.float8_e4m3fn
+    kp8 = torch.randn(npg, hkv, ps, d, device="cuda", generator=g).to(f8)
+    vp8 = torch.randn(npg, hkv, ps, d, device="cuda", generator=g).to(f8)
+    ks = torch.rand(npg * hkv, device="cuda", generator=g) * 0.09 + 0.01
+    vs = torch.rand(npg * hkv, device="cuda", generator=g) * 0.09 + 0.01
+    st8 = {"token_major_v": serving_step(kp8, vp8, "tokmajor", ks, vs),
+           "d_major_v": serving_step(kp8, vp8.view(npg, hkv, d, ps), "dmajor", ks, vs)}
+    st8["faster"] = min(("token_major_v", "d_major_v"), key=lambda k: st8[k]["step_us"])
+    st8["paged_kv_cache_default"] = kv_cache.PagedKvCache(1, hkv, d, 16, dtype=f8,
+                                                          device="cuda").v_layout
+    res["serving_step_page16_fp8"] = st8
+    del kp8, vp8, ks, vs
     torch.cuda.empty_cache()
     nhd = (torch.randn(npg, 2, ps, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
     kview, vview = kv_cache.nhd_views(nhd)

@@ -122,9 +122,27 @@ void sched_rt_timer_clear(void);
  * __sched_* slots hold right now (0 when disarmed), read back from the device
  * symbols. slots[0..3] = order, ctrl, timer, queue. Returns false on error. */
 bool sched_rt_slots(uint64_t slots[4]);
+/* Device addresses of the __sched_* slots themselves (addrs[0..3] = order,
+ * ctrl, timer, queue), no counterpart in the reference: its slots are symbols
+ * of the including translation unit, written with cudaMemcpyToSymbol; here
+ * they live in the library's code object, so a caller that writes a slot
+ * directly copies the 8-byte table pointer to this address (hipMemcpy). The
+ * kernels read the slots at every launch with SCHED_PD_FLAG_RT_TABLES.
+ * Returns false on error. */
+bool sched_rt_slot_addresses(uint64_t addrs[4]);
 /* Bulk timer read, no counterpart in the reference (its rows are host-mapped
  * and read in place): copies rows [0, n) (n clamped) into dst. */
 bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
+/* The reference's host-mapped timer readout (runtime/sched_rt.h:150-156,
+ * :178-181), opt-in: on = keep a pinned host copy of the timer rows, refreshed
+ * by an async device-to-host copy on the launch's stream after every
+ * sched_paged_decode launch with SCHED_PD_FLAG_RT_TABLES, and publish its
+ * address as timer_host_va in /tmp/sched_rt_<pid>.json, so a separate process
+ * can read the rows with no GPU call (they trail the device rows by the copy).
+ * The kernels add into device memory either way. Off by default. */
+bool sched_rt_set_timer_host_mirror(bool on);
+/* Address of the host copy of the timer rows (0 while the mirror is off). */
+uint64_t sched_rt_timer_host_va(void);
 
 /* ---- 2. decode launcher --------------------------------------------------- */
 
@@ -147,7 +165,11 @@ bool sched_rt_timer_read(unsigned long long *dst, unsigned n);
 #define SCHED_PD_TAU_PER_PAGE 1u
 
 /* flags */
-#define SCHED_PD_FLAG_RT_TABLES 0x1u    /* take order/ctrl/timer/queue from the C runtime's slots */
+#define SCHED_PD_FLAG_RT_TABLES 0x1u    /* take order/ctrl/timer/queue from the C runtime's
+                                           __sched_* slots: the kernel reads the pointers the
+                                           device slots hold when it starts; whether a queue
+                                           grid of `workers` is launched follows what
+                                           sched_rt_* last armed and pushed */
 #define SCHED_PD_FLAG_WALLCLOCK 0x2u    /* timer counts s_memrealtime (100 MHz) instead of s_memtime */
 #define SCHED_PD_FLAG_FORCE_VALU 0x4u   /* use the general VALU kernel (one workgroup per
                                            work item) even where another kernel applies */

@@ -140,8 +140,8 @@ __device__ __forceinline__ void item_task(const KParams &P, uint32_t wi, uint32_
     task = wi;
     chunk = 0u;
   } else {
-    task = (uint32_t)P.tiles[2 * wi];
-    chunk = (uint32_t)P.tiles[2 * wi + 1];
+    task = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi]);
+    chunk = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi + 1]);
   }
 }
 
@@ -194,7 +194,8 @@ __device__ __forceinline__ bool item_stale(const KParams &P, uint32_t wi, uint32
   const uint32_t last = wi - chunk + R.nchunks - 1u;
   if (last >= P.L.nitems)
     return true;
-  const int32_t lt = P.tiles[2 * last], lc = P.tiles[2 * last + 1];
+  const int32_t lt = __builtin_amdgcn_readfirstlane(P.tiles[2 * last]);
+  const int32_t lc = __builtin_amdgcn_readfirstlane(P.tiles[2 * last + 1]);
   return !((uint32_t)lt == task && (uint32_t)lc == R.nchunks - 1u);
 }
 

@@ -48,7 +48,8 @@ __device__ __forceinline__ int32_t page_of(const KParams &P, uint32_t r, uint32_
 }
 
 __device__ __forceinline__ uint32_t ctx_tokens(const KParams &P, uint32_t r) {
-  uint32_t c = (uint32_t)P.ctx[r];
+  // one request's length: the same on every lane, kept in a scalar register
+  uint32_t c = __builtin_amdgcn_readfirstlane((uint32_t)P.ctx[r]);
   return P.ctx_in_pages ? c * P.ps : c;
 }
 

@@ -624,7 +624,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     MfmaTask T;
     T.r = task / P.Hkv;
     T.h = task % P.Hkv;
-    T.row = P.indptr ? (int64_t)P.indptr[T.r] : (int64_t)T.r * P.bt_stride;
+    T.row = P.indptr ? (int64_t)__builtin_amdgcn_readfirstlane(P.indptr[T.r])
+                     : (int64_t)T.r * P.bt_stride;
     const TaskPolicy pol = task_policy(P.L, task);
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;

@@ -158,13 +158,14 @@ __device__ __forceinline__ void run_wave_tasks(const LeverTables &L, Body &&body
   const uint32_t pid = blockIdx.x * NWT + w;
   uint32_t ntasks = 0u;
   if (L.wq) {
-    const bool armed = L.queue != nullptr && L.ctrl != nullptr && gridDim.y == 1 &&
+    const bool armed = lt_queue(L) != nullptr && lt_ctrl(L) != nullptr && gridDim.y == 1 &&
                        gridDim.z == 1;
-    ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
+    ntasks = armed ? ld_u32(lt_ctrl(L) + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
   }
   if (ntasks == 0u) {
-    if (pid < L.nitems)
-      body(remap_static(L, pid, L.nitems));
+    // static grid (or a queue grid disarmed on the device): every item once
+    for (uint32_t v = pid; v < L.nitems; v += gridDim.x * NWT)
+      body(remap_static(L, v, L.nitems));
     return;
   }
   const uint32_t W = L.workers;
@@ -177,9 +178,9 @@ __device__ __forceinline__ void run_wave_tasks(const LeverTables &L, Body &&body
     body(remap_wq(L, raw, ntasks));
     uint32_t t = 0u;
     if (lane == 0u) {
-      t = __hip_atomic_fetch_add(L.queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t = __hip_atomic_fetch_add(lt_queue(L), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (t == last_ticket)
-        __hip_atomic_store(L.queue, W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(lt_queue(L), W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     raw = __builtin_amdgcn_readfirstlane(t);
     if (raw >= ntasks)
@@ -205,7 +206,8 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
     const uint32_t n = ctx_tokens(P, r);
     const uint32_t nload = load_extent(P, n, pol.budget);
     const uint32_t nchunks = (nload + 15u) / 16u;
-    const int64_t row = P.indptr ? (int64_t)P.indptr[r] : (int64_t)r * P.bt_stride;
+    const int64_t row = P.indptr ? (int64_t)__builtin_amdgcn_readfirstlane(P.indptr[r])
+                                 : (int64_t)r * P.bt_stride;
 
     // the lane's VN dims of q, pre-scaled into the exp2 domain
     float q[VN];
@@ -352,9 +354,10 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
       for (int e = 0; e < VN; ++e)
         store_out(P, o + e, st.acc[e] / st.l);
     }
-    if (lane == 0u && P.L.timer != nullptr && task < P.L.max_tasks && !toff) {
+    unsigned long long *timer = lt_timer(P.L);
+    if (lane == 0u && timer != nullptr && task < P.L.max_tasks && !toff) {
       const unsigned long long dt = read_clock(P.L.wallclock) - t0;
-      __hip_atomic_fetch_add(P.L.timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   });
 }

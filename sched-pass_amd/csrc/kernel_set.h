@@ -41,18 +41,23 @@
 #ifndef SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT
 #define SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT 5
 #endif
+// fp16 d-major V on 16-token pages: depth 4 needs 258 VGPRs; 3 fits.
+#ifndef SCHED_PD_MFMA_DEPTH_F16_URGENT
+#define SCHED_PD_MFMA_DEPTH_F16_URGENT 3
+#endif
 
 namespace schedpd {
 
 constexpr int mfma_ds(bool fp8) { return fp8 ? SCHED_PD_MFMA_DEPTH_FP8 : SCHED_PD_MFMA_DEPTH; }
 // Deepest ring (the urgent default). An urgent task's ring depth is any of
 // mfma_ds .. mfma_du (SchedDecodeArgs.pf_dist).
-constexpr int mfma_du(bool fp8, bool vt, bool pg) {
+constexpr int mfma_du(bool fp8, bool vt, bool pg, bool f16 = false) {
   return fp8 ? (vt ? SCHED_PD_MFMA_DEPTH_FP8_VT_URGENT
                 : pg ? SCHED_PD_MFMA_DEPTH_FP8_PG_URGENT
                      : SCHED_PD_MFMA_DEPTH_FP8_URGENT)
          : vt ? SCHED_PD_MFMA_DEPTH_VT_URGENT
-              : SCHED_PD_MFMA_DEPTH_URGENT;
+         : (f16 && !pg) ? SCHED_PD_MFMA_DEPTH_F16_URGENT
+                        : SCHED_PD_MFMA_DEPTH_URGENT;
 }
 
 } // namespace schedpd
@@ -62,7 +67,7 @@ constexpr int mfma_du(bool fp8, bool vt, bool pg) {
 #define SCHED_PD_MFMA_ONE(PRE, FP8, GMAX, LIN, VT, PG, F16)                                      \
   PRE template __global__ void schedpd::decode_mfma<FP8, SCHED_PD_MFMA_NW, GMAX,                 \
                                                     schedpd::mfma_ds(FP8),                       \
-                                                    schedpd::mfma_du(FP8, VT, PG), LIN, VT, PG, F16>( \
+                                                    schedpd::mfma_du(FP8, VT, PG, F16), LIN, VT, PG, F16>( \
       schedpd::KParams);
 #define SCHED_PD_MFMA_SOFTMAX(PRE, FP8, VT, PG, F16)                                             \
   SCHED_PD_MFMA_ONE(PRE, FP8, 4, false, VT, PG, F16)                                             \

@@ -25,6 +25,12 @@ struct LeverTables {
   uint32_t workers;          // W of a work-queue launch (per-wave kernels)
   uint32_t wallclock;        // timer source: 1 = s_memrealtime, 0 = s_memtime
   float dT, dR, H;           // policy marginal-exchange constants
+  // Runtime mode (SCHED_PD_FLAG_RT_TABLES): the device addresses of the four
+  // __sched_* slots; the kernel reads the table pointers they hold (lt_order,
+  // lt_ctrl, lt_timer, lt_queue), so a slot written directly on the device
+  // takes effect at the next launch.
+  uint64_t rt_slot[4];
+  uint32_t rt;
 };
 
 struct TaskPolicy {
@@ -33,11 +39,42 @@ struct TaskPolicy {
   uint32_t budget; // tokens; 0xFFFFFFFF = no cap
 };
 
+// The table pointers a kernel uses: the launch's own, or (runtime mode) the
+// ones the __sched_* slots hold, read with a scalar load at each use (no
+// kernel writes the slots, so every read of a launch sees the same pointer,
+// and the loads hit the scalar cache).
+typedef const __attribute__((address_space(4))) uint64_t slot_u64;
+// A 64-bit value every lane holds alike, kept wave-uniform for the compiler
+// (so what is derived from it stays in scalar registers).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t slot_or(const LeverTables &L, int k, const void *own) {
+  return L.rt ? uniform_u64(*(slot_u64 *)L.rt_slot[k]) : (uint64_t)(uintptr_t)own;
+}
+__device__ __forceinline__ const int32_t *lt_order(const LeverTables &L) {
+  return reinterpret_cast<const int32_t *>(slot_or(L, 0, L.order));
+}
+__device__ __forceinline__ const uint8_t *lt_ctrl(const LeverTables &L) {
+  return reinterpret_cast<const uint8_t *>(slot_or(L, 1, L.ctrl));
+}
+__device__ __forceinline__ unsigned long long *lt_timer(const LeverTables &L) {
+  return reinterpret_cast<unsigned long long *>(slot_or(L, 2, L.timer));
+}
+__device__ __forceinline__ uint32_t *lt_queue(const LeverTables &L) {
+  return reinterpret_cast<uint32_t *>(slot_or(L, 3, L.queue));
+}
+
+// Fields of the control block and entries of pi: the same for every lane of a
+// workgroup (task-uniform), kept in scalar registers (the tables may come from
+// loaded slot pointers, where the compiler could not otherwise tell).
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
-  return *reinterpret_cast<const uint32_t *>(p);
+  return __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(p));
 }
 __device__ __forceinline__ float ld_f32(const uint8_t *p) {
-  return *reinterpret_cast<const float *>(p);
+  return __uint_as_float(ld_u32(p));
 }
 
 __device__ __forceinline__ unsigned long long read_clock(uint32_t wallclock) {
@@ -49,12 +86,13 @@ __device__ __forceinline__ unsigned long long read_clock(uint32_t wallclock) {
 //   ctrl.order_size in {0, nctaid} (ctrl unarmed = unchecked); else pid.
 __device__ __forceinline__ uint32_t remap_static(const LeverTables &L, uint32_t pid,
                                                  uint32_t nctaid) {
-  if (L.order == nullptr || pid >= L.max_tasks)
+  const int32_t *order = lt_order(L);
+  if (order == nullptr || pid >= L.max_tasks)
     return pid;
-  uint32_t mapped = (uint32_t)L.order[pid];
+  uint32_t mapped = __builtin_amdgcn_readfirstlane((uint32_t)order[pid]);
   bool size_ok = true;
-  if (L.ctrl) {
-    uint32_t osz = ld_u32(L.ctrl + SCHED_CTRL_ORDER_SIZE_OFF);
+  if (const uint8_t *ctrl = lt_ctrl(L)) {
+    uint32_t osz = ld_u32(ctrl + SCHED_CTRL_ORDER_SIZE_OFF);
     size_ok = (osz == 0u) || (osz == nctaid);
   }
   return (mapped < nctaid && size_ok) ? mapped : pid;
@@ -65,10 +103,11 @@ __device__ __forceinline__ uint32_t remap_static(const LeverTables &L, uint32_t 
 // {0, num_tasks}. ctrl is armed on this path (the driver checked it).
 __device__ __forceinline__ uint32_t remap_wq(const LeverTables &L, uint32_t raw,
                                              uint32_t num_tasks) {
-  if (L.order == nullptr || raw >= L.max_tasks)
+  const int32_t *order = lt_order(L);
+  if (order == nullptr || raw >= L.max_tasks)
     return raw;
-  uint32_t mapped = (uint32_t)L.order[raw];
-  uint32_t osz = ld_u32(L.ctrl + SCHED_CTRL_ORDER_SIZE_OFF);
+  uint32_t mapped = __builtin_amdgcn_readfirstlane((uint32_t)order[raw]);
+  uint32_t osz = ld_u32(lt_ctrl(L) + SCHED_CTRL_ORDER_SIZE_OFF);
   bool ok = mapped < num_tasks && (osz == 0u || osz == num_tasks);
   return ok ? mapped : raw;
 }
@@ -78,10 +117,11 @@ __device__ __forceinline__ uint32_t remap_wq(const LeverTables &L, uint32_t raw,
 // from scalar loads.
 __device__ __forceinline__ TaskPolicy task_policy(const LeverTables &L, uint32_t task) {
   TaskPolicy P{false, false, 0xFFFFFFFFu};
-  if (L.ctrl == nullptr || task >= L.max_tasks)
+  const uint8_t *ctrl = lt_ctrl(L);
+  if (ctrl == nullptr || task >= L.max_tasks)
     return P;
-  const uint8_t *row = L.ctrl + SCHED_CTRL_ROWS_OFF + (size_t)task * SCHED_CTRL_ROW_SIZE;
-  float lam = ld_f32(L.ctrl + SCHED_CTRL_LAMBDA_OFF);
+  const uint8_t *row = ctrl + SCHED_CTRL_ROWS_OFF + (size_t)task * SCHED_CTRL_ROW_SIZE;
+  float lam = ld_f32(ctrl + SCHED_CTRL_LAMBDA_OFF);
   float q = ld_f32(row);
   uint32_t w1 = ld_u32(row + 4); // tau (u16) | hint (u8) << 16
   uint32_t tau = w1 & 0xFFFFu;
@@ -96,7 +136,8 @@ __device__ __forceinline__ TaskPolicy task_policy(const LeverTables &L, uint32_t
 // Timer-off gate latched at kernel entry (reference lib/SchedWeave.cpp:
 // 346-356, 979-1002): ctrl unarmed -> timer on.
 __device__ __forceinline__ bool timer_off_latched(const LeverTables &L) {
-  return L.ctrl != nullptr && (ld_u32(L.ctrl + SCHED_CTRL_FLAGS_OFF) & SCHED_CTRL_FLAG_TIMER_OFF);
+  const uint8_t *ctrl = lt_ctrl(L);
+  return ctrl != nullptr && (ld_u32(ctrl + SCHED_CTRL_FLAGS_OFF) & SCHED_CTRL_FLAG_TIMER_OFF);
 }
 
 // Epilogue of one task body (reference lib/SchedWeave.cpp:1004-1049): lane 0
@@ -104,9 +145,10 @@ __device__ __forceinline__ bool timer_off_latched(const LeverTables &L) {
 // scope; rows accumulate until cleared.
 __device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uint32_t task,
                                              unsigned long long t0) {
-  if (threadIdx.x == 0 && L.timer != nullptr && task < L.max_tasks && !off) {
+  unsigned long long *timer = lt_timer(L);
+  if (threadIdx.x == 0 && timer != nullptr && task < L.max_tasks && !off) {
     unsigned long long dt = read_clock(L.wallclock) - t0;
-    __hip_atomic_fetch_add(L.timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(timer + task, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -114,7 +156,9 @@ __device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uin
 // lib/SchedWorkQueue.cpp:345-448). `body(task)` runs one task with the whole
 // workgroup and must end with every thread past its last LDS use.
 //
-// Static launch (wq == 0): one task per workgroup, task = remap_static(ctaid).
+// Static launch (wq == 0): one task per workgroup, task = remap_static(ctaid)
+// with the launch's item count as the grid bound (the host launches one
+// workgroup per item).
 // Work-queue launch (wq == 1, grid = W workers):
 //   stock path if queue or ctrl is NULL, the grid is not 1-D, or num_tasks==0;
 //   otherwise raw = ctaid (exit if >= num_tasks), then loop: body(remap(raw)),
@@ -132,31 +176,44 @@ __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
   uint32_t ntasks = 0u;
   if (L.wq) {
     const bool grid1d = gridDim.y == 1 && gridDim.z == 1;
-    const bool armed = L.queue != nullptr && L.ctrl != nullptr && grid1d;
-    ntasks = armed ? ld_u32(L.ctrl + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
+    const bool armed = lt_queue(L) != nullptr && lt_ctrl(L) != nullptr && grid1d;
+    ntasks = armed ? ld_u32(lt_ctrl(L) + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
   }
   const bool queue = ntasks != 0u;
   if (queue && pid >= ntasks)
     return;
   __shared__ uint32_t s_next;
   const uint32_t last_ticket = gridDim.x + ntasks - 1u;
+  // Static grid (or the stock path of a queue launch): items pid, pid + grid,
+  // ... -- one per workgroup when the grid covers the items, as it does for
+  // a static launch; a queue grid whose tables were disarmed on the device
+  // still covers every item.
   uint32_t raw = pid;
   // One call site of the body (it is large: inlining it once keeps the
   // kernel's code and register allocation that of a single task body).
   while (true) {
-    body(queue ? remap_wq(L, raw, ntasks) : remap_static(L, pid, gridDim.x));
-    if (!queue)
+    if (!queue && raw >= L.nitems)
       return;
+    // the item is the same on every lane: keep it (and the addresses derived
+    // from it) in scalar registers
+    body(__builtin_amdgcn_readfirstlane(queue ? remap_wq(L, raw, ntasks)
+                                              : remap_static(L, raw, L.nitems)));
+    if (!queue) {
+      raw += gridDim.x;
+      if (raw < L.nitems)
+        __syncthreads();
+      continue;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-      uint32_t t = __hip_atomic_fetch_add(L.queue, 1u, __ATOMIC_RELAXED,
+      uint32_t t = __hip_atomic_fetch_add(lt_queue(L), 1u, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
       if (t == last_ticket)
-        __hip_atomic_store(L.queue, gridDim.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(lt_queue(L), gridDim.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_next = t;
     }
     __syncthreads();
-    raw = s_next;
+    raw = __builtin_amdgcn_readfirstlane(s_next);
     if (raw >= ntasks)
       return;
   }

@@ -56,7 +56,7 @@ uint32_t elem_bytes(uint32_t dt) {
 
 // fp16 cache with fp16 Q: 16-byte page-16 layouts, softmax mode.
 template <bool VT, bool PG = false> KernelFn mfma_kernel_f16(uint32_t G) {
-  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT, PG);
+  constexpr int NW = SCHED_PD_MFMA_NW, DS = mfma_ds(false), DU = mfma_du(false, VT, PG, true);
   if (G <= 4)
     return decode_mfma<false, NW, 4, DS, DU, false, VT, PG, true>;
   if (G <= 8)
@@ -141,7 +141,8 @@ void ring_depths(const SchedDecodeArgs *a, bool mfma, uint32_t *ds, uint32_t *du
   }
   const bool fp8 = a->kv_dtype == SCHED_PD_FP8_E4M3;
   *ds = (uint32_t)mfma_ds(fp8);
-  *du = (uint32_t)mfma_du(fp8, v_token_major(a), a->page_size > 16);
+  *du = (uint32_t)mfma_du(fp8, v_token_major(a), a->page_size > 16,
+                          a->kv_dtype == SCHED_PD_F16);
 }
 
 // The one-wave-per-task kernel's shape: softmax, one q-head per kv-head, no
@@ -241,12 +242,17 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   std::memset(kp, 0, sizeof *kp);
   const bool rt = (a->flags & SCHED_PD_FLAG_RT_TABLES) != 0;
   if (rt) {
+    // the kernel reads the tables from the device slots; the host snapshot
+    // (what sched_rt_* armed) only decides whether a queue grid is launched
     const RtSnapshot s = rt_snapshot();
     kp->L.order = s.order;
     kp->L.ctrl = static_cast<const uint8_t *>(s.ctrl);
     kp->L.timer = s.timer;
     kp->L.queue = s.queue;
     kp->L.max_tasks = SCHED_MAX_TASKS;
+    if (!rt_slot_addresses(kp->L.rt_slot))
+      return hipErrorInvalidSymbol;
+    kp->L.rt = 1u;
   } else {
     kp->L.order = a->order;
     kp->L.ctrl = static_cast<const uint8_t *>(a->ctrl);
@@ -507,6 +513,8 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(e, "kernel launch failed: %s", hipGetErrorString(e));
+  if (a->flags & SCHED_PD_FLAG_RT_TABLES)
+    return rt_after_launch(stream);
   return 0;
 }
 

@@ -18,6 +18,14 @@ struct RtSnapshot {
 
 RtSnapshot rt_snapshot();
 
+// Device addresses of the four __sched_* slots (order, ctrl, timer, queue) on
+// the current device; false (with the error recorded) if they cannot be had.
+bool rt_slot_addresses(uint64_t out[4]);
+
+// The runtime's host mirror of the timer rows, if enabled: enqueue its refresh
+// on `stream` after a launch that used the runtime's tables.
+int rt_after_launch(void *stream);
+
 // Record and print an error ("[sched_pd] ..."); returns `code`.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 void set_error_text(const char *text);

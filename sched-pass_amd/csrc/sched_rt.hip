@@ -8,7 +8,12 @@
 //     -0.5% for a device buffer, ROADMAP.md:1482-1488), so sched_rt_timer()
 //     is a small device-to-host copy instead of a plain host read;
 //   * the functions are exported, not `static inline` in a header, so the
-//     state is one per process (the library), not one per translation unit.
+//     state is one per process (the library), not one per translation unit;
+//   * an external reader that wants the rows with no GPU call turns on the
+//     host mirror: a pinned copy refreshed by an async copy after each launch
+//     that uses these tables, published as timer_host_va;
+//   * the kernels read the table pointers from the __sched_* slots at every
+//     launch, so slots written directly on the device take effect.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -38,10 +43,35 @@ struct RtState {
   uint32_t *d_queue = nullptr;
   SchedCtrl h_ctrl;
   bool armed = false;
+  // opt-in pinned host copy of the timer rows for external readers
+  unsigned long long *h_timer = nullptr;
+  bool mirror = false;
 };
 
 RtState g_rt;
 thread_local std::string g_err;
+
+// /tmp/sched_rt_<pid>.json (reference runtime/sched_rt.h:170-186): the table
+// addresses, plus timer_host_va, the host copy of the timer rows an external
+// reader can consume with no GPU call (0 unless the mirror is on).
+void publish() {
+  const RtState &S = g_rt;
+  char path[256];
+  std::snprintf(path, sizeof path, "/tmp/sched_rt_%d.json", (int)getpid());
+  if (FILE *f = std::fopen(path, "w")) {
+    std::fprintf(f,
+                 "{\"pid\":%d,\"max_tasks\":%d,\"order_dev\":%llu,\"ctrl_dev\":%llu,"
+                 "\"timer_dev\":%llu,\"timer_host_va\":%llu,\"timer_bytes\":%zu,"
+                 "\"queue_dev\":%llu}\n",
+                 (int)getpid(), SCHED_MAX_TASKS,
+                 (unsigned long long)(uintptr_t)S.d_order, (unsigned long long)(uintptr_t)S.d_ctrl,
+                 (unsigned long long)(uintptr_t)S.d_timer,
+                 (unsigned long long)(uintptr_t)(S.mirror ? S.h_timer : nullptr),
+                 (size_t)SCHED_MAX_TASKS * sizeof(unsigned long long),
+                 (unsigned long long)(uintptr_t)S.d_queue);
+    std::fclose(f);
+  }
+}
 
 bool rt_check(hipError_t e, const char *what) {
   if (e == hipSuccess)
@@ -84,6 +114,48 @@ int set_error(int code, const char *fmt, ...) {
   va_end(ap);
   set_error_text(buf);
   return code;
+}
+
+bool rt_slot_addresses(uint64_t out[4]) {
+  constexpr int kMaxDev = 64;
+  static uint64_t cache[kMaxDev][4];
+  static bool have[kMaxDev];
+  int dev = 0;
+  if (!rt_check(hipGetDevice(&dev), "hipGetDevice"))
+    return false;
+  if (dev < 0 || dev >= kMaxDev) {
+    set_error_text("[sched_rt] device index beyond the runtime's table");
+    return false;
+  }
+  if (!have[dev]) {
+    void *p[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (!rt_check(hipGetSymbolAddress(&p[0], HIP_SYMBOL(__sched_task_order)),
+                  "hipGetSymbolAddress(__sched_task_order)") ||
+        !rt_check(hipGetSymbolAddress(&p[1], HIP_SYMBOL(__sched_ctrl)),
+                  "hipGetSymbolAddress(__sched_ctrl)") ||
+        !rt_check(hipGetSymbolAddress(&p[2], HIP_SYMBOL(__sched_timer)),
+                  "hipGetSymbolAddress(__sched_timer)") ||
+        !rt_check(hipGetSymbolAddress(&p[3], HIP_SYMBOL(__sched_queue)),
+                  "hipGetSymbolAddress(__sched_queue)"))
+      return false;
+    for (int i = 0; i < 4; ++i)
+      cache[dev][i] = (uint64_t)(uintptr_t)p[i];
+    have[dev] = true;
+  }
+  for (int i = 0; i < 4; ++i)
+    out[i] = cache[dev][i];
+  return true;
+}
+
+int rt_after_launch(void *stream) {
+  if (!g_rt.mirror || g_rt.h_timer == nullptr || !g_rt.armed)
+    return 0;
+  hipError_t e = hipMemcpyAsync(g_rt.h_timer, g_rt.d_timer,
+                                SCHED_MAX_TASKS * sizeof(unsigned long long),
+                                hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return set_error(e, "timer mirror copy failed: %s", hipGetErrorString(e));
+  return 0;
 }
 
 RtSnapshot rt_snapshot() {
@@ -130,20 +202,7 @@ bool sched_rt_init(void) {
   }
   if (!write_slots(S.d_order, S.d_ctrl, S.d_timer, S.d_queue))
     return false;
-
-  char path[256];
-  std::snprintf(path, sizeof path, "/tmp/sched_rt_%d.json", (int)getpid());
-  if (FILE *f = std::fopen(path, "w")) {
-    std::fprintf(f,
-                 "{\"pid\":%d,\"max_tasks\":%d,\"order_dev\":%llu,\"ctrl_dev\":%llu,"
-                 "\"timer_dev\":%llu,\"timer_bytes\":%zu,\"queue_dev\":%llu}\n",
-                 (int)getpid(), SCHED_MAX_TASKS,
-                 (unsigned long long)(uintptr_t)S.d_order, (unsigned long long)(uintptr_t)S.d_ctrl,
-                 (unsigned long long)(uintptr_t)S.d_timer,
-                 (size_t)SCHED_MAX_TASKS * sizeof(unsigned long long),
-                 (unsigned long long)(uintptr_t)S.d_queue);
-    std::fclose(f);
-  }
+  publish();
   S.armed = true;
   return true;
 }
@@ -231,6 +290,35 @@ void sched_rt_timer_clear(void) {
   if (g_rt.d_timer)
     rt_check(hipMemset(g_rt.d_timer, 0, SCHED_MAX_TASKS * sizeof(unsigned long long)),
              "hipMemset(timer)");
+  if (g_rt.h_timer)
+    std::memset(g_rt.h_timer, 0, SCHED_MAX_TASKS * sizeof(unsigned long long));
+}
+
+bool sched_rt_set_timer_host_mirror(bool on) {
+  RtState &S = g_rt;
+  if (on && S.h_timer == nullptr) {
+    void *p = nullptr;
+    RT_CHECK(hipHostMalloc(&p, SCHED_MAX_TASKS * sizeof(unsigned long long),
+                           hipHostMallocDefault));
+    S.h_timer = static_cast<unsigned long long *>(p);
+    std::memset(S.h_timer, 0, SCHED_MAX_TASKS * sizeof(unsigned long long));
+  }
+  S.mirror = on;
+  if (S.armed)
+    publish();
+  return true;
+}
+
+bool sched_rt_slot_addresses(uint64_t addrs[4]) {
+  if (addrs == nullptr) {
+    schedpd::set_error_text("[sched_rt] sched_rt_slot_addresses failed: addrs is NULL");
+    return false;
+  }
+  return schedpd::rt_slot_addresses(addrs);
+}
+
+uint64_t sched_rt_timer_host_va(void) {
+  return g_rt.mirror ? (uint64_t)(uintptr_t)g_rt.h_timer : 0u;
 }
 
 bool sched_rt_timer_read(unsigned long long *dst, unsigned n) {

@@ -201,12 +201,19 @@ class PagedKvCache:
     [P, Hkv, page, d] (token-major); for an fp8 cache k_scale / v_scale
     [P * Hkv] (index page * Hkv + head).
 
-    v_layout "auto" picks d-major for 16-token pages and token-major for
-    larger ones (bf16, fp16 and fp8 caches): there a 16-token block of a
-    d-major V row is a partial row, and the decode measured 98 / 109 / 109 us
-    for 32- / 64- / 128-token bf16 pages against 87 / 86 / 86 us token-major,
-    fp8 54 / 62 us against 48 / 48 (Llama-3-8B decode batch, 64 x 2048
-    tokens; the same either way at 16)."""
+    v_layout "auto" is token-major V for every page size and dtype, chosen by
+    what a serving step costs (the writer appends each request's token, then
+    the decode reads the batch; Llama-3-8B batch, 64 x 2048 tokens):
+    - 16-token pages: bf16 87.8 us token-major against 90.7 us d-major (the
+      decode alone is ~1% faster d-major, but a d-major append writes one
+      token as a 128-row column, 7.7x its bytes); fp8 55.5 against 55.9 us;
+    - larger pages: a 16-token block of a d-major V row is a partial row, and
+      the decode alone measured 98 / 109 / 109 us for 32- / 64- / 128-token
+      bf16 pages against 87 / 86 / 86 us token-major, fp8 54 / 62 us against
+      48 / 48;
+    - fp32 caches (the VALU kernels) read token-major rows with coalesced
+      loads.
+    "dmajor" stays available."""
 
     def __init__(self, num_pages: int, num_kv_heads: int, head_dim: int, page_size: int = 16,
                  dtype=torch.bfloat16, device="cuda", v_layout: str = "auto"):
@@ -214,9 +221,7 @@ class PagedKvCache:
         self.dtype = dtype
         self.device = torch.device(device)
         if v_layout == "auto":
-            v_layout = "tokmajor" if page_size > 16 and dtype in (
-                torch.bfloat16, torch.float16, getattr(torch, "float8_e4m3fn", None)) \
-                else "dmajor"
+            v_layout = "tokmajor"
         if v_layout not in ("dmajor", "tokmajor"):
             raise ValueError(f"v_layout {v_layout!r}")
         self.v_layout = v_layout

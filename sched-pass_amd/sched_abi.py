@@ -130,6 +130,9 @@ SIGNATURES = {
     "sched_rt_timer_clear": (None, []),
     "sched_rt_slots": (_c_bool, [ctypes.POINTER(ctypes.c_uint64)]),
     "sched_rt_timer_read": (_c_bool, [ctypes.POINTER(ctypes.c_ulonglong), ctypes.c_uint]),
+    "sched_rt_set_timer_host_mirror": (_c_bool, [_c_bool]),
+    "sched_rt_slot_addresses": (_c_bool, [ctypes.POINTER(ctypes.c_uint64)]),
+    "sched_rt_timer_host_va": (ctypes.c_uint64, []),
     "sched_pd_default_args": (None, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),
     "sched_paged_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),

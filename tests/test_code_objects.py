@@ -40,3 +40,19 @@ def test_every_kernel_runs_without_scratch_or_spills(tmp_path):
     # lanes (v_writelane), not in memory, and are not checked
     counts = [int(x) for x in re.findall(r"\.vgpr_spill_count:\s+(\d+)", out)]
     assert counts and all(x == 0 for x in counts), counts
+
+
+def test_mfma_decode_kernels_keep_two_waves_per_simd(tmp_path):
+    """Occupancy guard: the MFMA decode kernels are built for two waves per
+    SIMD (a 512-entry register file per lane: VGPRs + AGPRs <= 256). A kernel
+    above that runs one wave per SIMD and streams at about half the rate (an
+    fp8 decode measured 3.2 instead of 6.1 TB/s), with no error anywhere."""
+    out = notes(tmp_path)
+    over = []
+    for blk in out.split(".agpr_count:")[1:]:
+        agpr = int(blk.split()[0])
+        name = re.search(r"\.name:\s+(\S+)", blk).group(1)
+        vgpr = int(re.search(r"\.vgpr_count:\s+(\d+)", blk).group(1))
+        if "decode_mfma" in name and vgpr + agpr > 256:
+            over.append((name, vgpr, agpr))
+    assert not over, over

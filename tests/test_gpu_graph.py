@@ -52,10 +52,11 @@ def test_captured_step_replays_match_eager(dtype, tile_pages):
     plane.push()
     a_app = kv_cache.build_append_args(k1, v1, app, ctx, cache.k_pool, cache.v_pool, bt,
                                        k_scale=cache.k_scale, v_scale=cache.v_scale,
-                                       max_append=1)
+                                       max_append=1, v_layout=cache.v_layout)
     a_dec = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out,
                                 k_scale=cache.k_scale, v_scale=cache.v_scale, plane=plane,
-                                workers=48, tiles=tiles, tile_pages=tile_pages)
+                                workers=48, tiles=tiles, tile_pages=tile_pages,
+                                v_layout=cache.v_layout)
 
     def step(stream):
         kv_cache.launch_append(a_app, stream)

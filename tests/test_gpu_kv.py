@@ -206,20 +206,24 @@ def test_hardware_16bit_rounding_on_ties_neighbours_and_extremes(dtype):
     assert np.array_equal(got_v, ref), int(np.sum(got_v != ref))
 
 
-@pytest.mark.parametrize("dtype,ps", [(torch.bfloat16, 16), (FP8, 16), (torch.float16, 16),
-                                      (torch.bfloat16, 32), (FP8, 32), (torch.float16, 32)])
-def test_cache_prefill_then_decode_loop(dtype, ps):
+@pytest.mark.parametrize("dtype,ps,layout", [
+    (torch.bfloat16, 16, "auto"), (torch.bfloat16, 16, "dmajor"), (FP8, 16, "auto"),
+    (FP8, 16, "dmajor"), (torch.float16, 16, "auto"), (torch.float16, 16, "dmajor"),
+    (torch.bfloat16, 32, "auto"), (FP8, 32, "auto"), (torch.float16, 32, "auto")])
+def test_cache_prefill_then_decode_loop(dtype, ps, layout):
     """PagedKvCache: a prefill append, then 20 one-token appends per request
     (page boundaries crossed), mirrored on the oracle; then a decode step over
     the cache against the oracle decode on the same pools. An fp16 cache is
     fed fp16 rows and decoded with fp16 Q (the reference's FlashInfer serving
-    dtype), the others bf16. 32-token pages keep V token-major."""
+    dtype), the others bf16. The default V layout is token-major; d-major on
+    request."""
     half = torch.float16 if dtype == torch.float16 else torch.bfloat16
     rng = np.random.default_rng(21)
     hkv, hq, d, R = 8, 32, 128, 6
-    cache = kv_cache.PagedKvCache(64 if ps == 16 else 40, hkv, d, ps, dtype=dtype)
+    cache = kv_cache.PagedKvCache(64 if ps == 16 else 40, hkv, d, ps, dtype=dtype,
+                                  v_layout=layout)
     lay = cache.v_layout
-    assert lay == ("tokmajor" if ps > 16 else "dmajor")
+    assert lay == ("tokmajor" if layout == "auto" else layout)
     rids = list(range(R))
     for r in rids:
         cache.add_request(r)

@@ -10,6 +10,7 @@ import torch
 
 import oracle
 import sched_abi as abi
+import sched_pd
 from parity import TOL_F32, par_err
 
 pytestmark = pytest.mark.gpu
@@ -260,3 +261,96 @@ def test_runtime_work_queue_through_rt_tables(lib):
 def test_occupancy_queries(lib):
     assert lib.paged_softmax_occupancy() > 0
     assert lib.sched_pd_cu_count() > 0
+
+
+def _hip():
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    return hip
+
+
+def _write_slot(hip, addr, value):
+    v = ctypes.c_uint64(value)
+    assert hip.hipMemcpy(ctypes.c_void_p(addr), ctypes.byref(v), 8, 1) == 0  # host to device
+
+
+def test_slots_written_directly_on_the_device_take_effect(lib):
+    """The reference's mechanism: the app writes a __sched_* slot itself
+    (cudaMemcpyToSymbol). Here the slot's device address comes from
+    sched_rt_slot_addresses and a plain copy writes it; the next launch reads
+    it. A reversed order and a fresh timer buffer written that way take
+    effect (same bits, rows in the new buffer); a device-side disarm of ctrl
+    and queue under a queue grid of fewer workers than tasks still serves
+    every task (stock path over the whole grid)."""
+    f = Fixture(fixture_paged_decode)
+    assert lib.sched_rt_init()
+    lib.sched_rt_set_num_tasks(0)
+    lib.sched_rt_timer_clear()
+    assert lib.sched_rt_push_ctrl()
+    golden = f.launch(lib)
+    assert close(golden.cpu(), f.reference())
+    lib.sched_rt_timer_clear()        # the golden launch filled the runtime's rows
+    addrs = (ctypes.c_uint64 * 4)()
+    assert lib.sched_rt_slot_addresses(addrs) and all(addrs)
+    held = (ctypes.c_uint64 * 4)()
+    assert lib.sched_rt_slots(held)
+    hip = _hip()
+    order = torch.arange(4096, dtype=torch.int32, device="cuda")
+    order[:f.nseq] = torch.arange(f.nseq - 1, -1, -1, dtype=torch.int32, device="cuda")
+    timer = torch.zeros(4096, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    _write_slot(hip, addrs[0], order.data_ptr())
+    _write_slot(hip, addrs[2], timer.data_ptr())
+    now = (ctypes.c_uint64 * 4)()
+    assert lib.sched_rt_slots(now)
+    assert now[0] == order.data_ptr() and now[2] == timer.data_ptr()
+    assert torch.equal(f.launch(lib), golden)
+    assert int((timer[:f.nseq] > 0).sum()) == f.nseq          # the kernel wrote the new rows
+    assert int((timer_rows(lib, f.nseq) > 0).sum()) == 0      # not the runtime's own
+    # the queue armed on the host (num_tasks pushed) and launched with 7
+    # workers, then ctrl and queue nulled on the device: the stock path
+    lib.sched_rt_set_num_tasks(f.nseq)
+    assert lib.sched_rt_push_ctrl()
+    assert lib.sched_rt_queue_reset(7)
+    _write_slot(hip, addrs[1], 0)
+    _write_slot(hip, addrs[3], 0)
+    args = sched_pd.build_args(f.q, f.kv.view(-1, 1, f.pt, 2 * SD)[..., :SD],
+                               f.kv.view(-1, 1, f.pt, 2 * SD)[..., SD:], f.bt, f.nbl,
+                               out=f.out, v_layout="tokmajor", sm_scale=0.125,
+                               tau_scope=abi.TAU_PER_PAGE, flags=abi.FLAG_CTX_IN_PAGES,
+                               rt_tables=True, workers=7)
+    f.out.zero_()
+    sched_pd.launch(args)
+    torch.cuda.synchronize()
+    assert torch.equal(f.out, golden)
+    # restore what sched_rt armed
+    for i in range(4):
+        _write_slot(hip, addrs[i], held[i])
+    lib.sched_rt_set_num_tasks(0)
+    assert lib.sched_rt_push_ctrl()
+
+
+def test_timer_host_mirror_for_external_readers(lib):
+    """Opt-in host copy of the timer rows: after a launch on the runtime's
+    tables the published timer_host_va holds the device rows, readable with no
+    GPU call; off again publishes 0."""
+    import json
+    import os
+    f = Fixture(fixture_paged_decode)
+    assert lib.sched_rt_init()
+    lib.sched_rt_set_num_tasks(0)
+    assert lib.sched_rt_push_ctrl()
+    assert lib.sched_rt_set_timer_host_mirror(True)
+    va = lib.sched_rt_timer_host_va()
+    assert va
+    pub = json.load(open(f"/tmp/sched_rt_{os.getpid()}.json"))
+    assert pub["timer_host_va"] == va and pub["timer_bytes"] == 4096 * 8
+    lib.sched_rt_timer_clear()
+    f.launch(lib)                      # synchronises: the mirror copy is done
+    host = np.frombuffer(ctypes.string_at(va, 4096 * 8), np.uint64)
+    dev = timer_rows(lib, 4096)
+    assert np.array_equal(host, dev) and int((host[:f.nseq] > 0).sum()) == f.nseq
+    assert lib.sched_rt_set_timer_host_mirror(False)
+    assert lib.sched_rt_timer_host_va() == 0
+    assert json.load(open(f"/tmp/sched_rt_{os.getpid()}.json"))["timer_host_va"] == 0
