@@ -1,7 +1,7 @@
 """Benchmark: paged-decode KV-read bandwidth and heterogeneous-batch makespan.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-hetero] [--no-cpu]
-                    [--sections hetero,shed,fp8,kv,layouts,pi,trace,fixture]
+                    [--sections hetero,shed,fp8,kv,layouts,pi,trace,fixture,serving]
 
 One step = one decode launch over the Llama-3-8B-shaped bf16 GQA batch (Hq 32,
 Hkv 8, d 128, page 16, 64 requests x 2048 tokens, levers null). The pool is
@@ -44,9 +44,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--no-hetero", action="store_true",
                    help="headline decode only (same as --sections '')")
-    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi,trace,fixture",
+    p.add_argument("--sections", default="hetero,shed,fp8,kv,layouts,pi,trace,fixture,serving",
                    help="comma list of the extra measurements: hetero, shed, fp8, kv, "
-                        "layouts, pi")
+                        "layouts, pi, trace, fixture, serving")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--tables", type=int, default=8)
     return p.parse_args()
@@ -973,6 +973,128 @@ def bench_fixture_hetero(torch, sched_pd, iters=100):
     return res
 
 
+def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
+    """An engine-style decode loop, the reference's stock / observe / enforce
+    A/B of its serving plugin (ROADMAP.md:820-830) without an engine: 256
+    requests of the Llama-3-8B shape (bf16, Hq 32 / Hkv 8, page 16) with
+    lognormal contexts (median 1024, sigma 1.2); per step the cache writer
+    appends one token per request, then the decode runs over 128-page split
+    tiles. Modes: stock (the same split plan, no lever tables), the serving
+    hooks observing only (bind, probe the timer 1 step in 8, never change the
+    schedule), and the hooks enforcing (controller orders, queue arming,
+    re-plan every 8 steps). Wall-clock per step with the host work the hooks
+    add, and GPU time between events around the loop."""
+    import time
+    import numpy as np
+    import kv_cache
+    from sched_rt import SchedPlane
+    from serving import HookConfig, ServingHooks
+    R, hkv, hq, d, ps, tp = 256, 8, 32, 128, 16, 128
+    rng = np.random.default_rng(0)
+    lens = workloads.lognormal_ctx(R, 1024, 1.2, 16, 32768, rng)
+    grow = 3 * (2 * steps + warm) + 1     # tokens appended over the three modes
+    npages = int((-(-(lens + grow) // ps)).sum()) + R
+    g = torch.Generator(device="cuda").manual_seed(9)
+    cache = kv_cache.PagedKvCache(npages, hkv, d, ps, dtype=torch.bfloat16)
+    rids = list(range(R))
+    for r in rids:
+        cache.add_request(r)
+    at = 0
+    while at < R:            # prefill in slices (bounded temporaries)
+        sl = list(range(at, min(at + 32, R)))
+        n = int(lens[sl].sum())
+        k = (torch.randn(n, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+        v = (torch.randn(n, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+        cache.append(sl, k, v, lens[sl].tolist())
+        at += len(sl)
+        del k, v
+    q = (torch.randn(R, hq, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    k1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    v1 = (torch.randn(R, hkv, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
+    out = torch.empty(R, hq, d, dtype=torch.bfloat16, device="cuda")
+    cu = sched_pd.cu_count()
+    bt0, ctx0 = cache.block_table(rids)
+    occ = sched_pd.occupancy(sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt0, ctx0,
+                                                 out=out, v_layout=cache.v_layout))
+    res = {"requests": R, "steps": steps, "tile_pages": tp, "resident": occ * cu}
+    stream = torch.cuda.current_stream()
+    for mode in ("stock", "observe", "enforce"):
+        hooks = None
+        if mode != "stock":
+            plane = SchedPlane(max_tasks=16384)
+            hooks = ServingHooks(plane, hkv, HookConfig(observe_only=mode == "observe",
+                                                        tile_pages=tp, resident=occ * cu))
+
+        host = [0.0]
+
+        def step(ev=None):
+            cache.append(rids, k1, v1)
+            now = [cache.lens[r] for r in rids]
+            h0 = time.perf_counter()
+            if hooks is None:
+                launch = {"tiles": sched_pd.plan_tiles(now, ps, tp, hkv), "tile_pages": tp}
+            else:
+                launch = hooks.on_batch_begin(rids, now)
+            host[0] += time.perf_counter() - h0
+            cache.decode(q, rids, out=out, **launch)
+            h0 = time.perf_counter()
+            if hooks is not None:
+                hooks.on_batch_end()
+            host[0] += time.perf_counter() - h0
+            if ev is not None:
+                # the step's decode again, 1 + 3 times with the same tables
+                # (timer gate already off): the last 3 back to back between
+                # the events, so the interval is GPU time, not host time
+                bt, ctx = cache.block_table(rids)
+                a = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out,
+                                        v_layout=cache.v_layout, **launch)
+                sched_pd.launch(a)
+                ev[0].record(stream)
+                for _ in range(3):
+                    sched_pd.launch(a)
+                ev[1].record(stream)
+        for _ in range(warm):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        host[0] = 0.0
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        plan_us = host[0] * 1e6 / steps
+        # the decode launches alone, per step (a separate pass, so the
+        # relaunches do not perturb the wall-clock figure)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for ev in evs:
+            step(ev)
+        torch.cuda.synchronize()
+        dec = sorted(a.elapsed_time(b) * 1e3 / 3 for a, b in evs)
+        res[mode] = {"wall_ms_per_step": round(wall, 3),
+                     "gpu_ms_per_step": round(e0.elapsed_time(e1) / steps, 3),
+                     "tokens_per_s": round(R / (wall * 1e-3), 1),
+                     "plan_host_us_per_step": round(plan_us, 1),
+                     "decode_us_median": round(dec[len(dec) // 2], 2),
+                     "decode_us_mean": round(sum(dec) / len(dec), 2)}
+        if hooks is not None:
+            res[mode]["probes_folded"] = hooks.probes_folded
+            res[mode]["hook_errors"] = hooks.hook_errors
+    for mode in ("observe", "enforce"):
+        res[mode]["vs_stock_pct"] = round(
+            100 * (res[mode]["wall_ms_per_step"] - res["stock"]["wall_ms_per_step"])
+            / res["stock"]["wall_ms_per_step"], 2)
+        res[mode]["decode_vs_stock_pct"] = round(
+            100 * (res[mode]["decode_us_mean"] - res["stock"]["decode_us_mean"])
+            / res["stock"]["decode_us_mean"], 2)
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's fp32 port (the reference CPU loop, OpenMP over tasks) on
     the uniform workload's shape (64 requests x 2048 tokens, a pool of just
@@ -1086,6 +1208,8 @@ def main():
         line["trace_eval"] = bench_trace_eval(torch, sched_pd)
     if "fixture" in sections:
         line["fixture_hetero"] = bench_fixture_hetero(torch, sched_pd)
+    if "serving" in sections:
+        line["serving_loop"] = bench_serving(torch, sched_pd, workloads)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, workloads)
     print(json.dumps(line), flush=True)

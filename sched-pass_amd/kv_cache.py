@@ -16,7 +16,6 @@ Appends run on the GPU through the C ABI; there is no CPU path.
 from __future__ import annotations
 
 import ctypes
-import math
 
 import numpy as np
 import torch
@@ -237,6 +236,7 @@ class PagedKvCache:
         self.allocator = PageAllocator(num_pages)
         self.pages: dict = {}
         self.lens: dict = {}
+        self._table = None       # the device block table of the last request list
 
     # -- bookkeeping ----------------------------------------------------------
     def add_request(self, rid) -> None:
@@ -248,33 +248,69 @@ class PagedKvCache:
     def release(self, rid) -> None:
         self.allocator.free(self.pages.pop(rid))
         del self.lens[rid]
+        self._table = None
 
     def reserve(self, rids, counts) -> None:
         """Allocate pages so that each request has room for counts[i] more
         tokens; all or nothing."""
-        need = []
-        for rid, n in zip(rids, counts):
-            want = math.ceil((self.lens[rid] + int(n)) / self.page_size)
-            need.append(max(0, want - len(self.pages[rid])))
-        total = sum(need)
+        rids = list(rids)
+        lens = np.fromiter((self.lens[r] for r in rids), np.int64, len(rids))
+        held = np.fromiter((len(self.pages[r]) for r in rids), np.int64, len(rids))
+        want = -(-(lens + np.asarray(counts, np.int64)) // self.page_size)
+        need = np.maximum(want - held, 0)
+        total = int(need.sum())
         if total > self.allocator.num_free:
             raise OutOfPages(f"need {total} pages, {self.allocator.num_free} free")
-        fresh = self.allocator.alloc(total)
+        if total == 0:
+            return
+        fresh = self.allocator.alloc(total).tolist()
         at = 0
-        for rid, k in zip(rids, need):
-            self.pages[rid].extend(fresh[at:at + k].tolist())
+        for i in np.nonzero(need)[0]:       # only the requests that cross a page
+            k = int(need[i])
+            self.pages[rids[i]].extend(fresh[at:at + k])
             at += k
 
     # -- tables ---------------------------------------------------------------
     def block_table(self, rids):
-        """(block_table [R, max_pages] int32, ctx_lens [R] int32) on the device;
-        unused entries are -1."""
-        width = max([len(self.pages[r]) for r in rids] + [1])
-        bt = np.full((len(rids), width), -1, dtype=np.int32)
-        for i, r in enumerate(rids):
-            bt[i, :len(self.pages[r])] = self.pages[r]
-        ctx = np.array([self.lens[r] for r in rids], dtype=np.int32)
-        return (torch.from_numpy(bt).to(self.device), torch.from_numpy(ctx).to(self.device))
+        """(block_table [R, width] int32, ctx_lens [R] int32) on the device;
+        unused entries are -1, width >= every request's page count.
+
+        The table for a list of requests stays on the device between calls:
+        a call with the same list uploads only the entries of pages added
+        since (a decode step adds at most one page per request), so a serving
+        step does not rebuild and copy R x max_pages entries. The update is
+        stream-ordered after the launches that read the previous contents. A
+        different list, a request that outgrew the width, or a released page
+        rebuilds the table (width with headroom)."""
+        rids = list(rids)
+        counts = np.fromiter((len(self.pages[r]) for r in rids), np.int64, len(rids))
+        ctx = np.fromiter((self.lens[r] for r in rids), np.int32, len(rids))
+        t = self._table
+        key = tuple(rids)
+        if (t is None or t["key"] != key or t["counts"].size != counts.size
+                or (counts.size and (counts.max() > t["width"]
+                                     or (counts < t["counts"]).any()))):
+            width = max(int(counts.max()) if counts.size else 1, 1)
+            width = -(-(width + width // 4 + 1) // 64) * 64     # headroom for growth
+            bt = np.full((len(rids), width), -1, dtype=np.int32)
+            for i, r in enumerate(rids):
+                bt[i, :counts[i]] = self.pages[r]
+            t = {"key": key, "width": width, "counts": counts,
+                 "dev": sched_pd.upload(bt, self.device)}
+            self._table = t
+        else:
+            grew = np.nonzero(counts > t["counts"])[0]
+            if grew.size:
+                rows, cols, vals = [], [], []
+                for i in grew:
+                    lo, hi = int(t["counts"][i]), int(counts[i])
+                    rows.extend([i] * (hi - lo))
+                    cols.extend(range(lo, hi))
+                    vals.extend(self.pages[rids[i]][lo:hi])
+                idx = sched_pd.upload(np.array([rows, cols], np.int64), self.device)
+                t["dev"][idx[0], idx[1]] = sched_pd.upload(np.array(vals, np.int32), self.device)
+                t["counts"] = counts
+        return t["dev"], sched_pd.upload(ctx, self.device)
 
     def csr(self, rids):
         """(page_indptr [R+1], indices, last_page_len [R]) int32 on the device."""
@@ -284,7 +320,7 @@ class PagedKvCache:
         indices = np.array([p for r in rids for p in self.pages[r]], dtype=np.int32)
         last = np.array([self.lens[r] - (len(self.pages[r]) - 1) * self.page_size
                          if self.pages[r] else 0 for r in rids], dtype=np.int32)
-        to = lambda x: torch.from_numpy(x).to(self.device)  # noqa: E731
+        to = lambda x: sched_pd.upload(x, self.device)  # noqa: E731
         return to(indptr), to(indices if indices.size else np.zeros(1, np.int32)), to(last)
 
     # -- writes and reads -----------------------------------------------------
@@ -304,7 +340,7 @@ class PagedKvCache:
             bt, ctx = self.block_table(rids)
             app = np.zeros(len(rids) + 1, dtype=np.int32)
             app[1:] = np.cumsum(counts)
-            append(k_new, v_new, torch.from_numpy(app).to(self.device), ctx, self.k_pool,
+            append(k_new, v_new, sched_pd.upload(app, self.device), ctx, self.k_pool,
                    self.v_pool, bt, v_layout=self.v_layout, k_scale=self.k_scale,
                    v_scale=self.v_scale,
                    max_append=max(counts + [0]), errors=errors)
@@ -314,6 +350,7 @@ class PagedKvCache:
                 self.lens[rid] -= n
                 self.allocator.free(self.pages[rid][held[rid]:])
                 del self.pages[rid][held[rid]:]
+            self._table = None
             raise
 
     def decode(self, q, rids, **kw):

@@ -28,6 +28,99 @@ if hasattr(torch, "float8_e4m3fn"):
     _DT[torch.float8_e4m3fn] = abi.FP8_E4M3
 
 
+class _StagingRing:
+    """Pinned host ring for the small uploads of one stream (page-table rows,
+    context lengths, split plans, orders): a copy into the ring, then an
+    asynchronous copy to the device on the stream, with no host allocation per
+    upload. The ring is cut into CHUNKS chunks; leaving a chunk records an
+    event on the stream after the copies out of it, and a chunk is written
+    again only once the event of its previous lap has completed (a wait only
+    when the device lags a whole ring behind the host)."""
+    BYTES = 4 << 20
+    CHUNKS = 16
+    ALIGN = 256
+
+    def __init__(self, stream):
+        self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
+        self.stream = stream
+        self.chunk = self.BYTES // self.CHUNKS
+        self.cur = 0
+        self.head = 0
+        self.done = [None] * self.CHUNKS
+
+    def put(self, t: torch.Tensor, out: torch.Tensor) -> bool:
+        """Stage contiguous host `t` and copy it into contiguous device `out`
+        (same bytes); False if `t` is too large for the ring."""
+        n = t.numel() * t.element_size()
+        if n > self.chunk:
+            return False
+        if n == 0:
+            return out
+        start = -(-self.head // self.ALIGN) * self.ALIGN
+        if start + n > (self.cur + 1) * self.chunk:
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+            self.done[self.cur] = ev
+            self.cur = (self.cur + 1) % self.CHUNKS
+            start = self.cur * self.chunk
+            if self.done[self.cur] is not None:
+                self.done[self.cur].synchronize()
+                self.done[self.cur] = None
+        self.head = start + n
+        view = self.buf[start:start + n]
+        view.copy_(t.reshape(-1).view(torch.uint8))
+        out.view(-1).view(torch.uint8).copy_(view, non_blocking=True)
+        return True
+
+
+_RINGS: dict = {}
+
+
+def _ring(dev: torch.device) -> _StagingRing:
+    stream = torch.cuda.current_stream(dev)
+    key = (dev.index, stream.cuda_stream)
+    ring = _RINGS.get(key)
+    if ring is None:
+        ring = _RINGS[key] = _StagingRing(stream)
+    return ring
+
+
+def upload_into(dst: torch.Tensor, src) -> None:
+    """Copy host `src` (numpy or CPU tensor, same bytes) into the contiguous
+    device tensor `dst` through the current stream's pinned ring, without
+    waiting for the device (see upload)."""
+    t = torch.from_numpy(np.ascontiguousarray(src)) if isinstance(src, np.ndarray) else src
+    t = t.contiguous()
+    if t.numel() * t.element_size() != dst.numel() * dst.element_size() or not dst.is_contiguous():
+        raise ValueError("upload_into: source and destination differ in size or layout")
+    if not dst.is_cuda:
+        dst.view(-1).view(torch.uint8).copy_(t.reshape(-1).view(torch.uint8))
+        return
+    if not _ring(dst.device).put(t, dst):
+        dst.view(-1).view(torch.uint8).copy_(t.reshape(-1).view(torch.uint8).pin_memory(),
+                                             non_blocking=True)
+
+
+def upload(a, device) -> torch.Tensor:
+    """A host array (numpy or CPU tensor) on `device`, without waiting for the
+    device: staged through a pinned ring of the current stream and copied
+    asynchronously on it (arrays over 256 KiB through pinned memory of their
+    own). A copy from pageable memory would first wait for every kernel
+    already queued, so a serving loop's host work would never overlap its GPU
+    work."""
+    t = torch.from_numpy(np.ascontiguousarray(a)) if isinstance(a, np.ndarray) else a
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return t.to(dev)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    t = t.contiguous()
+    out = torch.empty(t.shape, dtype=t.dtype, device=dev)
+    if not _ring(dev).put(t, out):
+        out.copy_(t.pin_memory(), non_blocking=True)
+    return out
+
+
 def _dtype_code(t: torch.Tensor, what: str) -> int:
     if t.dtype not in _DT:
         raise TypeError(f"{what}: unsupported dtype {t.dtype}")
@@ -262,13 +355,8 @@ def workspace_of(args: abi.SchedDecodeArgs) -> torch.Tensor | None:
     return None
 
 
-def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
-               device="cuda") -> torch.Tensor:
-    """Task-major split-KV plan: one (task, chunk) row per work item, chunk c
-    of task (r, h) covering pages [c*tile_pages, (c+1)*tile_pages). A task has
-    max(1, ceil(ceil(ctx/page_size) / tile_pages)) chunks. ctx_lens: host
-    sequence (the plan is built where the lengths are known, like a serving
-    scheduler's plan step)."""
+def plan_tiles_host(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int) -> np.ndarray:
+    """The plan of plan_tiles as a host int32 array [num_tiles, 2]."""
     ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
                      dtype=np.int64)
     npg = (ctx + page_size - 1) // page_size
@@ -277,7 +365,17 @@ def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
     tasks = np.repeat(np.arange(per_task.size, dtype=np.int64), per_task)
     starts = np.cumsum(per_task) - per_task
     chunks = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, per_task)
-    return torch.tensor(np.stack([tasks, chunks], 1), dtype=torch.int32, device=device)
+    return np.stack([tasks, chunks], 1).astype(np.int32)
+
+
+def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
+               device="cuda") -> torch.Tensor:
+    """Task-major split-KV plan: one (task, chunk) row per work item, chunk c
+    of task (r, h) covering pages [c*tile_pages, (c+1)*tile_pages). A task has
+    max(1, ceil(ceil(ctx/page_size) / tile_pages)) chunks. ctx_lens: host
+    sequence (the plan is built where the lengths are known, like a serving
+    scheduler's plan step), the lengths the launch will see."""
+    return upload(plan_tiles_host(ctx_lens, page_size, tile_pages, num_kv_heads), device)
 
 
 def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.Tensor:

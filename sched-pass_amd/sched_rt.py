@@ -26,6 +26,7 @@ import torch
 from sched_abi import (CTRL_FLAGS_OFF, CTRL_LAMBDA_OFF, CTRL_NUM_TASKS_OFF,
                        CTRL_ORDER_SIZE_OFF, CTRL_ROWS_OFF, FLAG_TIMER_OFF,
                        HINT_AUTO, HINT_POLITE, HINT_URGENT, ROW_SIZE)
+from sched_pd import upload_into
 
 __all__ = ["SchedPlane", "SchedArenaError", "HINT_AUTO", "HINT_URGENT",
            "HINT_POLITE", "FLAG_TIMER_OFF", "MANIFEST"]
@@ -73,6 +74,7 @@ class SchedPlane:
         self._timer_arena = self.arena[TIMER_OFF:TIMER_OFF + 8 * self.N].view(torch.int64)
         self._queue = self.arena[QUEUE_OFF:QUEUE_OFF + 4].view(torch.int32)
         self._ctrl_host = bytearray(self.ctrl_bytes)
+        self._rows_end = self.ctrl_bytes  # mirror bytes push() must copy (rows written)
         self._generation = 0
         self._timer_dev = None      # separate device row buffer (use_device_timer)
         self._timer_stream = None
@@ -117,7 +119,10 @@ class SchedPlane:
         the tail keeps its current entries)."""
         t = torch.as_tensor(tasks, dtype=torch.int32)
         n = min(t.numel(), self.N)
-        self._order_view()[:n].copy_(t[:n].to(self.dev, non_blocking=t.is_cuda))
+        if t.is_cuda:
+            self._order_view()[:n].copy_(t[:n])
+        else:
+            upload_into(self._order_view()[:n], t[:n])   # queued, not waited for
 
     def reset_order(self) -> None:
         self.set_order(torch.arange(self.N, dtype=torch.int32))
@@ -154,6 +159,7 @@ class SchedPlane:
             raise IndexError(f"row {i} outside [0, {self.N})")
         struct.pack_into("<fHBB", self._ctrl_host, CTRL_ROWS_OFF + ROW_SIZE * i,
                          float(q), int(tau) & 0xFFFF, int(hint) & 0xFF, 0)
+        self._rows_end = max(self._rows_end, CTRL_ROWS_OFF + ROW_SIZE * (i + 1))
 
     def set_rows(self, q=None, tau=None, hint=None, n: int | None = None) -> None:
         """Vectorised set_row over rows [0, n)."""
@@ -167,15 +173,21 @@ class SchedPlane:
         if hint is not None:
             rows["hint"] = np.asarray(torch.as_tensor(hint, dtype=torch.int64).cpu())[:n] & 0xFF
         self._ctrl_host[CTRL_ROWS_OFF:CTRL_ROWS_OFF + ROW_SIZE * n] = rows.tobytes()
+        self._rows_end = max(self._rows_end, CTRL_ROWS_OFF + ROW_SIZE * n)
 
     def push(self) -> None:
         """Publish the mirror (generation++): rows and header body first, the
         generation word last, in stream order."""
         self._generation += 1
         struct.pack_into("<I", self._ctrl_host, 0, self._generation)
-        host = torch.frombuffer(bytearray(self._ctrl_host), dtype=torch.uint8)
-        self._ctrl_dev[4:].copy_(host[4:])
-        self._ctrl_dev[:4].copy_(host[:4])
+        # the header plus the rows written since the last push (rows past
+        # them hold the same bytes on both sides)
+        end = max(CTRL_ROWS_OFF, self._rows_end)
+        self._rows_end = 0
+        host = torch.frombuffer(bytearray(self._ctrl_host[:end]), dtype=torch.uint8)
+        # pinned staging: the copies are queued, not waited for
+        upload_into(self._ctrl_dev[4:end], host[4:])
+        upload_into(self._ctrl_dev[:4], host[:4])
 
     # -- timer (python/sched_rt.py:446-462) -------------------------------------
     def clear_timer(self) -> None:
@@ -191,6 +203,22 @@ class SchedPlane:
             self._timer_stream.synchronize()
             return out
         return t.cpu()
+
+    def read_timer_async(self):
+        """(rows, event): a device-to-host copy of the per-task cycles into a
+        pinned int64 buffer, queued on the timer stream (use_device_timer) or
+        the current one; the rows are valid once event.query() is true. The
+        buffer is reused by the next call: read it first. The caller
+        guarantees the writing launches are complete."""
+        t = self._timer_view()
+        if getattr(self, "_timer_host", None) is None or self._timer_host.numel() != t.numel():
+            self._timer_host = torch.empty(t.numel(), dtype=torch.int64, pin_memory=True)
+        s = self._timer_stream or torch.cuda.current_stream(self.dev)
+        with torch.cuda.stream(s):
+            self._timer_host.copy_(t, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(s)
+        return self._timer_host, ev
 
     # -- work queue (python/sched_rt.py:464-471) --------------------------------
     def reset_queue(self, workers: int) -> None:

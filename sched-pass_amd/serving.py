@@ -5,12 +5,14 @@ objects; here the engine passes request ids and KV lengths).
 
 Per step, as in the reference:
   on_batch_begin(rids, kv_lens) -> launch arguments for sched_pd.paged_decode
+    * advance the last probe's readout, never waiting for the device: once
+      the GPU has passed the probe step (event query) its timer rows' copy to
+      pinned host memory is queued; once that copy is done (event query) the
+      rows are folded into the controller;
     * cadence gate: re-plan only every `plan_every` steps (and on probe
-      steps); in between the installed tables stay and nothing is read back;
+      steps); in between the installed tables stay;
     * bind work items to requests (one per (request, kv-head) task, or the
       split-KV tiles of plan_tiles);
-    * fold the last probe's timer rows into the controller once the GPU has
-      passed that step (event query, never a synchronize);
     * predict per-request cost, spread it over the work items;
     * regime gate: ticket queue armed (W = resident workgroups) when the
       batch has more items than resident slots, a heavy tail
@@ -70,12 +72,16 @@ class ServingHooks:
         self._event = event_factory or (lambda: torch.cuda.Event())
         self.step = 0
         self.timer_armed = False
-        self.pending = None      # (event, binding) of an unread probe step
+        self.pending = None      # (event, binding, rows) of an unread probe step
         self.inflight = None     # completion event of the last step
         self.binding = None      # (rids, kv_lens, item_to_req, nitems)
         self.order_n = None      # items of the live order, None = identity
         self.armed_n = None      # items the armed ticket queue covers
         self.launch = {"plane": plane, "workers": 0, "tiles": None, "tile_pages": 0}
+        if plane.dev.type == "cuda":
+            # probe rows read back on a side stream: the readout waits for the
+            # probe step only, not for the kernels queued after it
+            plane.use_device_timer()
         self.probes_folded = 0
         self.hook_errors = 0
         self._err_sites = set()
@@ -88,9 +94,10 @@ class ServingHooks:
         pages = -(-np.asarray(kv_lens, np.int64) // ps)
         if self.cfg.tile_pages > 0:
             import sched_pd
-            tiles = sched_pd.plan_tiles(kv_lens, ps, self.cfg.tile_pages, self.hkv,
-                                        device=self.plane.dev)
-            t = tiles.cpu().numpy()
+            # built on the host and uploaded once (reading a device plan back
+            # would wait for the previous step's kernels)
+            t = sched_pd.plan_tiles_host(kv_lens, ps, self.cfg.tile_pages, self.hkv)
+            tiles = sched_pd.upload(t, self.plane.dev)
             req = t[:, 0] // self.hkv
             first = t[:, 1] * self.cfg.tile_pages
             item_pages = np.clip(pages[req] - first, 0, self.cfg.tile_pages)
@@ -100,17 +107,22 @@ class ServingHooks:
 
     def _consume_probe(self) -> None:
         """Fold the pending probe's timer rows (per task) into per-request
-        cost once its event has fired (python/sched_sglang_plugin.py:
-        345-377)."""
+        cost (python/sched_sglang_plugin.py:345-377), never waiting for the
+        device: once the probe step's event has fired, the rows' copy to the
+        host is queued; once that copy's event has fired, they are folded."""
         if self.pending is None:
             return
-        ev, b = self.pending
+        ev, b, rows = self.pending
         if not ev.query():
+            return
+        if rows is None and self.plane.dev.type == "cuda":
+            rows, ev2 = self.plane.read_timer_async()
+            self.pending = (ev2, b, rows)
             return
         self.pending = None
         rids, kv_list = b[0], b[1]
         n = len(rids)
-        cyc = torch.as_tensor(self.plane.read_timer()).to(torch.int64)
+        cyc = (rows if rows is not None else torch.as_tensor(self.plane.read_timer())).to(torch.int64)
         m = min(n * self.hkv, cyc.numel())
         per_req = torch.zeros(n, dtype=torch.int64).scatter_add_(
             0, torch.arange(m) // self.hkv, cyc[:m])
@@ -124,6 +136,7 @@ class ServingHooks:
         cfg, p = self.cfg, self.plane
         step = self.step
         self.step += 1
+        self._consume_probe()
         probe = step % cfg.timer_every == 0 and self.pending is None
         kv_list = [int(x) for x in kv_lens]
         if step % cfg.plan_every != 0 and not probe:
@@ -149,7 +162,6 @@ class ServingHooks:
             # 99-118): a larger plane is the fix
             raise RuntimeError(f"batch of {nitems} work items / {n * self.hkv} tasks exceeds "
                                f"the plane's max_tasks {p.N}")
-        self._consume_probe()
 
         cost_req = self.ctl.predict(rids, kv_list)
         req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
@@ -200,7 +212,7 @@ class ServingHooks:
         ev.record()
         self.inflight = ev
         if self.timer_armed:
-            self.pending = (ev, self.binding)
+            self.pending = (ev, self.binding, None)
             self.plane.set_timer_enabled(False)
             self.plane.push()
 

@@ -1,13 +1,15 @@
 """A serving loop on the GPU: per step the writer appends one token per
 request, the hooks plan the step, the decode runs with the hooks' tables and
 launch arguments; every step's output is bit-identical to the stock decode of
-the same work-item plan (and within bf16 tolerance of the unsplit decode), and
-probe steps feed the controller."""
+the same work-item plan, within the tolerance of the unsplit decode and of the
+oracle on the cache's pools, with and without the L2 hints; probe steps feed
+the controller."""
 import numpy as np
 import pytest
 import torch
 
 import kv_cache
+import oracle
 import sched_pd
 from parity import TOL_BF16, par_err
 from sched_rt import SchedPlane
@@ -22,8 +24,10 @@ def lib(schedlib):
     return schedlib
 
 
-@pytest.mark.parametrize("clc,tile_pages", [("on", 0), ("off", 0), ("auto", 8), ("on", 8)])
-def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages):
+@pytest.mark.parametrize("clc,tile_pages,hints", [("on", 0, False), ("off", 0, False),
+                                                  ("auto", 8, False), ("on", 8, True),
+                                                  ("off", 0, True)])
+def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages, hints):
     rng = np.random.default_rng(3)
     R, hkv, hq, d, ps = 24, 8, 32, 128, 16
     lens = rng.integers(16, 1500, R)
@@ -37,8 +41,12 @@ def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages):
     v = torch.randn(T, hkv, d, device="cuda").bfloat16()
     cache.append(rids, k, v, lens.tolist())
     plane = SchedPlane(max_tasks=4096)
+    # hints: an L2 budget far below the batch's KV, so long requests run
+    # polite and short ones urgent
     hooks = ServingHooks(plane, hkv, HookConfig(plan_every=2, timer_every=3, resident=64,
-                                                clc=clc, tile_pages=tile_pages))
+                                                clc=clc, tile_pages=tile_pages,
+                                                kv_bytes_per_token=hkv * d * 2 * 2 if hints else 0,
+                                                l2_bytes=1 << 20))
     for step in range(8):
         print(f"step {step} clc={clc} tile_pages={tile_pages}", flush=True)
         k1 = (torch.randn(R, hkv, d, device="cuda") / d ** 0.5).bfloat16()
@@ -56,6 +64,11 @@ def test_serving_loop_keeps_outputs_bit_identical(clc, tile_pages):
         cache.decode(q, rids, out=ref, tiles=launch["tiles"], tile_pages=launch["tile_pages"])
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"step {step}"
+        if step % 3 == 0:
+            # the hooks-driven step against the oracle on the cache's pools
+            bt, ctx = cache.block_table(rids)
+            r = oracle.decode(q, cache.k_pool, cache.v_pool, bt, ctx, v_layout=cache.v_layout)
+            assert par_err(out.cpu(), r, f"serving step {step}") <= TOL_BF16
         if launch["tiles"] is not None:
             whole = torch.empty_like(out)
             cache.decode(q, rids, out=whole)

@@ -1,0 +1,73 @@
+"""Host-to-device staging of the per-step uploads (sched_pd.upload /
+upload_into through a pinned ring per stream) and the asynchronous timer
+readout: the bytes arrive intact while the ring wraps many times over, with
+the device queue kept busy, on two streams, and for arrays too large for the
+ring."""
+import numpy as np
+import pytest
+import torch
+
+import sched_pd
+from sched_rt import SchedPlane
+
+pytestmark = pytest.mark.gpu
+
+
+def _busy(n=4096):
+    # keep the stream's queue non-empty so that uploads really overlap
+    a = torch.randn(n, n, device="cuda")
+    return a @ a
+
+
+def test_uploads_survive_ring_wraps():
+    rng = np.random.default_rng(1)
+    sent, got = [], []
+    total = 0
+    while total < 3 * sched_pd._StagingRing.BYTES:
+        n = int(rng.integers(1, 40000))
+        a = rng.integers(-2**31, 2**31 - 1, n, dtype=np.int64).astype(np.int32)
+        if len(sent) % 25 == 0:
+            _busy(1024)
+        sent.append(a)
+        got.append(sched_pd.upload(a, "cuda"))
+        total += a.nbytes
+    torch.cuda.synchronize()
+    for a, t in zip(sent, got):
+        assert np.array_equal(t.cpu().numpy(), a)
+    print(f"{len(sent)} uploads, {total} B")
+
+
+def test_upload_on_two_streams_and_large_arrays():
+    rng = np.random.default_rng(2)
+    s1 = torch.cuda.Stream()
+    big = rng.standard_normal(200_000).astype(np.float32)       # 800 KB: own pinned copy
+    with torch.cuda.stream(s1):
+        _busy(2048)
+        a1 = [rng.integers(0, 1000, 5000).astype(np.int32) for _ in range(20)]
+        t1 = [sched_pd.upload(a, "cuda") for a in a1]
+        tb = sched_pd.upload(big, "cuda")
+    a0 = [rng.integers(0, 1000, 7000).astype(np.int64) for _ in range(20)]
+    t0 = [sched_pd.upload(a, "cuda") for a in a0]
+    torch.cuda.synchronize()
+    for a, t in list(zip(a1, t1)) + list(zip(a0, t0)):
+        assert np.array_equal(t.cpu().numpy(), a)
+    assert np.array_equal(tb.cpu().numpy(), big)
+    dst = torch.zeros(64, dtype=torch.int32, device="cuda")
+    sched_pd.upload_into(dst[8:40], np.arange(32, dtype=np.int32))
+    torch.cuda.synchronize()
+    want = np.zeros(64, np.int32)
+    want[8:40] = np.arange(32)
+    assert np.array_equal(dst.cpu().numpy(), want)
+    with pytest.raises(ValueError):
+        sched_pd.upload_into(dst[:4], np.arange(5, dtype=np.int32))
+
+
+def test_async_timer_readout_matches_sync():
+    p = SchedPlane(max_tasks=256)
+    p.use_device_timer()
+    p._timer_view().copy_(torch.arange(256, dtype=torch.int64, device="cuda") * 7 + 3)
+    torch.cuda.synchronize()
+    rows, ev = p.read_timer_async()
+    ev.synchronize()
+    assert torch.equal(rows.clone(), p.read_timer())
+    assert int(rows[255]) == 255 * 7 + 3

@@ -299,7 +299,9 @@ def test_cache_bookkeeping_and_tables_on_cpu():
     c.lens.update(a=5, b=4, c=0)
     assert [len(c.pages[r]) for r in "abc"] == [2, 1, 0]
     bt, ctx = c.block_table(["a", "b", "c"])
-    assert bt.shape == (3, 2) and ctx.tolist() == [5, 4, 0] and bt[1, 1] == -1
+    assert bt.shape[0] == 3 and bt.shape[1] >= 2 and ctx.tolist() == [5, 4, 0]
+    assert bt[0, :2].tolist() == c.pages["a"] and bt[1, 0] == c.pages["b"][0]
+    assert (bt[1, 1:] == -1).all() and (bt[2] == -1).all()
     indptr, idx, last = c.csr(["a", "b", "c"])
     assert indptr.tolist() == [0, 2, 3, 3] and last.tolist() == [1, 4, 0]
     assert ctx_lens_from_last_page_len(indptr, last, 4).tolist() == [5, 4, 0]
@@ -308,6 +310,47 @@ def test_cache_bookkeeping_and_tables_on_cpu():
     assert c.allocator.num_free == 7               # all or nothing
     c.release("a")
     assert c.allocator.num_free == 9
+
+
+def test_block_table_updates_in_place_like_a_rebuild():
+    """Steps that add pages to some requests upload only those entries; the
+    table then equals one built from scratch. Growing past the width, a new
+    request list and a release rebuild it."""
+    rng = np.random.default_rng(4)
+    c = PagedKvCache(4000, 2, 8, page_size=4, dtype=torch.bfloat16, device="cpu")
+    rids = list(range(12))
+    for r in rids:
+        c.add_request(r)
+
+    def fresh():
+        w = max(len(c.pages[r]) for r in rids)
+        t = np.full((len(rids), w), -1, np.int32)
+        for i, r in enumerate(rids):
+            t[i, :len(c.pages[r])] = c.pages[r]
+        return t
+
+    c.reserve(rids, rng.integers(1, 40, 12).tolist())
+    for r in rids:
+        c.lens[r] = 4 * len(c.pages[r])
+    bt, _ = c.block_table(rids)
+    first = bt
+    for step in range(60):
+        grow = rng.integers(0, 20, 12)
+        c.reserve(rids, grow.tolist())
+        for r, g in zip(rids, grow):
+            c.lens[r] += int(g)
+        bt, ctx = c.block_table(rids)
+        want = fresh()
+        got = bt.numpy()
+        assert np.array_equal(got[:, :want.shape[1]], want), step
+        assert (got[:, want.shape[1]:] == -1).all()
+        assert ctx.tolist() == [c.lens[r] for r in rids]
+    assert bt.shape[1] > first.shape[1]          # outgrew the width once at least
+    bt2, _ = c.block_table(rids[::-1])             # another list: rebuilt
+    assert np.array_equal(bt2.numpy()[:, :want.shape[1]], want[::-1])
+    c.release(rids[0])
+    bt3, _ = c.block_table(rids[1:])
+    assert np.array_equal(bt3.numpy()[:, :want.shape[1]], want[1:])
 
 
 def test_cache_append_rolls_back_a_rejected_launch():
