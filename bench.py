@@ -1189,8 +1189,12 @@ def main():
                      "random_page_bytes": u["page_bytes"],
                      "frac_of_random_page_ceiling": round(kern_gbs / u["random_page_ceiling_gbs"], 4)},
     }
+    # counter values are not measured by this run: they are read from the
+    # committed rocprofv3 summaries named beside them
     line["roofline"]["traffic"] = profiled_traffic()
+    line["roofline"]["traffic_source"] = "profiles/decode_mfma_llama3_8b_uniform_pmc.md"
     line["roofline"]["mfma_busy_pct"] = profiled_mfma_busy()
+    line["roofline"]["mfma_busy_source"] = "profiles/decode_mfma_busy.md"
     sections = set() if args.no_hetero else set(x for x in args.sections.split(",") if x)
     if "hetero" in sections:
         line["hetero_makespan"] = bench_hetero(torch, sched_pd, workloads, SchedPlane, cu)
