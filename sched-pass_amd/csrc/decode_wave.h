@@ -163,8 +163,21 @@ __device__ __forceinline__ void run_wave_tasks(const LeverTables &L, Body &&body
     ntasks = armed ? ld_u32(lt_ctrl(L) + SCHED_CTRL_NUM_TASKS_OFF) : 0u;
   }
   if (ntasks == 0u) {
-    // static grid (or a queue grid disarmed on the device): every item once
-    for (uint32_t v = pid; v < L.nitems; v += gridDim.x * NWT)
+    // Static grid (or a queue grid disarmed on the device): every position
+    // once. Within each round of `spread` workgroups (those resident at
+    // once) positions run wave-major: wave w of the round's j-th workgroup
+    // takes position w * (round size) + j, so consecutive positions of pi
+    // (the longest tasks first, under LPT) land in different workgroups and
+    // CUs instead of sharing the first workgroup's four waves. Positions of
+    // a later round start after those of an earlier one, as with the
+    // one-task-per-workgroup kernels.
+    uint32_t v0 = pid;
+    if (L.spread > 1u) {
+      const uint32_t R = L.spread, g = blockIdx.x / R, j = blockIdx.x % R;
+      const uint32_t Rg = min(R, gridDim.x - g * R);
+      v0 = g * R * NWT + w * Rg + j;
+    }
+    for (uint32_t v = v0; v < L.nitems; v += gridDim.x * NWT)
       body(remap_static(L, v, L.nitems));
     return;
   }

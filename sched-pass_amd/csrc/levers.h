@@ -23,6 +23,8 @@ struct LeverTables {
   uint32_t nitems;           // work items of this launch (static grid size)
   uint32_t wq;               // 1 = launched as W persistent workers
   uint32_t workers;          // W of a work-queue launch (per-wave kernels)
+  uint32_t spread;           // per-wave kernels, static grid: workgroups resident at once
+                             // (0 or 1: positions row-major, wave-minor)
   uint32_t wallclock;        // timer source: 1 = s_memrealtime, 0 = s_memtime
   float dT, dR, H;           // policy marginal-exchange constants
   // Runtime mode (SCHED_PD_FLAG_RT_TABLES): the device addresses of the four

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <mutex>
 
 #include "kernel_set.h"
@@ -489,6 +490,27 @@ void sched_pd_default_args(SchedDecodeArgs *a) {
   a->policy_H = 0.25f;
 }
 
+// Workgroups of `fn` resident on the current device at once (occupancy x
+// CUs), cached per (device, kernel); 0 if the runtime cannot say.
+static uint32_t resident_blocks(const void *fn, int block) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void *>, uint32_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return 0;
+  std::lock_guard<std::mutex> g(mu);
+  auto it = cache.find({dev, fn});
+  if (it != cache.end())
+    return it->second;
+  int blocks = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, block, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const uint32_t r = (uint32_t)(blocks > 0 ? blocks : 0) * (uint32_t)(cus > 0 ? cus : 0);
+  cache[{dev, fn}] = r;
+  return r;
+}
+
 int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   KParams kp;
   Selected sel;
@@ -509,6 +531,8 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   const uint32_t grid = (slots + sel.per_block - 1) / sel.per_block;
   kp.L.wq = wq ? 1u : 0u;
   kp.L.workers = wq ? a->workers : 0u;
+  if (sel.per_block > 1 && !wq)
+    kp.L.spread = min(grid, resident_blocks(reinterpret_cast<const void *>(sel.fn), sel.block));
   hipLaunchKernelGGL(sel.fn, dim3(grid), dim3(sel.block), 0, (hipStream_t)stream, kp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)

@@ -140,3 +140,36 @@ def test_wave_kernel_on_the_fixture_layout():
     r = oracle.decode(q, kv[..., :SD], kv[..., SD:], bt_t, nbl_t, v_layout="tokmajor",
                       sm_scale=0.125, tau_scope=abi.TAU_PER_PAGE, ctx_in_pages=True)
     assert par_err(out.cpu(), r, "fixture layout") <= TOL_F32
+
+
+def test_wave_static_positions_over_several_rounds():
+    """A static launch larger than the resident workgroups: positions run
+    wave-major within each round of resident workgroups (so consecutive pi
+    entries land in different workgroups), every task exactly once (its
+    timer row set), outputs bitwise against the stock launch under identity,
+    reversed and random pi, including a last round that is partial."""
+    res = sched_pd.occupancy(sched_pd.build_args(
+        torch.zeros(4, 1, 32, device="cuda"), torch.zeros(1, 1, 16, 32, device="cuda"),
+        torch.zeros(1, 1, 16, 32, device="cuda"), torch.zeros(4, 1, dtype=torch.int32,
+                                                              device="cuda"),
+        torch.ones(4, dtype=torch.int32, device="cuda"), out=torch.zeros(4, 1, 32, device="cuda"),
+        v_layout="tokmajor")) * sched_pd.cu_count()
+    n = min(16383, 2 * res + 7)
+    rng = np.random.default_rng(4)
+    ctx = rng.integers(1, 40, n)
+    b = batch(torch.float32, 32, 16, heads=1, ctx=ctx, seed=5)
+    out, kind = run(b)
+    assert kind == "wave"
+    print(f"resident items {res}, tasks {n}")
+    r = ref(b)
+    assert par_err(out.cpu(), r, "wave rounds") <= TOL_F32
+    plane = SchedPlane(max_tasks=n)
+    for name, order in (("identity", np.arange(n)), ("reversed", np.arange(n)[::-1]),
+                        ("random", rng.permutation(n))):
+        plane.set_order(torch.from_numpy(order.astype(np.int32).copy()))
+        plane.push()
+        plane.clear_timer()
+        o, _ = run(b, plane=plane)
+        assert same(o, out), name
+        rows = plane.read_timer()[:n].numpy()
+        assert (rows > 0).all(), name
