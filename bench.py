@@ -388,7 +388,8 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
     scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
     max 16384); ticket work queue over split tiles, timer on; then the same
     queue with pi over tiles (twice the size) by the timer's per-task cycles,
-    longest first."""
+    longest first; and with pi by the tasks' page counts (known before the
+    launch) over tiles three times the size."""
     import numpy as np
     b = workloads.workload("qwen2_7b_fp8", seed=0)
     R, ntask = 512, 512 * 4
@@ -428,10 +429,27 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
                                 out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane3,
                                 workers=W, tiles=tiles2, tile_pages=tp2)
     us_lpt = _makespan_us(torch, sched_pd, a_lpt, stream)
+    # open loop: pi by the tasks' page counts, known on the host before the
+    # launch (no probe), over 768-page tiles (the best of 256..1024 measured)
+    tp3 = 3 * tile_pages
+    tiles3 = sched_pd.plan_tiles(ctx, 16, tp3, 4)
+    nt3 = tiles3.shape[0]
+    plane4 = SchedPlane(max_tasks=max(nt3, ntask))
+    task_pages = np.repeat(-(-ctx // 16), 4).astype(np.float64)
+    plane4.install_order(sched_pd.tile_order_by_task_key(tiles3, task_pages), nt3)
+    plane4.set_num_tasks(nt3)
+    plane4.push()
+    plane4.reset_queue(W)
+    a_len = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane4,
+                                workers=W, tiles=tiles3, tile_pages=tp3)
+    us_len = _makespan_us(torch, sched_pd, a_len, stream)
     kv = b["kv_bytes"]
     return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
             "wq_tiles_lpt_timer_us": round(us_lpt, 2),
+            "wq_tiles_lpt_length_us": round(us_len, 2),
             "gbs": round(kv / us_wq / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
+            "gbs_lpt_length": round(kv / us_len / 1e3, 1), "lpt_length_tile_pages": tp3,
             "tiles": nt, "tile_pages": tile_pages, "lpt_tile_pages": tp2, "workers": W,
             "max_ctx": int(ctx.max()),
             "residency_cycles": {"p50": int(np.percentile(cyc, 50)),

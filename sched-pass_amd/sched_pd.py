@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 
 import numpy as np
 import torch
@@ -43,6 +44,7 @@ class _StagingRing:
     def __init__(self, stream):
         self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
         self.stream = stream
+        self.lock = threading.Lock()
         self.chunk = self.BYTES // self.CHUNKS
         self.cur = 0
         self.head = 0
@@ -55,7 +57,12 @@ class _StagingRing:
         if n > self.chunk:
             return False
         if n == 0:
-            return out
+            return True
+        with self.lock:
+            self._put(t, out, n)
+        return True
+
+    def _put(self, t: torch.Tensor, out: torch.Tensor, n: int) -> None:
         start = -(-self.head // self.ALIGN) * self.ALIGN
         if start + n > (self.cur + 1) * self.chunk:
             ev = torch.cuda.Event()
@@ -70,18 +77,21 @@ class _StagingRing:
         view = self.buf[start:start + n]
         view.copy_(t.reshape(-1).view(torch.uint8))
         out.view(-1).view(torch.uint8).copy_(view, non_blocking=True)
-        return True
 
 
 _RINGS: dict = {}
+_RINGS_LOCK = threading.Lock()
 
 
 def _ring(dev: torch.device) -> _StagingRing:
     stream = torch.cuda.current_stream(dev)
     key = (dev.index, stream.cuda_stream)
-    ring = _RINGS.get(key)
-    if ring is None:
-        ring = _RINGS[key] = _StagingRing(stream)
+    with _RINGS_LOCK:
+        ring = _RINGS.get(key)
+        if ring is None:
+            ring = _RINGS[key] = _StagingRing(stream)
+    # the live stream object (a handle can be reused by a later stream)
+    ring.stream = stream
     return ring
 
 
