@@ -84,9 +84,20 @@ class RequestTable:
         self.slot_of: dict = {}
         self.resid = np.zeros(64)
         self.seen = np.zeros(64, bool)
+        self._last = (None, None)   # (rids as a tuple, their slots): a batch repeats
 
     def slots(self, rids, create: bool = False) -> np.ndarray:
         """Slot of each rid (-1 for one never measured, unless create)."""
+        # One cached list: slots are only created here, so the cached lookup
+        # is current unless it holds -1 entries and this call creates slots.
+        key = tuple(rids)
+        if key == self._last[0] and (not create or (self._last[1] >= 0).all()):
+            return self._last[1]
+        out = self._lookup(key, create)
+        self._last = (key, out)
+        return out
+
+    def _lookup(self, rids, create: bool) -> np.ndarray:
         out = np.empty(len(rids), np.int64)
         for i, rid in enumerate(rids):
             s = self.slot_of.get(rid, -1)

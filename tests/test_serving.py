@@ -107,8 +107,23 @@ def test_queued_regime_installs_grouped_lpt_only_when_idle():
     h.on_batch_begin([0, 1, 2, 3], kv)
     assert h.order_n == 4
     assert order(p, 4) == SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32),
-                                                  0).tolist()
+                                                  0, block=1).tolist()
     assert ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 4
+
+
+def test_queued_regime_lpt_group_size():
+    # per-item longest-first by default; the reference's grouped form with
+    # lpt_block = 16
+    kv = [int(x) for x in np.random.default_rng(3).integers(16, 4096, 40)]
+    for block in (1, 16):
+        p = plane()
+        h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=100, resident=2, clc="off",
+                                          lpt_block=block), event_factory=lambda: Ev(done=True))
+        h.on_batch_begin(list(range(40)), kv)
+        want = SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32), 0, block=block)
+        assert order(p, 40) == want.tolist(), block
+    assert SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32), 0, block=1).tolist() \
+        != SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32), 0, block=16).tolist()
 
 
 def test_auto_arms_the_queue_only_for_an_uncertain_heavy_tail():
