@@ -1,11 +1,13 @@
 """paged_decode(): one decode step on torch-ROCm tensors through the C ABI
 (`sched_paged_decode` in include/sched_pd.h).
 
-Pool layout (HND pages; the MFMA kernel's layout):
+Pool layout (HND pages):
     k_pool [num_pages, Hkv, page_size, d]    token rows, dims contiguous
-    v_pool [num_pages, Hkv, d, page_size]    d-major ("dmajor", default)
-        or [num_pages, Hkv, page_size, d]    token-major ("tokmajor"; MFMA for
-                                             bf16, VALU for fp8)
+    v_pool [num_pages, Hkv, page_size, d]    token-major ("tokmajor"; what
+                                             kv_cache.PagedKvCache stores)
+        or [num_pages, Hkv, d, page_size]    d-major ("dmajor", build_args'
+                                             default argument)
+Both V layouts run on the MFMA kernel for bf16 / fp16 / fp8 with d 128.
 Any strides are accepted as long as the innermost listed dim is contiguous;
 they are passed to the kernel in elements.
 
