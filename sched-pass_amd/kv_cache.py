@@ -17,6 +17,8 @@ from __future__ import annotations
 
 import ctypes
 
+from collections.abc import MutableMapping
+
 import numpy as np
 import torch
 
@@ -193,6 +195,32 @@ class PageAllocator:
         self._top += pages.size
 
 
+class _Lengths(MutableMapping):
+    """PagedKvCache.lens: request id -> tokens held. A dict-like view of the
+    cache's per-request length array (writes go to the array). Requests come
+    and go through add_request / release."""
+
+    def __init__(self, cache):
+        self._c = cache
+
+    def __getitem__(self, rid):
+        return int(self._c._len[self._c._slot[rid]])
+
+    def __setitem__(self, rid, value):
+        if rid not in self._c._slot:
+            raise KeyError(f"request {rid!r} not in the cache (add_request first)")
+        self._c._len[self._c._slot[rid]] = int(value)
+
+    def __delitem__(self, rid):
+        raise TypeError("release(rid) removes a request")
+
+    def __iter__(self):
+        return iter(self._c._slot)
+
+    def __len__(self):
+        return len(self._c._slot)
+
+
 class PagedKvCache:
     """Pools + allocator + per-request page lists for one layer's KV.
 
@@ -234,30 +262,61 @@ class PagedKvCache:
                                    device=self.device) if fp8 else None
         self.v_scale = torch.zeros_like(self.k_scale) if fp8 else None
         self.allocator = PageAllocator(num_pages)
+        # Per request: its page list (pages[rid]) and, in arrays indexed by a
+        # slot, its token count and page count, so that a step's bookkeeping
+        # over a batch is array arithmetic rather than a loop over requests.
         self.pages: dict = {}
-        self.lens: dict = {}
+        self._slot: dict = {}
+        self._free_slots: list = []
+        self._len = np.zeros(64, np.int64)
+        self._npg = np.zeros(64, np.int64)
+        self.lens = _Lengths(self)
+        self._batch = (None, None)   # (rids as a tuple, their slots): a batch repeats
         self._table = None       # the device block table of the last request list
 
     # -- bookkeeping ----------------------------------------------------------
     def add_request(self, rid) -> None:
         if rid in self.pages:
             raise KeyError(f"request {rid!r} already present")
+        if self._free_slots:
+            slot = self._free_slots.pop()
+        else:
+            slot = len(self._slot)
+            if slot >= self._len.size:
+                self._len = np.concatenate([self._len, np.zeros_like(self._len)])
+                self._npg = np.concatenate([self._npg, np.zeros_like(self._npg)])
+        self._slot[rid] = slot
+        self._len[slot] = 0
+        self._npg[slot] = 0
         self.pages[rid] = []
-        self.lens[rid] = 0
+        self._batch = (None, None)
 
     def release(self, rid) -> None:
         self.allocator.free(self.pages.pop(rid))
-        del self.lens[rid]
+        slot = self._slot.pop(rid)
+        self._len[slot] = 0
+        self._npg[slot] = 0
+        self._free_slots.append(slot)
+        self._batch = (None, None)
         self._table = None
+
+    def _slots(self, rids) -> tuple:
+        """(rids as a tuple, their slots), cached for a repeated list."""
+        key = tuple(rids)
+        if key != self._batch[0]:
+            try:
+                slots = np.fromiter((self._slot[r] for r in key), np.int64, len(key))
+            except KeyError as e:
+                raise KeyError(f"request {e.args[0]!r} not in the cache") from None
+            self._batch = (key, slots)
+        return self._batch
 
     def reserve(self, rids, counts) -> None:
         """Allocate pages so that each request has room for counts[i] more
         tokens; all or nothing."""
-        rids = list(rids)
-        lens = np.fromiter((self.lens[r] for r in rids), np.int64, len(rids))
-        held = np.fromiter((len(self.pages[r]) for r in rids), np.int64, len(rids))
-        want = -(-(lens + np.asarray(counts, np.int64)) // self.page_size)
-        need = np.maximum(want - held, 0)
+        key, s = self._slots(rids)
+        want = -(-(self._len[s] + np.asarray(counts, np.int64)) // self.page_size)
+        need = np.maximum(want - self._npg[s], 0)
         total = int(need.sum())
         if total > self.allocator.num_free:
             raise OutOfPages(f"need {total} pages, {self.allocator.num_free} free")
@@ -267,8 +326,9 @@ class PagedKvCache:
         at = 0
         for i in np.nonzero(need)[0]:       # only the requests that cross a page
             k = int(need[i])
-            self.pages[rids[i]].extend(fresh[at:at + k])
+            self.pages[key[i]].extend(fresh[at:at + k])
             at += k
+        np.add.at(self._npg, s, need)
 
     # -- tables ---------------------------------------------------------------
     def block_table(self, rids):
@@ -282,11 +342,11 @@ class PagedKvCache:
         stream-ordered after the launches that read the previous contents. A
         different list, a request that outgrew the width, or a released page
         rebuilds the table (width with headroom)."""
-        rids = list(rids)
-        counts = np.fromiter((len(self.pages[r]) for r in rids), np.int64, len(rids))
-        ctx = np.fromiter((self.lens[r] for r in rids), np.int32, len(rids))
+        key, s = self._slots(rids)
+        rids = key
+        counts = self._npg[s]
+        ctx = self._len[s].astype(np.int32)
         t = self._table
-        key = tuple(rids)
         if (t is None or t["key"] != key or t["counts"].size != counts.size
                 or (counts.size and (counts.max() > t["width"]
                                      or (counts < t["counts"]).any()))):
@@ -307,8 +367,9 @@ class PagedKvCache:
                     rows.extend([i] * (hi - lo))
                     cols.extend(range(lo, hi))
                     vals.extend(self.pages[rids[i]][lo:hi])
-                idx = sched_pd.upload(np.array([rows, cols], np.int64), self.device)
-                t["dev"][idx[0], idx[1]] = sched_pd.upload(np.array(vals, np.int32), self.device)
+                # rows, columns and values in one upload
+                upd = sched_pd.upload(np.array([rows, cols, vals], np.int64), self.device)
+                t["dev"][upd[0], upd[1]] = upd[2].to(torch.int32)
                 t["counts"] = counts
         return t["dev"], sched_pd.upload(ctx, self.device)
 
@@ -327,29 +388,35 @@ class PagedKvCache:
     def append(self, rids, k_new, v_new, counts=None, errors=None) -> None:
         """Append counts[i] rows (default 1 each) of k_new / v_new [T, Hkv, d]
         to request rids[i], rows in request order."""
-        counts = [1] * len(rids) if counts is None else [int(c) for c in counts]
-        if len(set(rids)) != len(rids):
+        key, s = self._slots(rids)
+        counts = (np.ones(len(key), np.int64) if counts is None
+                  else np.asarray([int(c) for c in counts], np.int64))
+        if counts.size != len(key):
+            raise ValueError(f"{counts.size} counts for {len(key)} requests")
+        if np.unique(s).size != s.size:
             raise ValueError("a request appears twice in one append")
-        if any(c < 0 for c in counts) or sum(counts) != k_new.shape[0]:
-            raise ValueError(f"counts sum to {sum(counts)}, sources have {k_new.shape[0]} rows")
-        held = {rid: len(self.pages[rid]) for rid in rids}
-        self.reserve(rids, counts)
+        if (counts < 0).any() or int(counts.sum()) != k_new.shape[0]:
+            raise ValueError(f"counts sum to {int(counts.sum())}, sources have "
+                             f"{k_new.shape[0]} rows")
+        held = self._npg[s].copy()
+        self.reserve(key, counts)
         try:
-            for rid, n in zip(rids, counts):
-                self.lens[rid] += n
-            bt, ctx = self.block_table(rids)
-            app = np.zeros(len(rids) + 1, dtype=np.int32)
+            self._len[s] += counts
+            bt, ctx = self.block_table(key)
+            app = np.zeros(len(key) + 1, dtype=np.int32)
             app[1:] = np.cumsum(counts)
             append(k_new, v_new, sched_pd.upload(app, self.device), ctx, self.k_pool,
                    self.v_pool, bt, v_layout=self.v_layout, k_scale=self.k_scale,
                    v_scale=self.v_scale,
-                   max_append=max(counts + [0]), errors=errors)
+                   max_append=int(counts.max()) if counts.size else 0, errors=errors)
         except Exception:
             # a rejected launch leaves the cache as it was
-            for rid, n in zip(rids, counts):
-                self.lens[rid] -= n
-                self.allocator.free(self.pages[rid][held[rid]:])
-                del self.pages[rid][held[rid]:]
+            self._len[s] -= counts
+            for i in np.nonzero(self._npg[s] != held)[0]:
+                rid = key[i]
+                self.allocator.free(self.pages[rid][held[i]:])
+                del self.pages[rid][held[i]:]
+            self._npg[s] = held
             self._table = None
             raise
 

@@ -380,3 +380,34 @@ def test_cache_v_layout_choice():
     assert tuple(c.v_pool.shape) == (4, 2, 8, 32)
     with pytest.raises(ValueError):
         PagedKvCache(4, 2, 8, page_size=32, device="cpu", v_layout="hnd")
+
+
+def test_lengths_view_slots_and_failed_append_rollback():
+    """cache.lens reads and writes the per-request arrays; released slots are
+    reused; an append whose launch is rejected (here: host pools) leaves
+    lengths, page lists and the allocator as they were."""
+    c = PagedKvCache(64, 2, 8, page_size=4, dtype=torch.bfloat16, device="cpu")
+    for rid in ("a", "b", "c"):
+        c.add_request(rid)
+    c.reserve(["a", "b", "c"], [6, 1, 9])
+    c.lens.update(a=6, b=1, c=9)
+    assert dict(c.lens) == {"a": 6, "b": 1, "c": 9} and len(c.lens) == 3
+    with pytest.raises(KeyError):
+        c.lens["zz"] = 3
+    with pytest.raises(TypeError):
+        del c.lens["a"]
+    before = ({r: list(p) for r, p in c.pages.items()}, dict(c.lens), c.allocator.num_free)
+    k = torch.zeros(3 + 4 + 8, 2, 8, dtype=torch.bfloat16)
+    with pytest.raises(Exception):
+        c.append(["a", "b", "c"], k, k, [3, 4, 8])
+    assert ({r: list(p) for r, p in c.pages.items()}, dict(c.lens),
+            c.allocator.num_free) == before
+    with pytest.raises(ValueError):
+        c.append(["a", "a"], k[:2], k[:2], [1, 1])
+    c.release("b")
+    c.add_request("d")                      # takes b's slot
+    assert c.lens["d"] == 0 and c.pages["d"] == [] and "b" not in c.lens
+    c.reserve(["d", "a"], [5, 2])
+    c.lens["d"] = 5
+    bt, ctx = c.block_table(["d", "a"])
+    assert ctx.tolist() == [5, 6] and bt[0, :2].tolist() == c.pages["d"]
