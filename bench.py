@@ -597,6 +597,15 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
         out_ = {}
         for name, f in (("append", fa), ("decode", fd), ("step", both)):
             out_[name + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+        if layout == "tokmajor" and k_pool.dtype in (torch.bfloat16, torch.float16):
+            # the same step as one launch (the decode writes the token first)
+            ff = lambda i: sched_pd.launch_with_append(dec[i % tables], ins[i % tables],  # noqa: E731
+                                                       stream)
+            for i in range(2 * tables):
+                ff(i)
+            torch.cuda.synchronize()
+            out_["fused_step_us"] = round(min(time_region(ff, 20, stream) for _ in range(3)) * 1e3,
+                                          2)
         return out_
 
     res = {}
@@ -997,11 +1006,18 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
     requests of the Llama-3-8B shape (bf16, Hq 32 / Hkv 8, page 16) with
     lognormal contexts (median 1024, sigma 1.2); per step the cache writer
     appends one token per request, then the decode runs over 128-page split
-    tiles. Modes: stock (the same split plan, no lever tables), the serving
+    tiles; the step is PagedKvCache.decode_step (the append fused into the
+    decode: one launch per step). Modes: stock (the same split plan, no lever
+    tables), stock as two launches (the writer, then the decode), the serving
     hooks observing only (bind, probe the timer 1 step in 8, never change the
     schedule), and the hooks enforcing (controller orders, queue arming,
-    re-plan every 8 steps). Wall-clock per step with the host work the hooks
-    add, and GPU time between events around the loop."""
+    re-plan every 8 steps). Reported per mode: wall
+    clock per step, GPU time between events around the loop, the host time
+    of the plan (stock: the split plan; hooks: begin + end), and the decode
+    launches' own GPU time (each step's launch re-run back to back in a
+    second pass; for the fused mode the fused launch, which rewrites the
+    same token): the last is what the levers change, the plan time is what
+    they cost the host."""
     import time
     import numpy as np
     import kv_cache
@@ -1010,7 +1026,7 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
     R, hkv, hq, d, ps, tp = 256, 8, 32, 128, 16, 128
     rng = np.random.default_rng(0)
     lens = workloads.lognormal_ctx(R, 1024, 1.2, 16, 32768, rng)
-    grow = 3 * (2 * steps + warm) + 1     # tokens appended over the three modes
+    grow = 2 * steps + warm + 1           # tokens one mode appends (each starts over)
     npages = int((-(-(lens + grow) // ps)).sum()) + R
     g = torch.Generator(device="cuda").manual_seed(9)
     cache = kv_cache.PagedKvCache(npages, hkv, d, ps, dtype=torch.bfloat16)
@@ -1036,29 +1052,46 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
                                                  out=out, v_layout=cache.v_layout))
     res = {"requests": R, "steps": steps, "tile_pages": tp, "resident": occ * cu}
     stream = torch.cuda.current_stream()
-    for mode in ("stock", "observe", "enforce"):
+    start = [cache.lens[r] for r in rids]
+    for mode in ("stock_two_launches", "stock", "observe", "enforce"):
+        cache.truncate(rids, start)       # every mode decodes the same contexts
         hooks = None
-        if mode != "stock":
+        fused = mode != "stock_two_launches"
+        if mode in ("observe", "enforce"):
             plane = SchedPlane(max_tasks=16384)
             hooks = ServingHooks(plane, hkv, HookConfig(observe_only=mode == "observe",
                                                         tile_pages=tp, resident=occ * cu))
 
         host = [0.0]
+        inflight = []
 
         def step(ev=None):
-            cache.append(rids, k1, v1)
-            now = [cache.lens[r] for r in rids]
+            # at most two steps in flight, as an engine that reads a step's
+            # sampled tokens one step later keeps (an unbounded run-ahead
+            # fills the device queue and stalls in ways no engine sees)
+            if len(inflight) >= 2:
+                inflight.pop(0).synchronize()
+            if not fused:
+                cache.append(rids, k1, v1)
+            # the plan is built from the lengths the decode will see
+            now = [cache.lens[r] + (1 if fused else 0) for r in rids]
             h0 = time.perf_counter()
             if hooks is None:
                 launch = {"tiles": sched_pd.plan_tiles(now, ps, tp, hkv), "tile_pages": tp}
             else:
                 launch = hooks.on_batch_begin(rids, now)
             host[0] += time.perf_counter() - h0
-            cache.decode(q, rids, out=out, **launch)
+            if fused:
+                cache.decode_step(q, rids, k1, v1, out=out, **launch)
+            else:
+                cache.decode(q, rids, out=out, **launch)
             h0 = time.perf_counter()
             if hooks is not None:
                 hooks.on_batch_end()
             host[0] += time.perf_counter() - h0
+            done = torch.cuda.Event()
+            done.record(stream)
+            inflight.append(done)
             if ev is not None:
                 # the step's decode again, 1 + 3 times with the same tables
                 # (timer gate already off): the last 3 back to back between
@@ -1066,10 +1099,18 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
                 bt, ctx = cache.block_table(rids)
                 a = sched_pd.build_args(q, cache.k_pool, cache.v_pool, bt, ctx, out=out,
                                         v_layout=cache.v_layout, **launch)
-                sched_pd.launch(a)
+                run = lambda: sched_pd.launch(a)  # noqa: E731
+                if fused:
+                    # the fused launch rewrites the step's token in place: the
+                    # same bytes every time
+                    app = kv_cache.build_append_args(
+                        k1, v1, torch.arange(R + 1, dtype=torch.int32, device="cuda"), ctx,
+                        cache.k_pool, cache.v_pool, bt, v_layout=cache.v_layout, max_append=1)
+                    run = lambda: sched_pd.launch_with_append(a, app)  # noqa: E731
+                run()
                 ev[0].record(stream)
                 for _ in range(3):
-                    sched_pd.launch(a)
+                    run()
                 ev[1].record(stream)
         for _ in range(warm):
             step()
@@ -1101,7 +1142,7 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
         if hooks is not None:
             res[mode]["probes_folded"] = hooks.probes_folded
             res[mode]["hook_errors"] = hooks.hook_errors
-    for mode in ("observe", "enforce"):
+    for mode in ("stock_two_launches", "observe", "enforce"):
         res[mode]["vs_stock_pct"] = round(
             100 * (res[mode]["wall_ms_per_step"] - res["stock"]["wall_ms_per_step"])
             / res["stock"]["wall_ms_per_step"], 2)

@@ -38,6 +38,12 @@ struct KParams {
   uint32_t *ws_count;  // per-task arrival counters
   float *ws_ml;        // per-work-item (m, l) per head
   void *ws_acc;        // per-work-item partial accumulators
+  // Fused append (sched_paged_decode_append; nullptr = none): request r's
+  // new token is source row r, written into the cache before it is read.
+  const void *app_k;
+  const void *app_v;
+  int64_t app_ts, app_hs; // source strides (elements): row, kv-head
+  uint32_t app_f32;       // fp32 source rows (else the cache's 16-bit type)
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();

@@ -581,6 +581,37 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
   }
 }
 
+// Fused append: the K and V rows of request r's new token (source row r,
+// kv-head h) into slot `slot` of page `page`, in the cache's 16-bit type (an
+// fp32 source rounds to nearest even); lane l writes dims 2l, 2l+1 of both
+// rows (head dim 128). Called by the one wave that streams that page, which
+// waits for its stores before it loads anything, so it reads the token back
+// from the cache like every other token (each page of an item is streamed
+// by exactly one wave, and no other workgroup reads this (page, kv-head)).
+template <bool F16>
+__device__ __forceinline__ void append_token(const KParams &P, uint32_t r, uint32_t h,
+                                             int64_t page, uint32_t slot, uint32_t lane) {
+  const uint32_t j = 2u * lane;
+  const int64_t src = (int64_t)r * P.app_ts + (int64_t)h * P.app_hs + j;
+  uint32_t kw, vw;
+  if (P.app_f32) {
+    const float *ks = static_cast<const float *>(P.app_k) + src;
+    const float *vs = static_cast<const float *>(P.app_v) + src;
+    kw = F16 ? pack_f16_rne(ks[0], ks[1]) : pack_bf16_rne(ks[0], ks[1]);
+    vw = F16 ? pack_f16_rne(vs[0], vs[1]) : pack_bf16_rne(vs[0], vs[1]);
+  } else {
+    kw = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(P.app_k) + src);
+    vw = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(P.app_v) + src);
+  }
+  uint16_t *kd = static_cast<uint16_t *>(const_cast<void *>(P.k_pool)) + page * P.kps +
+                 (int64_t)h * P.khs + (int64_t)slot * P.kts + j;
+  uint16_t *vd = static_cast<uint16_t *>(const_cast<void *>(P.v_pool)) + page * P.vps +
+                 (int64_t)h * P.vhs + (int64_t)slot * P.vts + j;
+  *reinterpret_cast<uint32_t *>(kd) = kw;
+  *reinterpret_cast<uint32_t *>(vd) = vw;
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
 // An urgent task's stream at the launch's ring depth: any depth in
 // [DLO, DHI] the host accepted (SchedDecodeArgs.pf_dist); 0 = DHI. Every
 // depth computes the same pages in the same order, so the bits do not change.
@@ -645,6 +676,20 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       T.p1 = R.p1;
     }
     T.w = w;
+    if constexpr (!FP8 && !LINEAR && VT) {
+      // fused append: the item holding the new token writes it (in the
+      // wave that streams its page) before streaming
+      if (P.app_k != nullptr && T.n > 0u) {
+        const uint32_t pos = T.n - 1u, pg = pos / P.ps;
+        if (P.tiles == nullptr || chunk == pg / P.tile_pages) {
+          const uint32_t rel = (PG ? pos / 16u : pg) - T.p0;
+          if (rel % (uint32_t)NW == w)
+            append_token<F16>(P, T.r, T.h,
+                              __builtin_amdgcn_readfirstlane(P.bt[T.row + pg]), pos % P.ps,
+                              lane);
+        }
+      }
+    }
     T.kbase = static_cast<const uint8_t *>(P.k_pool) + (int64_t)c16 * P.kts * EB + 16u * g4;
     // fp8: whole row 16*g4 + c16; bf16: half g4/2 of row 16*(g4%2) + c16;
     // token-major: dims 8*c16.. of token 4*g4 (then rows 4*g4 + 1..3)

@@ -12,6 +12,7 @@
 #include <mutex>
 
 #include "kernel_set.h"
+#include "../../include/sched_kv.h"
 #include "rt_internal.h"
 
 SCHED_PD_DECLARE_ALL_KERNELS
@@ -511,12 +512,31 @@ static uint32_t resident_blocks(const void *fn, int block) {
   return r;
 }
 
-int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
+// The step's new tokens for a fused append (sched_paged_decode_append).
+struct AppendRows {
+  const void *k, *v;
+  int64_t ts, hs;
+  bool f32;
+};
+
+static int launch_decode(const SchedDecodeArgs *a, const AppendRows *app, void *stream) {
   KParams kp;
   Selected sel;
   int rc = prepare(a, &kp, &sel);
   if (rc)
     return rc;
+  if (app != nullptr) {
+    if (sel.mfma != 1)
+      return set_error(hipErrorInvalidValue,
+                       "fused append: these arguments select the %s kernel; the append is "
+                       "fused into the MFMA kernel only (call sched_kv_append, then "
+                       "sched_paged_decode)", sel.mfma == 2 ? "one-wave-per-task" : "VALU");
+    kp.app_k = app->k;
+    kp.app_v = app->v;
+    kp.app_ts = app->ts;
+    kp.app_hs = app->hs;
+    kp.app_f32 = app->f32 ? 1u : 0u;
+  }
   const uint32_t nitems = kp.L.nitems;
   if (nitems == 0 || kp.ntasks == 0)
     return 0;
@@ -540,6 +560,60 @@ int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
   if (a->flags & SCHED_PD_FLAG_RT_TABLES)
     return rt_after_launch(stream);
   return 0;
+}
+
+int sched_paged_decode(const SchedDecodeArgs *a, void *stream) {
+  return launch_decode(a, nullptr, stream);
+}
+
+int sched_paged_decode_append(const SchedDecodeArgs *a, const SchedKvAppendArgs *w,
+                              void *stream) {
+  if (a == nullptr || w == nullptr)
+    return set_error(hipErrorInvalidValue, "args is NULL");
+  if (w->abi_version != SCHED_KV_ABI_VERSION)
+    return set_error(hipErrorInvalidValue, "append args: abi_version %u, expected %u",
+                     w->abi_version, SCHED_KV_ABI_VERSION);
+  if (a->mode != SCHED_PD_SOFTMAX || (a->flags & SCHED_PD_FLAG_CTX_IN_PAGES))
+    return set_error(hipErrorInvalidValue,
+                     "fused append: softmax decode with ctx_lens in tokens only");
+  if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_F16)
+    return set_error(hipErrorInvalidValue,
+                     "fused append: bf16 or fp16 caches only (an fp8 cache's scales are "
+                     "updated by sched_kv_append)");
+  if (w->kv_dtype != a->kv_dtype || (w->src_dtype != a->kv_dtype && w->src_dtype != SCHED_PD_F32))
+    return set_error(hipErrorInvalidValue,
+                     "fused append: the cache dtypes differ, or the source is neither fp32 nor "
+                     "the cache's dtype");
+  if (a->head_dim != 128 || a->v_dim_stride != 1 || a->v_tok_stride % 2 ||
+      a->k_tok_stride % 2 || a->k_page_stride % 2 || a->k_head_stride % 2 ||
+      a->v_page_stride % 2 || a->v_head_stride % 2)
+    return set_error(hipErrorInvalidValue,
+                     "fused append: head dim 128, token-major V (v_dim_stride 1) and even "
+                     "strides only");
+  if (w->num_requests != a->num_requests || w->num_kv_heads != a->num_kv_heads ||
+      w->head_dim != a->head_dim || w->page_size != a->page_size ||
+      w->num_tokens != w->num_requests)
+    return set_error(hipErrorInvalidValue,
+                     "fused append: one token per request (num_tokens == num_requests) of the "
+                     "decode's shape");
+  if (w->k_pool != a->k_pool || w->v_pool != a->v_pool || w->ctx_lens != a->ctx_lens ||
+      w->block_table != a->block_table || w->page_indptr != a->page_indptr ||
+      (a->page_indptr == nullptr && w->bt_stride != a->bt_stride) ||
+      w->k_page_stride != a->k_page_stride || w->k_head_stride != a->k_head_stride ||
+      w->k_tok_stride != a->k_tok_stride || w->v_page_stride != a->v_page_stride ||
+      w->v_head_stride != a->v_head_stride || w->v_tok_stride != a->v_tok_stride ||
+      w->v_dim_stride != a->v_dim_stride)
+    return set_error(hipErrorInvalidValue,
+                     "fused append: pools, strides, page table and ctx_lens must be the "
+                     "decode's");
+  if (w->k_src == nullptr || w->v_src == nullptr || w->src_tok_stride % 2 ||
+      w->src_head_stride % 2 || (reinterpret_cast<uintptr_t>(w->k_src) & 3u) ||
+      (reinterpret_cast<uintptr_t>(w->v_src) & 3u))
+    return set_error(hipErrorInvalidValue,
+                     "fused append: source rows must be 4-byte aligned with even strides");
+  AppendRows app{w->k_src, w->v_src, w->src_tok_stride, w->src_head_stride,
+                 w->src_dtype == SCHED_PD_F32};
+  return launch_decode(a, &app, stream);
 }
 
 int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a) {

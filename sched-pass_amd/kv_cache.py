@@ -300,6 +300,23 @@ class PagedKvCache:
         self._batch = (None, None)
         self._table = None
 
+    def truncate(self, rids, lens) -> None:
+        """Drop request rids[i]'s tokens past lens[i] (at most its length) and
+        free the pages they alone used (a rejected speculation, or a replay
+        from an earlier state)."""
+        key, s = self._slots(rids)
+        new = np.asarray(lens, np.int64)
+        if new.size != len(key) or (new < 0).any() or (new > self._len[s]).any():
+            raise ValueError("truncate: lengths must be within the requests' lengths")
+        keep = -(-new // self.page_size)
+        for i in np.nonzero(keep < self._npg[s])[0]:
+            pages = self.pages[key[i]]
+            self.allocator.free(pages[keep[i]:])
+            del pages[keep[i]:]
+        self._len[s] = new
+        self._npg[s] = np.minimum(self._npg[s], keep)
+        self._table = None
+
     def _slots(self, rids) -> tuple:
         """(rids as a tuple, their slots), cached for a repeated list."""
         key = tuple(rids)
@@ -367,9 +384,10 @@ class PagedKvCache:
                     rows.extend([i] * (hi - lo))
                     cols.extend(range(lo, hi))
                     vals.extend(self.pages[rids[i]][lo:hi])
-                # rows, columns and values in one upload
-                upd = sched_pd.upload(np.array([rows, cols, vals], np.int64), self.device)
-                t["dev"][upd[0], upd[1]] = upd[2].to(torch.int32)
+                # rows, columns and values in one int32 upload (no conversion
+                # kernel: int32 indices index directly)
+                upd = sched_pd.upload(np.array([rows, cols, vals], np.int32), self.device)
+                t["dev"][upd[0], upd[1]] = upd[2]
                 t["counts"] = counts
         return t["dev"], sched_pd.upload(ctx, self.device)
 
@@ -419,6 +437,60 @@ class PagedKvCache:
             self._npg[s] = held
             self._table = None
             raise
+
+    def decode_step(self, q, rids, k_new, v_new, **kw):
+        """One serving step: append each request's new token (k_new / v_new
+        [R, Hkv, d], row i for rids[i]) and decode over the contexts that now
+        hold it. A bf16 / fp16 cache with token-major V and head dim 128 does
+        both in one launch (the decode writes the token into its page before
+        reading it); other caches run the writer, then the decode. Keyword
+        arguments are those of decode() (`out`, `plane`, `tiles`, ...); a
+        split plan must be built from the lengths after the append."""
+        # the MFMA kernel's shapes (16-bit Q of the cache's type, 1..16 q-heads
+        # per kv-head, head dim 128)
+        G = q.shape[1] // self.num_kv_heads if q.shape[1] % self.num_kv_heads == 0 else 0
+        fusable = (self.dtype in (torch.bfloat16, torch.float16) and q.dtype == self.dtype
+                   and 1 <= G <= 16 and self.v_layout == "tokmajor" and self.head_dim == 128
+                   and self.page_size in (16, 32, 64, 128, 256)
+                   and kw.get("mode", abi.SOFTMAX) == abi.SOFTMAX
+                   and not (kw.get("flags", 0) & (abi.FLAG_FORCE_VALU | abi.FLAG_CTX_IN_PAGES)))
+        if not fusable:
+            self.append(rids, k_new, v_new)
+            return self.decode(q, rids, **kw)
+        key, s = self._slots(rids)
+        if k_new.shape[0] != len(key) or v_new.shape[0] != len(key):
+            raise ValueError(f"{k_new.shape[0]} source rows for {len(key)} requests")
+        if np.unique(s).size != s.size:
+            raise ValueError("a request appears twice in one step")
+        held = self._npg[s].copy()
+        self.reserve(key, np.ones(len(key), np.int64))
+        try:
+            self._len[s] += 1
+            bt, ctx = self.block_table(key)
+            kw.setdefault("v_layout", self.v_layout)
+            out = kw.pop("out", None)
+            if out is None:
+                dt = kw.pop("out_dtype", None) or q.dtype
+                out = torch.empty(len(key), q.shape[1], self.head_dim, dtype=dt,
+                                  device=self.device)
+            args = sched_pd.build_args(q, self.k_pool, self.v_pool, bt, ctx, out=out, **kw)
+            if getattr(self, "_app_indptr", None) is None or \
+                    self._app_indptr.numel() != len(key) + 1:
+                self._app_indptr = torch.arange(len(key) + 1, dtype=torch.int32,
+                                                device=self.device)
+            app = build_append_args(k_new, v_new, self._app_indptr, ctx, self.k_pool,
+                                    self.v_pool, bt, v_layout=self.v_layout, max_append=1)
+            sched_pd.launch_with_append(args, app, kw.get("stream"))
+        except Exception:
+            self._len[s] -= 1
+            for i in np.nonzero(self._npg[s] != held)[0]:
+                rid = key[i]
+                self.allocator.free(self.pages[rid][held[i]:])
+                del self.pages[rid][held[i]:]
+            self._npg[s] = held
+            self._table = None
+            raise
+        return out
 
     def decode(self, q, rids, **kw):
         """One decode step over the requests' current contexts."""

@@ -148,6 +148,8 @@ SIGNATURES = {
     "sched_pd_last_error": (ctypes.c_char_p, []),
     "sched_kv_default_args": (None, [ctypes.POINTER(SchedKvAppendArgs)]),
     "sched_kv_append": (ctypes.c_int, [ctypes.POINTER(SchedKvAppendArgs), _p]),
+    "sched_paged_decode_append": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs),
+                                                 ctypes.POINTER(SchedKvAppendArgs), _p]),
     "launch_paged_softmax": (None, [_p, _p, _p, _p, _p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, _p]),
     "paged_softmax_occupancy": (ctypes.c_int, []),

@@ -32,14 +32,17 @@ if hasattr(torch, "float8_e4m3fn"):
 
 
 class _StagingRing:
-    """Pinned host ring for the small uploads of one stream (page-table rows,
-    context lengths, split plans, orders): a copy into the ring, then an
-    asynchronous copy to the device on the stream, with no host allocation per
-    upload. The ring is cut into CHUNKS chunks; leaving a chunk records an
-    event on the stream after the copies out of it, and a chunk is written
-    again only once the event of its previous lap has completed (a wait only
-    when the device lags a whole ring behind the host)."""
-    BYTES = 4 << 20
+    """Pinned host ring for the uploads of one stream (page-table rows and
+    updates, context lengths, split plans, orders): a copy into the ring,
+    then an asynchronous copy to the device on the stream, with no host
+    allocation per upload. The ring is cut into CHUNKS chunks. An upload
+    that does not fit in the rest of the current chunk starts at the next
+    chunk boundary and may span several chunks. Leaving a chunk, and
+    finishing an upload that spans chunks, records an event on the stream
+    after the copies out of them; a chunk is written again only once the
+    event of its previous lap has completed (a wait only when the device lags
+    a whole ring behind the host)."""
+    BYTES = 16 << 20
     CHUNKS = 16
     ALIGN = 256
 
@@ -56,7 +59,7 @@ class _StagingRing:
         """Stage contiguous host `t` and copy it into contiguous device `out`
         (same bytes); False if `t` is too large for the ring."""
         n = t.numel() * t.element_size()
-        if n > self.chunk:
+        if n > (self.CHUNKS - 1) * self.chunk:
             return False
         if n == 0:
             return True
@@ -64,21 +67,38 @@ class _StagingRing:
             self._put(t, out, n)
         return True
 
+    def _enter(self, c: int) -> None:
+        if self.done[c] is not None:
+            self.done[c].synchronize()
+            self.done[c] = None
+
     def _put(self, t: torch.Tensor, out: torch.Tensor, n: int) -> None:
         start = -(-self.head // self.ALIGN) * self.ALIGN
+        span = None
         if start + n > (self.cur + 1) * self.chunk:
             ev = torch.cuda.Event()
             ev.record(self.stream)
             self.done[self.cur] = ev
-            self.cur = (self.cur + 1) % self.CHUNKS
-            start = self.cur * self.chunk
-            if self.done[self.cur] is not None:
-                self.done[self.cur].synchronize()
-                self.done[self.cur] = None
+            k = -(-n // self.chunk)                 # chunks the upload covers
+            c0 = self.cur + 1
+            if c0 + k > self.CHUNKS:
+                c0 = 0
+            for c in range(c0, c0 + k):
+                self._enter(c)
+            self.cur = c0 + k - 1
+            start = c0 * self.chunk
+            if k > 1:
+                span = range(c0, c0 + k - 1)
         self.head = start + n
         view = self.buf[start:start + n]
         view.copy_(t.reshape(-1).view(torch.uint8))
         out.view(-1).view(torch.uint8).copy_(view, non_blocking=True)
+        if span is not None:
+            # the chunks before the last one are left now: mark them
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+            for c in span:
+                self.done[c] = ev
 
 
 _RINGS: dict = {}
@@ -433,6 +453,20 @@ def launch(args: abi.SchedDecodeArgs, stream=None) -> None:
     rc = lib.sched_paged_decode(ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
     if rc != 0:
         raise RuntimeError(f"sched_paged_decode failed ({rc}): {abi.last_error()}")
+
+
+def launch_with_append(args: abi.SchedDecodeArgs, append_args, stream=None) -> None:
+    """One launch that writes each request's new token (the one-token-per-
+    request append `append_args`, a SchedKvAppendArgs) and decodes `args`
+    over contexts that include it (sched_paged_decode_append): bf16 / fp16
+    caches with token-major V on the MFMA kernel. Raises RuntimeError with
+    the library's message for anything else."""
+    lib = abi.load_library()
+    s = torch.cuda.current_stream() if stream is None else stream
+    rc = lib.sched_paged_decode_append(ctypes.byref(args), ctypes.byref(append_args),
+                                       ctypes.c_void_p(s.cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"sched_paged_decode_append failed ({rc}): {abi.last_error()}")
 
 
 def paged_decode(q, k_pool, v_pool, block_table, ctx_lens, *, out=None,

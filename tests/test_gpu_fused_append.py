@@ -1,0 +1,127 @@
+"""The fused append + decode step (sched_paged_decode_append through
+PagedKvCache.decode_step) against the writer followed by the decode on a
+second cache with the same contents: pools and outputs bitwise equal, over a
+multi-step loop with tokens that open new pages, for bf16 and fp16 caches,
+16- and 64-token pages, 1 and 4 q-heads per kv-head, fp32 and 16-bit source
+rows, with split tiles, the ticket queue and pi; and the oracle on the
+result. Caches the fused path does not take (fp8, d-major V) fall back to
+the two launches with the same result; a direct fused launch on them is
+refused."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sched_abi as abi
+import sched_pd
+from kv_cache import PagedKvCache, build_append_args
+from parity import TOL_BF16, par_err
+from sched_rt import SchedPlane
+
+pytestmark = pytest.mark.gpu
+
+HKV, D = 2, 128
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib(schedlib):
+    torch.cuda.init()
+    return schedlib
+
+
+def make_pair(dtype, ps, lens, v_layout="tokmajor", seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    R = len(lens)
+    npages = int(sum(-(-(n + 8) // ps) for n in lens)) + R + 4
+    caches = [PagedKvCache(npages, HKV, D, ps, dtype=dtype, v_layout=v_layout) for _ in range(2)]
+    T = int(sum(lens))
+    src = torch.float32 if dtype == torch.float8_e4m3fn else dtype
+    k = (torch.randn(T, HKV, D, device="cuda", generator=g) / D ** 0.5).to(src)
+    v = (torch.randn(T, HKV, D, device="cuda", generator=g) / D ** 0.5).to(src)
+    for c in caches:
+        for r in range(R):
+            c.add_request(r)
+        c.append(list(range(R)), k, v, list(lens))
+    return caches, g
+
+
+def same(a, b):
+    return bool(torch.equal(a.view(torch.uint8), b.view(torch.uint8)))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ps", [16, 64])
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("src32", [False, True])
+def test_fused_step_equals_append_then_decode(dtype, ps, G, src32):
+    # lengths just below, at and past page boundaries, so steps open pages
+    lens = [1, 15, 16, 17, 31, 47, 63, 64, 65, 100, 127, 200]
+    (fa, sep), g = make_pair(dtype, ps, lens, seed=ps + G)
+    R = len(lens)
+    rids = list(range(R))
+    q = (torch.randn(R, HKV * G, D, device="cuda", generator=g) / D ** 0.5).to(dtype)
+    for step in range(5):
+        st = torch.float32 if src32 else dtype
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(st)
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(st)
+        o_fused = fa.decode_step(q, rids, k1, v1)
+        sep.append(rids, k1, v1)
+        o_sep = sep.decode(q, rids)
+        torch.cuda.synchronize()
+        assert same(o_fused, o_sep), step
+        assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
+        assert [fa.lens[r] for r in rids] == [sep.lens[r] for r in rids]
+    bt, ctx = fa.block_table(rids)
+    ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor")
+    assert par_err(o_fused.float().cpu(), ref, f"fused {dtype} p{ps} G{G}") <= TOL_BF16
+
+
+def test_fused_step_with_tiles_queue_and_pi():
+    lens = [int(x) for x in np.random.default_rng(2).integers(1, 900, 40)]
+    (fa, sep), g = make_pair(torch.bfloat16, 16, lens, seed=3)
+    R = len(lens)
+    rids = list(range(R))
+    q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    tp = 8
+    for step in range(4):
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        after = [fa.lens[r] + 1 for r in rids]          # plan from the post-append lengths
+        tiles = sched_pd.plan_tiles(after, 16, tp, HKV)
+        nt = tiles.shape[0]
+        plane = SchedPlane(max_tasks=max(nt, R * HKV))
+        plane.install_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32), nt)
+        plane.set_num_tasks(nt)
+        plane.push()
+        plane.reset_queue(7)
+        o_fused = fa.decode_step(q, rids, k1, v1, tiles=tiles, tile_pages=tp, plane=plane,
+                                 workers=7)
+        sep.append(rids, k1, v1)
+        o_sep = sep.decode(q, rids, tiles=tiles, tile_pages=tp)
+        torch.cuda.synchronize()
+        assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
+        assert same(o_fused, o_sep), step
+
+
+def test_caches_without_the_fused_path_fall_back_and_direct_launch_is_refused():
+    lens = [5, 16, 40]
+    for dtype, layout in ((torch.float8_e4m3fn, "tokmajor"), (torch.bfloat16, "dmajor")):
+        (fa, sep), g = make_pair(dtype, 16, lens, v_layout=layout, seed=7)
+        rids = [0, 1, 2]
+        q = (torch.randn(3, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        k1 = (torch.randn(3, HKV, D, device="cuda", generator=g) / D ** 0.5)
+        k1 = k1 if dtype == torch.float8_e4m3fn else k1.bfloat16()
+        o = fa.decode_step(q, rids, k1, k1)
+        sep.append(rids, k1, k1)
+        o2 = sep.decode(q, rids)
+        torch.cuda.synchronize()
+        assert same(o, o2), (dtype, layout)
+        bt, ctx = fa.block_table(rids)
+        out = torch.empty(3, HKV * 4, D, dtype=torch.bfloat16, device="cuda")
+        args = sched_pd.build_args(q, fa.k_pool, fa.v_pool, bt, ctx, out=out, v_layout=layout,
+                                   k_scale=fa.k_scale, v_scale=fa.v_scale)
+        app = build_append_args(k1, k1, torch.arange(4, dtype=torch.int32, device="cuda"), ctx,
+                                fa.k_pool, fa.v_pool, bt, v_layout=layout, k_scale=fa.k_scale,
+                                v_scale=fa.v_scale, max_append=1)
+        with pytest.raises(RuntimeError, match="fused append"):
+            sched_pd.launch_with_append(args, app)

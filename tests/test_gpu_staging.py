@@ -1,8 +1,8 @@
 """Host-to-device staging of the per-step uploads (sched_pd.upload /
 upload_into through a pinned ring per stream) and the asynchronous timer
-readout: the bytes arrive intact while the ring wraps many times over, with
-the device queue kept busy, on two streams, and for arrays too large for the
-ring."""
+readout: the bytes arrive intact while the ring wraps several times over,
+with uploads inside one chunk and spanning chunks, with the device queue
+kept busy, on two streams, and for arrays too large for the ring."""
 import numpy as np
 import pytest
 import torch
@@ -24,7 +24,8 @@ def test_uploads_survive_ring_wraps():
     sent, got = [], []
     total = 0
     while total < 3 * sched_pd._StagingRing.BYTES:
-        n = int(rng.integers(1, 40000))
+        # mostly small, every 20th spanning several chunks
+        n = int(rng.integers(1, 40000)) if len(sent) % 20 else int(rng.integers(300_000, 900_000))
         a = rng.integers(-2**31, 2**31 - 1, n, dtype=np.int64).astype(np.int32)
         if len(sent) % 25 == 0:
             _busy(1024)
@@ -40,7 +41,7 @@ def test_uploads_survive_ring_wraps():
 def test_upload_on_two_streams_and_large_arrays():
     rng = np.random.default_rng(2)
     s1 = torch.cuda.Stream()
-    big = rng.standard_normal(200_000).astype(np.float32)       # 800 KB: own pinned copy
+    big = rng.standard_normal(5_000_000).astype(np.float32)     # 20 MB: its own pinned copy
     with torch.cuda.stream(s1):
         _busy(2048)
         a1 = [rng.integers(0, 1000, 5000).astype(np.int32) for _ in range(20)]

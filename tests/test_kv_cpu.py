@@ -411,3 +411,22 @@ def test_lengths_view_slots_and_failed_append_rollback():
     c.lens["d"] = 5
     bt, ctx = c.block_table(["d", "a"])
     assert ctx.tolist() == [5, 6] and bt[0, :2].tolist() == c.pages["d"]
+
+
+def test_truncate_frees_the_pages_past_the_new_lengths():
+    c = PagedKvCache(32, 1, 8, page_size=4, dtype=torch.bfloat16, device="cpu")
+    for rid in ("a", "b"):
+        c.add_request(rid)
+    c.reserve(["a", "b"], [10, 3])
+    c.lens.update(a=10, b=3)
+    free0 = c.allocator.num_free
+    pa = list(c.pages["a"])
+    c.truncate(["a", "b"], [5, 3])
+    assert c.lens["a"] == 5 and c.pages["a"] == pa[:2] and c.lens["b"] == 3
+    assert c.allocator.num_free == free0 + 1
+    with pytest.raises(ValueError):
+        c.truncate(["a"], [6])
+    c.truncate(["a"], [0])
+    assert c.pages["a"] == [] and c.allocator.num_free == free0 + 3
+    bt, ctx = c.block_table(["a", "b"])
+    assert ctx.tolist() == [0, 3] and (bt[0] == -1).all()
