@@ -125,3 +125,42 @@ def test_caches_without_the_fused_path_fall_back_and_direct_launch_is_refused():
                                 v_scale=fa.v_scale, max_append=1)
         with pytest.raises(RuntimeError, match="fused append"):
             sched_pd.launch_with_append(args, app)
+
+
+def test_fused_launch_over_a_csr_page_table():
+    """The C entry point with a CSR table (page_indptr + indices), against
+    sched_kv_append + sched_paged_decode over copies of the same pools."""
+    from kv_cache import append as kv_append
+    from kv_cache import ctx_lens_from_last_page_len
+    lens = [3, 16, 33, 70, 129]
+    (c, _), g = make_pair(torch.bfloat16, 16, lens, seed=11)
+    rids = list(range(len(lens)))
+    c.reserve(rids, [1] * len(lens))
+    for r in rids:
+        c.lens[r] += 1                      # room for this step's token
+    indptr, idx, last = c.csr(rids)
+    ctx = ctx_lens_from_last_page_len(indptr, last, 16).to(torch.int32)
+    R = len(lens)
+    q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    app_ptr = torch.arange(R + 1, dtype=torch.int32, device="cuda")
+    outs, pools = [], []
+    for fused in (True, False):
+        kp, vp = c.k_pool.clone(), c.v_pool.clone()
+        out = torch.empty(R, HKV * 4, D, dtype=torch.bfloat16, device="cuda")
+        args = sched_pd.build_args(q, kp, vp, idx, ctx, out=out, page_indptr=indptr,
+                                   v_layout="tokmajor")
+        if fused:
+            app = build_append_args(k1, v1, app_ptr, ctx, kp, vp, idx, page_indptr=indptr,
+                                    v_layout="tokmajor", max_append=1)
+            sched_pd.launch_with_append(args, app)
+        else:
+            kv_append(k1, v1, app_ptr, ctx, kp, vp, idx, page_indptr=indptr,
+                      v_layout="tokmajor", max_append=1)
+            sched_pd.launch(args)
+        torch.cuda.synchronize()
+        outs.append(out)
+        pools.append((kp, vp))
+    assert same(outs[0], outs[1])
+    assert same(pools[0][0], pools[1][0]) and same(pools[0][1], pools[1][1])
