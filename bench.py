@@ -1077,7 +1077,7 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
             now = [cache.lens[r] + (1 if fused else 0) for r in rids]
             h0 = time.perf_counter()
             if hooks is None:
-                launch = {"tiles": sched_pd.plan_tiles(now, ps, tp, hkv), "tile_pages": tp}
+                launch = {"tiles": sched_pd.plan_tiles_host(now, ps, tp, hkv), "tile_pages": tp}
             else:
                 launch = hooks.on_batch_begin(rids, now)
             host[0] += time.perf_counter() - h0

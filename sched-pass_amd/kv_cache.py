@@ -360,17 +360,24 @@ class PagedKvCache:
         different list, a request that outgrew the width, or a released page
         rebuilds the table (width with headroom)."""
         key, s = self._slots(rids)
-        rids = key
+        bt, ctx, _ = self._table_step(key, s)
+        return bt, ctx
+
+    def _table_step(self, key, s, extra=()):
+        """block_table() for the batch (key, s), with the host int32 arrays
+        `extra` uploaded in the same copy as the lengths and the table
+        update; returns (table, ctx_lens, [extra on the device])."""
         counts = self._npg[s]
         ctx = self._len[s].astype(np.int32)
         t = self._table
+        parts, upd_n = [ctx], 0
         if (t is None or t["key"] != key or t["counts"].size != counts.size
                 or (counts.size and (counts.max() > t["width"]
                                      or (counts < t["counts"]).any()))):
             width = max(int(counts.max()) if counts.size else 1, 1)
             width = -(-(width + width // 4 + 1) // 64) * 64     # headroom for growth
-            bt = np.full((len(rids), width), -1, dtype=np.int32)
-            for i, r in enumerate(rids):
+            bt = np.full((len(key), width), -1, dtype=np.int32)
+            for i, r in enumerate(key):
                 bt[i, :counts[i]] = self.pages[r]
             t = {"key": key, "width": width, "counts": counts,
                  "dev": sched_pd.upload(bt, self.device)}
@@ -383,13 +390,25 @@ class PagedKvCache:
                     lo, hi = int(t["counts"][i]), int(counts[i])
                     rows.extend([i] * (hi - lo))
                     cols.extend(range(lo, hi))
-                    vals.extend(self.pages[rids[i]][lo:hi])
-                # rows, columns and values in one int32 upload (no conversion
-                # kernel: int32 indices index directly)
-                upd = sched_pd.upload(np.array([rows, cols, vals], np.int32), self.device)
-                t["dev"][upd[0], upd[1]] = upd[2]
+                    vals.extend(self.pages[key[i]][lo:hi])
+                parts.append(np.array([rows, cols, vals], np.int32).ravel())
+                upd_n = len(rows)
                 t["counts"] = counts
-        return t["dev"], sched_pd.upload(ctx, self.device)
+        extra = [np.ascontiguousarray(e, dtype=np.int32) for e in extra]
+        parts.extend(e.ravel() for e in extra)
+        # one copy for the lengths, the table update and the extras
+        dev = sched_pd.upload(np.concatenate(parts) if len(parts) > 1 else ctx, self.device)
+        n = len(key)
+        ctx_dev, off = dev[:n], n
+        if upd_n:
+            upd = dev[off:off + 3 * upd_n].view(3, upd_n)
+            t["dev"][upd[0], upd[1]] = upd[2]       # int32 indices index directly
+            off += 3 * upd_n
+        out = []
+        for e in extra:
+            out.append(dev[off:off + e.size].view(e.shape))
+            off += e.size
+        return t["dev"], ctx_dev, out
 
     def csr(self, rids):
         """(page_indptr [R+1], indices, last_page_len [R]) int32 on the device."""
@@ -420,10 +439,10 @@ class PagedKvCache:
         self.reserve(key, counts)
         try:
             self._len[s] += counts
-            bt, ctx = self.block_table(key)
             app = np.zeros(len(key) + 1, dtype=np.int32)
             app[1:] = np.cumsum(counts)
-            append(k_new, v_new, sched_pd.upload(app, self.device), ctx, self.k_pool,
+            bt, ctx, (app_dev,) = self._table_step(key, s, (app,))
+            append(k_new, v_new, app_dev, ctx, self.k_pool,
                    self.v_pool, bt, v_layout=self.v_layout, k_scale=self.k_scale,
                    v_scale=self.v_scale,
                    max_append=int(counts.max()) if counts.size else 0, errors=errors)
@@ -466,7 +485,11 @@ class PagedKvCache:
         self.reserve(key, np.ones(len(key), np.int64))
         try:
             self._len[s] += 1
-            bt, ctx = self.block_table(key)
+            tiles = kw.get("tiles")
+            host_plan = isinstance(tiles, np.ndarray)
+            bt, ctx, ex = self._table_step(key, s, (tiles,) if host_plan else ())
+            if host_plan:
+                kw["tiles"] = ex[0]      # uploaded with the lengths and table update
             kw.setdefault("v_layout", self.v_layout)
             out = kw.pop("out", None)
             if out is None:
@@ -493,8 +516,15 @@ class PagedKvCache:
         return out
 
     def decode(self, q, rids, **kw):
-        """One decode step over the requests' current contexts."""
-        bt, ctx = self.block_table(rids)
+        """One decode step over the requests' current contexts. A host split
+        plan (`tiles` from sched_pd.plan_tiles_host) is uploaded together with
+        the lengths and table update."""
+        key, s = self._slots(rids)
+        tiles = kw.get("tiles")
+        host_plan = isinstance(tiles, np.ndarray)
+        bt, ctx, ex = self._table_step(key, s, (tiles,) if host_plan else ())
+        if host_plan:
+            kw["tiles"] = ex[0]
         kw.setdefault("v_layout", self.v_layout)
         return sched_pd.paged_decode(q, self.k_pool, self.v_pool, bt, ctx, k_scale=self.k_scale,
                                      v_scale=self.v_scale, **kw)

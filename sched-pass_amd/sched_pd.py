@@ -176,7 +176,8 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                policy=(1.0, 1.0, 0.25), tiles=None, tile_pages=0,
                workspace=None, check_tables=False, stream=None) -> abi.SchedDecodeArgs:
     """Fill a SchedDecodeArgs from tensors (no launch). With `tiles` (from
-    plan_tiles, built from these ctx_lens) long tasks run as several work
+    plan_tiles, or a host array from plan_tiles_host, which is uploaded here;
+    built from these ctx_lens) long tasks run as several work
     items; the workspace is taken from a cache with one per (device, stream)
     unless one is given (`stream`: the stream the launch will use, default the
     current one). The kernels trust the page table (as the reference's do);
@@ -260,6 +261,11 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
     a.pf_dist = pf_dist
     a.policy_dT, a.policy_dR, a.policy_H = (float(x) for x in policy)
     a.flags = flags
+    if isinstance(tiles, np.ndarray):
+        # a host plan (plan_tiles_host): uploaded here, without waiting, and
+        # held by the arguments until they are dropped
+        tiles = upload(np.ascontiguousarray(tiles, dtype=np.int32), k_pool.device)
+        a._tiles = tiles
     if tiles is not None:
         _need_cuda(tiles, "tiles")
         if tiles.dtype != torch.int32 or tiles.dim() != 2 or tiles.shape[1] != 2 \

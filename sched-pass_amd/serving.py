@@ -102,10 +102,11 @@ class ServingHooks:
         pages = -(-np.asarray(kv_lens, np.int64) // ps)
         if self.cfg.tile_pages > 0:
             import sched_pd
-            # built on the host and uploaded once (reading a device plan back
-            # would wait for the previous step's kernels)
+            # built on the host (reading a device plan back would wait for
+            # the previous step's kernels); the decode uploads it with its
+            # other per-step arrays
             t = sched_pd.plan_tiles_host(kv_lens, ps, self.cfg.tile_pages, self.hkv)
-            tiles = sched_pd.upload(t, self.plane.dev)
+            tiles = t
             req = t[:, 0] // self.hkv
             first = t[:, 1] * self.cfg.tile_pages
             item_pages = np.clip(pages[req] - first, 0, self.cfg.tile_pages)
@@ -140,7 +141,8 @@ class ServingHooks:
     # -- the hooks ---------------------------------------------------------------
     def on_batch_begin(self, rids, kv_lens) -> dict:
         """Tables for this step; returns the launch arguments to pass to
-        sched_pd.paged_decode (plane, workers, tiles, tile_pages)."""
+        sched_pd.paged_decode or PagedKvCache.decode / decode_step (plane,
+        workers, tiles as a host int32 array, tile_pages)."""
         cfg, p = self.cfg, self.plane
         step = self.step
         self.step += 1
@@ -154,9 +156,8 @@ class ServingHooks:
             tiles = None
             if cfg.tile_pages > 0:
                 import sched_pd
-                tiles = sched_pd.upload(
-                    sched_pd.plan_tiles_host(kv_lens, cfg.page_size, cfg.tile_pages, self.hkv),
-                    p.dev)
+                tiles = sched_pd.plan_tiles_host(kv_lens, cfg.page_size, cfg.tile_pages,
+                                                 self.hkv)
             nitems = tiles.shape[0] if tiles is not None else len(kv_lens) * self.hkv
             workers = self.launch["workers"]
             if workers and nitems != self.armed_n:
