@@ -105,10 +105,9 @@ class ServingHooks:
             # built on the host (reading a device plan back would wait for
             # the previous step's kernels); the decode uploads it with its
             # other per-step arrays
-            t = sched_pd.plan_tiles_host(kv_lens, ps, self.cfg.tile_pages, self.hkv)
-            tiles = t
-            req = t[:, 0] // self.hkv
-            first = t[:, 1] * self.cfg.tile_pages
+            tiles = sched_pd.plan_tiles_host(kv_lens, ps, self.cfg.tile_pages, self.hkv)
+            req = tiles[:, 0] // self.hkv
+            first = tiles[:, 1] * self.cfg.tile_pages
             item_pages = np.clip(pages[req] - first, 0, self.cfg.tile_pages)
             return tiles, req, item_pages
         req = np.repeat(np.arange(n), self.hkv)
