@@ -176,15 +176,16 @@ class ServingHooks:
             raise RuntimeError(f"batch of {nitems} work items / {n * self.hkv} tasks exceeds "
                                f"the plane's max_tasks {p.N}")
 
-        cost_req = self.ctl.predict(rids, kv_list)
-        req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
-        cost_item = torch.as_tensor(cost_req[item_req] * item_pages / req_pages[item_req],
-                                    dtype=torch.float32)
-
         p.set_timer_enabled(probe)
         self.timer_armed = probe
         workers = 0
         if not cfg.observe_only:
+            # predicted cost per request, spread over its work items by pages
+            # (observing needs no prediction)
+            cost_req = self.ctl.predict(rids, kv_list)
+            req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
+            cost_item = torch.as_tensor(cost_req[item_req] * item_pages / req_pages[item_req],
+                                        dtype=torch.float32)
             R = cfg.resident
             imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6)) \
                 if nitems else 1.0
