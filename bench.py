@@ -209,7 +209,9 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     """256 requests, lognormal contexts; pi by a uniform-random urgency per
     task. Static grid (one workgroup per task) against the ticket work queue
     with W = 2 x CU persistent workers; the queue claims split-KV tiles of
-    `tile_pages` pages. The other two corners are reported as well."""
+    `tile_pages` pages. The other two corners are reported as well, the
+    queue with LPT from the timer, and pi alone (longest-first by pages over
+    the static grid of tiles)."""
     import numpy as np
     b = workloads.workload("llama3_8b_hetero", seed=0)
     ntask = 256 * 8
@@ -264,6 +266,15 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     a_lpt = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                 plane=p_lpt, workers=W, tiles=tiles2, tile_pages=tp2, **common)
     res["wq_tiles_lpt_timer"] = round(_makespan_us(torch, sched_pd, a_lpt, stream), 2)
+    # pi alone: the static grid over the 128-page tiles ordered longest-first
+    # by the pages each reads (known on the host), no queue
+    p_st = SchedPlane(max_tasks=max(nt, ntask))
+    p_st.install_order(sched_pd.tile_order_lpt(
+        sched_pd.tile_pages_loaded(tiles, b["ctx_lens"], 16, tile_pages, 8)), nt)
+    p_st.push()
+    a_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                               plane=p_st, workers=0, tiles=tiles, tile_pages=tile_pages, **common)
+    res["static_tiles_lpt_pages"] = round(_makespan_us(torch, sched_pd, a_st, stream), 2)
     kv = b["kv_bytes"]
 
     def cut(a, b_):
@@ -278,6 +289,7 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
         "queue_cut_pct": cut("static_tiles", "wq_tiles"),
         "queue_over_tasks_cut_pct": cut("static_task", "wq_task"),
         "queue_plus_split_plus_lpt_timer_cut_pct": cut("static_task", "wq_tiles_lpt_timer"),
+        "split_plus_lpt_static_cut_pct": cut("static_task", "static_tiles_lpt_pages"),
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
         "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
