@@ -320,3 +320,42 @@ def test_check_page_table_accepts_reachable_ids_and_names_the_bad_request():
         check_page_table(flat, ctx, 16, 5, page_indptr=torch.tensor([0, 3, 2], dtype=torch.int32))
     with pytest.raises(ValueError, match="CSR"):
         check_page_table(flat, ctx, 16, 5, page_indptr=torch.tensor([0, 2, 6], dtype=torch.int32))
+
+
+def test_fused_append_refusals_without_the_gpu(schedlib):
+    """sched_paged_decode_append checks its two argument blocks on the host
+    and names what it does not take (nothing is launched)."""
+    a = fake_args(v_tok_stride=128, v_dim_stride=1)          # token-major V
+    w = abi.default_kv_args()
+    w.num_requests, w.num_kv_heads, w.head_dim, w.page_size = 4, 8, 128, 16
+    w.num_tokens, w.bt_stride = 4, 8
+    w.src_dtype = w.kv_dtype = abi.BF16
+    w.k_src, w.v_src = ctypes.c_void_p(0x70000), ctypes.c_void_p(0x80000)
+    for f in ("k_pool", "v_pool", "ctx_lens", "block_table"):
+        setattr(w, f, getattr(a, f))
+    for f in ("k_page_stride", "k_head_stride", "k_tok_stride", "v_page_stride",
+              "v_head_stride", "v_tok_stride", "v_dim_stride"):
+        setattr(w, f, getattr(a, f))
+    w.src_tok_stride, w.src_head_stride = 8 * 128, 128
+    fn = schedlib.sched_paged_decode_append
+
+    def refused(word, **changes):
+        saved = {k: getattr(w, k) for k in changes}
+        for k, v in changes.items():
+            setattr(w, k, v)
+        rc = fn(ctypes.byref(a), ctypes.byref(w), None)
+        for k, v in saved.items():
+            setattr(w, k, v)
+        return rc != 0 and word in abi.last_error()
+
+    assert fn(None, ctypes.byref(w), None) != 0
+    assert refused("abi_version", abi_version=99)
+    assert refused("one token per request", num_tokens=5)
+    assert refused("must be the decode's", ctx_lens=ctypes.c_void_p(0x990000))
+    assert refused("4-byte aligned", k_src=ctypes.c_void_p(0x70002))
+    assert refused("cache dtypes differ", kv_dtype=abi.F16)
+    a.kv_dtype = w.kv_dtype = abi.FP8_E4M3
+    assert refused("bf16 or fp16 caches only")
+    a.kv_dtype = w.kv_dtype = abi.BF16
+    a.v_tok_stride, a.v_dim_stride = 1, 16                  # d-major V
+    assert refused("token-major V")
