@@ -164,6 +164,10 @@ uint64_t sched_rt_timer_host_va(void);
 #define SCHED_PD_TAU_PREFIX 0u
 #define SCHED_PD_TAU_PER_PAGE 1u
 
+/* split-KV tile row formats (tile_format) */
+#define SCHED_PD_TILES_PAIRS 0u  /* (task, chunk); chunks of tile_pages pages */
+#define SCHED_PD_TILES_RANGED 1u /* (task, chunk | nchunks << 16, p0, p1) */
+
 /* flags */
 #define SCHED_PD_FLAG_RT_TABLES 0x1u    /* take order/ctrl/timer/queue from the C runtime's
                                            __sched_* slots: the kernel reads the pointers the
@@ -230,19 +234,29 @@ typedef struct SchedDecodeArgs {
   const void *ctrl;           /* SchedCtrl layout, rows[max_tasks] */
   unsigned long long *timer;  /* u64[max_tasks] residency accumulators */
   uint32_t *queue;            /* ticket counter */
-  /* Split-KV work items (NULL = one work item per task). tiles[2*i],
-   * tiles[2*i+1] = (task, chunk) of work item i; chunk c of a task covers
-   * its pages [c*tile_pages, (c+1)*tile_pages). The list is task-major: the
-   * ceil(ceil(ctx/page_size)/tile_pages) chunks of a task (at least 1) are
-   * consecutive and in chunk order. pi, num_tasks, order_size and the ticket
-   * queue count work items; policy rows and timer rows stay per task.
-   * Plan the list from the ctx_lens of the launch: chunks a shorter context
-   * does not reach are skipped (the result is unchanged), but a task whose
-   * context needs a chunk the list lacks is stale -- its output rows are
-   * written as NaN and it is counted in the workspace's stale counter. */
+  /* Split-KV work items (NULL = one work item per task), in one of two row
+   * formats (tile_format):
+   * SCHED_PD_TILES_PAIRS: tiles[2*i], tiles[2*i+1] = (task, chunk) of work
+   *   item i; chunk c of a task covers its pages [c*tile_pages,
+   *   (c+1)*tile_pages). A task has ceil(ceil(ctx/page_size)/tile_pages)
+   *   chunks (at least 1).
+   * SCHED_PD_TILES_RANGED: tiles[4*i .. 4*i+3] = (task, chunk | nchunks << 16,
+   *   p0, p1): chunk `chunk` of the task's `nchunks` covers its pages
+   *   [p0, p1), so chunk sizes may differ (tile_pages is unused). The ranges
+   *   of a task's chunks are contiguous from page 0 (chunk c+1's p0 = chunk
+   *   c's p1), every row of a task carries the same nchunks (1..65535), and
+   *   the last range ends at or past the context's last page; a range past
+   *   the context reads nothing.
+   * Either list is task-major: the chunks of a task are consecutive and in
+   * chunk order. pi, num_tasks, order_size and the ticket queue count work
+   * items; policy rows and timer rows stay per task. Plan the list from the
+   * ctx_lens of the launch: chunks a shorter context does not reach add
+   * nothing (the result is unchanged), but a task whose context reaches past
+   * the list's last chunk is stale -- its output rows are written as NaN and
+   * it is counted in the workspace's stale counter. */
   const int32_t *tiles;
   uint32_t num_tiles;
-  uint32_t _pad0;
+  uint32_t tile_format;  /* SCHED_PD_TILES_PAIRS (0) or SCHED_PD_TILES_RANGED */
   /* Device scratch for split tasks (sched_paged_decode_workspace_bytes),
    * 256-byte aligned: bytes [0, 4) a u32 stale-plan counter (tasks found
    * stale, see tiles; the launcher only adds to it: read it after the launch

@@ -140,32 +140,54 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
   }
 }
 
-// Work item -> (task, chunk): the tile list, or work item = task.
-__device__ __forceinline__ void item_task(const KParams &P, uint32_t wi, uint32_t &task,
-                                          uint32_t &chunk) {
-  if (P.tiles == nullptr) {
-    task = wi;
-    chunk = 0u;
+// A work item's plan row. Pair rows (task, chunk) cover pages
+// [chunk * tile_pages, (chunk + 1) * tile_pages) of the task, the chunk count
+// following from the context length. Ranged rows (task, chunk | nchunks << 16,
+// p0, p1) carry the task's chunk count and the chunk's page range, so the
+// chunks of one task may differ in size. Without a list, work item = task.
+struct ItemRow {
+  uint32_t task, chunk, nchunks, p0, p1;
+};
+
+__device__ __forceinline__ ItemRow item_row(const KParams &P, uint32_t wi) {
+  ItemRow I{wi, 0u, 1u, 0u, 0u};
+  if (P.tiles == nullptr)
+    return I;
+  if (P.tile_ranged) {
+    const int32_t *row = P.tiles + 4 * (size_t)wi;
+    I.task = __builtin_amdgcn_readfirstlane((uint32_t)row[0]);
+    const uint32_t cc = __builtin_amdgcn_readfirstlane((uint32_t)row[1]);
+    I.chunk = cc & 0xFFFFu;
+    I.nchunks = cc >> 16;
+    I.p0 = __builtin_amdgcn_readfirstlane((uint32_t)row[2]);
+    I.p1 = __builtin_amdgcn_readfirstlane((uint32_t)row[3]);
   } else {
-    task = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi]);
-    chunk = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi + 1]);
+    I.task = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi]);
+    I.chunk = __builtin_amdgcn_readfirstlane((uint32_t)P.tiles[2 * wi + 1]);
   }
+  return I;
 }
 
-// Chunks of a task with n context tokens, and the page range [p0, p1) of
-// chunk `chunk` within the npages_load pages that are read.
+// The task's chunk count and the page range [p0, p1) the item reads, within
+// the npages_load pages of the task that are read at all (n context tokens).
 struct ItemRange {
   uint32_t nchunks, p0, p1;
 };
 
-__device__ __forceinline__ ItemRange item_range(const KParams &P, uint32_t chunk, uint32_t n,
+__device__ __forceinline__ ItemRange item_range(const KParams &P, const ItemRow &I, uint32_t n,
                                                 uint32_t npages_load) {
   if (P.tiles == nullptr)
     return ItemRange{1u, 0u, npages_load};
-  const uint32_t npages_ctx = (n + P.ps - 1) / P.ps;
   ItemRange it;
+  if (P.tile_ranged) {
+    it.nchunks = I.nchunks;
+    it.p1 = min(I.p1, npages_load);
+    it.p0 = min(I.p0, it.p1);
+    return it;
+  }
+  const uint32_t npages_ctx = (n + P.ps - 1) / P.ps;
   it.nchunks = npages_ctx ? (npages_ctx + P.tile_pages - 1) / P.tile_pages : 1u;
-  it.p0 = min(chunk * P.tile_pages, npages_load);
+  it.p0 = min(I.chunk * P.tile_pages, npages_load);
   it.p1 = min(it.p0 + P.tile_pages, npages_load);
   return it;
 }
@@ -173,37 +195,50 @@ __device__ __forceinline__ ItemRange item_range(const KParams &P, uint32_t chunk
 // What a work item does, decided from the plan and the launch's context
 // length. It runs (streams its pages and takes part in the task's merge)
 // unless
-//   - it is skipped: a chunk the context does not reach (the plan was built
-//     for a longer context; the task's other chunks cover it), or a chunk
-//     index that cannot be task-major;
-//   - its task is stale: the context needs chunk nchunks-1 and the plan does
-//     not hold it right after the task's chunk 0 (the plan was built for a
-//     shorter context). No item of such a task merges or touches its arrival
-//     counter: chunk 0 writes the task's output rows as NaN and counts the
-//     task in the workspace's stale counter.
-// Every item of a task reads the same rows and lengths, so they all decide
-// alike. The merge only ever reads items [wi - chunk, wi - chunk + nchunks),
-// which a running item keeps inside the list.
-// Skip: the chunk lies past what the context reaches, or cannot be
-// task-major. Decided without a load.
-__device__ __forceinline__ bool item_skip(const KParams &P, uint32_t wi, uint32_t chunk,
+//   - it is skipped: a pair-row chunk the context does not reach (the plan
+//     was built for a longer context; the task's other chunks cover it), or
+//     a chunk index that cannot be task-major;
+//   - its task is stale: the plan does not cover the context (pair rows: the
+//     row of chunk nchunks-1 is not where the task's chunk 0 puts it;
+//     ranged rows: that row is missing or its range ends before the
+//     context's last page). No item of such a task merges or touches its
+//     arrival counter: chunk 0 writes the task's output rows as NaN and
+//     counts the task in the workspace's stale counter.
+// A ranged chunk past the context reads no page and merges an empty
+// partial. Every item of a task reads the same rows and lengths, so they all
+// decide alike. The merge only ever reads items [wi - chunk, wi - chunk +
+// nchunks), which a running item keeps inside the list.
+__device__ __forceinline__ bool item_skip(const KParams &P, uint32_t wi, const ItemRow &I,
                                          const ItemRange &R) {
-  return P.tiles != nullptr && (chunk > wi || chunk >= R.nchunks);
+  return P.tiles != nullptr && (I.chunk > wi || I.chunk >= R.nchunks);
 }
 
-// Stale: the context needs more chunks than the plan holds for the task (the
-// row of its chunk nchunks-1 is missing). One tile-row load, issued when the
-// item starts and consumed at its merge.
-__device__ __forceinline__ bool item_stale(const KParams &P, uint32_t wi, uint32_t task,
-                                           uint32_t chunk, const ItemRange &R) {
-  if (P.tiles == nullptr || R.nchunks == 1u)
+// One tile-row load, issued when the item starts and consumed at its merge.
+__device__ __forceinline__ bool item_stale(const KParams &P, uint32_t wi, const ItemRow &I,
+                                           const ItemRange &R, uint32_t n) {
+  if (P.tiles == nullptr)
     return false;
-  const uint32_t last = wi - chunk + R.nchunks - 1u;
+  if (P.tile_ranged) {
+    const uint32_t npages_ctx = (n + P.ps - 1) / P.ps;
+    if (R.nchunks == 1u)
+      return I.p1 < npages_ctx;
+    const uint32_t last = wi - I.chunk + R.nchunks - 1u;
+    if (last >= P.L.nitems)
+      return true;
+    const int32_t *row = P.tiles + 4 * (size_t)last;
+    const uint32_t lt = __builtin_amdgcn_readfirstlane((uint32_t)row[0]);
+    const uint32_t lc = __builtin_amdgcn_readfirstlane((uint32_t)row[1]);
+    const uint32_t lp1 = __builtin_amdgcn_readfirstlane((uint32_t)row[3]);
+    return !(lt == I.task && lc == ((R.nchunks << 16) | (R.nchunks - 1u)) && lp1 >= npages_ctx);
+  }
+  if (R.nchunks == 1u)
+    return false;
+  const uint32_t last = wi - I.chunk + R.nchunks - 1u;
   if (last >= P.L.nitems)
     return true;
   const int32_t lt = __builtin_amdgcn_readfirstlane(P.tiles[2 * last]);
   const int32_t lc = __builtin_amdgcn_readfirstlane(P.tiles[2 * last + 1]);
-  return !((uint32_t)lt == task && (uint32_t)lc == R.nchunks - 1u);
+  return !((uint32_t)lt == I.task && (uint32_t)lc == R.nchunks - 1u);
 }
 
 // A stale task's signal: output rows NaN (chunk 0's item writes them), one

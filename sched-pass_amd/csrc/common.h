@@ -34,6 +34,7 @@ struct KParams {
   const int32_t *tiles;
   uint32_t ntasks;     // requests x kv-heads
   uint32_t tile_pages;
+  uint32_t tile_ranged; // rows (task, chunk | nchunks << 16, p0, p1), else (task, chunk)
   uint32_t *ws_stale;  // tasks found with a stale plan (item_verdict)
   uint32_t *ws_count;  // per-task arrival counters
   float *ws_ml;        // per-work-item (m, l) per head

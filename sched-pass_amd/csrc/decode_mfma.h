@@ -648,8 +648,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
-    uint32_t task, chunk;
-    item_task(P, wi, task, chunk);
+    const ItemRow I = item_row(P, wi);
+    const uint32_t task = I.task;
     if (task >= P.ntasks)
       return;
     MfmaTask T;
@@ -661,10 +661,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.n = ctx_tokens(P, T.r);
     T.budget = pol.budget;
     const uint32_t ext = load_extent(P, T.n, pol.budget);
-    const ItemRange R = item_range(P, chunk, T.n, PG ? (ext + P.ps - 1u) / P.ps : (ext + 15u) / 16u);
-    if (item_skip(P, wi, chunk, R))
+    const ItemRange R = item_range(P, I, T.n, PG ? (ext + P.ps - 1u) / P.ps : (ext + 15u) / 16u);
+    if (item_skip(P, wi, I, R))
       return;
-    const bool stale = item_stale(P, wi, task, chunk, R);
+    const bool stale = item_stale(P, wi, I, R, T.n);
     if constexpr (PG) {
       // pages [p0, p1) of the item as 16-token blocks, up to the last read
       T.bshift = 31u - __builtin_clz(P.ps >> 4);
@@ -681,7 +681,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       // wave that streams its page) before streaming
       if (P.app_k != nullptr && T.n > 0u) {
         const uint32_t pos = T.n - 1u, pg = pos / P.ps;
-        if (P.tiles == nullptr || chunk == pg / P.tile_pages) {
+        if (P.tiles == nullptr ||
+            (P.tile_ranged ? pg >= I.p0 && pg < I.p1 : I.chunk == pg / P.tile_pages)) {
           const uint32_t rel = (PG ? pos / 16u : pg) - T.p0;
           if (rel % (uint32_t)NW == w)
             append_token<F16>(P, T.r, T.h,
@@ -770,9 +771,9 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     }
     __syncthreads();
     if (stale)
-      mark_stale<NW, 128, LINEAR>(P, chunk, T.r, T.h, G);
+      mark_stale<NW, 128, LINEAR>(P, I.chunk, T.r, T.h, G);
     else
-      finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, chunk, R.nchunks, T.r, T.h, G,
+      finish_item<NW, GMAX, 128, float, LINEAR>(P, wi, task, I.chunk, R.nchunks, T.r, T.h, G,
                                                 s_acc, s_m, s_l);
     timer_commit(P.L, toff, task, t0);
   });

@@ -114,18 +114,18 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
     if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
-    uint32_t task, chunk;
-    item_task(P, wi, task, chunk);
+    const ItemRow I = item_row(P, wi);
+    const uint32_t task = I.task;
     if (task >= P.ntasks)
       return;
     const uint32_t r = task / P.Hkv, h = task % P.Hkv;
     const TaskPolicy pol = task_policy(P.L, task);
     const uint32_t n = ctx_tokens(P, r);
     const uint32_t nload = load_extent(P, n, pol.budget);
-    const ItemRange R = item_range(P, chunk, n, (nload + P.ps - 1) / P.ps);
-    if (item_skip(P, wi, chunk, R))
+    const ItemRange R = item_range(P, I, n, (nload + P.ps - 1) / P.ps);
+    if (item_skip(P, wi, I, R))
       return;
-    const bool stale = item_stale(P, wi, task, chunk, R);
+    const bool stale = item_stale(P, wi, I, R, n);
     const uint32_t G = LINEAR ? 1u : P.G;
     const bool fp8 = sizeof(KVT) == 1;
 
@@ -277,9 +277,9 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
     }
     __syncthreads();
     if (stale)
-      mark_stale<NW, D, LINEAR>(P, chunk, r, h, G);
+      mark_stale<NW, D, LINEAR>(P, I.chunk, r, h, G);
     else
-      finish_item<NW, GH, D, Acc, LINEAR>(P, wi, task, chunk, R.nchunks, r, h, G, s_acc, s_m,
+      finish_item<NW, GH, D, Acc, LINEAR>(P, wi, task, I.chunk, R.nchunks, r, h, G, s_acc, s_m,
                                           s_l);
     timer_commit(P.L, toff, task, t0);
   });

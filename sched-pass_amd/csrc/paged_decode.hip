@@ -265,8 +265,12 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->ntasks = a->num_requests * a->num_kv_heads;
   kp->L.nitems = kp->ntasks;
   if (a->tiles) {
-    if (a->num_tiles == 0 || a->tile_pages == 0)
-      return set_error(hipErrorInvalidValue, "tiles need num_tiles > 0 and tile_pages > 0");
+    if (a->tile_format > SCHED_PD_TILES_RANGED)
+      return set_error(hipErrorInvalidValue, "tile_format %u is not a tile row format",
+                       a->tile_format);
+    if (a->num_tiles == 0 || (a->tile_format == SCHED_PD_TILES_PAIRS && a->tile_pages == 0))
+      return set_error(hipErrorInvalidValue,
+                       "tiles need num_tiles > 0 (and tile_pages > 0 for (task, chunk) rows)");
     const WsLayout W = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < W.total || ((uintptr_t)a->workspace & 255u))
       return set_error(hipErrorInvalidValue,
@@ -275,6 +279,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     uint8_t *ws = static_cast<uint8_t *>(a->workspace);
     kp->tiles = a->tiles;
     kp->tile_pages = a->tile_pages;
+    kp->tile_ranged = a->tile_format == SCHED_PD_TILES_RANGED ? 1u : 0u;
     kp->L.nitems = a->num_tiles;
     kp->ws_stale = reinterpret_cast<uint32_t *>(ws + W.stale_off);
     kp->ws_count = reinterpret_cast<uint32_t *>(ws + W.count_off);

@@ -221,6 +221,16 @@ class _Lengths(MutableMapping):
         return len(self._c._slot)
 
 
+def _host_plan(tiles):
+    """A host split plan to upload with the step's other arrays (ranged rows
+    checked first), or None for no plan or one already on the device."""
+    if not isinstance(tiles, np.ndarray):
+        return None
+    if tiles.ndim == 2 and tiles.shape[1] == 4:
+        sched_pd.check_ranged_plan(tiles)
+    return tiles
+
+
 class PagedKvCache:
     """Pools + allocator + per-request page lists for one layer's KV.
 
@@ -485,10 +495,9 @@ class PagedKvCache:
         self.reserve(key, np.ones(len(key), np.int64))
         try:
             self._len[s] += 1
-            tiles = kw.get("tiles")
-            host_plan = isinstance(tiles, np.ndarray)
-            bt, ctx, ex = self._table_step(key, s, (tiles,) if host_plan else ())
-            if host_plan:
+            tiles = _host_plan(kw.get("tiles"))
+            bt, ctx, ex = self._table_step(key, s, () if tiles is None else (tiles,))
+            if tiles is not None:
                 kw["tiles"] = ex[0]      # uploaded with the lengths and table update
             kw.setdefault("v_layout", self.v_layout)
             out = kw.pop("out", None)
@@ -517,13 +526,12 @@ class PagedKvCache:
 
     def decode(self, q, rids, **kw):
         """One decode step over the requests' current contexts. A host split
-        plan (`tiles` from sched_pd.plan_tiles_host) is uploaded together with
-        the lengths and table update."""
+        plan (`tiles` from sched_pd.plan_tiles_host or plan_ranges_host) is
+        uploaded together with the lengths and table update."""
         key, s = self._slots(rids)
-        tiles = kw.get("tiles")
-        host_plan = isinstance(tiles, np.ndarray)
-        bt, ctx, ex = self._table_step(key, s, (tiles,) if host_plan else ())
-        if host_plan:
+        tiles = _host_plan(kw.get("tiles"))
+        bt, ctx, ex = self._table_step(key, s, () if tiles is None else (tiles,))
+        if tiles is not None:
             kw["tiles"] = ex[0]
         kw.setdefault("v_layout", self.v_layout)
         return sched_pd.paged_decode(q, self.k_pool, self.v_pool, bt, ctx, k_scale=self.k_scale,

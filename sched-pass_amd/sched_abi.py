@@ -38,6 +38,7 @@ FLAG_FORCE_VALU = 0x4
 FLAG_CTX_IN_PAGES = 0x8
 FLAG_SHED_LOADS = 0x10
 FLAG_NO_WAVE = 0x20
+TILES_PAIRS, TILES_RANGED = 0, 1
 
 _u32, _f32, _i64, _p = ctypes.c_uint32, ctypes.c_float, ctypes.c_int64, ctypes.c_void_p
 
@@ -62,7 +63,7 @@ class SchedDecodeArgs(ctypes.Structure):
         ("block_table", _p), ("page_indptr", _p), ("ctx_lens", _p),
         ("lin_w", _p),
         ("order", _p), ("ctrl", _p), ("timer", _p), ("queue", _p),
-        ("tiles", _p), ("num_tiles", _u32), ("_pad0", _u32),
+        ("tiles", _p), ("num_tiles", _u32), ("tile_format", _u32),
         ("workspace", _p), ("workspace_bytes", ctypes.c_uint64),
     ]
 

@@ -176,9 +176,10 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                policy=(1.0, 1.0, 0.25), tiles=None, tile_pages=0,
                workspace=None, check_tables=False, stream=None) -> abi.SchedDecodeArgs:
     """Fill a SchedDecodeArgs from tensors (no launch). With `tiles` (from
-    plan_tiles, or a host array from plan_tiles_host, which is uploaded here;
-    built from these ctx_lens) long tasks run as several work
-    items; the workspace is taken from a cache with one per (device, stream)
+    plan_tiles, or a host array from plan_tiles_host or plan_ranges_host,
+    which is uploaded here; built from these ctx_lens) long tasks run as
+    several work items: [n, 2] (task, chunk) rows of tile_pages pages, or
+    [n, 4] ranged rows (task, chunk | nchunks << 16, p0, p1); the workspace is taken from a cache with one per (device, stream)
     unless one is given (`stream`: the stream the launch will use, default the
     current one). The kernels trust the page table (as the reference's do);
     check_tables=True verifies it on the host first (check_page_table; this
@@ -262,18 +263,22 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
     a.policy_dT, a.policy_dR, a.policy_H = (float(x) for x in policy)
     a.flags = flags
     if isinstance(tiles, np.ndarray):
-        # a host plan (plan_tiles_host): uploaded here, without waiting, and
-        # held by the arguments until they are dropped
+        # a host plan (plan_tiles_host, plan_ranges_host): uploaded here,
+        # without waiting, and held by the arguments until they are dropped
+        if tiles.ndim == 2 and tiles.shape[1] == 4:
+            check_ranged_plan(tiles)
         tiles = upload(np.ascontiguousarray(tiles, dtype=np.int32), k_pool.device)
         a._tiles = tiles
     if tiles is not None:
         _need_cuda(tiles, "tiles")
-        if tiles.dtype != torch.int32 or tiles.dim() != 2 or tiles.shape[1] != 2 \
+        if tiles.dtype != torch.int32 or tiles.dim() != 2 or tiles.shape[1] not in (2, 4) \
                 or not tiles.is_contiguous():
-            raise ValueError("tiles must be a contiguous int32 [num_tiles, 2] tensor")
+            raise ValueError("tiles must be a contiguous int32 [num_tiles, 2] or "
+                             "[num_tiles, 4] tensor")
         a.tiles = _ptr(tiles)
         a.num_tiles = tiles.shape[0]
-        a.tile_pages = int(tile_pages)
+        a.tile_format = abi.TILES_RANGED if tiles.shape[1] == 4 else abi.TILES_PAIRS
+        a.tile_pages = int(tile_pages) if tiles.shape[1] == 2 else 0
         need = abi.load_library().sched_paged_decode_workspace_bytes(ctypes.byref(a))
         if need < 0:
             raise RuntimeError(abi.last_error())
@@ -416,6 +421,79 @@ def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
     return upload(plan_tiles_host(ctx_lens, page_size, tile_pages, num_kv_heads), device)
 
 
+def plan_ranges_host(ctx_lens, page_size: int, num_kv_heads: int, task_order=None,
+                     tile_pages: int = 128, tail_pages: int = 32,
+                     tail_frac: float = 0.1, tau=None) -> np.ndarray:
+    """A task-major ranged plan (int32 [num_tiles, 4] rows (task, chunk |
+    nchunks << 16, p0, p1)) whose chunk size shrinks at the end of a claim
+    order. `task_order` lists the tasks in the order a ticket queue will
+    reach them (e.g. by urgency; None = task index). Tasks that start in the
+    first 1 - tail_frac of the order's pages are cut into tile_pages-page
+    chunks, the rest into tail_pages-page chunks: the work items claimed last
+    are short, so the workers finish closer together. Each chunk but a task's
+    last holds exactly its size; a task with no pages has one empty chunk.
+    `tau`: per-task prefix budgets in tokens (0 = no cap), for launches that
+    skip the pages past them: only the pages read are cut into chunks and
+    counted, and each task's last range runs on to its context's last page,
+    so no work item is empty and the plan still covers the context.
+    ctx_lens: the lengths the launch will see."""
+    ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
+                     dtype=np.int64)
+    if tile_pages < 1 or tail_pages < 1 or not 0.0 <= tail_frac <= 1.0:
+        raise ValueError("tile_pages and tail_pages must be >= 1, tail_frac in [0, 1]")
+    n = np.repeat(ctx, num_kv_heads)
+    npg_ctx = (n + page_size - 1) // page_size
+    if tau is not None:
+        tau = np.asarray(tau, dtype=np.int64)
+        if tau.shape != n.shape:
+            raise ValueError(f"tau needs one budget per task ({n.size})")
+        n = np.where(tau > 0, np.minimum(n, tau), n)
+    npg = (n + page_size - 1) // page_size
+    ntask = npg.size
+    order = np.arange(ntask) if task_order is None else np.asarray(task_order, dtype=np.int64)
+    if order.shape != (ntask,) or not np.array_equal(np.sort(order), np.arange(ntask)):
+        raise ValueError(f"task_order must be a permutation of the {ntask} tasks")
+    # pages claimed before each task starts, in claim order
+    before = np.empty(ntask, np.int64)
+    before[order] = np.cumsum(npg[order]) - npg[order]
+    size = np.where(before < (1.0 - tail_frac) * npg.sum(), tile_pages, tail_pages)
+    nch = np.maximum(1, (npg + size - 1) // size)
+    if nch.max(initial=1) > 0xFFFF:
+        raise ValueError("a task needs more than 65535 chunks; raise the chunk sizes")
+    tasks = np.repeat(np.arange(ntask, dtype=np.int64), nch)
+    starts = np.cumsum(nch) - nch
+    chunk = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, nch)
+    p0 = chunk * size[tasks]
+    p1 = np.where(chunk == nch[tasks] - 1, npg_ctx[tasks],
+                  np.minimum(p0 + size[tasks], npg[tasks]))
+    return np.stack([tasks, chunk | (nch[tasks] << 16), p0, p1], 1).astype(np.int32)
+
+
+def check_ranged_plan(tiles) -> None:
+    """Raise ValueError unless `tiles` ([n, 4] ranged rows) is task-major:
+    each task's chunks consecutive, numbered 0..nchunks-1 with one nchunks,
+    their page ranges contiguous from page 0. (Coverage of the context is
+    the launch's check: a task whose context passes its last range is
+    stale.)"""
+    t = np.asarray(tiles, dtype=np.int64)
+    if t.ndim != 2 or t.shape[1] != 4 or t.shape[0] == 0:
+        raise ValueError("ranged tiles must be a non-empty [num_tiles, 4] array")
+    task, chunk, nch = t[:, 0], t[:, 1] & 0xFFFF, t[:, 1] >> 16
+    p0, p1 = t[:, 2], t[:, 3]
+    first = chunk == 0
+    start = np.maximum.accumulate(np.where(first, np.arange(len(t)), 0))
+    ok = (nch >= 1) & (chunk < nch) & (p0 <= p1) & (p0 >= 0) & (task >= 0)
+    ok &= chunk == np.arange(len(t)) - start          # chunk c sits c rows after chunk 0
+    ok &= (task == task[start]) & (nch == nch[start])
+    ok &= np.where(first, p0 == 0, p0 == np.roll(p1, 1))
+    last = chunk == nch - 1
+    ok &= np.where(last, True, np.roll(chunk, -1) == chunk + 1)
+    if not ok.all():
+        i = int(np.flatnonzero(~ok)[0])
+        raise ValueError(f"ranged tiles row {i} {t[i].tolist()} is not task-major with "
+                         "contiguous ranges from page 0")
+
+
 def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.Tensor:
     """pi over work items that follows a per-task key (e.g. urgency or
     predicted cost): tiles of higher-key tasks first, chunk order kept."""
@@ -428,11 +506,12 @@ def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.T
 
 def tile_pages_loaded(tiles: torch.Tensor, ctx_lens, page_size: int, tile_pages: int,
                       num_kv_heads: int, tau=None, tau_scope: int = abi.TAU_PREFIX) -> np.ndarray:
-    """Pages each work item of a plan_tiles() plan reads when shed pages are
-    skipped: task t reads ceil(n_t / page_size) pages, n_t = ctx, or
+    """Pages each work item of a plan_tiles() or plan_ranges_host() plan
+    reads when shed pages are skipped: task t reads ceil(n_t / page_size) pages, n_t = ctx, or
     min(ctx, tau_t) under a prefix budget (tau_t = 0: no cap; the per-page
     scope reads every page). Chunk c holds the pages of [c*tile_pages,
-    (c+1)*tile_pages) among them (0 for a chunk wholly past the budget)."""
+    (c+1)*tile_pages) among them, a ranged row those of [p0, p1) (0 for a
+    chunk wholly past the budget)."""
     t = tiles.cpu().numpy() if isinstance(tiles, torch.Tensor) else np.asarray(tiles)
     ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
                      dtype=np.int64)
@@ -441,6 +520,10 @@ def tile_pages_loaded(tiles: torch.Tensor, ctx_lens, page_size: int, tile_pages:
         tau = np.asarray(tau, dtype=np.int64)[:n.size]
         n = np.where(tau > 0, np.minimum(n, tau), n)
     pages = (n + page_size - 1) // page_size
+    if t.shape[1] == 4:         # ranged rows: pages [p0, p1) of those read
+        load = pages[t[:, 0]]
+        p1 = np.minimum(t[:, 3].astype(np.int64), load)
+        return np.maximum(0, p1 - np.minimum(t[:, 2].astype(np.int64), p1))
     return np.clip(pages[t[:, 0]] - t[:, 1].astype(np.int64) * tile_pages, 0, tile_pages)
 
 

@@ -80,6 +80,8 @@ def test_plane_constants_mirror_header():
     assert define("SCHED_CTRL_ORDER_SIZE_OFF") == abi.CTRL_ORDER_SIZE_OFF
     assert define("SCHED_PD_ABI_VERSION") == abi.ABI_VERSION
     assert define("SCHED_PD_FLAG_SHED_LOADS") == abi.FLAG_SHED_LOADS
+    assert define("SCHED_PD_TILES_PAIRS") == abi.TILES_PAIRS
+    assert define("SCHED_PD_TILES_RANGED") == abi.TILES_RANGED
     import sched_rt
     assert (sched_rt.ORDER_OFF, sched_rt.CTRL_OFF, sched_rt.TIMER_OFF, sched_rt.QUEUE_OFF) == \
         (0, 0x40000, 0x80000, 0xC0000)
@@ -279,6 +281,97 @@ def test_tile_pages_loaded_and_lpt_order():
     assert sorted(o.tolist()) == list(range(14))
     assert all(got[o[i]] >= got[o[i + 1]] for i in range(13))
     assert o[:3].tolist() == [4, 5, 6]   # ties keep index order
+
+
+def _ranged_by_loops(ctx, ps, hkv, order, tp, tail, frac):
+    # the ranged plan written out one task at a time, in claim order
+    npg = [-(-c // ps) for c in ctx for _ in range(hkv)]
+    total, before, size = sum(npg), 0, {}
+    for t in order:
+        size[t] = tp if before < (1 - frac) * total else tail
+        before += npg[t]
+    rows = []
+    for t in range(len(npg)):
+        nch = max(1, -(-npg[t] // size[t]))
+        for c in range(nch):
+            rows.append([t, c | nch << 16, c * size[t], min((c + 1) * size[t], npg[t])])
+    return rows
+
+
+def test_ranged_plan_rows_and_tail():
+    import numpy as np
+    import sched_pd
+    ctx = [0, 16, 17, 100, 3000, 250]
+    pairs = sched_pd.plan_tiles_host(ctx, 16, 4, 2)
+    # no tail: the pair plan's chunks with their page ranges spelled out
+    r = sched_pd.plan_ranges_host(ctx, 16, 2, tile_pages=4, tail_frac=0.0)
+    assert np.array_equal(r[:, 0], pairs[:, 0]) and np.array_equal(r[:, 1] & 0xFFFF, pairs[:, 1])
+    npg = np.repeat((np.array(ctx) + 15) // 16, 2)
+    nch = np.maximum(1, (npg + 3) // 4)
+    assert np.array_equal(r[:, 1] >> 16, nch[r[:, 0]])
+    assert np.array_equal(r[:, 2], 4 * pairs[:, 1])
+    assert np.array_equal(r[:, 3], np.minimum(4 * pairs[:, 1] + 4, npg[r[:, 0]]))
+    rng = np.random.default_rng(5)
+    for frac, tp, tail in ((0.0, 4, 1), (0.3, 8, 2), (0.6, 16, 3), (1.0, 5, 2)):
+        order = rng.permutation(len(ctx) * 2)
+        got = sched_pd.plan_ranges_host(ctx, 16, 2, task_order=order, tile_pages=tp,
+                                        tail_pages=tail, tail_frac=frac)
+        assert got.tolist() == _ranged_by_loops(ctx, 16, 2, order, tp, tail, frac)
+        sched_pd.check_ranged_plan(got)
+    # under prefix budgets only the pages read are cut; the last range runs
+    # to the context's end
+    tau = np.array([0, 0, 5, 5, 40, 0, 1000, 17, 0, 0, 100, 240])
+    got = sched_pd.plan_ranges_host(ctx, 16, 2, tile_pages=2, tail_frac=0.0, tau=tau)
+    sched_pd.check_ranged_plan(got)
+    load = (np.where(tau > 0, np.minimum(np.repeat(ctx, 2), tau), np.repeat(ctx, 2)) + 15) // 16
+    for t in range(12):
+        rows = got[got[:, 0] == t]
+        assert len(rows) == max(1, -(-load[t] // 2))
+        assert rows[-1, 3] == npg[t] and (rows[:-1, 3] - rows[:-1, 2] == 2).all()
+    read = sched_pd.tile_pages_loaded(got, ctx, 16, 0, 2, tau=tau)
+    assert np.bincount(got[:, 0], weights=read, minlength=12).tolist() == load.tolist()
+    assert ((read > 0) | (load[got[:, 0]] == 0)).all()            # no empty item
+    with pytest.raises(ValueError):
+        sched_pd.plan_ranges_host(ctx, 16, 2, task_order=[0, 1])
+    with pytest.raises(ValueError):
+        sched_pd.plan_ranges_host(ctx, 16, 2, tail_pages=0)
+
+
+def test_check_ranged_plan_rejects_malformed_lists():
+    import numpy as np
+    import sched_pd
+    good = sched_pd.plan_ranges_host([100, 40], 16, 1, tile_pages=2, tail_frac=0.0)
+    # request 0: 7 pages in 4 chunks, request 1: 3 pages in 2 chunks
+    assert good.tolist() == [[0, 0 | 4 << 16, 0, 2], [0, 1 | 4 << 16, 2, 4],
+                             [0, 2 | 4 << 16, 4, 6], [0, 3 | 4 << 16, 6, 7],
+                             [1, 0 | 2 << 16, 0, 2], [1, 1 | 2 << 16, 2, 3]]
+    sched_pd.check_ranged_plan(good)
+    bad = []
+    b = good.copy(); b[[1, 2]] = b[[2, 1]]; bad.append(b)             # chunks out of order
+    b = good.copy(); b[2, 2] = 5; bad.append(b)                       # gap in the ranges
+    b = good.copy(); b[3, 1] = 3 | 5 << 16; bad.append(b)             # nchunks differ
+    bad.append(good[:5].copy())                                       # last task cut short
+    b = good.copy(); b[4, 2] = 1; bad.append(b)                       # chunk 0 not from page 0
+    b = good.copy(); b[5, 0] = 0; bad.append(b)                       # task changes mid-chunks
+    b = good.copy(); b[1, 3] = 1; bad.append(b)                       # p1 < p0
+    for b in bad:
+        with pytest.raises(ValueError):
+            sched_pd.check_ranged_plan(b)
+    with pytest.raises(ValueError):
+        sched_pd.check_ranged_plan(np.zeros((0, 4), np.int32))
+    # pages read under a prefix budget: task 0 capped at 40 tokens = 3 pages
+    got = sched_pd.tile_pages_loaded(good, [100, 40], 16, 0, 1, tau=np.array([40, 0]))
+    assert got.tolist() == [2, 1, 0, 0, 2, 1]
+
+
+def test_ranged_tile_format_validated(schedlib):
+    ws = dict(tiles=ctypes.c_void_p(0x90000), num_tiles=8, workspace=ctypes.c_void_p(0xA0000),
+              workspace_bytes=1 << 20)
+    assert kind(schedlib, fake_args(**ws, tile_format=abi.TILES_RANGED)) == 1  # no tile_pages
+    assert kind(schedlib, fake_args(**ws, tile_format=abi.TILES_PAIRS)) == -1
+    assert "tile_pages" in abi.last_error()
+    assert kind(schedlib, fake_args(**ws, tile_format=2, tile_pages=4)) == -1
+    assert "tile_format" in abi.last_error()
 
 
 def torch_tiles(t):

@@ -76,7 +76,8 @@ def test_fused_step_equals_append_then_decode(dtype, ps, G, src32):
     assert par_err(o_fused.float().cpu(), ref, f"fused {dtype} p{ps} G{G}") <= TOL_BF16
 
 
-def test_fused_step_with_tiles_queue_and_pi():
+@pytest.mark.parametrize("ranged", [False, True])
+def test_fused_step_with_tiles_queue_and_pi(ranged):
     lens = [int(x) for x in np.random.default_rng(2).integers(1, 900, 40)]
     (fa, sep), g = make_pair(torch.bfloat16, 16, lens, seed=3)
     R = len(lens)
@@ -87,17 +88,21 @@ def test_fused_step_with_tiles_queue_and_pi():
         k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
         v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
         after = [fa.lens[r] + 1 for r in rids]          # plan from the post-append lengths
-        tiles = sched_pd.plan_tiles(after, 16, tp, HKV)
+        if ranged:     # host rows, chunks of 8 pages and of 3 at the end of pi
+            tiles = sched_pd.plan_ranges_host(after, 16, HKV, task_order=np.arange(R * HKV)[::-1],
+                                              tile_pages=tp, tail_pages=3, tail_frac=0.5)
+        else:
+            tiles = sched_pd.plan_tiles(after, 16, tp, HKV)
         nt = tiles.shape[0]
         plane = SchedPlane(max_tasks=max(nt, R * HKV))
         plane.install_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32), nt)
         plane.set_num_tasks(nt)
         plane.push()
         plane.reset_queue(7)
-        o_fused = fa.decode_step(q, rids, k1, v1, tiles=tiles, tile_pages=tp, plane=plane,
-                                 workers=7)
+        tkw = dict(tiles=tiles) if ranged else dict(tiles=tiles, tile_pages=tp)
+        o_fused = fa.decode_step(q, rids, k1, v1, plane=plane, workers=7, **tkw)
         sep.append(rids, k1, v1)
-        o_sep = sep.decode(q, rids, tiles=tiles, tile_pages=tp)
+        o_sep = sep.decode(q, rids, **tkw)
         torch.cuda.synchronize()
         assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
         assert same(o_fused, o_sep), step
