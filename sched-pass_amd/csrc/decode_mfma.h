@@ -666,11 +666,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       return;
     const bool stale = item_stale(P, wi, I, R, T.n);
     if constexpr (PG) {
-      // pages [p0, p1) of the item as 16-token blocks, up to the last read
+      // pages [p0, p1) of the item as 16-token blocks, up to the last read.
+      // A chunk wholly past a budget that ends inside a page has R.p0 =
+      // R.p1 = the page count, whose first block lies past the last block
+      // read: p0 is clamped to p1 so that the span is empty, never negative.
       T.bshift = 31u - __builtin_clz(P.ps >> 4);
       T.bmask = (1u << T.bshift) - 1u;
-      T.p0 = R.p0 << T.bshift;
       T.p1 = min(R.p1 << T.bshift, (ext + 15u) / 16u);
+      T.p0 = min(R.p0 << T.bshift, T.p1);
     } else {
       T.p0 = R.p0;
       T.p1 = R.p1;

@@ -238,6 +238,40 @@ def test_pages_of_32_tokens_shed_and_linear(scope):
     assert e <= TOL_BF16
 
 
+@pytest.mark.parametrize("ranged", [False, True])
+def test_split_pages_of_32_tokens_under_a_mid_page_budget(ranged):
+    """Split tiles over 32-token pages with prefix budgets that end inside a
+    page (40 tokens: 2 pages, 3 of their 16-token blocks) and chunks wholly
+    past the budget: those chunks read nothing (their block range is empty,
+    not reversed), the rest match the oracle, and loading + masking the shed
+    tokens gives the same bits."""
+    rng = np.random.default_rng(29)
+    ctx = np.array([3000, 2000, 700, 90])
+    hkv, ps, tp = 8, 32, 2
+    b = workloads.make_batch(ctx, num_q_heads=32, num_kv_heads=hkv, page_size=ps, seed=29,
+                             device="cuda")
+    n = ctx.size * hkv
+    tau = rng.integers(1, 1200, size=n)
+    tau[::3] = 40
+    tau[1::5] = 0                                  # no cap
+    if ranged:
+        tiles = sched_pd.plan_ranges_host(ctx, ps, hkv, task_order=rng.permutation(n),
+                                          tile_pages=tp, tail_pages=1, tail_frac=0.5)
+        kw = dict(tiles=tiles)
+    else:
+        tiles = sched_pd.plan_tiles_host(ctx, ps, tp, hkv)
+        kw = dict(tiles=tiles, tile_pages=tp)
+    assert (sched_pd.tile_pages_loaded(tiles, ctx, ps, tp, hkv, tau=tau) == 0).any()
+    plane = SchedPlane(max_tasks=max(n, tiles.shape[0]))
+    plane.set_rows(tau=tau, n=n)
+    plane.push()
+    s = run(b, plane=plane, **kw)
+    e = par_err(s.cpu(), ref(b, plane))
+    print(f"split page 32 mid-page budget ranged={ranged} err {e:.3g}", flush=True)
+    assert e <= TOL_BF16
+    assert torch.equal(run(b, plane=plane, flags=abi.FLAG_SHED_LOADS, **kw), s)
+
+
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4), (16, 2), (64, 4)])
 def test_fp16_cache_parity(hq, hkv):
     """An fp16 cache with fp16 Q (FlashInfer's dtype in the reference's
