@@ -290,6 +290,11 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
             raise ValueError(f"workspace holds {workspace.numel()} bytes, needs {need}")
         a.workspace = _ptr(workspace)
         a.workspace_bytes = workspace.numel() * workspace.element_size()
+        # held by the arguments: a later launch that needs a larger one
+        # replaces the cached workspace, and these arguments must not then
+        # point into memory the allocator has handed to another tensor (the
+        # old workspace's counters stay zero, as each launch leaves them)
+        a._ws = workspace
     if rt_tables:
         a.flags |= abi.FLAG_RT_TABLES
         a.workers = workers

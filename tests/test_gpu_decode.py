@@ -688,6 +688,36 @@ def test_split_kv_with_shed_valu_and_linear():
     assert par_err(o.cpu(), r) <= TOL_BF16
 
 
+def test_split_args_keep_their_workspace_when_the_cache_grows():
+    """Arguments built for a small plan, then for one that needs a larger
+    workspace (the cache replaces its tensor), then new allocations of the
+    old size filled with garbage: relaunching the first arguments still
+    writes into their own workspace and gives the oracle's result."""
+    small = batch([3000, 40], seed=43)
+    big = batch([3000] * 24, seed=44)
+    outs = [torch.empty(2, 32, 128, device="cuda"), torch.empty(24, 32, 128, device="cuda")]
+    a_small = sched_pd.build_args(small["q"], small["k_pool"], small["v_pool"],
+                                  small["block_table"], small["ctx_lens"], out=outs[0],
+                                  tiles=sched_pd.plan_tiles_host([3000, 40], 16, 16, 8),
+                                  tile_pages=16)
+    ws_small = sched_pd.workspace_of(a_small)
+    n_small = ws_small.numel()
+    a_big = sched_pd.build_args(big["q"], big["k_pool"], big["v_pool"], big["block_table"],
+                                big["ctx_lens"], out=outs[1],
+                                tiles=sched_pd.plan_tiles_host([3000] * 24, 16, 16, 8),
+                                tile_pages=16)
+    assert a_big.workspace != a_small.workspace
+    junk = [torch.full((n_small,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    for _ in range(2):
+        sched_pd.launch(a_small)
+        sched_pd.launch(a_big)
+    torch.cuda.synchronize()
+    assert par_err(outs[0].cpu(), ref(small)) <= TOL_BF16
+    assert par_err(outs[1].cpu(), ref(big)) <= TOL_BF16
+    assert int(a_small._ws[:sched_pd.WS_COUNTERS_OFF + 4 * 16].view(torch.int32).abs().sum()) == 0
+    del junk
+
+
 def test_split_workspace_counters_grow_safely():
     small = batch([3000, 40], seed=41)
     big = batch([3000] * 12, seed=42)
