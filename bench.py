@@ -185,6 +185,9 @@ def tile_pages_for(elem_bytes, page=16, head_dim=128):
 
 
 TILE_PAGES = tile_pages_for(2)
+# ranged plans under an order unrelated to cost: the tasks that start in the
+# last 10% of the order's pages run as 64-page chunks
+TAIL_PAGES, TAIL_FRAC = 64, 0.1
 
 
 def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):
@@ -211,7 +214,8 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     with W = 2 x CU persistent workers; the queue claims split-KV tiles of
     `tile_pages` pages. The other two corners are reported as well, the
     queue with LPT from the timer, and pi alone (longest-first by pages over
-    the static grid of tiles)."""
+    the static grid of tiles); and the queue, pi still by urgency, over a
+    ranged plan whose last-claimed tasks run as TAIL_PAGES-page chunks."""
     import numpy as np
     b = workloads.workload("llama3_8b_hetero", seed=0)
     ntask = 256 * 8
@@ -275,6 +279,21 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     a_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                plane=p_st, workers=0, tiles=tiles, tile_pages=tile_pages, **common)
     res["static_tiles_lpt_pages"] = round(_makespan_us(torch, sched_pd, a_st, stream), 2)
+    # the queue over a ranged plan: pi by urgency as above, the tasks claimed
+    # last cut into shorter chunks
+    ctx = b["ctx_lens"].cpu().numpy()
+    rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-q, kind="stable"),
+                                       tile_pages=tile_pages, tail_pages=TAIL_PAGES,
+                                       tail_frac=TAIL_FRAC)
+    ntr = rtiles.shape[0]
+    p_rng = SchedPlane(max_tasks=max(ntr, ntask))
+    p_rng.install_order(sched_pd.tile_order_by_task_key(torch.from_numpy(rtiles), q), ntr)
+    p_rng.set_num_tasks(ntr)
+    p_rng.push()
+    p_rng.reset_queue(W)
+    a_rng = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                plane=p_rng, workers=W, tiles=rtiles, **common)
+    res["wq_ranged_tail"] = round(_makespan_us(torch, sched_pd, a_rng, stream), 2)
     kv = b["kv_bytes"]
 
     def cut(a, b_):
@@ -290,6 +309,9 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
         "queue_over_tasks_cut_pct": cut("static_task", "wq_task"),
         "queue_plus_split_plus_lpt_timer_cut_pct": cut("static_task", "wq_tiles_lpt_timer"),
         "split_plus_lpt_static_cut_pct": cut("static_task", "static_tiles_lpt_pages"),
+        "queue_plus_ranged_tail_cut_pct": cut("static_task", "wq_ranged_tail"),
+        "ranged_tail_vs_tiles_pct": -cut("wq_tiles", "wq_ranged_tail"),
+        "ranged_tiles": ntr, "tail_pages": TAIL_PAGES, "tail_frac": TAIL_FRAC,
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
         "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
@@ -305,9 +327,11 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     urgent, all polite) on the softmax skip launch. Online softmax (score -> -inf) and linear contraction (value -> 0)
     variants; pages past the budget skipped (default) or loaded and masked
     (the reference weave's behaviour). Work queue over split tiles, pi by
-    urgency; then the skip variants with pi = longest-first over tiles of
-    twice the size by the pages each reads (known on the host from ctx and
-    tau)."""
+    urgency; the softmax skip launch over a ranged plan cut from the pages
+    each task reads (no empty work items past the budgets), its
+    last-claimed tasks in TAIL_PAGES-page chunks; then the skip variants with
+    pi = longest-first over tiles of twice the size by the pages each reads
+    (known on the host from ctx and tau)."""
     import numpy as np
     import sched_abi as abi
     b = workloads.workload("llama3_8b_shed", seed=0)
@@ -372,6 +396,31 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     ab["firing_vs_priced_out_pct"] = round(
         100.0 * (ab["firing_us"] - ab["priced_out_us"]) / ab["priced_out_us"], 2)
     res["policy_ab"] = ab
+    rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
+                                                                          kind="stable"),
+                                       tile_pages=tile_pages, tail_pages=TAIL_PAGES,
+                                       tail_frac=TAIL_FRAC, tau=b["tau"][:ntask])
+    ntr = rtiles.shape[0]
+    plane_r = SchedPlane(max_tasks=max(ntr, ntask))
+    plane_r.set_lambda(0.5)
+    plane_r.set_rows(q=b["urgency"], tau=b["tau"], n=ntask)
+    plane_r.install_order(sched_pd.tile_order_by_task_key(torch.from_numpy(rtiles),
+                                                          b["urgency"]), ntr)
+    plane_r.set_num_tasks(ntr)
+    plane_r.push()
+    plane_r.reset_queue(W)
+    a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                            out=out, plane=plane_r, workers=W, tiles=rtiles,
+                            policy=(1.0, 1.0, 0.1), pf_dist=4)
+    us = _makespan_us(torch, sched_pd, a, stream)
+    res["softmax_skip_ranged_tail"] = {
+        "us": round(us, 2), "gbs_loaded": round(kept / us / 1e3, 1),
+        "gbs_ctx_equiv": round(full / us / 1e3, 1), "tiles": ntr,
+        "vs_tiles_pct": round(100.0 * (us - res["softmax_skip"]["us"]) / res["softmax_skip"]["us"], 2)}
+    sched_pd.launch(a, stream)
+    torch.cuda.synchronize()
+    if not torch.equal(torch.isfinite(out), torch.ones_like(out, dtype=torch.bool)):
+        raise AssertionError("the ranged shed launch left non-finite outputs")
     tp2 = 2 * tile_pages
     tiles2 = sched_pd.plan_tiles(ctx, 16, tp2, 8)
     nt2 = tiles2.shape[0]
