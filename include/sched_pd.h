@@ -216,7 +216,7 @@ typedef struct SchedDecodeArgs {
   float sm_scale;        /* 0 = 1/sqrt(head_dim) */
   float policy_dT, policy_dR, policy_H; /* urgent iff q*dT - lambda_bw*dR - H > 0 */
   uint32_t lin_w_period; /* linear mode: w index = pos % period (0 = pos) */
-  uint32_t tile_pages;   /* split-KV tile size in pages (with `tiles`) */
+  uint32_t tile_pages;   /* split-KV tile size in pages (pair rows, see tiles) */
   const void *q;         /* [num_requests][num_q_heads][head_dim] */
   void *out;             /* softmax: [R][Hq][d]; linear: [R][Hkv][d] */
   const void *k_pool;
