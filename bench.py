@@ -185,9 +185,16 @@ def tile_pages_for(elem_bytes, page=16, head_dim=128):
 
 
 TILE_PAGES = tile_pages_for(2)
-# ranged plans under an order unrelated to cost: the tasks that start in the
-# last 10% of the order's pages run as 64-page chunks
-TAIL_PAGES, TAIL_FRAC = 64, 0.1
+# ranged plans under an order unrelated to cost: 1.25 MiB chunks of one
+# kv-head's KV, and 0.5 MiB chunks for the tasks that start in the last 10%
+# of the order's pages (bf16: 160 and 64 pages; fp8: 320 and 128)
+RANGED_BYTES, TAIL_BYTES, TAIL_FRAC = 5 << 18, 1 << 19, 0.1
+
+
+def ranged_pages(elem_bytes):
+    """(chunk pages, tail chunk pages) of the ranged plans."""
+    per_page = 16 * 128 * 2 * elem_bytes
+    return RANGED_BYTES // per_page, TAIL_BYTES // per_page
 
 
 def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):
@@ -215,7 +222,7 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     `tile_pages` pages. The other two corners are reported as well, the
     queue with LPT from the timer, and pi alone (longest-first by pages over
     the static grid of tiles); and the queue, pi still by urgency, over a
-    ranged plan whose last-claimed tasks run as TAIL_PAGES-page chunks."""
+    ranged plan whose last-claimed tasks run as shorter chunks."""
     import numpy as np
     b = workloads.workload("llama3_8b_hetero", seed=0)
     ntask = 256 * 8
@@ -282,9 +289,9 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     # the queue over a ranged plan: pi by urgency as above, the tasks claimed
     # last cut into shorter chunks
     ctx = b["ctx_lens"].cpu().numpy()
+    rp, rt = ranged_pages(2)
     rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-q, kind="stable"),
-                                       tile_pages=tile_pages, tail_pages=TAIL_PAGES,
-                                       tail_frac=TAIL_FRAC)
+                                       tile_pages=rp, tail_pages=rt, tail_frac=TAIL_FRAC)
     ntr = rtiles.shape[0]
     p_rng = SchedPlane(max_tasks=max(ntr, ntask))
     p_rng.install_order(sched_pd.tile_order_by_task_key(torch.from_numpy(rtiles), q), ntr)
@@ -311,7 +318,7 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
         "split_plus_lpt_static_cut_pct": cut("static_task", "static_tiles_lpt_pages"),
         "queue_plus_ranged_tail_cut_pct": cut("static_task", "wq_ranged_tail"),
         "ranged_tail_vs_tiles_pct": -cut("wq_tiles", "wq_ranged_tail"),
-        "ranged_tiles": ntr, "tail_pages": TAIL_PAGES, "tail_frac": TAIL_FRAC,
+        "ranged_tiles": ntr, "ranged_pages": rp, "tail_pages": rt, "tail_frac": TAIL_FRAC,
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
         "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
@@ -329,7 +336,7 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     (the reference weave's behaviour). Work queue over split tiles, pi by
     urgency; the softmax skip launch over a ranged plan cut from the pages
     each task reads (no empty work items past the budgets), its
-    last-claimed tasks in TAIL_PAGES-page chunks; then the skip variants with
+    last-claimed tasks in shorter chunks; then the skip variants with
     pi = longest-first over tiles of twice the size by the pages each reads
     (known on the host from ctx and tau)."""
     import numpy as np
@@ -396,10 +403,11 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     ab["firing_vs_priced_out_pct"] = round(
         100.0 * (ab["firing_us"] - ab["priced_out_us"]) / ab["priced_out_us"], 2)
     res["policy_ab"] = ab
+    rp, rt = ranged_pages(2)
     rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
                                                                           kind="stable"),
-                                       tile_pages=tile_pages, tail_pages=TAIL_PAGES,
-                                       tail_frac=TAIL_FRAC, tau=b["tau"][:ntask])
+                                       tile_pages=rp, tail_pages=rt, tail_frac=TAIL_FRAC,
+                                       tau=b["tau"][:ntask])
     ntr = rtiles.shape[0]
     plane_r = SchedPlane(max_tasks=max(ntr, ntask))
     plane_r.set_lambda(0.5)
@@ -415,7 +423,8 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     us = _makespan_us(torch, sched_pd, a, stream)
     res["softmax_skip_ranged_tail"] = {
         "us": round(us, 2), "gbs_loaded": round(kept / us / 1e3, 1),
-        "gbs_ctx_equiv": round(full / us / 1e3, 1), "tiles": ntr,
+        "gbs_ctx_equiv": round(full / us / 1e3, 1), "tiles": ntr, "ranged_pages": rp,
+        "tail_pages": rt,
         "vs_tiles_pct": round(100.0 * (us - res["softmax_skip"]["us"]) / res["softmax_skip"]["us"], 2)}
     sched_pd.launch(a, stream)
     torch.cuda.synchronize()
@@ -447,10 +456,11 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
 def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_for(1)):
     """Qwen2-7B shape (Hq 28 / Hkv 4), fp8-e4m3fn KV with per-(page, head)
     scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
-    max 16384); ticket work queue over split tiles, timer on; then the same
-    queue with pi over tiles (twice the size) by the timer's per-task cycles,
-    longest first; and with pi by the tasks' page counts (known before the
-    launch) over tiles three times the size."""
+    max 16384); ticket work queue over split tiles, timer on; the same queue
+    (identity pi) over a ranged plan with shorter chunks for the tasks
+    claimed last; then the queue with pi over tiles (twice the size) by the
+    timer's per-task cycles, longest first; and with pi by the tasks' page
+    counts (known before the launch) over tiles three times the size."""
     import numpy as np
     b = workloads.workload("qwen2_7b_fp8", seed=0)
     R, ntask = 512, 512 * 4
@@ -505,8 +515,22 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
                                 out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane4,
                                 workers=W, tiles=tiles3, tile_pages=tp3)
     us_len = _makespan_us(torch, sched_pd, a_len, stream)
+    rp, rt = ranged_pages(1)
+    rtiles = sched_pd.plan_ranges_host(ctx, 16, 4, tile_pages=rp, tail_pages=rt,
+                                       tail_frac=TAIL_FRAC)
+    ntr = rtiles.shape[0]
+    plane5 = SchedPlane(max_tasks=max(ntr, ntask))
+    plane5.set_num_tasks(ntr)
+    plane5.push()
+    plane5.reset_queue(W)
+    a_rng = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane5,
+                                workers=W, tiles=rtiles)
+    us_rng = _makespan_us(torch, sched_pd, a_rng, stream)
     kv = b["kv_bytes"]
     return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
+            "wq_ranged_tail_us": round(us_rng, 2), "gbs_ranged_tail": round(kv / us_rng / 1e3, 1),
+            "ranged_tiles": ntr, "ranged_pages": rp, "tail_pages": rt, "tail_frac": TAIL_FRAC,
             "wq_tiles_lpt_timer_us": round(us_lpt, 2),
             "wq_tiles_lpt_length_us": round(us_len, 2),
             "gbs": round(kv / us_wq / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
