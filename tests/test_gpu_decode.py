@@ -692,25 +692,29 @@ def test_split_args_keep_their_workspace_when_the_cache_grows():
     """Arguments built for a small plan, then for one that needs a larger
     workspace (the cache replaces its tensor), then new allocations of the
     old size filled with garbage: relaunching the first arguments still
-    writes into their own workspace and gives the oracle's result."""
+    writes into their own workspace and gives the oracle's result. A stream
+    of its own gives the test a workspace cache entry of its own."""
     small = batch([3000, 40], seed=43)
     big = batch([3000] * 24, seed=44)
     outs = [torch.empty(2, 32, 128, device="cuda"), torch.empty(24, 32, 128, device="cuda")]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
     a_small = sched_pd.build_args(small["q"], small["k_pool"], small["v_pool"],
                                   small["block_table"], small["ctx_lens"], out=outs[0],
                                   tiles=sched_pd.plan_tiles_host([3000, 40], 16, 16, 8),
-                                  tile_pages=16)
-    ws_small = sched_pd.workspace_of(a_small)
-    n_small = ws_small.numel()
+                                  tile_pages=16, stream=s)
+    n_small = a_small._ws.numel()
     a_big = sched_pd.build_args(big["q"], big["k_pool"], big["v_pool"], big["block_table"],
                                 big["ctx_lens"], out=outs[1],
                                 tiles=sched_pd.plan_tiles_host([3000] * 24, 16, 16, 8),
-                                tile_pages=16)
-    assert a_big.workspace != a_small.workspace
-    junk = [torch.full((n_small,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(4)]
-    for _ in range(2):
-        sched_pd.launch(a_small)
-        sched_pd.launch(a_big)
+                                tile_pages=16, stream=s)
+    assert a_big.workspace != a_small.workspace            # the cache grew
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        junk = [torch.full((n_small,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(4)]
+        for _ in range(2):
+            sched_pd.launch(a_small, s)
+            sched_pd.launch(a_big, s)
     torch.cuda.synchronize()
     assert par_err(outs[0].cpu(), ref(small)) <= TOL_BF16
     assert par_err(outs[1].cpu(), ref(big)) <= TOL_BF16

@@ -2,8 +2,9 @@
 sched_paged_decode with a workspace: the same kernels over the same split
 plan, so the same bits. Two calls in a row, the second over a smaller batch
 (the scratch keeps the first call's partials; the counters are cleared per
-call), with pi and the ticket queue armed; a launch without tiles; and the
-refusals (a workspace passed in, a plan beyond the scratch)."""
+call), with pi and the ticket queue armed, over pair and ranged plans; a
+launch without tiles; and the refusals (a workspace passed in, a plan
+beyond the scratch)."""
 import ctypes
 
 import numpy as np
@@ -45,14 +46,18 @@ def _noalloc(lib, args):
     return lib.sched_paged_decode_noalloc(ctypes.byref(a), ctypes.c_void_p(s.cuda_stream))
 
 
-@pytest.mark.parametrize("workers", [0, 97])
-def test_noalloc_matches_the_workspace_entry_point(lib, workers):
+@pytest.mark.parametrize("workers,ranged", [(0, False), (97, False), (97, True)])
+def test_noalloc_matches_the_workspace_entry_point(lib, workers, ranged):
     for step, (ctx, seed) in enumerate((([16, 3000, 9000, 700, 5000, 1, 2048, 4100], 1),
                                         ([600, 33, 1500], 2))):
-        print(f"noalloc step {step} workers {workers} ctx {ctx}", flush=True)
+        print(f"noalloc step {step} workers {workers} ranged {ranged} ctx {ctx}", flush=True)
         b = _batch(ctx, seed)
         tp = 32
-        tiles = sched_pd.plan_tiles(ctx, 16, tp, 8)
+        if ranged:     # 32-page chunks, 7-page ones for the later half of the pages
+            tiles = sched_pd.plan_ranges_host(ctx, 16, 8, tile_pages=tp, tail_pages=7,
+                                              tail_frac=0.5)
+        else:
+            tiles = sched_pd.plan_tiles(ctx, 16, tp, 8)
         nt = tiles.shape[0]
         plane = SchedPlane(max_tasks=max(nt, len(ctx) * 8))
         plane.install_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32), nt)
