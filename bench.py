@@ -377,8 +377,17 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     # it (q > lambda_bw + H: urgent tasks keep pf_dist = 4 pages in flight per
     # wave instead of 2), against priced out (lambda_bw = 1000: no task
     # urgent), every task urgent and every task polite. Same bits every time.
+    # Per class (the tasks the pricing makes urgent, q > 0.6, and the rest):
+    # the timer's residency cycles per page read, summed over each task's
+    # tiles and over 5 launches of each variant -- what the action changes
+    # is how fast a task streams, which the makespan need not show.
     ab = {}
     base = None
+    kept_tok = np.repeat(ctx, 8).astype(np.int64)
+    tau_t = np.asarray(b["tau"][:ntask], dtype=np.int64)
+    kept_tok = np.where(tau_t > 0, np.minimum(kept_tok, tau_t), kept_tok)
+    task_pages = (kept_tok + 15) // 16
+    urgent = np.asarray(b["urgency"][:ntask]) > 0.6
     for name, lam, hint in (("firing", 0.5, None), ("priced_out", 1000.0, None),
                             ("all_urgent", 0.5, abi.HINT_URGENT),
                             ("all_polite", 0.5, abi.HINT_POLITE)):
@@ -390,8 +399,13 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
                                 b["ctx_lens"], out=out, plane=plane, workers=W, tiles=tiles,
                                 tile_pages=tile_pages, policy=(1.0, 1.0, 0.1), pf_dist=4)
         ab[name + "_us"] = round(_makespan_us(torch, sched_pd, a, stream), 2)
-        sched_pd.launch(a, stream)
+        plane.clear_timer()
+        for _ in range(5):
+            sched_pd.launch(a, stream)
         torch.cuda.synchronize()
+        cyc = plane.read_timer()[:ntask].numpy().astype(np.float64) / 5
+        for cls, m in (("urgent", urgent), ("other", ~urgent)):
+            ab[f"{name}_{cls}_cycles_per_page"] = round(float(cyc[m].sum() / task_pages[m].sum()), 1)
         if base is None:
             base = out.clone()
         elif not torch.equal(out, base):
@@ -402,6 +416,9 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     ab["bit_exact"] = True
     ab["firing_vs_priced_out_pct"] = round(
         100.0 * (ab["firing_us"] - ab["priced_out_us"]) / ab["priced_out_us"], 2)
+    for cls in ("urgent", "other"):
+        f_, p_ = ab[f"firing_{cls}_cycles_per_page"], ab[f"priced_out_{cls}_cycles_per_page"]
+        ab[f"firing_vs_priced_out_{cls}_cycles_pct"] = round(100.0 * (f_ - p_) / p_, 2)
     res["policy_ab"] = ab
     rp, rt = ranged_pages(2)
     rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
