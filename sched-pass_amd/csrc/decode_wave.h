@@ -7,7 +7,10 @@
 // arithmetic, so what bounds it is how many bytes are in flight and how long
 // the chain ctx -> page id -> KV takes, not compute. A workgroup of NWT waves
 // runs NWT independent tasks (no LDS, no barrier), so many tasks' chains
-// overlap and each wave keeps DEPTH 16-token chunks of loads in flight.
+// overlap and each wave keeps DEPTH 16-token chunks of loads in flight. One
+// wave per workgroup is the default: a wave that finishes a short task frees
+// its slot for the next workgroup at once, instead of waiting for the
+// longest task of its group.
 //
 // Lane layout: a K or V row of D elements is LPR = D / VN lanes of 16-byte
 // loads (VN elements each); lane = ts * LPR + ds holds dims ds*VN..+VN-1 of
@@ -39,7 +42,7 @@ namespace schedpd {
 #endif
 // Waves (tasks) per workgroup.
 #ifndef SCHED_PD_WAVE_NWT
-#define SCHED_PD_WAVE_NWT 4
+#define SCHED_PD_WAVE_NWT 1
 #endif
 
 typedef __attribute__((ext_vector_type(4))) unsigned wave_u4;
