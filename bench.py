@@ -1176,7 +1176,7 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
             if not fused:
                 cache.append(rids, k1, v1)
             # the plan is built from the lengths the decode will see
-            now = [cache.lens[r] + (1 if fused else 0) for r in rids]
+            now = cache.lengths(rids) + (1 if fused else 0)
             h0 = time.perf_counter()
             if hooks is None:
                 launch = {"tiles": sched_pd.plan_tiles_host(now, ps, tp, hkv), "tile_pages": tp}

@@ -116,6 +116,16 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream);
 int sched_paged_decode_append(const SchedDecodeArgs *a, const SchedKvAppendArgs *w,
                               void *stream);
 
+/* Block-table update on `stream`: table[row * width + col] = val for each of
+ * the n (row, col, val) triples, packed in device memory as n rows, then n
+ * cols, then n vals (int32). Entries outside [0, num_rows) x [0, width) are
+ * ignored. One small launch; n == 0 launches nothing. Returns 0, or -1 with
+ * sched_pd_last_error() set. No counterpart in the reference (its engine
+ * owns the block table): it is how PagedKvCache adds a step's new pages to
+ * the device table it keeps between steps. */
+int sched_kv_table_update(int32_t *table, int64_t num_rows, int64_t width,
+                          const int32_t *updates, uint32_t n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -839,7 +839,37 @@ bool mult8(int64_t s) { return s % 8 == 0; }
 
 } // namespace
 
+// Block-table updates: table[row * width + col] = val for each of the n
+// (row, col, val) triples packed as rows[n] | cols[n] | vals[n]. One lane per
+// update; entries outside the table are ignored.
+__global__ void __launch_bounds__(256) table_update_kernel(int32_t *table, int64_t num_rows,
+                                                           int64_t width, const int32_t *upd,
+                                                           uint32_t n) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n)
+    return;
+  const int64_t r = upd[i], c = upd[(size_t)n + i];
+  if (r < 0 || c < 0 || r >= num_rows || c >= width)
+    return;
+  table[r * width + c] = upd[2 * (size_t)n + i];
+}
+
 extern "C" {
+
+int sched_kv_table_update(int32_t *table, int64_t num_rows, int64_t width,
+                          const int32_t *updates, uint32_t n, void *stream) {
+  if (n == 0)
+    return 0;
+  if (table == nullptr || updates == nullptr || num_rows <= 0 || width <= 0)
+    return set_error(-1, "sched_kv_table_update: needs a table of num_rows x width > 0 "
+                         "and an update list");
+  hipLaunchKernelGGL(table_update_kernel, dim3((n + 255u) / 256u), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), table, num_rows, width, updates, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(-1, "sched_kv_table_update: launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
 
 void sched_kv_default_args(SchedKvAppendArgs *a) {
   if (!a)

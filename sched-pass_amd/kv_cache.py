@@ -338,6 +338,11 @@ class PagedKvCache:
             self._batch = (key, slots)
         return self._batch
 
+    def lengths(self, rids) -> np.ndarray:
+        """Tokens each request holds, as an int64 array in rids' order (a
+        copy; one gather instead of a lookup per request)."""
+        return self._len[self._slots(rids)[1]]
+
     def reserve(self, rids, counts) -> None:
         """Allocate pages so that each request has room for counts[i] more
         tokens; all or nothing."""
@@ -411,8 +416,20 @@ class PagedKvCache:
         n = len(key)
         ctx_dev, off = dev[:n], n
         if upd_n:
-            upd = dev[off:off + 3 * upd_n].view(3, upd_n)
-            t["dev"][upd[0], upd[1]] = upd[2]       # int32 indices index directly
+            upd = dev[off:off + 3 * upd_n]
+            tab = t["dev"]
+            if tab.is_cuda:
+                # one small kernel of the library (torch's indexed assignment
+                # would add two index conversions and an index_put per step)
+                rc = abi.load_library().sched_kv_table_update(
+                    ctypes.c_void_p(tab.data_ptr()), tab.shape[0], tab.shape[1],
+                    ctypes.c_void_p(upd.data_ptr()), upd_n,
+                    ctypes.c_void_p(torch.cuda.current_stream(tab.device).cuda_stream))
+                if rc != 0:
+                    raise RuntimeError(abi.last_error())
+            else:
+                u = upd.view(3, upd_n).long()
+                tab[u[0], u[1]] = u[2].int()
             off += 3 * upd_n
         out = []
         for e in extra:

@@ -151,6 +151,7 @@ SIGNATURES = {
     "sched_kv_append": (ctypes.c_int, [ctypes.POINTER(SchedKvAppendArgs), _p]),
     "sched_paged_decode_append": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs),
                                                  ctypes.POINTER(SchedKvAppendArgs), _p]),
+    "sched_kv_table_update": (ctypes.c_int, [_p, ctypes.c_int64, ctypes.c_int64, _p, _u32, _p]),
     "launch_paged_softmax": (None, [_p, _p, _p, _p, _p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, _p]),
     "paged_softmax_occupancy": (ctypes.c_int, []),

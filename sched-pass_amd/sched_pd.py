@@ -403,17 +403,31 @@ def workspace_of(args: abi.SchedDecodeArgs) -> torch.Tensor | None:
     return None
 
 
+# The last plan built: a serving loop re-plans every step, and a request's
+# chunk count changes only every tile_pages * page_size tokens.
+_LAST_PLAN = None
+
+
 def plan_tiles_host(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int) -> np.ndarray:
-    """The plan of plan_tiles as a host int32 array [num_tiles, 2]."""
+    """The plan of plan_tiles as a host int32 array [num_tiles, 2] (a new
+    array each call)."""
+    global _LAST_PLAN
     ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
                      dtype=np.int64)
     npg = (ctx + page_size - 1) // page_size
     nch = np.maximum(1, (npg + tile_pages - 1) // tile_pages)
+    key = (int(page_size), int(tile_pages), int(num_kv_heads))
+    last = _LAST_PLAN
+    if last is not None and last[0] == key and np.array_equal(last[1], nch):
+        return last[2].copy()
     per_task = np.repeat(nch, num_kv_heads)
-    tasks = np.repeat(np.arange(per_task.size, dtype=np.int64), per_task)
+    tasks = np.repeat(np.arange(per_task.size, dtype=np.int32), per_task)
     starts = np.cumsum(per_task) - per_task
-    chunks = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, per_task)
-    return np.stack([tasks, chunks], 1).astype(np.int32)
+    plan = np.empty((tasks.size, 2), np.int32)
+    plan[:, 0] = tasks
+    plan[:, 1] = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, per_task)
+    _LAST_PLAN = (key, nch, plan)
+    return plan.copy()
 
 
 def plan_tiles(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int,
@@ -499,14 +513,32 @@ def check_ranged_plan(tiles) -> None:
                          "contiguous ranges from page 0")
 
 
+def desc_order(cost) -> np.ndarray:
+    """Indices of `cost` from the largest value to the smallest, ties in
+    ascending index: np.argsort(-cost, kind="stable"), as int64. Values
+    that are exact in float32 (page counts, float32 costs) sort as one
+    packed 64-bit key per entry, the order-preserving float32 bits above
+    the index (all keys distinct, so any sort gives the stable order),
+    about 3x faster than the stable float sort; other inputs take that
+    sort."""
+    c = np.asarray(cost, dtype=np.float64).ravel()
+    n = c.size
+    f = c.astype(np.float32) + np.float32(0.0)          # -0.0 ties with +0.0
+    if n >= 1 << 32 or not np.array_equal(f, c):        # (NaN is never equal)
+        return np.argsort(-c, kind="stable")
+    bits = f.view(np.uint32).astype(np.uint64)
+    # ascending order-preserving map of the float32 bits, then descending
+    up = np.where(bits >> np.uint64(31), ~bits & np.uint64(0xFFFFFFFF), bits | np.uint64(1 << 31))
+    keys = ((np.uint64(0xFFFFFFFF) - up) << np.uint64(32)) | np.arange(n, dtype=np.uint64)
+    return (np.sort(keys) & np.uint64(0xFFFFFFFF)).astype(np.int64)
+
+
 def tile_order_by_task_key(tiles: torch.Tensor, key, descending=True) -> torch.Tensor:
     """pi over work items that follows a per-task key (e.g. urgency or
     predicted cost): tiles of higher-key tasks first, chunk order kept."""
-    t = tiles[:, 0].cpu().numpy()
+    t = tiles[:, 0].cpu().numpy() if isinstance(tiles, torch.Tensor) else np.asarray(tiles)[:, 0]
     k = np.asarray(key, dtype=np.float64)[t]
-    idx = np.arange(t.size)
-    order = np.lexsort((idx, -k if descending else k))
-    return torch.tensor(order, dtype=torch.int32)
+    return torch.from_numpy(desc_order(k if descending else -k).astype(np.int32))
 
 
 def tile_pages_loaded(tiles: torch.Tensor, ctx_lens, page_size: int, tile_pages: int,
@@ -535,8 +567,7 @@ def tile_pages_loaded(tiles: torch.Tensor, ctx_lens, page_size: int, tile_pages:
 def tile_order_lpt(cost) -> torch.Tensor:
     """pi over work items, heaviest first (ties keep index order): the
     longest-processing-time list order for the ticket queue."""
-    c = np.asarray(cost, dtype=np.float64)
-    return torch.tensor(np.argsort(-c, kind="stable"), dtype=torch.int32)
+    return torch.from_numpy(desc_order(cost).astype(np.int32))
 
 
 def launch(args: abi.SchedDecodeArgs, stream=None) -> None:

@@ -26,7 +26,7 @@ import torch
 from sched_abi import (CTRL_FLAGS_OFF, CTRL_LAMBDA_OFF, CTRL_NUM_TASKS_OFF,
                        CTRL_ORDER_SIZE_OFF, CTRL_ROWS_OFF, FLAG_TIMER_OFF,
                        HINT_AUTO, HINT_POLITE, HINT_URGENT, ROW_SIZE)
-from sched_pd import upload_into
+from sched_pd import desc_order, upload_into
 
 __all__ = ["SchedPlane", "SchedArenaError", "HINT_AUTO", "HINT_URGENT",
            "HINT_POLITE", "FLAG_TIMER_OFF", "MANIFEST"]
@@ -250,13 +250,14 @@ class SchedPlane:
         cost = np.asarray(torch.as_tensor(c).float().flatten(), np.float64)
         n = cost.size
         if block <= 1 or n <= block:
-            return torch.from_numpy(np.argsort(-cost, kind="stable").astype(np.int32))
+            return torch.from_numpy(desc_order(cost).astype(np.int32))
         group = np.arange(n) // block
         group_cost = np.bincount(group, weights=cost)
         rank = np.empty(group_cost.size, np.int64)
-        rank[np.argsort(-group_cost, kind="stable")] = np.arange(group_cost.size)
-        # primary key: the group's rank; secondary: the tile index
-        order = np.lexsort((np.arange(n), rank[group]))
+        rank[desc_order(group_cost)] = np.arange(group_cost.size)
+        # primary key: the group's rank; secondary: the tile index (a stable
+        # ascending sort by rank)
+        order = desc_order(-rank[group].astype(np.float64))
         return torch.from_numpy(order.astype(np.int32))
 
     @staticmethod
@@ -273,7 +274,7 @@ class SchedPlane:
         if R <= 0 or n <= int(R):
             return SchedPlane._grouped_lpt(torch.from_numpy(c), 16 if block is None else block)
         R = int(R)
-        by_cost = np.argsort(-c, kind="stable")
+        by_cost = desc_order(c)
         n_heavy = (R + 1) // 2
         n_light = R - n_heavy
         heavy, middle, light = np.split(by_cost, [n_heavy, n - n_light])

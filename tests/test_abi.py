@@ -379,6 +379,14 @@ def torch_tiles(t):
     return torch.from_numpy(t)
 
 
+def test_table_update_validates_without_the_gpu(schedlib):
+    p = ctypes.c_void_p
+    assert schedlib.sched_kv_table_update(None, 4, 8, None, 0, None) == 0     # nothing to do
+    assert schedlib.sched_kv_table_update(None, 4, 8, p(0x10000), 3, None) != 0
+    assert "sched_kv_table_update" in abi.last_error()
+    assert schedlib.sched_kv_table_update(p(0x10000), 4, 0, p(0x20000), 3, None) != 0
+
+
 def test_block_probe_validates_arguments_without_the_gpu(schedlib):
     buf = ctypes.c_void_p(0x10000)
     ids = (ctypes.c_int32 * 4)(0, 1, 2, 3)

@@ -268,6 +268,60 @@ def test_cache_prefill_then_decode_loop(dtype, ps, layout):
     assert sched_pd.kernel_kind(args) == "mfma"
 
 
+def test_table_update_kernel_writes_exactly_the_updates():
+    """sched_kv_table_update against numpy: in-range triples written (the
+    last of duplicates is not relied on: none here), out-of-range ones
+    ignored, n == 0 a no-op; the table around the updates untouched."""
+    import ctypes
+    import sched_abi as abi
+    lib = abi.load_library()
+    rng = np.random.default_rng(4)
+    rows, width = 37, 70
+    host = rng.integers(-5, 1000, (rows, width)).astype(np.int32)
+    tab = torch.from_numpy(host).cuda()
+    cells = rng.choice(rows * width, 300, replace=False)
+    r, c = (cells // width).astype(np.int32), (cells % width).astype(np.int32)
+    v = rng.integers(0, 1 << 30, 300).astype(np.int32)
+    r[:5] = [-1, rows, -100, rows + 3, rows + 7]  # out of range: ignored
+    c[5:9] = [-2, width, width + 1, 1 << 30]
+    upd = torch.from_numpy(np.concatenate([r, c, v])).cuda()
+    s = torch.cuda.current_stream()
+    ptr = ctypes.c_void_p
+    assert lib.sched_kv_table_update(ptr(tab.data_ptr()), rows, width, ptr(upd.data_ptr()), 300,
+                                     ptr(s.cuda_stream)) == 0
+    assert lib.sched_kv_table_update(ptr(tab.data_ptr()), rows, width, ptr(upd.data_ptr()), 0,
+                                     ptr(s.cuda_stream)) == 0
+    torch.cuda.synchronize()
+    want = host.copy()
+    ok = (r >= 0) & (r < rows) & (c >= 0) & (c < width)
+    want[r[ok], c[ok]] = v[ok]
+    assert ok.sum() == 300 - 9
+    assert np.array_equal(tab.cpu().numpy(), want)
+
+
+def test_incremental_block_table_matches_a_rebuild():
+    """Steps of one-token and multi-token appends (pages added every few
+    steps, rows of different lengths): after each, the device table the
+    cache keeps between steps equals the table rebuilt from its page lists."""
+    rng = np.random.default_rng(8)
+    cache = kv_cache.PagedKvCache(600, 2, 64, 16, dtype=torch.bfloat16)
+    rids = list(range(9))
+    for r in rids:
+        cache.add_request(r)
+    k = torch.zeros(400, 2, 64, dtype=torch.bfloat16, device="cuda")
+    cache.append(rids, k[:9 * 20], k[:9 * 20], [20] * 9)
+    for step in range(60):
+        counts = [1] * 9 if step % 7 else rng.integers(1, 40, 9).tolist()
+        cache.append(rids, k[:sum(counts)], k[:sum(counts)], counts)
+        bt, ctx = cache.block_table(rids)
+        got = bt.cpu().numpy()
+        for i, r in enumerate(rids):
+            n = len(cache.pages[r])
+            assert got[i, :n].tolist() == cache.pages[r], (step, r)
+            assert (got[i, n:] == -1).all(), (step, r)
+        assert ctx.cpu().tolist() == [cache.lens[r] for r in rids]
+
+
 def _full_size(dtype):
     """Llama-3-8B decode KV (64 requests x 2048 tokens, Hkv 8, d 128, page 16)
     written by one bulk append into a shuffled pool (fp16 rows into an fp16

@@ -392,6 +392,12 @@ def test_lengths_view_slots_and_failed_append_rollback():
     c.reserve(["a", "b", "c"], [6, 1, 9])
     c.lens.update(a=6, b=1, c=9)
     assert dict(c.lens) == {"a": 6, "b": 1, "c": 9} and len(c.lens) == 3
+    got = c.lengths(["c", "a"])
+    assert got.tolist() == [9, 6]
+    got[0] = 100                            # a copy
+    assert c.lens["c"] == 9
+    with pytest.raises(KeyError):
+        c.lengths(["a", "zz"])
     with pytest.raises(KeyError):
         c.lens["zz"] = 3
     with pytest.raises(TypeError):

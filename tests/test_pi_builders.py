@@ -43,3 +43,38 @@ def test_builders_are_permutations():
                   SchedPlane.region_order(c, int(rng.integers(0, 250)))):
             assert o.dtype == torch.int32
             assert sorted(L(o)) == list(range(n))
+
+
+def test_desc_order_is_the_stable_descending_sort():
+    """The packed-key sort against numpy's stable sort of -cost, on what the
+    builders see (float32 costs, page counts with many ties) and the cases
+    the packing must get right: signed zeros tie, infinities order, and
+    inputs that float32 cannot hold exactly (or NaN) take the plain sort."""
+    import sched_pd
+    rng = np.random.default_rng(1)
+    cases = [rng.random(3352).astype(np.float32), rng.integers(0, 129, 3352).astype(np.float64),
+             np.array([]), np.array([5.0]), np.array([0.0, -0.0, 0.0, -0.0, 1.0, -1.0]),
+             np.array([np.inf, -np.inf, 3.0, np.inf, -1.0, -np.inf]), rng.random(100),
+             np.array([1.0, np.nan, 2.0, np.nan]), rng.standard_normal(5000).astype(np.float32),
+             np.array([1e-45, 0.0, -1e-45, 3.4e38, -3.4e38], np.float32)]
+    for c in cases:
+        got = sched_pd.desc_order(c)
+        assert got.dtype == np.int64
+        assert np.array_equal(got, np.argsort(-np.asarray(c, np.float64), kind="stable")), c
+
+
+def test_plan_tiles_host_reuses_the_last_plan_safely():
+    import sched_pd
+    lens = np.array([1, 300, 2047, 2048, 2049, 5000])
+    a = sched_pd.plan_tiles_host(lens, 16, 128, 2)
+    a[:] = -1                                       # a copy: the cache is untouched
+    b = sched_pd.plan_tiles_host(lens + 1, 16, 128, 2)   # same chunk counts
+    per_req = [1, 1, 1, 2, 2, 3]                    # chunks of 128 pages after +1 token
+    assert b.shape == (2 * sum(per_req), 2)
+    assert b[:, 0].tolist() == [t for t in range(12) for _ in range(per_req[t // 2])]
+    c = sched_pd.plan_tiles_host(lens + 100, 16, 128, 2)  # request 2 crosses a boundary
+    assert c.shape[0] == b.shape[0] + 2
+    d = sched_pd.plan_tiles_host(lens + 100, 16, 64, 2)   # other tile size: rebuilt
+    assert d.shape[0] > c.shape[0]
+    e = sched_pd.plan_tiles_host(lens + 100, 16, 128, 1)  # other head count: rebuilt
+    assert e.shape[0] == c.shape[0] // 2
