@@ -9,8 +9,12 @@ Per step, as in the reference:
       the GPU has passed the probe step (event query) its timer rows' copy to
       pinned host memory is queued; once that copy is done (event query) the
       rows are folded into the controller;
-    * cadence gate: re-plan only every `plan_every` steps (and on probe
-      steps); in between the installed tables stay;
+    * cadence gate: re-plan every `plan_every` steps, on probe steps, and
+      whenever the step's split plan has a different number of work items
+      than the installed order or armed queue covers (a request crossed a
+      tile boundary: an order of the wrong size would fall back to identity
+      in the kernel, a queue would be disarmed); in between the installed
+      tables stay;
     * bind work items to requests (one per (request, kv-head) task, or the
       split-KV tiles of plan_tiles);
     * predict per-request cost, spread it over the work items;
@@ -19,8 +23,11 @@ Per step, as in the reference:
       (max/mean > clc_imbalance) and uncertain predictions
       (> clc_resid); one wave (items <= R): any live order retired, stock
       grid; otherwise the LPT order over items (in groups of lpt_block,
-      per item by default) when the previous step's kernels are done,
-      stock grid;
+      per item by default), stock grid. Tables are installed at once:
+      every write is a copy on the current stream, ordered behind the
+      previous step's kernels (the reference plugin writes host-mapped
+      tables and waits for the GPU to go idle first). Call the hooks with
+      the decode's stream current;
     * hints when the batch's KV exceeds the L2: long requests polite, short
       ones urgent, q = predicted cost;
     * push; clear the timer on probe steps.
@@ -147,29 +154,18 @@ class ServingHooks:
         self.step += 1
         self._consume_probe()
         probe = step % cfg.timer_every == 0 and self.pending is None
-        if step % cfg.plan_every != 0 and not probe:
-            # off cadence: the tables stay. The split plan is rebuilt (it is
-            # the engine's per-step plan, from host lengths), and an armed
-            # queue whose item count no longer matches is switched off.
+        # the engine's per-step plan, from host lengths
+        tiles, item_req, item_pages = self._items(kv_lens)
+        nitems = int(item_req.size)
+        live = self.armed_n if self.launch["workers"] else self.order_n
+        if step % cfg.plan_every != 0 and not probe and (live is None or live == nitems):
+            # off cadence, and the installed tables still cover the plan
             self.timer_armed = False
-            tiles = None
-            if cfg.tile_pages > 0:
-                import sched_pd
-                tiles = sched_pd.plan_tiles_host(kv_lens, cfg.page_size, cfg.tile_pages,
-                                                 self.hkv)
-            nitems = tiles.shape[0] if tiles is not None else len(kv_lens) * self.hkv
-            workers = self.launch["workers"]
-            if workers and nitems != self.armed_n:
-                p.set_num_tasks(0)
-                p.push()
-                workers = 0
-            self.launch = dict(self.launch, workers=workers, tiles=tiles)
+            self.launch = dict(self.launch, tiles=tiles)
             return self.launch
         kv_list = [int(x) for x in kv_lens]
         rids = list(rids)
         n = len(rids)
-        tiles, item_req, item_pages = self._items(kv_list)
-        nitems = int(item_req.size)
         if max(nitems, n * self.hkv) > p.N:
             # never truncate a batch to the tables (python/sched_sglang_plugin.py:
             # 99-118): a larger plane is the fix
@@ -202,10 +198,9 @@ class ServingHooks:
                 self._retire_order()
                 p.set_num_tasks(0)
             else:
-                if self.inflight is None or self.inflight.query():
-                    p.install_order(SchedPlane.region_order(cost_item, 0, block=cfg.lpt_block),
-                                    nitems)
-                    self.order_n = nitems
+                p.install_order(SchedPlane.region_order(cost_item, 0, block=cfg.lpt_block),
+                                nitems)
+                self.order_n = nitems
                 p.set_num_tasks(0)
             self._hints(kv_list, cost_req, item_req, cost_item)
         else:

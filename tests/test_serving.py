@@ -94,16 +94,15 @@ def test_one_wave_retires_order_and_stays_static():
     assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 0
 
 
-def test_queued_regime_installs_grouped_lpt_only_when_idle():
+def test_queued_regime_installs_lpt_with_a_step_in_flight():
+    # the order is a stream-ordered copy behind the previous step's kernels:
+    # installed at once, without waiting for the GPU to go idle
     p = plane()
     ev = Ev(done=False)
     h = ServingHooks(p, 1, HookConfig(plan_every=1, timer_every=100, resident=2, clc="off"),
                      event_factory=lambda: ev)
     kv = [16, 4096, 512, 64]
     h.on_batch_end()                         # a step in flight
-    h.on_batch_begin([0, 1, 2, 3], kv)
-    assert h.order_n is None                 # busy: table left alone
-    ev.done = True
     h.on_batch_begin([0, 1, 2, 3], kv)
     assert h.order_n == 4
     assert order(p, 4) == SchedPlane.region_order(torch.tensor(kv, dtype=torch.float32),
@@ -173,17 +172,33 @@ def test_split_items_spread_cost_by_pages():
     assert sorted(o) == list(range(8))
 
 
-def test_off_cadence_rebuilds_tiles_and_disarms_a_mismatched_queue():
+def test_off_cadence_replans_when_the_item_count_changes():
+    # a request crossing a tile boundary between re-plans: the armed queue
+    # (and the order) are rebuilt for the new item count, not disarmed
     p = plane()
     h = ServingHooks(p, 1, HookConfig(plan_every=4, timer_every=100, resident=2, clc="on",
                                       tile_pages=1), event_factory=Ev)
     first = h.on_batch_begin([0, 1, 2], [32, 32, 32])           # 2 one-page chunks each
     assert first["workers"] == 2 and first["tiles"].shape[0] == 6
+    g = p._generation
     same = h.on_batch_begin([0, 1, 2], [32, 32, 32])
-    assert same["workers"] == 2                                 # still matches
+    assert same["workers"] == 2 and p._generation == g         # still matches: no writes
     grown = h.on_batch_begin([0, 1, 2], [33, 32, 32])           # 3 chunks for r0
-    assert grown["tiles"].shape[0] == 7 and grown["workers"] == 0
-    assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 0
+    assert grown["tiles"].shape[0] == 7 and grown["workers"] == 2
+    assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 7 and h.armed_n == 7
+    assert ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 7
+    assert sorted(order(p, 7)) == list(range(7))
+
+
+def test_off_cadence_lpt_order_follows_the_item_count():
+    p = plane()
+    h = ServingHooks(p, 1, HookConfig(plan_every=8, timer_every=100, resident=2, clc="off",
+                                      tile_pages=1), event_factory=Ev)
+    h.on_batch_begin([0, 1, 2], [32, 16, 48])                   # 2 + 1 + 3 items
+    assert h.order_n == 6 and ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 6
+    h.on_batch_begin([0, 1, 2], [32, 17, 48])                   # r1 grows to 2 chunks
+    assert h.order_n == 7 and ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 7
+    assert sorted(order(p, 7)) == list(range(7))
 
 
 def test_oversized_batch_raises_and_begin_degrades_to_stock(capsys):
