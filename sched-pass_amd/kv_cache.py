@@ -15,6 +15,7 @@ Appends run on the GPU through the C ABI; there is no CPU path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 from collections.abc import MutableMapping
@@ -219,6 +220,11 @@ class _Lengths(MutableMapping):
 
     def __len__(self):
         return len(self._c._slot)
+
+
+def _on_stream(stream):
+    """The stream a step's work goes to: `stream`, or the current one."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
 
 
 def _host_plan(tiles):
@@ -491,7 +497,13 @@ class PagedKvCache:
         both in one launch (the decode writes the token into its page before
         reading it); other caches run the writer, then the decode. Keyword
         arguments are those of decode() (`out`, `plane`, `tiles`, ...); a
-        split plan must be built from the lengths after the append."""
+        split plan must be built from the lengths after the append. With
+        `stream`, the step's uploads, table update and launches all go to
+        that stream."""
+        with _on_stream(kw.get("stream")):
+            return self._decode_step(q, rids, k_new, v_new, **kw)
+
+    def _decode_step(self, q, rids, k_new, v_new, **kw):
         # the MFMA kernel's shapes (16-bit Q of the cache's type, 1..16 q-heads
         # per kv-head, head dim 128)
         G = q.shape[1] // self.num_kv_heads if q.shape[1] % self.num_kv_heads == 0 else 0
@@ -544,7 +556,12 @@ class PagedKvCache:
     def decode(self, q, rids, **kw):
         """One decode step over the requests' current contexts. A host split
         plan (`tiles` from sched_pd.plan_tiles_host or plan_ranges_host) is
-        uploaded together with the lengths and table update."""
+        uploaded together with the lengths and table update. With `stream`,
+        the uploads, table update and launch all go to that stream."""
+        with _on_stream(kw.get("stream")):
+            return self._decode(q, rids, **kw)
+
+    def _decode(self, q, rids, **kw):
         key, s = self._slots(rids)
         tiles = _host_plan(kw.get("tiles"))
         bt, ctx, ex = self._table_step(key, s, () if tiles is None else (tiles,))

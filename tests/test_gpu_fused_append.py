@@ -108,6 +108,34 @@ def test_fused_step_with_tiles_queue_and_pi(ranged):
         assert same(o_fused, o_sep), step
 
 
+@pytest.mark.parametrize("layout", ["tokmajor", "dmajor"])
+def test_steps_on_a_side_stream_match_the_current_stream(layout):
+    """decode_step with stream=: the step's uploads, table update, append
+    and decode all go to that stream (the fused launch, or the writer then
+    the decode for d-major V); pools and outputs equal the same steps on the
+    current stream, which is kept busy meanwhile."""
+    lens = [int(x) for x in np.random.default_rng(5).integers(1, 600, 24)]
+    (a, b), g = make_pair(torch.bfloat16, 16, lens, v_layout=layout, seed=11)
+    R = len(lens)
+    rids = list(range(R))
+    q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    side = torch.cuda.Stream()
+    busy = torch.randn(2048, 2048, device="cuda")
+    for step in range(6):
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        tiles = sched_pd.plan_tiles_host(a.lengths(rids) + 1, 16, 4, HKV)
+        o_a = a.decode_step(q, rids, k1, v1, tiles=tiles, tile_pages=4)
+        side.wait_stream(torch.cuda.current_stream())
+        for _ in range(3):
+            busy = busy @ busy / 64.0        # the current stream stays busy
+        o_b = b.decode_step(q, rids, k1, v1, tiles=tiles, tile_pages=4, stream=side)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert same(a.k_pool, b.k_pool) and same(a.v_pool, b.v_pool), (layout, step)
+        assert same(o_a, o_b), (layout, step)
+
+
 def test_caches_without_the_fused_path_fall_back_and_direct_launch_is_refused():
     lens = [5, 16, 40]
     for dtype, layout in ((torch.float8_e4m3fn, "tokmajor"), (torch.bfloat16, "dmajor")):
