@@ -18,6 +18,7 @@ from a SchedPlane (its device tables), from the C runtime's armed slots
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 import threading
 
@@ -168,6 +169,20 @@ def _need_cuda(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what} must be a device tensor (got {t.device})")
 
 
+def _on_launch_stream(fn):
+    """Run `fn` with its `stream` argument current, so that what it queues
+    on the device (uploads of host arrays, workspace clears, the queue
+    counter's priming) is ordered with the launch on that stream."""
+    @functools.wraps(fn)
+    def run(*a, stream=None, **kw):
+        if stream is None:
+            return fn(*a, stream=None, **kw)
+        with torch.cuda.stream(stream):
+            return fn(*a, stream=stream, **kw)
+    return run
+
+
+@_on_launch_stream
 def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
                mode=abi.SOFTMAX, v_layout="dmajor", page_indptr=None,
                sm_scale=None, k_scale=None, v_scale=None,
@@ -179,9 +194,12 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
     plan_tiles, or a host array from plan_tiles_host or plan_ranges_host,
     which is uploaded here; built from these ctx_lens) long tasks run as
     several work items: [n, 2] (task, chunk) rows of tile_pages pages, or
-    [n, 4] ranged rows (task, chunk | nchunks << 16, p0, p1); the workspace is taken from a cache with one per (device, stream)
-    unless one is given (`stream`: the stream the launch will use, default the
-    current one). The kernels trust the page table (as the reference's do);
+    [n, 4] ranged rows (task, chunk | nchunks << 16, p0, p1). The workspace
+    is taken from a cache with one per (device, stream) unless one is given.
+    `stream` is the stream the launch will use (default: the current one);
+    what this call queues on the device goes there too (the plan's upload,
+    workspace clears, the queue counter's priming). The kernels trust the
+    page table (as the reference's do);
     check_tables=True verifies it on the host first (check_page_table; this
     synchronises)."""
     a = abi.default_args()

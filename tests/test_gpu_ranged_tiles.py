@@ -184,3 +184,24 @@ def test_malformed_host_plan_is_refused_before_launch():
     plan[1, 2] += 1                                                  # gap in task 0's ranges
     with pytest.raises(ValueError):
         run(b, tiles=plan)
+
+
+def test_host_plan_on_a_side_stream():
+    """paged_decode(stream=side) with a host plan: the plan's upload, the
+    workspace and the launch all go to the side stream, so the result equals
+    the current stream's while that stream is kept busy."""
+    b = batch(CTX, seed=29)
+    tiles = sched_pd.plan_ranges_host(CTX, 16, 8, tile_pages=24, tail_pages=5, tail_frac=0.5)
+    want = run(b, tiles=tiles)
+    side = torch.cuda.Stream()
+    busy = torch.randn(2048, 2048, device="cuda")
+    for _ in range(3):
+        out = torch.full_like(want, float("nan"))
+        side.wait_stream(torch.cuda.current_stream())
+        for _ in range(3):
+            busy = busy @ busy / 64.0
+        sched_pd.paged_decode(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                              out=out, tiles=tiles, stream=side)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert same(out, want)
