@@ -148,6 +148,23 @@ def test_hetero_batch_full_size():
     unsplit = decode(b)
     assert par_err(unsplit.cpu(), static_tiles.cpu()) <= TOL_BF16
     check_sample(b, static_tiles, sample(ctx, 5, 2), 8)
+    # a ranged plan with short chunks for the tasks claimed last (pi by
+    # urgency): the queue gives the static grid's bits over the same plan
+    rt = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
+                                                                    kind="stable"),
+                                   tile_pages=160, tail_pages=64, tail_frac=0.1)
+    nr = rt.shape[0]
+    rplane = SchedPlane(max_tasks=max(nr, ntask))
+    rplane.set_num_tasks(0)
+    rplane.push()
+    ranged_static = decode(b, plane=rplane, tiles=rt)
+    rplane.install_order(sched_pd.tile_order_by_task_key(rt, b["urgency"]), nr)
+    rplane.set_num_tasks(nr)
+    rplane.push()
+    rplane.reset_queue(W)
+    assert torch.equal(decode(b, plane=rplane, workers=W, tiles=rt), ranged_static)
+    assert par_err(ranged_static.cpu(), static_tiles.cpu()) <= TOL_BF16
+    check_sample(b, ranged_static, sample(ctx, 5, 5), 8)
 
 
 @pytest.mark.parametrize("mode", [abi.SOFTMAX, abi.LINEAR])
@@ -188,6 +205,28 @@ def test_shed_full_size(mode):
     plane.push()
     assert torch.equal(decode(b, **kw), skip)
     check_sample(b, skip, sample(ctx, 5, 3), 8, tau=b["tau"], **okw)
+    # a ranged plan cut from the pages each task reads (pi by urgency, short
+    # chunks for the tasks claimed last): loading and masking the shed
+    # tokens gives the bits of skipping them; sampled requests match
+    rt = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
+                                                                    kind="stable"),
+                                   tile_pages=160, tail_pages=64, tail_frac=0.1,
+                                   tau=b["tau"][:ntask])
+    nr = rt.shape[0]
+    rplane = SchedPlane(max_tasks=max(nr, ntask))
+    rplane.set_lambda(0.5)
+    rplane.set_rows(q=b["urgency"], tau=b["tau"], n=ntask)
+    rplane.install_order(sched_pd.tile_order_by_task_key(rt, b["urgency"]), nr)
+    rplane.set_num_tasks(nr)
+    rplane.push()
+    rplane.reset_queue(W)
+    rkw = dict(kw, plane=rplane, tiles=rt)
+    del rkw["tile_pages"]
+    rskip = decode(b, **rkw)
+    assert torch.isfinite(rskip).all()
+    assert torch.equal(decode(b, flags=abi.FLAG_SHED_LOADS, **rkw), rskip)
+    assert par_err(rskip.cpu(), skip.cpu()) <= TOL_BF16
+    check_sample(b, rskip, sample(ctx, 5, 6), 8, tau=b["tau"], **okw)
 
 
 def test_qwen2_fp8_full_size():
@@ -214,3 +253,15 @@ def test_qwen2_fp8_full_size():
     static = decode(b)
     assert par_err(static.cpu(), wq.cpu()) <= TOL_BF16
     check_sample(b, wq, sample(ctx, 6, 4), 4)
+    # the queue over a ranged plan (320-page chunks, 128-page ones for the
+    # last tenth of the pages)
+    rt = sched_pd.plan_ranges_host(ctx, 16, 4, tile_pages=320, tail_pages=128, tail_frac=0.1)
+    nr = rt.shape[0]
+    rplane = SchedPlane(max_tasks=max(nr, ntask))
+    rplane.set_num_tasks(nr)
+    rplane.push()
+    rplane.reset_queue(W)
+    rq = decode(b, plane=rplane, workers=W, tiles=rt)
+    assert torch.isfinite(rq).all()
+    assert par_err(static.cpu(), rq.cpu()) <= TOL_BF16
+    check_sample(b, rq, sample(ctx, 6, 7), 4)
