@@ -336,7 +336,8 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     (the reference weave's behaviour). Work queue over split tiles, pi by
     urgency; the softmax skip launch over a ranged plan cut from the pages
     each task reads (no empty work items past the budgets), its
-    last-claimed tasks in shorter chunks; then the skip variants with
+    last-claimed tasks in shorter chunks (and the linear skip launch over
+    the same plan); then the skip variants with
     pi = longest-first over tiles of twice the size by the pages each reads
     (known on the host from ctx and tau)."""
     import numpy as np
@@ -447,6 +448,13 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     torch.cuda.synchronize()
     if not torch.equal(torch.isfinite(out), torch.ones_like(out, dtype=torch.bool)):
         raise AssertionError("the ranged shed launch left non-finite outputs")
+    a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                            out=lout, plane=plane_r, workers=W, tiles=rtiles, mode=abi.LINEAR,
+                            lin_w=w, policy=(1.0, 1.0, 0.1), pf_dist=4)
+    us = _makespan_us(torch, sched_pd, a, stream)
+    res["linear_skip_ranged_tail"] = {
+        "us": round(us, 2), "gbs_loaded": round(kept * 0.5 / us / 1e3, 1),
+        "vs_tiles_pct": round(100.0 * (us - res["linear_skip"]["us"]) / res["linear_skip"]["us"], 2)}
     tp2 = 2 * tile_pages
     tiles2 = sched_pd.plan_tiles(ctx, 16, tp2, 8)
     nt2 = tiles2.shape[0]
