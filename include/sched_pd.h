@@ -253,7 +253,12 @@ typedef struct SchedDecodeArgs {
    * ctx_lens of the launch: chunks a shorter context does not reach add
    * nothing (the result is unchanged), but a task whose context reaches past
    * the list's last chunk is stale -- its output rows are written as NaN and
-   * it is counted in the workspace's stale counter. */
+   * it is counted in the workspace's stale counter. A list that is not
+   * task-major (chunks out of order, a task's rows not consecutive, ranged
+   * rows disagreeing on nchunks) gives undefined output rows and may leave
+   * arrival counters nonzero: zero the workspace before its next use. The
+   * kernels read and write nothing outside the tables, the workspace and
+   * the output either way. */
   const int32_t *tiles;
   uint32_t num_tiles;
   uint32_t tile_format;  /* SCHED_PD_TILES_PAIRS (0) or SCHED_PD_TILES_RANGED */
