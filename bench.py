@@ -1121,7 +1121,8 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
     tables), stock as two launches (the writer, then the decode), the serving
     hooks observing only (bind, probe the timer 1 step in 8, never change the
     schedule), and the hooks enforcing (controller orders, queue arming,
-    re-plan every 8 steps). Reported per mode: wall
+    re-plan every 8 steps; the LPT order over 192-page tiles). Reported per
+    mode: wall
     clock per step, GPU time between events around the loop, the host time
     of the plan (stock: the split plan; hooks: begin + end), and the decode
     launches' own GPU time (each step's launch re-run back to back in a
@@ -1169,8 +1170,10 @@ def bench_serving(torch, sched_pd, workloads, steps=40, warm=8):
         fused = mode != "stock_two_launches"
         if mode in ("observe", "enforce"):
             plane = SchedPlane(max_tasks=16384)
+            # the LPT order over 1.5 MiB tiles of one kv-head's KV (192 pages)
             hooks = ServingHooks(plane, hkv, HookConfig(observe_only=mode == "observe",
-                                                        tile_pages=tp, resident=occ * cu))
+                                                        tile_pages=tp, lpt_tile_pages=3 * tp // 2,
+                                                        resident=occ * cu))
 
         host = [0.0]
         inflight = []

@@ -421,30 +421,33 @@ def workspace_of(args: abi.SchedDecodeArgs) -> torch.Tensor | None:
     return None
 
 
-# The last plan built: a serving loop re-plans every step, and a request's
-# chunk count changes only every tile_pages * page_size tokens.
-_LAST_PLAN = None
+# The last plan built per (page size, tile size, kv-heads), a few at most: a
+# serving loop re-plans every step, and a request's chunk count changes only
+# every tile_pages * page_size tokens.
+_PLANS = {}
+_PLANS_MAX = 4
 
 
 def plan_tiles_host(ctx_lens, page_size: int, tile_pages: int, num_kv_heads: int) -> np.ndarray:
     """The plan of plan_tiles as a host int32 array [num_tiles, 2] (a new
     array each call)."""
-    global _LAST_PLAN
     ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
                      dtype=np.int64)
     npg = (ctx + page_size - 1) // page_size
     nch = np.maximum(1, (npg + tile_pages - 1) // tile_pages)
     key = (int(page_size), int(tile_pages), int(num_kv_heads))
-    last = _LAST_PLAN
-    if last is not None and last[0] == key and np.array_equal(last[1], nch):
-        return last[2].copy()
+    last = _PLANS.get(key)
+    if last is not None and np.array_equal(last[0], nch):
+        return last[1].copy()
     per_task = np.repeat(nch, num_kv_heads)
     tasks = np.repeat(np.arange(per_task.size, dtype=np.int32), per_task)
     starts = np.cumsum(per_task) - per_task
     plan = np.empty((tasks.size, 2), np.int32)
     plan[:, 0] = tasks
     plan[:, 1] = np.arange(tasks.size, dtype=np.int64) - np.repeat(starts, per_task)
-    _LAST_PLAN = (key, nch, plan)
+    if key not in _PLANS and len(_PLANS) >= _PLANS_MAX:
+        _PLANS.pop(next(iter(_PLANS)))
+    _PLANS[key] = (nch, plan)
     return plan.copy()
 
 

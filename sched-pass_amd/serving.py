@@ -65,6 +65,13 @@ class HookConfig:
     l2_bytes: int = 0            # hint threshold (0 = the device's L2 size)
     page_size: int = 16
     tile_pages: int = 0          # split-KV tile (pages); 0 = one item per task
+    # Tile size of the plan under the LPT order (0 = tile_pages). With the
+    # heaviest items first the last items are short anyway, and fewer,
+    # larger items cost less start-up: on 256 requests (lognormal contexts)
+    # the enforcing loop's decode ran 371 us over 128-page tiles, 350 us
+    # over 192 and 359 us over 256, while the stock (identity) order wants
+    # the smaller tiles (410 / 419 / 423 us).
+    lpt_tile_pages: int = 0
     policy: str = "lpt"
     # Group size of the LPT order in the queued regime (the reference's
     # SCHED_LPT_BLOCK, default 16 there for locality between neighbouring
@@ -89,10 +96,11 @@ class ServingHooks:
         self.timer_armed = False
         self.pending = None      # (event, binding, rows) of an unread probe step
         self.inflight = None     # completion event of the last step
-        self.binding = None      # (rids, kv_lens, item_to_req, nitems)
+        self.binding = None      # (rids, kv_lens, nitems) of the last plan
         self.order_n = None      # items of the live order, None = identity
         self.armed_n = None      # items the armed ticket queue covers
         self.launch = {"plane": plane, "workers": 0, "tiles": None, "tile_pages": 0}
+        self.plan_tp = self.cfg.tile_pages   # tile size of the live plan
         if plane.dev.type == "cuda":
             # probe rows read back on a side stream: the readout waits for the
             # probe step only, not for the kernels queued after it
@@ -102,23 +110,34 @@ class ServingHooks:
         self._err_sites = set()
 
     # -- helpers ---------------------------------------------------------------
-    def _items(self, kv_lens):
-        """(tiles or None, item -> request index, pages per item)."""
+    def _items(self, kv_lens, tile_pages=None):
+        """(tiles or None, item -> request index, pages per item) of the
+        plan over tiles of `tile_pages` pages (default: the live plan's)."""
         n = len(kv_lens)
         ps = self.cfg.page_size
+        tp = self.plan_tp if tile_pages is None else tile_pages
         pages = -(-np.asarray(kv_lens, np.int64) // ps)
-        if self.cfg.tile_pages > 0:
+        if tp > 0:
             import sched_pd
             # built on the host (reading a device plan back would wait for
             # the previous step's kernels); the decode uploads it with its
             # other per-step arrays
-            tiles = sched_pd.plan_tiles_host(kv_lens, ps, self.cfg.tile_pages, self.hkv)
+            tiles = sched_pd.plan_tiles_host(kv_lens, ps, tp, self.hkv)
             req = tiles[:, 0] // self.hkv
-            first = tiles[:, 1] * self.cfg.tile_pages
-            item_pages = np.clip(pages[req] - first, 0, self.cfg.tile_pages)
+            first = tiles[:, 1] * tp
+            item_pages = np.clip(pages[req] - first, 0, tp)
             return tiles, req, item_pages
         req = np.repeat(np.arange(n), self.hkv)
         return None, req, pages[req]
+
+    def _count(self, kv_lens, tile_pages) -> int:
+        """Work items of the plan over tiles of `tile_pages` pages (without
+        building it)."""
+        n = len(kv_lens)
+        if tile_pages <= 0:
+            return n * self.hkv
+        pages = -(-np.asarray(kv_lens, np.int64) // self.cfg.page_size)
+        return int(np.maximum(1, -(-pages // tile_pages)).sum()) * self.hkv
 
     def _consume_probe(self) -> None:
         """Fold the pending probe's timer rows (per task) into per-request
@@ -154,18 +173,26 @@ class ServingHooks:
         self.step += 1
         self._consume_probe()
         probe = step % cfg.timer_every == 0 and self.pending is None
-        # the engine's per-step plan, from host lengths
-        tiles, item_req, item_pages = self._items(kv_lens)
-        nitems = int(item_req.size)
         live = self.armed_n if self.launch["workers"] else self.order_n
-        if step % cfg.plan_every != 0 and not probe and (live is None or live == nitems):
-            # off cadence, and the installed tables still cover the plan
+        if step % cfg.plan_every != 0 and not probe and \
+                (live is None or live == self._count(kv_lens, self.plan_tp)):
+            # off cadence, and the installed tables still cover the engine's
+            # per-step plan (from host lengths, at the live plan's tile size)
             self.timer_armed = False
+            tiles = None
+            if self.plan_tp > 0:
+                import sched_pd
+                tiles = sched_pd.plan_tiles_host(kv_lens, cfg.page_size, self.plan_tp,
+                                                 self.hkv)
             self.launch = dict(self.launch, tiles=tiles)
             return self.launch
-        kv_list = [int(x) for x in kv_lens]
+        # re-plan: the regime is decided over the configured tiles
+        kv_list = kv_lens.tolist() if isinstance(kv_lens, np.ndarray) else \
+            [int(x) for x in kv_lens]
         rids = list(rids)
         n = len(rids)
+        tp = cfg.tile_pages
+        nitems = self._count(kv_list, tp)
         if max(nitems, n * self.hkv) > p.N:
             # never truncate a batch to the tables (python/sched_sglang_plugin.py:
             # 99-118): a larger plane is the fix
@@ -175,43 +202,63 @@ class ServingHooks:
         p.set_timer_enabled(probe)
         self.timer_armed = probe
         workers = 0
+        plan = None          # (tiles, cost per item) of the plan the launch takes
         if not cfg.observe_only:
             # predicted cost per request, spread over its work items by pages
             # (observing needs no prediction)
             cost_req = self.ctl.predict(rids, kv_list)
             req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
-            cost_item = torch.as_tensor(cost_req[item_req] * item_pages / req_pages[item_req],
-                                        dtype=torch.float32)
+
+            def costed(tile_pages):
+                tiles, item_req, item_pages = self._items(kv_list, tile_pages)
+                return tiles, torch.as_tensor(
+                    cost_req[item_req] * item_pages / req_pages[item_req], dtype=torch.float32)
+
             R = cfg.resident
-            imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6)) \
-                if nitems else 1.0
-            arm = cfg.clc == "on" or (
-                cfg.clc == "auto" and R > 0 and nitems > R and imbalance > cfg.clc_imbalance
-                and self.ctl.uncertainty(rids, kv_list) > cfg.clc_resid)
+            arm = cfg.clc == "on"
+            if cfg.clc == "auto" and R > 0 and nitems > R and \
+                    self.ctl.uncertainty(rids, kv_list) > cfg.clc_resid:
+                plan = costed(tp)
+                cost_item = plan[1]
+                imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6))
+                arm = imbalance > cfg.clc_imbalance
             if arm:
-                p.install_order(SchedPlane.region_order(cost_item, R), nitems)
+                plan = plan or costed(tp)
+                p.install_order(SchedPlane.region_order(plan[1], R), nitems)
                 self.order_n = nitems
                 p.set_num_tasks(nitems)
                 self.armed_n = nitems
                 workers = R if R > 0 else 2 * p.sm_count()
+                self.plan_tp = tp
             elif R > 0 and nitems <= R:
                 self._retire_order()
                 p.set_num_tasks(0)
+                self.plan_tp = tp
             else:
-                p.install_order(SchedPlane.region_order(cost_item, 0, block=cfg.lpt_block),
+                # the LPT order, over its own (larger) tiles when configured
+                self.plan_tp = (cfg.lpt_tile_pages or tp) if tp > 0 else 0
+                if plan is None or self.plan_tp != tp:
+                    plan = costed(self.plan_tp)
+                nitems = plan[1].numel()
+                p.install_order(SchedPlane.region_order(plan[1], 0, block=cfg.lpt_block),
                                 nitems)
                 self.order_n = nitems
                 p.set_num_tasks(0)
-            self._hints(kv_list, cost_req, item_req, cost_item)
+            self._hints(kv_list, cost_req)
         else:
             self._retire_order()
             p.set_num_tasks(0)
+            self.plan_tp = tp
         p.push()
         if probe:
             p.clear_timer()
-        self.binding = (rids, kv_list, item_req, nitems)
+        self.binding = (rids, kv_list, nitems)
+        if plan is not None:
+            tiles = plan[0]
+        else:
+            tiles = self._items(kv_list, self.plan_tp)[0]
         self.launch = {"plane": p, "workers": workers, "tiles": tiles,
-                       "tile_pages": cfg.tile_pages if tiles is not None else 0}
+                       "tile_pages": self.plan_tp if tiles is not None else 0}
         return self.launch
 
     def on_batch_end(self) -> None:
@@ -259,7 +306,7 @@ class ServingHooks:
             self.plane.set_order_size(0)
             self.order_n = None
 
-    def _hints(self, kv_list, cost_req, item_req, cost_item) -> None:
+    def _hints(self, kv_list, cost_req) -> None:
         """Residency hints when the batch's KV exceeds the L2 (reference
         python/sched_sglang_plugin.py:290-301). Rows are per task: the
         kernels read policy rows by task, not by split item."""
@@ -282,7 +329,7 @@ class ServingHooks:
         """One status line (python/sched_sglang_plugin.py:302-309)."""
         b = self.binding
         u = self.ctl.uncertainty(b[0], b[1]) if b and b[0] else 0.0
-        return (f"[sched-serving] step={self.step} items={b[3] if b else 0} "
+        return (f"[sched-serving] step={self.step} items={b[2] if b else 0} "
                 f"R={self.cfg.resident} probes={self.probes_folded} uncert={u:.2f} "
                 f"hook_errors={self.hook_errors} "
                 f"mode={'observe' if self.cfg.observe_only else 'enforce'}")

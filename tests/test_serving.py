@@ -215,3 +215,24 @@ def test_oversized_batch_raises_and_begin_degrades_to_stock(capsys):
     assert out.count("begin hook error") == 1                 # first per site only
     assert "hook_errors=2" in h.stats()
     assert h.begin([0, 1], [16, 32])["plane"] is p            # recovers on a valid batch
+
+
+def test_lpt_regime_plans_over_its_own_tile_size():
+    p = plane()
+    h = ServingHooks(p, 1, HookConfig(plan_every=4, timer_every=100, resident=2, clc="off",
+                                      tile_pages=1, lpt_tile_pages=2), event_factory=Ev)
+    kv = [64, 16, 48]                                   # 4 + 1 + 3 pages
+    launch = h.on_batch_begin([0, 1, 2], kv)            # LPT regime: 2-page tiles
+    assert launch["tile_pages"] == 2 and launch["tiles"].shape[0] == 2 + 1 + 2
+    assert h.order_n == 5 and ctrl_u32(p, abi.CTRL_ORDER_SIZE_OFF) == 5
+    assert sorted(order(p, 5)) == list(range(5))
+    off = h.on_batch_begin([0, 1, 2], kv)               # off cadence: same plan size
+    assert off["tile_pages"] == 2 and off["tiles"].shape[0] == 5
+    grown = h.on_batch_begin([0, 1, 2], [64, 40, 48])   # r1 to 3 pages: re-plan at 2
+    assert grown["tile_pages"] == 2 and grown["tiles"].shape[0] == 6 and h.order_n == 6
+    # the queue regime keeps the configured tiles
+    q = ServingHooks(plane(), 1, HookConfig(plan_every=1, timer_every=100, resident=2,
+                                            clc="on", tile_pages=1, lpt_tile_pages=2),
+                     event_factory=Ev)
+    armed = q.on_batch_begin([0, 1, 2], kv)
+    assert armed["workers"] == 2 and armed["tile_pages"] == 1 and armed["tiles"].shape[0] == 8
