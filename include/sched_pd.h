@@ -326,6 +326,14 @@ int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
 /* Compute-unit count of the current device (0 on error). */
 int sched_pd_cu_count(void);
 
+/* Host-to-device copy of `bytes` from `src` to `dst` on `stream`
+ * (hipMemcpyAsync; asynchronous when `src` is pinned). No counterpart in
+ * the reference: the Python layer stages each step's small host arrays
+ * (lengths, split plan, block-table update, order, control rows) in a
+ * pinned ring and copies them with this call. Returns 0 or a hipError_t
+ * code. */
+int sched_pd_copy_to_device(void *dst, const void *src, uint64_t bytes, void *stream);
+
 /* Streaming-read ceiling probe, no counterpart in the reference: reads
  * `bytes` (16-byte aligned) of `buf` once on `stream`, writes nothing (sink
  * may be NULL). Timing it gives the device's achievable read bandwidth, the
