@@ -49,6 +49,7 @@ class CostModel:
         self.gram = np.zeros((2, 2))   # sum of [x, 1]^T [x, 1]
         self.moment = np.zeros(2)      # sum of [x, 1]^T cost
         self.samples = 0               # samples seen (not discounted)
+        self._coef = None              # (alpha, beta) of the current sums
 
     def add(self, x, cost) -> None:
         """Fold one step's samples in (arrays of equal length)."""
@@ -60,8 +61,16 @@ class CostModel:
         self.gram = self.forget * self.gram + a.T @ a
         self.moment = self.forget * self.moment + a.T @ y
         self.samples += x.size
+        self._coef = None
 
     def coefficients(self) -> tuple[float, float]:
+        """(alpha, beta), solved once per change of the sums (a serving
+        loop predicts every re-plan and folds samples one step in 8)."""
+        if self._coef is None:
+            self._coef = self._solve()
+        return self._coef
+
+    def _solve(self) -> tuple[float, float]:
         sum_x, sum_y = self.gram[0, 1], self.moment[1]
         proportional = (float(sum_y / sum_x), 0.0) if sum_x > 0 else (1.0, 0.0)
         if self.samples < 2:
