@@ -301,6 +301,14 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     a_rng = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                 plane=p_rng, workers=W, tiles=rtiles, **common)
     res["wq_ranged_tail"] = round(_makespan_us(torch, sched_pd, a_rng, stream), 2)
+    # the static grid over the same ranged plan and pi: the queue's own part
+    p_rng_st = SchedPlane(max_tasks=max(ntr, ntask))
+    p_rng_st.install_order(sched_pd.tile_order_by_task_key(rtiles, q), ntr)
+    p_rng_st.push()
+    a_rng_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                   b["ctx_lens"], plane=p_rng_st, workers=0, tiles=rtiles,
+                                   **common)
+    res["static_ranged_tail"] = round(_makespan_us(torch, sched_pd, a_rng_st, stream), 2)
     kv = b["kv_bytes"]
 
     def cut(a, b_):
@@ -318,6 +326,7 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
         "split_plus_lpt_static_cut_pct": cut("static_task", "static_tiles_lpt_pages"),
         "queue_plus_ranged_tail_cut_pct": cut("static_task", "wq_ranged_tail"),
         "ranged_tail_vs_tiles_pct": -cut("wq_tiles", "wq_ranged_tail"),
+        "queue_cut_ranged_pct": cut("static_ranged_tail", "wq_ranged_tail"),
         "ranged_tiles": ntr, "ranged_pages": rp, "tail_pages": rt, "tail_frac": TAIL_FRAC,
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
