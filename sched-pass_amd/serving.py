@@ -34,6 +34,7 @@ Per step, as in the reference:
   on_batch_end()
     * record the step's completion event; on a probe step keep (event,
       binding) pending and switch the timer off for the following steps.
+Observing only, a step without a probe launches without the lever tables.
 
 begin() / end() wrap the two hooks for an engine loop: a failure is counted,
 logged once per site, and that step runs the stock decode. A batch larger
@@ -185,7 +186,7 @@ class ServingHooks:
                 tiles = sched_pd.plan_tiles_host(kv_lens, cfg.page_size, self.plan_tp,
                                                  self.hkv)
             self.launch = dict(self.launch, tiles=tiles)
-            return self.launch
+            return self._observed(self.launch)
         # re-plan: the regime is decided over the configured tiles
         kv_list = kv_lens.tolist() if isinstance(kv_lens, np.ndarray) else \
             [int(x) for x in kv_lens]
@@ -259,7 +260,15 @@ class ServingHooks:
             tiles = self._items(kv_list, self.plan_tp)[0]
         self.launch = {"plane": p, "workers": workers, "tiles": tiles,
                        "tile_pages": self.plan_tp if tiles is not None else 0}
-        return self.launch
+        return self._observed(self.launch)
+
+    def _observed(self, launch: dict) -> dict:
+        """Observing, a step without a probe has nothing to measure and no
+        schedule to change: it launches without the lever tables (the same
+        bits, without the per-item pi and policy-row reads)."""
+        if self.cfg.observe_only and not self.timer_armed:
+            return dict(launch, plane=None, workers=0)
+        return launch
 
     def on_batch_end(self) -> None:
         """After the step's launches (python/sched_sglang_plugin.py:311-342):

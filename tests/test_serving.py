@@ -236,3 +236,18 @@ def test_lpt_regime_plans_over_its_own_tile_size():
                      event_factory=Ev)
     armed = q.on_batch_begin([0, 1, 2], kv)
     assert armed["workers"] == 2 and armed["tile_pages"] == 1 and armed["tiles"].shape[0] == 8
+
+
+def test_observing_binds_the_plane_only_on_probe_steps():
+    p = plane()
+    h = ServingHooks(p, 1, HookConfig(plan_every=2, timer_every=4, observe_only=True),
+                     event_factory=Ev)
+    planes = []
+    for step in range(8):
+        launch = h.on_batch_begin([0, 1], [100, 300])
+        planes.append(launch["plane"] is p)
+        assert launch["workers"] == 0
+        h.on_batch_end()
+    # probes at steps 0 and 4 (each read back before the next); the rest
+    # run without the tables
+    assert planes == [True, False, False, False, True, False, False, False]
