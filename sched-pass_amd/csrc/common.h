@@ -35,7 +35,7 @@ struct KParams {
   uint32_t ntasks;     // requests x kv-heads
   uint32_t tile_pages;
   uint32_t tile_ranged; // rows (task, chunk | nchunks << 16, p0, p1), else (task, chunk)
-  uint32_t *ws_stale;  // tasks found with a stale plan (item_verdict)
+  uint32_t *ws_stale;  // tasks found with a stale plan (item_stale)
   uint32_t *ws_count;  // per-task arrival counters
   float *ws_ml;        // per-work-item (m, l) per head
   void *ws_acc;        // per-work-item partial accumulators

@@ -8,9 +8,9 @@ memory: one 1 MiB device arena with the reference's offsets (ORDER 0x0,
 CTRL 0x40000, TIMER 0x80000, QUEUE 0xC0000). Consequences:
   * setters write a host mirror; push() copies it to the device in stream
     order (rows first, the generation word last, as the reference does);
-  * the timer rows are device memory already (the reference's own verdict for
-    the observation channel: device atomics are ~free, host-mapped ones cost
-    +26.5%); read_timer() is a device-to-host copy on a side stream;
+  * the timer rows are device memory already (what the reference measured
+    for the observation channel: device atomics are ~free, host-mapped ones
+    cost +26.5%); read_timer() is a device-to-host copy on a side stream;
   * clear_timer() is a fill kernel, so it is safe inside captured graphs.
 Out of scope on purpose (they exist for the reference's clang-JIT cache or
 inspect NVIDIA binaries): bake_env, arm_process_env, compute_bake_env,
