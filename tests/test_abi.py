@@ -379,6 +379,14 @@ def torch_tiles(t):
     return torch.from_numpy(t)
 
 
+def test_copy_to_device_validates_without_the_gpu(schedlib):
+    p = ctypes.c_void_p
+    assert schedlib.sched_pd_copy_to_device(None, None, 0, None) == 0         # nothing to copy
+    assert schedlib.sched_pd_copy_to_device(None, p(0x10000), 64, None) != 0
+    assert "NULL" in abi.last_error()
+    assert schedlib.sched_pd_copy_to_device(p(0x10000), None, 64, None) != 0
+
+
 def test_table_update_validates_without_the_gpu(schedlib):
     p = ctypes.c_void_p
     assert schedlib.sched_kv_table_update(None, 4, 8, None, 0, None) == 0     # nothing to do
