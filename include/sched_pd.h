@@ -326,13 +326,24 @@ int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
 /* Compute-unit count of the current device (0 on error). */
 int sched_pd_cu_count(void);
 
-/* Host-to-device copy of `bytes` from `src` to `dst` on `stream`
- * (hipMemcpyAsync; asynchronous when `src` is pinned). No counterpart in
- * the reference: the Python layer stages each step's small host arrays
- * (lengths, split plan, block-table update, order, control rows) in a
- * pinned ring and copies them with this call. Returns 0 or a hipError_t
- * code. */
+/* Host-to-device copy of `bytes` from `src` to `dst` on `stream`. No
+ * counterpart in the reference: the Python layer stages each step's small
+ * host arrays (lengths, split plan, block-table update, order, control rows)
+ * in a pinned ring and copies them with this call. When `src..src+bytes`
+ * lies in memory from sched_pd_staging_alloc, `dst` is device memory and
+ * `bytes` is at most 1 MiB, a kernel on `stream` does the copy, reading the
+ * host memory directly (no hand-off to the copy engine and back); otherwise
+ * hipMemcpyAsync (asynchronous when `src` is pinned). Either way the bytes
+ * are read when the copy runs on the stream, not at the call. Returns 0 or
+ * a hipError_t code. */
 int sched_pd_copy_to_device(void *dst, const void *src, uint64_t bytes, void *stream);
+
+/* Pinned host memory of `bytes` (1 B to 4 GiB), mapped into every device's
+ * address space and coherent, for staging uploads that
+ * sched_pd_copy_to_device runs as a kernel. No counterpart in the
+ * reference. Held until the process ends (at most 64 regions). NULL on
+ * error (sched_pd_last_error). */
+void *sched_pd_staging_alloc(uint64_t bytes);
 
 /* Streaming-read ceiling probe, no counterpart in the reference: reads
  * `bytes` (16-byte aligned) of `buf` once on `stream`, writes nothing (sink

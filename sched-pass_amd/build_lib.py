@@ -18,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libschedpd.so")
-SOURCES = ["sched_rt.hip", "paged_decode.hip", "probe.hip", "kv_append.hip",
+SOURCES = ["sched_rt.hip", "paged_decode.hip", "probe.hip", "kv_append.hip", "staging.hip",
            # the decode kernels, one instantiation group per unit (kernel_set.h)
            "kernels_bf16_page16.hip", "kernels_bf16_pageblocks.hip", "kernels_fp8.hip", "kernels_fp8_tokmajor.hip",
            "kernels_f16.hip", "kernels_f16_pageblocks.hip", "kernels_valu.hip",

@@ -679,18 +679,6 @@ int sched_pd_cu_count(void) {
   return n;
 }
 
-int sched_pd_copy_to_device(void *dst, const void *src, uint64_t bytes, void *stream) {
-  if (bytes == 0)
-    return 0;
-  if (dst == nullptr || src == nullptr)
-    return set_error(hipErrorInvalidValue, "sched_pd_copy_to_device: NULL pointer");
-  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
-                                      static_cast<hipStream_t>(stream));
-  if (e != hipSuccess)
-    return set_error(e, "sched_pd_copy_to_device: %s", hipGetErrorString(e));
-  return 0;
-}
-
 // reference python/kernels/paged_softmax.cu:47-54
 static void compat_args(SchedDecodeArgs *a, const void *kv, const void *bt, const void *nbl,
                         const void *q, void *out, int nseq, int bt_stride, int page_tokens) {

@@ -145,6 +145,7 @@ SIGNATURES = {
                                                          ctypes.POINTER(_u32)]),
     "sched_pd_cu_count": (ctypes.c_int, []),
     "sched_pd_copy_to_device": (ctypes.c_int, [_p, _p, ctypes.c_uint64, _p]),
+    "sched_pd_staging_alloc": (_p, [ctypes.c_uint64]),
     "sched_pd_read_probe": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _p]),
     "sched_pd_read_probe_blocks": (ctypes.c_int, [_p, ctypes.c_uint64, _p, _u32, _u32, _p, _p]),
     "sched_pd_last_error": (ctypes.c_char_p, []),

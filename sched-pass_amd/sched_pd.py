@@ -36,7 +36,10 @@ class _StagingRing:
     """Pinned host ring for the uploads of one stream (page-table rows and
     updates, context lengths, split plans, orders): a copy into the ring,
     then an asynchronous copy to the device on the stream, with no host
-    allocation per upload. The ring is cut into CHUNKS chunks. An upload
+    allocation per upload. The ring's memory comes from
+    sched_pd_staging_alloc (mapped into the device), so an upload of up to
+    1 MiB runs as a copy kernel on the stream rather than on the copy
+    engine. The ring is cut into CHUNKS chunks. An upload
     that does not fit in the rest of the current chunk starts at the next
     chunk boundary and may span several chunks. Leaving a chunk, and
     finishing an upload that spans chunks, records an event on the stream
@@ -48,10 +51,13 @@ class _StagingRing:
     ALIGN = 256
 
     def __init__(self, stream):
-        self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
-        self.np = self.buf.numpy()                 # the same pinned bytes
-        self.base = self.buf.data_ptr()
-        self.copy = abi.load_library().sched_pd_copy_to_device
+        lib = abi.load_library()
+        base = lib.sched_pd_staging_alloc(ctypes.c_uint64(self.BYTES))
+        if not base:
+            raise RuntimeError(abi.last_error())
+        self.base = base                           # held until the process ends
+        self.np = np.ctypeslib.as_array((ctypes.c_uint8 * self.BYTES).from_address(base))
+        self.copy = lib.sched_pd_copy_to_device
         self.stream = stream
         self.lock = threading.Lock()
         self.chunk = self.BYTES // self.CHUNKS
@@ -94,8 +100,8 @@ class _StagingRing:
             if k > 1:
                 span = range(c0, c0 + k - 1)
         self.head = start + n
-        # numpy into the pinned bytes, then one hipMemcpyAsync on the stream
-        # (torch's copy_ pair costs ~20 us of dispatch per small upload)
+        # numpy into the pinned bytes, then one copy on the stream (torch's
+        # copy_ pair costs ~20 us of dispatch per small upload)
         self.np[start:start + n] = t.reshape(-1).view(torch.uint8).numpy()
         rc = self.copy(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(self.base + start),
                        ctypes.c_uint64(n), ctypes.c_void_p(self.stream.cuda_stream))

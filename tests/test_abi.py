@@ -385,6 +385,9 @@ def test_copy_to_device_validates_without_the_gpu(schedlib):
     assert schedlib.sched_pd_copy_to_device(None, p(0x10000), 64, None) != 0
     assert "NULL" in abi.last_error()
     assert schedlib.sched_pd_copy_to_device(p(0x10000), None, 64, None) != 0
+    assert not schedlib.sched_pd_staging_alloc(0)
+    assert "sched_pd_staging_alloc" in abi.last_error()
+    assert not schedlib.sched_pd_staging_alloc((1 << 32) + 1)
 
 
 def test_table_update_validates_without_the_gpu(schedlib):

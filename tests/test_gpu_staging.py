@@ -2,11 +2,17 @@
 upload_into through a pinned ring per stream) and the asynchronous timer
 readout: the bytes arrive intact while the ring wraps several times over,
 with uploads inside one chunk and spanning chunks, with the device queue
-kept busy, on two streams, and for arrays too large for the ring."""
+kept busy, on two streams, and for arrays too large for the ring. The
+copy out of staging memory (a kernel up to 1 MiB, the copy engine above)
+moves exactly the bytes asked for at every alignment, and sees the host's
+latest writes to the same bytes."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
+import sched_abi as abi
 import sched_pd
 from sched_rt import SchedPlane
 
@@ -72,3 +78,32 @@ def test_async_timer_readout_matches_sync():
     ev.synchronize()
     assert torch.equal(rows.clone(), p.read_timer())
     assert int(rows[255]) == 255 * 7 + 3
+
+
+def test_staging_copy_sizes_alignments_and_rewrites():
+    lib = abi.load_library()
+    n = (1 << 20) + 64
+    base = lib.sched_pd_staging_alloc(ctypes.c_uint64(n))
+    assert base, abi.last_error()
+    host = np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(base))
+    dst = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(5)
+    cases = 0
+    for size in (1, 3, 4, 7, 8, 9, 255, 256, 2049, 65541, 1 << 20, (1 << 20) + 1):
+        for so, do in ((0, 0), (4, 4), (8, 0), (1, 3), (3, 8), (0, 5), (16, 1)):
+            if so + size > n or do + size > n:
+                continue
+            data = rng.integers(0, 256, size, dtype=np.uint8)
+            host[so:so + size] = data                 # rewrites bytes an earlier case copied
+            dst.zero_()
+            _busy(512)
+            rc = lib.sched_pd_copy_to_device(ctypes.c_void_p(dst.data_ptr() + do),
+                                             ctypes.c_void_p(base + so), ctypes.c_uint64(size),
+                                             ctypes.c_void_p(stream.cuda_stream))
+            assert rc == 0, abi.last_error()
+            got = dst.cpu().numpy()
+            assert np.array_equal(got[do:do + size], data), (size, so, do)
+            assert not got[:do].any() and not got[do + size:].any(), (size, so, do)
+            cases += 1
+    print(f"{cases} copies")
