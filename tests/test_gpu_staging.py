@@ -107,3 +107,38 @@ def test_staging_copy_sizes_alignments_and_rewrites():
             assert not got[:do].any() and not got[do + size:].any(), (size, so, do)
             cases += 1
     print(f"{cases} copies")
+
+
+def test_staged_copy_captured_in_a_graph_reads_the_host_bytes_at_each_replay():
+    """A serving step captured with its uploads: the copy kernel node reads
+    the staging memory when it runs, so each replay moves the bytes the host
+    wrote last (two copies: 8-byte aligned, and unaligned with an odd
+    size)."""
+    lib = abi.load_library()
+    n = 8192
+    base = lib.sched_pd_staging_alloc(ctypes.c_uint64(n))
+    assert base, abi.last_error()
+    host = np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(base))
+    host[:] = 0
+    dst = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    spans = [(0, 0, 4096), (4096 + 3, 4096 + 1, 2001)]        # (src off, dst off, bytes)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream()
+        for so, do, size in spans:
+            rc = lib.sched_pd_copy_to_device(ctypes.c_void_p(dst.data_ptr() + do),
+                                             ctypes.c_void_p(base + so), ctypes.c_uint64(size),
+                                             ctypes.c_void_p(s.cuda_stream))
+            assert rc == 0, abi.last_error()
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(9)
+    for rep in range(4):
+        host[:] = rng.integers(0, 256, n, dtype=np.uint8)
+        want = np.zeros(n, np.uint8)
+        for so, do, size in spans:
+            want[do:do + size] = host[so:so + size]
+        dst.zero_()
+        _busy(256)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.cpu().numpy(), want), rep
