@@ -39,7 +39,8 @@ class _StagingRing:
     allocation per upload. The ring's memory comes from
     sched_pd_staging_alloc (mapped into the device), so an upload of up to
     1 MiB runs as a copy kernel on the stream rather than on the copy
-    engine. The ring is cut into CHUNKS chunks. An upload
+    engine (past the library's 64 staging regions, torch's pinned memory
+    and the copy engine). The ring is cut into CHUNKS chunks. An upload
     that does not fit in the rest of the current chunk starts at the next
     chunk boundary and may span several chunks. Leaving a chunk, and
     finishing an upload that spans chunks, records an event on the stream
@@ -53,10 +54,16 @@ class _StagingRing:
     def __init__(self, stream):
         lib = abi.load_library()
         base = lib.sched_pd_staging_alloc(ctypes.c_uint64(self.BYTES))
-        if not base:
-            raise RuntimeError(abi.last_error())
-        self.base = base                           # held until the process ends
-        self.np = np.ctypeslib.as_array((ctypes.c_uint8 * self.BYTES).from_address(base))
+        if base:                                   # held until the process ends
+            self.buf = None
+            self.np = np.ctypeslib.as_array((ctypes.c_uint8 * self.BYTES).from_address(base))
+        else:
+            # the library's regions are used up (64 rings): torch's pinned
+            # memory, which the copy engine moves
+            self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
+            self.np = self.buf.numpy()
+            base = self.buf.data_ptr()
+        self.base = base
         self.copy = lib.sched_pd_copy_to_device
         self.stream = stream
         self.lock = threading.Lock()

@@ -142,3 +142,23 @@ def test_staged_copy_captured_in_a_graph_reads_the_host_bytes_at_each_replay():
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(dst.cpu().numpy(), want), rep
+
+
+def test_ring_without_staging_memory_falls_back_to_the_copy_engine(monkeypatch):
+    """When the library has no staging region left, a ring takes torch's
+    pinned memory and the same uploads arrive through hipMemcpyAsync."""
+    lib = abi.load_library()
+    monkeypatch.setattr(lib, "sched_pd_staging_alloc", lambda n: None)
+    ring = sched_pd._StagingRing(torch.cuda.current_stream())
+    assert ring.buf is not None
+    rng = np.random.default_rng(4)
+    sent = [rng.integers(0, 2**31 - 1, int(k), dtype=np.int64).astype(np.int32)
+            for k in rng.integers(1, 5000, 30)]
+    got = []
+    for a in sent:
+        out = torch.empty(a.size, dtype=torch.int32, device="cuda")
+        assert ring.put(torch.from_numpy(a), out)
+        got.append(out)
+    torch.cuda.synchronize()
+    for a, t in zip(sent, got):
+        assert np.array_equal(t.cpu().numpy(), a)
