@@ -197,7 +197,7 @@ def ranged_pages(elem_bytes):
     return RANGED_BYTES // per_page, TAIL_BYTES // per_page
 
 
-def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=10):
+def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=20):
     """Min over `reps` of the mean of `launches` back-to-back launches (HIP
     events on the launch stream), microseconds."""
     for _ in range(3):
@@ -799,7 +799,7 @@ def bench_pi_makespan(torch, sched_pd, batch_sizes=(256, 1024, 4096, 8192)):
     GQA decode (Hq 16 / Hkv 2, d 128, page 16), fp16 Q and NHD cache, pages
     per request ~ exp(N(2.6, 1.1)) clipped to [1, 512], static grid; pi
     identity, longest-first and shortest-first by pages (over (request,
-    kv-head) tasks). Min over 5 repeats of the mean of 10 launches."""
+    kv-head) tasks). Min over 5 repeats of the mean of 20 launches."""
     import numpy as np
     from flashinfer_compat import BatchDecodeWithPagedKVCacheWrapper
     from sched_rt import SchedPlane
