@@ -76,6 +76,7 @@ class SchedPlane:
         self._ctrl_host = bytearray(self.ctrl_bytes)
         self._rows_end = self.ctrl_bytes  # mirror bytes push() must copy (rows written)
         self._generation = 0
+        self._pushed_hdr = None    # header body (bytes 4 .. rows) last published
         self._timer_dev = None      # separate device row buffer (use_device_timer)
         self._timer_stream = None
         self._order_dev = None      # separate device order table (use_device_order)
@@ -177,7 +178,13 @@ class SchedPlane:
 
     def push(self) -> None:
         """Publish the mirror (generation++): rows and header body first, the
-        generation word last, in stream order."""
+        generation word last, in stream order. Nothing is queued when no row
+        was written since the last push and the header body holds the bytes
+        last published (the kernels only read the block)."""
+        hdr = bytes(self._ctrl_host[4:CTRL_ROWS_OFF])
+        if self._rows_end == 0 and hdr == self._pushed_hdr:
+            return
+        self._pushed_hdr = hdr
         self._generation += 1
         struct.pack_into("<I", self._ctrl_host, 0, self._generation)
         # the header plus the rows written since the last push (rows past

@@ -34,7 +34,9 @@ Per step, as in the reference:
   on_batch_end()
     * record the step's completion event; on a probe step keep (event,
       binding) pending and switch the timer off for the following steps.
-Observing only, a step without a probe launches without the lever tables.
+Observing only, a step without a probe launches without the lever tables,
+and the plane's timer flag stays on, so the hooks publish the plane once
+and then only when the batch's task count or order changes.
 
 begin() / end() wrap the two hooks for an engine loop: a failure is counted,
 logged once per site, and that step runs the stock decode. A batch larger
@@ -200,7 +202,9 @@ class ServingHooks:
             raise RuntimeError(f"batch of {nitems} work items / {n * self.hkv} tasks exceeds "
                                f"the plane's max_tasks {p.N}")
 
-        p.set_timer_enabled(probe)
+        # observing, the plane is bound on probe steps only, so its timer
+        # flag stays on and a re-plan publishes nothing new
+        p.set_timer_enabled(probe or cfg.observe_only)
         self.timer_armed = probe
         workers = 0
         plan = None          # (tiles, cost per item) of the plan the launch takes
@@ -279,8 +283,10 @@ class ServingHooks:
         self.inflight = ev
         if self.timer_armed:
             self.pending = (ev, self.binding, None)
-            self.plane.set_timer_enabled(False)
-            self.plane.push()
+            if not self.cfg.observe_only:
+                # enforcing, the next steps launch with the plane: timer off
+                self.plane.set_timer_enabled(False)
+                self.plane.push()
 
     # -- engine-facing wrappers: a hook never takes the serving loop down --------
     STOCK = {"plane": None, "workers": 0, "tiles": None, "tile_pages": 0}

@@ -251,3 +251,44 @@ def test_observing_binds_the_plane_only_on_probe_steps():
     # probes at steps 0 and 4 (each read back before the next); the rest
     # run without the tables
     assert planes == [True, False, False, False, True, False, False, False]
+
+
+def test_push_without_changes_publishes_nothing():
+    p = plane()
+    p.set_num_tasks(5)
+    p.push()
+    g = p._generation
+    p.push()
+    p.set_num_tasks(5)                        # the same bytes
+    p.push()
+    assert p._generation == g
+    p.set_row(3, q=1.0)                       # a row written
+    p.push()
+    assert p._generation == g + 1
+    p.set_timer_enabled(False)                # a header change
+    p.push()
+    assert p._generation == g + 2
+    assert ctrl_u32(p, abi.CTRL_NUM_TASKS_OFF) == 5
+    assert ctrl_u32(p, abi.CTRL_FLAGS_OFF) & abi.FLAG_TIMER_OFF
+    assert struct.unpack_from("<fHBB", bytes(p._ctrl_dev.numpy()),
+                              abi.CTRL_ROWS_OFF + 3 * abi.ROW_SIZE)[0] == 1.0
+
+
+def test_observing_publishes_the_plane_once():
+    """Observing binds the plane on probe steps only, with the timer on; the
+    plane is published on the first step and not again while the batch keeps
+    its shape."""
+    p = plane()
+    h = ServingHooks(p, 2, HookConfig(observe_only=True, plan_every=4, timer_every=4),
+                     event_factory=Ev)
+    rids, kv = [10, 11, 12], [100, 900, 300]
+    gens, bound = [], []
+    for _ in range(13):
+        launch = h.on_batch_begin(rids, kv)
+        bound.append(launch["plane"] is p)
+        assert bound[-1] == h.timer_armed
+        h.on_batch_end()
+        gens.append(p._generation)
+    assert gens == [gens[0]] * len(gens)
+    assert sum(bound) >= 2 and h.probes_folded >= 1
+    assert ctrl_u32(p, abi.CTRL_FLAGS_OFF) & abi.FLAG_TIMER_OFF == 0
