@@ -330,12 +330,12 @@ int sched_pd_cu_count(void);
  * counterpart in the reference: the Python layer stages each step's small
  * host arrays (lengths, split plan, block-table update, order, control rows)
  * in a pinned ring and copies them with this call. When `src..src+bytes`
- * lies in memory from sched_pd_staging_alloc, `dst` is device memory and
- * `bytes` is at most 1 MiB, a kernel on `stream` does the copy, reading the
- * host memory directly (no hand-off to the copy engine and back); otherwise
- * hipMemcpyAsync (asynchronous when `src` is pinned). Either way the bytes
- * are read when the copy runs on the stream, not at the call. Returns 0 or
- * a hipError_t code. */
+ * lies in memory from sched_pd_staging_alloc, `dst..dst+bytes` lies in one
+ * device allocation and `bytes` is at most 1 MiB, a kernel on `stream` does
+ * the copy, reading the host memory directly (no hand-off to the copy
+ * engine and back); otherwise hipMemcpyAsync (asynchronous when `src` is
+ * pinned). Either way the bytes are read when the copy runs on the stream,
+ * not at the call. Returns 0 or a hipError_t code. */
 int sched_pd_copy_to_device(void *dst, const void *src, uint64_t bytes, void *stream);
 
 /* Pinned host memory of `bytes` (1 B to 4 GiB), mapped into every device's

@@ -65,13 +65,27 @@ uintptr_t staged_device_address(const void *src, uint64_t bytes) {
   return 0;
 }
 
-bool is_device_memory(const void *p) {
+// True when [p, p + bytes) lies in one device allocation. hipMemcpyAsync
+// refuses a copy past its destination's allocation; the kernel would write
+// past it, so it runs only where the range is known to fit.
+bool fits_device_allocation(const void *p, uint64_t bytes) {
   hipPointerAttribute_t at;
   if (hipPointerGetAttributes(&at, p) != hipSuccess) {
     (void)hipGetLastError();       // an unknown pointer is an answer, not an error
     return false;
   }
-  return at.type == hipMemoryTypeDevice;
+  if (at.type != hipMemoryTypeDevice)
+    return false;
+  hipDeviceptr_t dp = reinterpret_cast<hipDeviceptr_t>(const_cast<void *>(p));
+  uintptr_t start = 0;
+  size_t size = 0;
+  if (hipPointerGetAttribute(&start, HIP_POINTER_ATTRIBUTE_RANGE_START_ADDR, dp) != hipSuccess ||
+      hipPointerGetAttribute(&size, HIP_POINTER_ATTRIBUTE_RANGE_SIZE, dp) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const uintptr_t d = reinterpret_cast<uintptr_t>(p);
+  return start != 0 && d >= start && bytes <= size && d - start <= size - bytes;
 }
 
 template <typename W>
@@ -130,7 +144,7 @@ int sched_pd_copy_to_device(void *dst, const void *src, uint64_t bytes, void *st
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const uintptr_t dsrc = bytes <= kKernelCopyMax ? staged_device_address(src, bytes) : 0;
   hipError_t e;
-  if (dsrc != 0 && is_device_memory(dst)) {
+  if (dsrc != 0 && fits_device_allocation(dst, bytes)) {
     const uintptr_t d = reinterpret_cast<uintptr_t>(dst);
     if (((d | dsrc) & 7u) == 0)
       e = launch_copy<uint64_t>(d, dsrc, bytes, s);
