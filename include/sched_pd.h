@@ -117,6 +117,29 @@ bool sched_rt_queue_reset(uint32_t workers);
 unsigned long long sched_rt_timer(unsigned i);
 void sched_rt_timer_clear(void);
 
+/* Rows a caller's tables may hold for sched_rt_bind_tables: the reference
+ * plane's per-table window (python/sched_rt.py:89). */
+#define SCHED_RT_BIND_MAX_TASKS 16384
+
+/* Point the four __sched_* slots at caller-owned device tables instead of the
+ * runtime's own, no counterpart in the reference: its Python plane
+ * (python/sched_rt.py:489-555) bakes the addresses of its arena into a
+ * JIT-compiled kernel, so that kernel's levers follow the plane. Here the
+ * launchers that take their levers from the slots (launch_paged_softmax, and
+ * sched_paged_decode with SCHED_PD_FLAG_RT_TABLES) then run with these
+ * tables: order i32[max_tasks], ctrl in the SchedCtrl layout with max_tasks
+ * rows, timer u64[max_tasks], queue one u32. Any pointer may be NULL (that
+ * lever's stock behaviour). Task ids >= max_tasks (at most
+ * SCHED_RT_BIND_MAX_TASKS) get no levers. The tables' owner writes them
+ * (e.g. SchedPlane.push): the sched_rt_set_* / push / timer calls keep
+ * working on the runtime's own tables, which stay allocated. A queue launch
+ * over bound tables starts `workers` workgroups whatever num_tasks the owner
+ * pushed (the kernels take the stock path when it is 0). sched_rt_init()
+ * puts the runtime's own tables back, sched_rt_disarm() nulls the slots.
+ * Synchronous; returns false on error. */
+bool sched_rt_bind_tables(const int32_t *order, const void *ctrl, unsigned long long *timer,
+                          uint32_t *queue, uint32_t max_tasks);
+
 /* Introspection, no counterpart in the reference (its tables are static
  * globals of the including translation unit): the device addresses the
  * __sched_* slots hold right now (0 when disarmed), read back from the device

@@ -681,11 +681,16 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     T.w = w;
     if constexpr (!FP8 && !LINEAR && VT) {
       // fused append: the item holding the new token writes it (in the
-      // wave that streams its page) before streaming
+      // wave that streams its page) before streaming. A stale plan may hold
+      // no item for that page; then chunk 0's item writes it too, so the
+      // cache gets the token whatever the plan (the task's output is NaN
+      // then, and a second writer stores the same bytes).
       if (P.app_k != nullptr && T.n > 0u) {
         const uint32_t pos = T.n - 1u, pg = pos / P.ps;
-        if (P.tiles == nullptr ||
-            (P.tile_ranged ? pg >= I.p0 && pg < I.p1 : I.chunk == pg / P.tile_pages)) {
+        const bool holds =
+            P.tiles == nullptr ||
+            (P.tile_ranged ? pg >= I.p0 && pg < I.p1 : I.chunk == pg / P.tile_pages);
+        if (holds || (stale && I.chunk == 0u)) {
           const uint32_t rel = (PG ? pos / 16u : pg) - T.p0;
           if (rel % (uint32_t)NW == w)
             append_token<F16>(P, T.r, T.h,

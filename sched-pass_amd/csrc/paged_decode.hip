@@ -251,7 +251,7 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     kp->L.ctrl = static_cast<const uint8_t *>(s.ctrl);
     kp->L.timer = s.timer;
     kp->L.queue = s.queue;
-    kp->L.max_tasks = SCHED_MAX_TASKS;
+    kp->L.max_tasks = s.rows;
     if (!rt_slot_addresses(kp->L.rt_slot))
       return hipErrorInvalidSymbol;
     kp->L.rt = 1u;
@@ -451,18 +451,20 @@ int sched_paged_decode_noalloc(const SchedDecodeArgs *a, void *stream) {
   KParams kp;
   Selected sel;
   SchedDecodeArgs b = *a;
-  // validate first with a stand-in workspace address (nothing is launched)
+  // validate first with a stand-in workspace address and an unbounded size
+  // (nothing is launched): prepare checks the head counts before anything
+  // divides by them, then the scratch's size is checked against the layout
   b.workspace = reinterpret_cast<void *>(uintptr_t(256));
-  b.workspace_bytes = kScratchBytes;
+  b.workspace_bytes = ~uint64_t(0);
+  int rc = prepare(&b, &kp, &sel);
+  if (rc)
+    return rc;
   const WsLayout W = ws_layout(a);
   if (W.total > kScratchBytes)
     return set_error(hipErrorInvalidValue,
                      "this launch needs %llu bytes of split workspace; the no-allocation entry "
                      "point holds %llu (use sched_paged_decode with a workspace)",
                      (unsigned long long)W.total, (unsigned long long)kScratchBytes);
-  int rc = prepare(&b, &kp, &sel);
-  if (rc)
-    return rc;
   int dev = 0;
   void *ptr = scratch_address(&dev);
   if (ptr == nullptr)
@@ -550,8 +552,11 @@ static int launch_decode(const SchedDecodeArgs *a, const AppendRows *app, void *
   // must then cover every task. For the runtime's tables the pushed num_tasks
   // is known here too (0 = the per-step disarm switch).
   bool wq = a->workers > 0 && kp.L.queue != nullptr && kp.L.ctrl != nullptr;
-  if (wq && (a->flags & SCHED_PD_FLAG_RT_TABLES) && rt_snapshot().num_tasks == 0)
-    wq = false;
+  if (wq && (a->flags & SCHED_PD_FLAG_RT_TABLES)) {
+    const RtSnapshot s = rt_snapshot();
+    if (s.num_tasks_known && s.num_tasks == 0)
+      wq = false;
+  }
   const uint32_t slots = wq ? a->workers : nitems;
   const uint32_t grid = (slots + sel.per_block - 1) / sel.per_block;
   kp.L.wq = wq ? 1u : 0u;

@@ -12,8 +12,10 @@ struct RtSnapshot {
   const void *ctrl;
   unsigned long long *timer;
   uint32_t *queue;
-  uint32_t num_tasks; // host mirror of ctrl.num_tasks as last pushed
-  bool armed;
+  uint32_t num_tasks;   // host mirror of ctrl.num_tasks as last pushed
+  uint32_t rows;        // rows of order / ctrl / timer (the kernels' task bound)
+  bool num_tasks_known; // false while caller tables are bound (their owner pushes it)
+  bool armed;           // the slots hold tables (the runtime's own or bound ones)
 };
 
 RtSnapshot rt_snapshot();

@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unistd.h>
 
@@ -46,6 +47,14 @@ struct RtState {
   // opt-in pinned host copy of the timer rows for external readers
   unsigned long long *h_timer = nullptr;
   bool mirror = false;
+  // caller-owned tables in the slots (sched_rt_bind_tables): their pointers
+  // and row count; the runtime's own buffers stay allocated meanwhile
+  bool bound = false;
+  const int32_t *b_order = nullptr;
+  const void *b_ctrl = nullptr;
+  unsigned long long *b_timer = nullptr;
+  uint32_t *b_queue = nullptr;
+  uint32_t b_rows = 0;
 };
 
 RtState g_rt;
@@ -54,21 +63,26 @@ thread_local std::string g_err;
 // /tmp/sched_rt_<pid>.json (reference runtime/sched_rt.h:170-186): the table
 // addresses, plus timer_host_va, the host copy of the timer rows an external
 // reader can consume with no GPU call (0 unless the mirror is on).
+// While caller tables are bound, the file names them and their row count
+// (and no host copy: the mirror follows the runtime's own rows only).
 void publish() {
   const RtState &S = g_rt;
+  const bool b = S.bound;
+  const uint32_t rows = b ? S.b_rows : (uint32_t)SCHED_MAX_TASKS;
   char path[256];
   std::snprintf(path, sizeof path, "/tmp/sched_rt_%d.json", (int)getpid());
   if (FILE *f = std::fopen(path, "w")) {
     std::fprintf(f,
-                 "{\"pid\":%d,\"max_tasks\":%d,\"order_dev\":%llu,\"ctrl_dev\":%llu,"
+                 "{\"pid\":%d,\"max_tasks\":%u,\"order_dev\":%llu,\"ctrl_dev\":%llu,"
                  "\"timer_dev\":%llu,\"timer_host_va\":%llu,\"timer_bytes\":%zu,"
-                 "\"queue_dev\":%llu}\n",
-                 (int)getpid(), SCHED_MAX_TASKS,
-                 (unsigned long long)(uintptr_t)S.d_order, (unsigned long long)(uintptr_t)S.d_ctrl,
-                 (unsigned long long)(uintptr_t)S.d_timer,
-                 (unsigned long long)(uintptr_t)(S.mirror ? S.h_timer : nullptr),
-                 (size_t)SCHED_MAX_TASKS * sizeof(unsigned long long),
-                 (unsigned long long)(uintptr_t)S.d_queue);
+                 "\"queue_dev\":%llu,\"bound\":%d}\n",
+                 (int)getpid(), rows,
+                 (unsigned long long)(uintptr_t)(b ? (const void *)S.b_order : S.d_order),
+                 (unsigned long long)(uintptr_t)(b ? S.b_ctrl : (const void *)S.d_ctrl),
+                 (unsigned long long)(uintptr_t)(b ? S.b_timer : S.d_timer),
+                 (unsigned long long)(uintptr_t)(S.mirror && !b ? S.h_timer : nullptr),
+                 (size_t)rows * sizeof(unsigned long long),
+                 (unsigned long long)(uintptr_t)(b ? S.b_queue : S.d_queue), b ? 1 : 0);
     std::fclose(f);
   }
 }
@@ -88,7 +102,8 @@ bool rt_check(hipError_t e, const char *what) {
       return false;                                                            \
   } while (0)
 
-bool write_slots(int32_t *order, SchedCtrl *ctrl, unsigned long long *timer, uint32_t *queue) {
+bool write_slots(const int32_t *order, const void *ctrl, unsigned long long *timer,
+                 uint32_t *queue) {
   RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_task_order), &order, sizeof(void *)));
   RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_ctrl), &ctrl, sizeof(void *)));
   RT_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(__sched_timer), &timer, sizeof(void *)));
@@ -120,6 +135,7 @@ bool rt_slot_addresses(uint64_t out[4]) {
   constexpr int kMaxDev = 64;
   static uint64_t cache[kMaxDev][4];
   static bool have[kMaxDev];
+  static std::mutex mu;
   int dev = 0;
   if (!rt_check(hipGetDevice(&dev), "hipGetDevice"))
     return false;
@@ -127,6 +143,9 @@ bool rt_slot_addresses(uint64_t out[4]) {
     set_error_text("[sched_rt] device index beyond the runtime's table");
     return false;
   }
+  // threads making their first launch on a device at once fill the entry
+  // under the lock, so none reads it half written
+  std::lock_guard<std::mutex> lock(mu);
   if (!have[dev]) {
     void *p[4] = {nullptr, nullptr, nullptr, nullptr};
     if (!rt_check(hipGetSymbolAddress(&p[0], HIP_SYMBOL(__sched_task_order)),
@@ -148,7 +167,7 @@ bool rt_slot_addresses(uint64_t out[4]) {
 }
 
 int rt_after_launch(void *stream) {
-  if (!g_rt.mirror || g_rt.h_timer == nullptr || !g_rt.armed)
+  if (!g_rt.mirror || g_rt.h_timer == nullptr || !g_rt.armed || g_rt.bound)
     return 0;
   hipError_t e = hipMemcpyAsync(g_rt.h_timer, g_rt.d_timer,
                                 SCHED_MAX_TASKS * sizeof(unsigned long long),
@@ -160,8 +179,17 @@ int rt_after_launch(void *stream) {
 
 RtSnapshot rt_snapshot() {
   RtSnapshot s{};
-  s.armed = g_rt.armed;
-  if (g_rt.armed) {
+  s.armed = g_rt.armed || g_rt.bound;
+  s.rows = SCHED_MAX_TASKS;
+  s.num_tasks_known = true;
+  if (g_rt.bound) {
+    s.order = g_rt.b_order;
+    s.ctrl = g_rt.b_ctrl;
+    s.timer = g_rt.b_timer;
+    s.queue = g_rt.b_queue;
+    s.rows = g_rt.b_rows;
+    s.num_tasks_known = false; // the tables' owner pushes num_tasks
+  } else if (g_rt.armed) {
     s.order = g_rt.d_order;
     s.ctrl = g_rt.d_ctrl;
     s.timer = g_rt.d_timer;
@@ -180,7 +208,7 @@ const char *sched_pd_last_error(void) { return g_err.c_str(); }
 // reference runtime/sched_rt.h:121-189
 bool sched_rt_init(void) {
   RtState &S = g_rt;
-  if (S.armed)
+  if (S.armed && !S.bound)
     return true;
   if (S.d_order == nullptr) {
     RT_CHECK(hipMalloc(&S.d_order, SCHED_MAX_TASKS * sizeof(int32_t)));
@@ -202,8 +230,9 @@ bool sched_rt_init(void) {
   }
   if (!write_slots(S.d_order, S.d_ctrl, S.d_timer, S.d_queue))
     return false;
-  publish();
+  S.bound = false;
   S.armed = true;
+  publish();
   return true;
 }
 
@@ -212,6 +241,34 @@ bool sched_rt_disarm(void) {
   if (!write_slots(nullptr, nullptr, nullptr, nullptr))
     return false;
   g_rt.armed = false;
+  g_rt.bound = false;
+  return true;
+}
+
+// No counterpart in the reference, whose Python plane bakes its table
+// addresses into a JIT-compiled kernel (python/sched_rt.py:489-555): here
+// the plane's tables go into the slots the launchers read at every launch.
+bool sched_rt_bind_tables(const int32_t *order, const void *ctrl, unsigned long long *timer,
+                          uint32_t *queue, uint32_t max_tasks) {
+  if (max_tasks > SCHED_RT_BIND_MAX_TASKS) {
+    char buf[160];
+    std::snprintf(buf, sizeof buf,
+                  "[sched_rt] sched_rt_bind_tables failed: max_tasks %u > %u", max_tasks,
+                  (unsigned)SCHED_RT_BIND_MAX_TASKS);
+    schedpd::set_error_text(buf);
+    return false;
+  }
+  if (!write_slots(order, ctrl, timer, queue))
+    return false;
+  RtState &S = g_rt;
+  S.b_order = order;
+  S.b_ctrl = ctrl;
+  S.b_timer = timer;
+  S.b_queue = queue;
+  S.b_rows = max_tasks;
+  S.bound = true;
+  S.armed = false;
+  publish();
   return true;
 }
 

@@ -234,6 +234,8 @@ def _host_plan(tiles):
         return None
     if tiles.ndim == 2 and tiles.shape[1] == 4:
         sched_pd.check_ranged_plan(tiles)
+    elif tiles.ndim == 2 and tiles.shape[1] == 2:
+        sched_pd.check_pair_plan(tiles)
     return tiles
 
 
@@ -525,6 +527,11 @@ class PagedKvCache:
         try:
             self._len[s] += 1
             tiles = _host_plan(kw.get("tiles"))
+            if tiles is not None:
+                # a stale plan would leave this step's output rows NaN: refuse
+                # it before anything is written
+                sched_pd.check_plan_covers(tiles, self._len[s], self.page_size,
+                                           self.num_kv_heads, kw.get("tile_pages", 0))
             bt, ctx, ex = self._table_step(key, s, () if tiles is None else (tiles,))
             if tiles is not None:
                 kw["tiles"] = ex[0]      # uploaded with the lengths and table update

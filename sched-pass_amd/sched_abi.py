@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libschedpd.so")
 
 # --- runtime contract (include/sched_pd.h; reference runtime/sched_rt.h) ----
 SCHED_MAX_TASKS = 4096
+RT_BIND_MAX_TASKS = 16384   # SCHED_RT_BIND_MAX_TASKS
 CTRL_NUM_TASKS_OFF = 4
 CTRL_LAMBDA_OFF = 8
 CTRL_FLAGS_OFF = 24
@@ -134,6 +135,7 @@ SIGNATURES = {
     "sched_rt_set_timer_host_mirror": (_c_bool, [_c_bool]),
     "sched_rt_slot_addresses": (_c_bool, [ctypes.POINTER(ctypes.c_uint64)]),
     "sched_rt_timer_host_va": (ctypes.c_uint64, []),
+    "sched_rt_bind_tables": (_c_bool, [_p, _p, _p, _p, _u32]),
     "sched_pd_default_args": (None, [ctypes.POINTER(SchedDecodeArgs)]),
     "sched_paged_decode": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),
     "sched_paged_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(SchedDecodeArgs), _p]),

@@ -17,6 +17,7 @@ from a SchedPlane (its device tables), from the C runtime's armed slots
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import functools
 import math
@@ -51,19 +52,22 @@ class _StagingRing:
     CHUNKS = 16
     ALIGN = 256
 
-    def __init__(self, stream):
+    def __init__(self, stream, memory=None):
         lib = abi.load_library()
-        base = lib.sched_pd_staging_alloc(ctypes.c_uint64(self.BYTES))
-        if base:                                   # held until the process ends
-            self.buf = None
-            self.np = np.ctypeslib.as_array((ctypes.c_uint8 * self.BYTES).from_address(base))
+        if memory is not None:                     # a retired ring's memory
+            self.base, self.np, self.buf = memory
         else:
-            # the library's regions are used up (64 rings): torch's pinned
-            # memory, which the copy engine moves
-            self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
-            self.np = self.buf.numpy()
-            base = self.buf.data_ptr()
-        self.base = base
+            base = lib.sched_pd_staging_alloc(ctypes.c_uint64(self.BYTES))
+            if base:                               # held until the process ends
+                self.buf = None
+                self.np = np.ctypeslib.as_array((ctypes.c_uint8 * self.BYTES).from_address(base))
+            else:
+                # the library's regions are used up: torch's pinned memory,
+                # which the copy engine moves
+                self.buf = torch.empty(self.BYTES, dtype=torch.uint8, pin_memory=True)
+                self.np = self.buf.numpy()
+                base = self.buf.data_ptr()
+            self.base = base
         self.copy = lib.sched_pd_copy_to_device
         self.stream = stream
         self.lock = threading.Lock()
@@ -71,6 +75,7 @@ class _StagingRing:
         self.cur = 0
         self.head = 0
         self.done = [None] * self.CHUNKS
+        self.retired = False
 
     def put(self, t: torch.Tensor, out: torch.Tensor) -> bool:
         """Stage contiguous host `t` and copy it into contiguous device `out`
@@ -81,6 +86,8 @@ class _StagingRing:
         if n == 0:
             return True
         with self.lock:
+            if self.retired:        # its memory went to another ring meanwhile
+                return False
             self._put(t, out, n)
         return True
 
@@ -122,7 +129,24 @@ class _StagingRing:
                 self.done[c] = ev
 
 
-_RINGS: dict = {}
+    def retire(self):
+        """Wait until every copy out of the ring has run (everything queued
+        on its stream so far) and hand back its memory for another ring."""
+        with self.lock:
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+            ev.synchronize()
+            self.done = [None] * self.CHUNKS
+            self.retired = True
+            return self.base, self.np, self.buf
+
+
+# One ring per (device, stream handle), least recently used first. A process
+# that keeps making streams reuses the memory of the ring used longest ago
+# (after its copies have run) once _RINGS_MAX rings exist, so the pinned
+# memory held stays at _RINGS_MAX x 16 MiB.
+_RINGS: "collections.OrderedDict" = collections.OrderedDict()
+_RINGS_MAX = 16
 _RINGS_LOCK = threading.Lock()
 
 
@@ -132,7 +156,13 @@ def _ring(dev: torch.device) -> _StagingRing:
     with _RINGS_LOCK:
         ring = _RINGS.get(key)
         if ring is None:
-            ring = _RINGS[key] = _StagingRing(stream)
+            memory = None
+            if len(_RINGS) >= _RINGS_MAX:
+                _, old = _RINGS.popitem(last=False)
+                memory = old.retire()
+            ring = _RINGS[key] = _StagingRing(stream, memory)
+        else:
+            _RINGS.move_to_end(key)
     # the live stream object (a handle can be reused by a later stream)
     ring.stream = stream
     return ring
@@ -157,8 +187,8 @@ def upload_into(dst: torch.Tensor, src) -> None:
 def upload(a, device) -> torch.Tensor:
     """A host array (numpy or CPU tensor) on `device`, without waiting for the
     device: staged through a pinned ring of the current stream and copied
-    asynchronously on it (arrays over 256 KiB through pinned memory of their
-    own). A copy from pageable memory would first wait for every kernel
+    asynchronously on it (arrays over 15 MiB, more than the ring takes,
+    through pinned memory of their own). A copy from pageable memory would first wait for every kernel
     already queued, so a serving loop's host work would never overlap its GPU
     work."""
     t = torch.from_numpy(np.ascontiguousarray(a)) if isinstance(a, np.ndarray) else a
@@ -305,6 +335,8 @@ def build_args(q, k_pool, v_pool, block_table, ctx_lens, *, out,
         # without waiting, and held by the arguments until they are dropped
         if tiles.ndim == 2 and tiles.shape[1] == 4:
             check_ranged_plan(tiles)
+        elif tiles.ndim == 2 and tiles.shape[1] == 2:
+            check_pair_plan(tiles)
         tiles = upload(np.ascontiguousarray(tiles, dtype=np.int32), k_pool.device)
         a._tiles = tiles
     if tiles is not None:
@@ -552,6 +584,65 @@ def check_ranged_plan(tiles) -> None:
         i = int(np.flatnonzero(~ok)[0])
         raise ValueError(f"ranged tiles row {i} {t[i].tolist()} is not task-major with "
                          "contiguous ranges from page 0")
+    _check_one_group_per_task(task[first], "ranged")
+
+
+def _check_one_group_per_task(first_tasks, what: str) -> None:
+    """A task may start (chunk 0) on one row only: a second group of its rows
+    would merge into the same arrival counter and could leave it nonzero."""
+    u, n = np.unique(first_tasks, return_counts=True)
+    if (n > 1).any():
+        raise ValueError(f"{what} tiles list task {int(u[np.argmax(n > 1)])} in more than "
+                         "one group of rows")
+
+
+def check_plan_covers(tiles, ctx_lens, page_size: int, num_kv_heads: int,
+                      tile_pages: int = 0) -> None:
+    """Raise ValueError unless the host plan `tiles` ([n, 2] pair rows of
+    tile_pages pages, or [n, 4] ranged rows) reaches every page of the
+    contexts `ctx_lens` (tokens): the check the kernels make per task (a
+    task it fails is stale: NaN output rows), made on the host before a
+    launch that must not run stale, such as a fused append."""
+    t = np.asarray(tiles, dtype=np.int64)
+    ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
+                     dtype=np.int64)
+    npg = np.repeat((ctx + page_size - 1) // page_size, num_kv_heads)
+    ntask = npg.size
+    if t.shape[1] == 4:
+        last = (t[:, 1] & 0xFFFF) == (t[:, 1] >> 16) - 1
+        reach = np.full(ntask, -1, np.int64)
+        lt = t[last]
+        ok = (lt[:, 0] >= 0) & (lt[:, 0] < ntask)
+        np.maximum.at(reach, lt[ok, 0], lt[ok, 3])
+    else:
+        if tile_pages <= 0:
+            raise ValueError("pair rows need tile_pages > 0")
+        ok = (t[:, 0] >= 0) & (t[:, 0] < ntask)
+        nch = np.bincount(t[ok, 0], minlength=ntask)[:ntask]
+        reach = np.where(nch > 0, nch * tile_pages, -1)
+    short = reach < npg
+    if short.any():
+        k = int(np.argmax(short))
+        raise ValueError(f"the split plan is stale: task {k} (request {k // num_kv_heads}) "
+                         f"has {int(npg[k])} pages, the plan reaches {max(int(reach[k]), 0)}")
+
+
+def check_pair_plan(tiles) -> None:
+    """Raise ValueError unless `tiles` ([n, 2] (task, chunk) rows) is
+    task-major: each task's chunks consecutive and numbered from 0, each
+    task in one group of rows. (Coverage is the launch's check.)"""
+    t = np.asarray(tiles, dtype=np.int64)
+    if t.ndim != 2 or t.shape[1] != 2 or t.shape[0] == 0:
+        raise ValueError("pair tiles must be a non-empty [num_tiles, 2] array")
+    task, chunk = t[:, 0], t[:, 1]
+    first = chunk == 0
+    start = np.maximum.accumulate(np.where(first, np.arange(len(t)), 0))
+    ok = (task >= 0) & (chunk >= 0) & (chunk == np.arange(len(t)) - start)
+    ok &= task == task[start]
+    if not ok.all():
+        i = int(np.flatnonzero(~ok)[0])
+        raise ValueError(f"pair tiles row {i} {t[i].tolist()} is not task-major")
+    _check_one_group_per_task(task[first], "pair")
 
 
 def desc_order(cost) -> np.ndarray:

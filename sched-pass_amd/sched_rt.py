@@ -18,6 +18,7 @@ _weave_tag, the fixed-VA guarantee, r_for_cached_so.
 """
 from __future__ import annotations
 
+import ctypes
 import struct
 
 import numpy as np
@@ -25,11 +26,12 @@ import torch
 
 from sched_abi import (CTRL_FLAGS_OFF, CTRL_LAMBDA_OFF, CTRL_NUM_TASKS_OFF,
                        CTRL_ORDER_SIZE_OFF, CTRL_ROWS_OFF, FLAG_TIMER_OFF,
-                       HINT_AUTO, HINT_POLITE, HINT_URGENT, ROW_SIZE)
+                       HINT_AUTO, HINT_POLITE, HINT_URGENT, ROW_SIZE, last_error,
+                       load_library)
 from sched_pd import desc_order, upload_into
 
 __all__ = ["SchedPlane", "SchedArenaError", "HINT_AUTO", "HINT_URGENT",
-           "HINT_POLITE", "FLAG_TIMER_OFF", "MANIFEST"]
+           "HINT_POLITE", "FLAG_TIMER_OFF", "MANIFEST", "LEVER_ARMING"]
 
 # Arena layout (reference python/sched_rt.py:84-89).
 ORDER_OFF = 0x00000
@@ -39,20 +41,41 @@ QUEUE_OFF = 0xC0000
 ARENA_BYTES = 0x100000
 MAX_TASKS_LIMIT = 16384
 
-# Lever manifest (reference include/sched/SchedManifest.h:76-105 and its
-# mirror python/sched_rt.py:72-79): name, effect type, what it reads, and how
-# this library arms it. Order = the order the kernels apply them in.
+# Lever manifest in the row shape of reference python/sched_rt.py:72-79 (the
+# mirror of include/sched/SchedManifest.h:76-105): name, effect, min_sm, compile
+# knob, disable sense, cache tag; list order = the order the kernels apply the
+# levers in (the claim loop, then the remap, the budget, the stream's policy,
+# the timer's commit). The last four fields belong to the reference's
+# compile-time weave and do not apply here: every lever runs on gfx950
+# (min_sm 0), none is compiled in or out (knob None, disable False) and there
+# is no JIT cache (tag ""); each is armed per launch by its table. The
+# reference's sixth row, "pdl" (programmatic dependent launch, sm90), has no
+# counterpart on a HIP stream and is not listed.
 MANIFEST = [
-    ("workqueue", "acquire", "ctrl,queue", "launch with workers=W and num_tasks>0"),
-    ("pi", "E1/permute", "order,ctrl", "order table (identity by default)"),
-    ("shed", "E2/budget", "ctrl", "row tau > 0"),
-    ("policy", "E0/hint", "ctrl", "row hint / q*dT - lambda_bw*dR - H > 0"),
-    ("timer", "O/observe", "timer,ctrl", "timer table + flags bit0 clear"),
+    ("workqueue", "acquire", 0, None, False, ""),
+    ("pi", "E1/permute", 0, None, False, ""),
+    ("shed", "E2/budget", 0, None, False, ""),
+    ("policy", "E0/hint", 0, None, False, ""),
+    ("timer", "O/observe", 0, None, False, ""),
 ]
+
+# How each lever is armed here: the tables it reads and the switch.
+LEVER_ARMING = {
+    "workqueue": ("ctrl,queue", "launch with workers=W and num_tasks > 0"),
+    "pi": ("order,ctrl", "order table (identity by default), order_size in {0, N}"),
+    "shed": ("ctrl", "row tau > 0"),
+    "policy": ("ctrl", "row hint, or q*dT - lambda_bw*dR - H > 0"),
+    "timer": ("timer,ctrl", "timer table, flags bit0 clear"),
+}
 
 
 class SchedArenaError(RuntimeError):
-    """The device arena could not be created."""
+    """The device arena could not be created, or its tables not bound."""
+
+
+# The plane last bound to the library's __sched_* slots (bind_launcher),
+# held so that its tables outlive the launches that read them there.
+_BOUND = None
 
 
 class SchedPlane:
@@ -96,6 +119,57 @@ class SchedPlane:
                 "timer": self._timer_view().data_ptr(),
                 "queue": self._queue.data_ptr()}
 
+    # -- the slot-reading launchers ---------------------------------------------
+    def bind_launcher(self) -> None:
+        """Put this plane's tables into the library's __sched_* slots, so the
+        launchers that read their levers from the slots -- the reference's
+        launch_paged_softmax (python/kernels/paged_softmax.cu:47-54), and
+        paged_decode(..., rt_tables=True) -- run with this plane's pi, rows,
+        timer and queue, its max_tasks rows bounding the task ids that get
+        levers. The reference reaches the same by baking the plane's
+        addresses into a JIT build (bake_env, python/sched_rt.py:489-555).
+        What the plane pushes afterwards takes effect at the next launch;
+        use_device_timer / use_device_order re-bind the moved table. One
+        plane is bound per process (the slots are the library's); another
+        plane's bind_launcher, unbind_launcher, or the C runtime's
+        sched_rt_init / sched_rt_disarm end the binding. The module holds
+        the bound plane, so its tables outlive every launch that reads them
+        from the slots."""
+        global _BOUND
+        with torch.cuda.device(self.dev):
+            t = self.tables()
+            lib = load_library()
+            if not lib.sched_rt_bind_tables(ctypes.c_void_p(t["order"]),
+                                            ctypes.c_void_p(t["ctrl"]),
+                                            ctypes.c_void_p(t["timer"]),
+                                            ctypes.c_void_p(t["queue"]), self.N):
+                raise SchedArenaError(f"binding the plane's tables failed: {last_error()}")
+        _BOUND = self
+
+    def unbind_launcher(self) -> None:
+        """Null the slots if they hold this plane's tables (the slot-reading
+        launchers then run stock)."""
+        global _BOUND
+        if self.bound:
+            with torch.cuda.device(self.dev):
+                if not load_library().sched_rt_disarm():
+                    raise SchedArenaError(f"unbinding failed: {last_error()}")
+        if _BOUND is self:
+            _BOUND = None
+
+    @property
+    def bound(self) -> bool:
+        """True while the slots hold this plane's tables (read back from the
+        device: synchronous)."""
+        if _BOUND is not self:
+            return False
+        slots = (ctypes.c_uint64 * 4)()
+        with torch.cuda.device(self.dev):
+            if not load_library().sched_rt_slots(slots):
+                raise SchedArenaError(f"reading the slots failed: {last_error()}")
+        t = self.tables()
+        return list(slots) == [t["order"], t["ctrl"], t["timer"], t["queue"]]
+
     @property
     def num_tasks(self) -> int:
         return struct.unpack_from("<I", self._ctrl_host, CTRL_NUM_TASKS_OFF)[0]
@@ -104,15 +178,21 @@ class SchedPlane:
         """Move the observation rows to their own device buffer, read back on
         a side stream (reference python/sched_rt.py:319-331)."""
         if self._timer_dev is None:
+            was_bound = self.bound
             self._timer_dev = torch.zeros(self.N, dtype=torch.int64, device=self.dev)
             self._timer_stream = torch.cuda.Stream(device=self.dev)
+            if was_bound:
+                self.bind_launcher()
 
     def use_device_order(self) -> None:
         """Kernel-resident order table in its own device tensor, installable
         device-to-device without a host sync (python/sched_rt.py:333-347).
         Starts as identity."""
         if self._order_dev is None:
+            was_bound = self.bound
             self._order_dev = torch.arange(self.N, dtype=torch.int32, device=self.dev)
+            if was_bound:
+                self.bind_launcher()
 
     # -- pi (python/sched_rt.py:365-395) ---------------------------------------
     def set_order(self, tasks) -> None:

@@ -233,6 +233,22 @@ def test_noalloc_refuses_a_workspace_and_oversized_plans_without_the_gpu(schedli
     assert schedlib.sched_paged_decode_noalloc(ctypes.byref(a), None) != 0
     assert "holds 16777216" in abi.last_error()
     assert schedlib.sched_paged_decode_noalloc(None, None) != 0
+    # zero kv-heads with a plan: rejected (not a division by zero in the host)
+    a.num_tiles = 8
+    a.num_kv_heads = 0
+    assert schedlib.sched_paged_decode_noalloc(ctypes.byref(a), None) != 0
+    assert "num_kv_heads is 0" in abi.last_error()
+    a.num_kv_heads, a.num_q_heads = 4, 6
+    assert schedlib.sched_paged_decode_noalloc(ctypes.byref(a), None) != 0
+    assert "not a multiple" in abi.last_error()
+
+
+def test_bind_tables_row_limit_without_the_gpu(schedlib):
+    """sched_rt_bind_tables refuses more rows than the plane window holds
+    before it touches a slot."""
+    assert not schedlib.sched_rt_bind_tables(None, None, None, None,
+                                             abi.RT_BIND_MAX_TASKS + 1)
+    assert "max_tasks 16385 > 16384" in abi.last_error()
 
 
 def test_split_arguments_validated(schedlib):
@@ -354,6 +370,7 @@ def test_check_ranged_plan_rejects_malformed_lists():
     b = good.copy(); b[4, 2] = 1; bad.append(b)                       # chunk 0 not from page 0
     b = good.copy(); b[5, 0] = 0; bad.append(b)                       # task changes mid-chunks
     b = good.copy(); b[1, 3] = 1; bad.append(b)                       # p1 < p0
+    b = good.copy(); b[4:, 0] = 0; bad.append(b)                      # a task's second group
     for b in bad:
         with pytest.raises(ValueError):
             sched_pd.check_ranged_plan(b)

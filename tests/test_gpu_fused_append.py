@@ -197,3 +197,91 @@ def test_fused_launch_over_a_csr_page_table():
         pools.append((kp, vp))
     assert same(outs[0], outs[1])
     assert same(pools[0][0], pools[1][0]) and same(pools[0][1], pools[1][1])
+
+
+@pytest.mark.parametrize("ranged", [False, True])
+def test_fused_launch_with_a_stale_plan_still_writes_the_token(ranged):
+    """A plan built from the lengths before the append, where the new token
+    opens a page in a chunk the plan does not hold (64 tokens in 4-page
+    chunks of 16-token pages: the 65th token starts chunk 1). The fused
+    launch flags those tasks stale (NaN rows, counted), yet writes every
+    token: the pools equal the writer's, and the tasks the plan still covers
+    equal append-then-decode. Through PagedKvCache.decode_step a host plan
+    this stale is refused before anything is written."""
+    from kv_cache import append as kv_append
+    lens = [64, 10, 128, 40]          # requests 0 and 2 open a page in a new chunk
+    (c, _), g = make_pair(torch.bfloat16, 16, lens, seed=13)
+    rids = list(range(len(lens)))
+    R, tp = len(lens), 4
+    before = c.lengths(rids)
+    if ranged:
+        plan_h = sched_pd.plan_ranges_host(before, 16, HKV, tile_pages=tp, tail_pages=tp)
+    else:
+        plan_h = sched_pd.plan_tiles_host(before, 16, tp, HKV)
+    q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    # the cache refuses a stale host plan for its fused step, and is unchanged
+    kp0, vp0 = c.k_pool.clone(), c.v_pool.clone()
+    tkw = dict(tiles=plan_h) if ranged else dict(tiles=plan_h, tile_pages=tp)
+    with pytest.raises(ValueError, match="stale"):
+        c.decode_step(q, rids, k1, v1, **tkw)
+    assert c.lengths(rids).tolist() == list(before)
+    assert same(c.k_pool, kp0) and same(c.v_pool, vp0)
+    # the kernel path: one launch with the stale plan, against the writer
+    c.reserve(rids, [1] * R)
+    for r in rids:
+        c.lens[r] += 1
+    bt, ctx = c.block_table(rids)
+    app_ptr = torch.arange(R + 1, dtype=torch.int32, device="cuda")
+    plan = torch.from_numpy(plan_h).cuda()
+    outs, pools = [], []
+    for fused in (True, False):
+        kp, vp = c.k_pool.clone(), c.v_pool.clone()
+        out = torch.empty(R, HKV * 4, D, dtype=torch.bfloat16, device="cuda")
+        ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+        kw = dict(tiles=plan, workspace=ws) if ranged else \
+            dict(tiles=plan, tile_pages=tp, workspace=ws)
+        args = sched_pd.build_args(q, kp, vp, bt, ctx, out=out, v_layout="tokmajor", **kw)
+        if fused:
+            app = build_append_args(k1, v1, app_ptr, ctx, kp, vp, bt, v_layout="tokmajor",
+                                    max_append=1)
+            sched_pd.launch_with_append(args, app)
+        else:
+            kv_append(k1, v1, app_ptr, ctx, kp, vp, bt, v_layout="tokmajor", max_append=1)
+            sched_pd.launch(args)
+        torch.cuda.synchronize()
+        outs.append(out)
+        pools.append((kp, vp))
+        assert sched_pd.stale_plan_count(ws) == 2 * HKV
+        assert int(ws[sched_pd.WS_COUNTERS_OFF:sched_pd.WS_COUNTERS_OFF + 4 * R * HKV]
+                   .view(torch.int32).abs().sum()) == 0
+    assert same(pools[0][0], pools[1][0]) and same(pools[0][1], pools[1][1])
+    got = outs[0].float()
+    assert torch.isnan(got[[0, 2]]).all() and torch.isfinite(got[[1, 3]]).all()
+    assert same(outs[0][[1, 3]], outs[1][[1, 3]])
+    ref = oracle.decode(q, pools[0][0], pools[0][1], bt, ctx, v_layout="tokmajor")
+    assert par_err(got[[1, 3]].cpu(), np.asarray(ref)[[1, 3]]) <= TOL_BF16
+
+
+def test_fused_step_under_a_shed_budget():
+    """Prefix budgets below the new token's position: the token is still
+    written (the pages past the budget are not read), and the output equals
+    append-then-decode under the same rows."""
+    lens = [30, 100, 250, 17]
+    (fa, sep), g = make_pair(torch.bfloat16, 16, lens, seed=17)
+    R = len(lens)
+    rids = list(range(R))
+    q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+    plane = SchedPlane(max_tasks=R * HKV)
+    plane.set_rows(tau=[5, 8, 40, 300, 16, 0, 1, 2], n=R * HKV)
+    plane.push()
+    for step in range(3):
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        o_fused = fa.decode_step(q, rids, k1, v1, plane=plane)
+        sep.append(rids, k1, v1)
+        o_sep = sep.decode(q, rids, plane=plane)
+        torch.cuda.synchronize()
+        assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
+        assert same(o_fused, o_sep), step
