@@ -192,16 +192,17 @@ def tile_pages_for(elem_bytes, page=16, head_dim=128):
 
 
 TILE_PAGES = tile_pages_for(2)
-# ranged plans under an order unrelated to cost: 1.25 MiB chunks of one
-# kv-head's KV, and 0.5 MiB chunks for the tasks that start in the last 10%
-# of the order's pages (bf16: 160 and 64 pages; fp8: 320 and 128)
-RANGED_BYTES, TAIL_BYTES, TAIL_FRAC = 5 << 18, 1 << 19, 0.1
+# Graded plans for queue launches under an order unrelated to cost (identity,
+# urgency): chunks of one kv-head's KV of 1.25 MiB, then 0.5 MiB for the pages
+# claimed after the first 90% of the step's, then 128 KiB after 98% (bf16:
+# 160 / 64 / 16 pages; fp8: 320 / 128 / 32).
+GRADED_BYTES = ((0.0, 5 << 18), (0.9, 1 << 19), (0.98, 1 << 17))
 
 
-def ranged_pages(elem_bytes):
-    """(chunk pages, tail chunk pages) of the ranged plans."""
+def graded_sizes(elem_bytes):
+    """The graded plan's (fraction, chunk pages) levels for a KV element size."""
     per_page = 16 * 128 * 2 * elem_bytes
-    return RANGED_BYTES // per_page, TAIL_BYTES // per_page
+    return tuple((f, nbytes // per_page) for f, nbytes in GRADED_BYTES)
 
 
 def _makespan_us(torch, sched_pd, a, stream, reps=5, launches=20):
@@ -229,7 +230,8 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     `tile_pages` pages. The other two corners are reported as well, the
     queue with LPT from the timer, and pi alone (longest-first by pages over
     the static grid of tiles); and the queue, pi still by urgency, over a
-    ranged plan whose last-claimed tasks run as shorter chunks."""
+    graded plan whose chunks are cut smaller the later they are claimed (the
+    configuration's queue launch, reported as ticket_wq_us)."""
     import numpy as np
     b = workloads.workload("llama3_8b_hetero", seed=0)
     ntask = 256 * 8
@@ -293,51 +295,57 @@ def bench_hetero(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAG
     a_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                                plane=p_st, workers=0, tiles=tiles, tile_pages=tile_pages, **common)
     res["static_tiles_lpt_pages"] = round(_makespan_us(torch, sched_pd, a_st, stream), 2)
-    # the queue over a ranged plan: pi by urgency as above, the tasks claimed
-    # last cut into shorter chunks
+    # the queue over the graded plan: pi by urgency as above, chunks cut
+    # smaller the later they are claimed (the configuration's queue launch)
     ctx = b["ctx_lens"].cpu().numpy()
-    rp, rt = ranged_pages(2)
-    rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-q, kind="stable"),
-                                       tile_pages=rp, tail_pages=rt, tail_frac=TAIL_FRAC)
-    ntr = rtiles.shape[0]
-    p_rng = SchedPlane(max_tasks=max(ntr, ntask))
-    p_rng.install_order(sched_pd.tile_order_by_task_key(torch.from_numpy(rtiles), q), ntr)
-    p_rng.set_num_tasks(ntr)
-    p_rng.push()
-    p_rng.reset_queue(W)
-    a_rng = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
-                                plane=p_rng, workers=W, tiles=rtiles, **common)
-    res["wq_ranged_tail"] = round(_makespan_us(torch, sched_pd, a_rng, stream), 2)
-    # the static grid over the same ranged plan and pi: the queue's own part
-    p_rng_st = SchedPlane(max_tasks=max(ntr, ntask))
-    p_rng_st.install_order(sched_pd.tile_order_by_task_key(rtiles, q), ntr)
-    p_rng_st.push()
-    a_rng_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
-                                   b["ctx_lens"], plane=p_rng_st, workers=0, tiles=rtiles,
+    sizes = graded_sizes(2)
+    gtiles = sched_pd.plan_graded_host(ctx, 16, 8, task_order=np.argsort(-q, kind="stable"),
+                                       sizes=sizes)
+    ntg = gtiles.shape[0]
+    p_grd = SchedPlane(max_tasks=max(ntg, ntask))
+    p_grd.install_order(sched_pd.tile_order_by_task_key(torch.from_numpy(gtiles), q), ntg)
+    p_grd.set_num_tasks(ntg)
+    p_grd.push()
+    p_grd.reset_queue(W)
+    a_grd = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
+                                plane=p_grd, workers=W, tiles=gtiles, **common)
+    res["wq_graded"] = round(_makespan_us(torch, sched_pd, a_grd, stream), 2)
+    # the static grid over the same graded plan and pi: the queue's own part
+    p_grd_st = SchedPlane(max_tasks=max(ntg, ntask))
+    p_grd_st.install_order(sched_pd.tile_order_by_task_key(gtiles, q), ntg)
+    p_grd_st.push()
+    a_grd_st = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"],
+                                   b["ctx_lens"], plane=p_grd_st, workers=0, tiles=gtiles,
                                    **common)
-    res["static_ranged_tail"] = round(_makespan_us(torch, sched_pd, a_rng_st, stream), 2)
+    res["static_graded"] = round(_makespan_us(torch, sched_pd, a_grd_st, stream), 2)
     kv = b["kv_bytes"]
 
     def cut(a, b_):
         return round(100.0 * (res[a] - res[b_]) / res[a], 2)
 
     return {
-        "static_us": res["static_task"], "ticket_wq_us": res["wq_tiles"],
-        # the config's comparison (queue over split tiles vs one workgroup per
-        # task), then its two parts on one decomposition each
-        "queue_plus_split_cut_pct": cut("static_task", "wq_tiles"),
-        "split_cut_pct": cut("static_task", "static_tiles"),
-        "queue_cut_pct": cut("static_tiles", "wq_tiles"),
+        # the configuration's comparison: the queue (over the graded plan)
+        # against the static grid of one workgroup per task, both under pi
+        # by urgency; then its two parts, the split alone (static grid over
+        # the same plan) and the queue alone over that plan and over tasks
+        "static_us": res["static_task"], "ticket_wq_us": res["wq_graded"],
+        "queue_plus_split_cut_pct": cut("static_task", "wq_graded"),
+        "split_cut_pct": cut("static_task", "static_graded"),
+        "queue_cut_pct": cut("static_graded", "wq_graded"),
         "queue_over_tasks_cut_pct": cut("static_task", "wq_task"),
+        # the same over 128-page pair tiles
+        "pair_tiles": {"queue_plus_split_cut_pct": cut("static_task", "wq_tiles"),
+                       "split_cut_pct": cut("static_task", "static_tiles"),
+                       "queue_cut_pct": cut("static_tiles", "wq_tiles")},
+        "graded_vs_pair_tiles_pct": -cut("wq_tiles", "wq_graded"),
+        # orders by cost, for reference: LPT from the timer (queue), LPT by
+        # pages on the static grid
         "queue_plus_split_plus_lpt_timer_cut_pct": cut("static_task", "wq_tiles_lpt_timer"),
         "split_plus_lpt_static_cut_pct": cut("static_task", "static_tiles_lpt_pages"),
-        "queue_plus_ranged_tail_cut_pct": cut("static_task", "wq_ranged_tail"),
-        "ranged_tail_vs_tiles_pct": -cut("wq_tiles", "wq_ranged_tail"),
-        "queue_cut_ranged_pct": cut("static_ranged_tail", "wq_ranged_tail"),
-        "ranged_tiles": ntr, "ranged_pages": rp, "tail_pages": rt, "tail_frac": TAIL_FRAC,
+        "graded_tiles": ntg, "graded_sizes": [list(x) for x in sizes],
         "corners_us": res, "workers": W, "tasks": ntask, "tiles": nt, "tile_pages": tile_pages,
         "lpt_tile_pages": tp2,
-        "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_tiles"] * 1e-6) / 1e9, 1),
+        "kv_bytes": kv, "wq_kv_gbs": round(kv / (res["wq_graded"] * 1e-6) / 1e9, 1),
         "residency_cycles": {"p50": int(np.percentile(cyc, 50)),
                              "p99": int(np.percentile(cyc, 99)), "max": int(cyc.max())},
     }
@@ -350,10 +358,10 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
     urgent, all polite) on the softmax skip launch. Online softmax (score -> -inf) and linear contraction (value -> 0)
     variants; pages past the budget skipped (default) or loaded and masked
     (the reference weave's behaviour). Work queue over split tiles, pi by
-    urgency; the softmax skip launch over a ranged plan cut from the pages
-    each task reads (no empty work items past the budgets), its
-    last-claimed tasks in shorter chunks (and the linear skip launch over
-    the same plan); then the skip variants with
+    urgency; the softmax skip launch over a graded plan cut from the pages
+    each task reads (no empty work items past the budgets), chunks smaller
+    the later they are claimed (and the linear skip launch over the same
+    plan); then the skip variants with
     pi = longest-first over tiles of twice the size by the pages each reads
     (known on the host from ctx and tau)."""
     import numpy as np
@@ -437,11 +445,10 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
         f_, p_ = ab[f"firing_{cls}_cycles_per_page"], ab[f"priced_out_{cls}_cycles_per_page"]
         ab[f"firing_vs_priced_out_{cls}_cycles_pct"] = round(100.0 * (f_ - p_) / p_, 2)
     res["policy_ab"] = ab
-    rp, rt = ranged_pages(2)
-    rtiles = sched_pd.plan_ranges_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
+    sizes = graded_sizes(2)
+    rtiles = sched_pd.plan_graded_host(ctx, 16, 8, task_order=np.argsort(-b["urgency"],
                                                                           kind="stable"),
-                                       tile_pages=rp, tail_pages=rt, tail_frac=TAIL_FRAC,
-                                       tau=b["tau"][:ntask])
+                                       sizes=sizes, tau=b["tau"][:ntask])
     ntr = rtiles.shape[0]
     plane_r = SchedPlane(max_tasks=max(ntr, ntask))
     plane_r.set_lambda(0.5)
@@ -455,20 +462,20 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
                             out=out, plane=plane_r, workers=W, tiles=rtiles,
                             policy=(1.0, 1.0, 0.1), pf_dist=4)
     us = _makespan_us(torch, sched_pd, a, stream)
-    res["softmax_skip_ranged_tail"] = {
+    res["softmax_skip_graded"] = {
         "us": round(us, 2), "gbs_loaded": round(kept / us / 1e3, 1),
-        "gbs_ctx_equiv": round(full / us / 1e3, 1), "tiles": ntr, "ranged_pages": rp,
-        "tail_pages": rt,
+        "gbs_ctx_equiv": round(full / us / 1e3, 1), "tiles": ntr,
+        "graded_sizes": [list(x) for x in sizes],
         "vs_tiles_pct": round(100.0 * (us - res["softmax_skip"]["us"]) / res["softmax_skip"]["us"], 2)}
     sched_pd.launch(a, stream)
     torch.cuda.synchronize()
     if not torch.equal(torch.isfinite(out), torch.ones_like(out, dtype=torch.bool)):
-        raise AssertionError("the ranged shed launch left non-finite outputs")
+        raise AssertionError("the graded shed launch left non-finite outputs")
     a = sched_pd.build_args(b["q"], b["k_pool"], b["v_pool"], b["block_table"], b["ctx_lens"],
                             out=lout, plane=plane_r, workers=W, tiles=rtiles, mode=abi.LINEAR,
                             lin_w=w, policy=(1.0, 1.0, 0.1), pf_dist=4)
     us = _makespan_us(torch, sched_pd, a, stream)
-    res["linear_skip_ranged_tail"] = {
+    res["linear_skip_graded"] = {
         "us": round(us, 2), "gbs_loaded": round(kept * 0.5 / us / 1e3, 1),
         "vs_tiles_pct": round(100.0 * (us - res["linear_skip"]["us"]) / res["linear_skip"]["us"], 2)}
     tp2 = 2 * tile_pages
@@ -496,12 +503,14 @@ def bench_shed(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=TILE_PAGES
 
 def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_for(1)):
     """Qwen2-7B shape (Hq 28 / Hkv 4), fp8-e4m3fn KV with per-(page, head)
-    scales, bf16 Q/out, 512 requests, lognormal ctx (median 2048, sigma 1.2,
-    max 16384); ticket work queue over split tiles, timer on; the same queue
-    (identity pi) over a ranged plan with shorter chunks for the tasks
-    claimed last; then the queue with pi over tiles (twice the size) by the
-    timer's per-task cycles, longest first; and with pi by the tasks' page
-    counts (known before the launch) over tiles three times the size."""
+    scales ((K, V) pairs per (page, head)), bf16 Q/out, 512 requests,
+    lognormal ctx (median 2048, sigma 1.2, max 16384). The configuration's
+    launch: the ticket work queue (identity pi, timer on) over the graded
+    plan, chunks cut smaller the later they are claimed; beside it the same
+    queue over 256-page pair tiles, the static grid of one workgroup per
+    task, the queue with pi over tiles (twice the size) by the timer's
+    per-task cycles, longest first, and with pi by the tasks' page counts
+    (known before the launch) over tiles three times the size."""
     import numpy as np
     b = workloads.workload("qwen2_7b_fp8", seed=0)
     R, ntask = 512, 512 * 4
@@ -556,9 +565,8 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
                                 out=out, k_scale=b["k_scale"], v_scale=b["v_scale"], plane=plane4,
                                 workers=W, tiles=tiles3, tile_pages=tp3)
     us_len = _makespan_us(torch, sched_pd, a_len, stream)
-    rp, rt = ranged_pages(1)
-    rtiles = sched_pd.plan_ranges_host(ctx, 16, 4, tile_pages=rp, tail_pages=rt,
-                                       tail_frac=TAIL_FRAC)
+    sizes = graded_sizes(1)
+    rtiles = sched_pd.plan_graded_host(ctx, 16, 4, sizes=sizes)
     ntr = rtiles.shape[0]
     plane5 = SchedPlane(max_tasks=max(ntr, ntask))
     plane5.set_num_tasks(ntr)
@@ -569,12 +577,15 @@ def bench_fp8(torch, sched_pd, workloads, SchedPlane, cu, tile_pages=tile_pages_
                                 workers=W, tiles=rtiles)
     us_rng = _makespan_us(torch, sched_pd, a_rng, stream)
     kv = b["kv_bytes"]
-    return {"kv_bytes": kv, "ticket_wq_us": round(us_wq, 2), "static_task_us": round(us_st, 2),
-            "wq_ranged_tail_us": round(us_rng, 2), "gbs_ranged_tail": round(kv / us_rng / 1e3, 1),
-            "ranged_tiles": ntr, "ranged_pages": rp, "tail_pages": rt, "tail_frac": TAIL_FRAC,
+    # the configuration's launch (ticket queue, identity pi, timer on) is the
+    # queue over the graded plan; the queue over 256-page pair tiles beside it
+    return {"kv_bytes": kv, "ticket_wq_us": round(us_rng, 2), "static_task_us": round(us_st, 2),
+            "ticket_wq_plan": "graded", "graded_tiles": ntr,
+            "graded_sizes": [list(x) for x in sizes],
+            "wq_pair_tiles_us": round(us_wq, 2), "gbs_pair_tiles": round(kv / us_wq / 1e3, 1),
             "wq_tiles_lpt_timer_us": round(us_lpt, 2),
             "wq_tiles_lpt_length_us": round(us_len, 2),
-            "gbs": round(kv / us_wq / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
+            "gbs": round(kv / us_rng / 1e3, 1), "gbs_lpt_timer": round(kv / us_lpt / 1e3, 1),
             "gbs_lpt_length": round(kv / us_len / 1e3, 1), "lpt_length_tile_pages": tp3,
             "tiles": nt, "tile_pages": tile_pages, "lpt_tile_pages": tp2, "workers": W,
             "max_ctx": int(ctx.max()),

@@ -20,6 +20,8 @@ struct KParams {
   int64_t vps, vhs, vts, vds; // V strides (elements): page, head, token, dim
   const float *k_scale;
   const float *v_scale;
+  uint32_t scale_stride; // floats between the scales of consecutive (page, head)s: 2 when
+                         // K and V scales are interleaved pairs (v_scale == k_scale + 1)
   const int32_t *bt;
   const int32_t *indptr;
   const int32_t *ctx;

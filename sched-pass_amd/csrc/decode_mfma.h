@@ -315,7 +315,7 @@ __device__ __forceinline__ void issue_page(const KParams &P, const MfmaTask &T, 
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
         B.k[cc] = gload<NT>(reinterpret_cast<const u32x4_t *>(kp + 64 * cc));
-    const int64_t si = (int64_t)page * P.Hkv + T.h;
+    const int64_t si = ((int64_t)page * P.Hkv + T.h) * P.scale_stride;
     B.ks = (!LINEAR && P.k_scale) ? P.k_scale[si] : 1.f;
     B.vs = P.v_scale ? P.v_scale[si] : 1.f;
     if constexpr (VT) {

@@ -162,8 +162,9 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
     for (uint32_t c = R.p0 * cpp + w; c < c_end; c += NW) {
       const uint32_t pos0 = c * 16u, b = pos0 / P.ps, o = pos0 % P.ps;
       const int64_t page = b - R.p0 < ncache ? s_page[b - R.p0] : page_of(P, r, b);
-      const float ks = (fp8 && P.k_scale) ? P.k_scale[page * P.Hkv + h] : 1.f;
-      const float vs = (fp8 && P.v_scale) ? P.v_scale[page * P.Hkv + h] : 1.f;
+      const int64_t si = ((int64_t)page * P.Hkv + h) * P.scale_stride;
+      const float ks = (fp8 && P.k_scale) ? P.k_scale[si] : 1.f;
+      const float vs = (fp8 && P.v_scale) ? P.v_scale[si] : 1.f;
       float p_hp[NP], c_hp[NP];
 
 

@@ -47,6 +47,7 @@ struct AParams {
   void *k_pool, *v_pool;
   int64_t kps, khs, kts, vps, vhs, vts, vds;
   float *k_scale, *v_scale;
+  uint32_t scale_stride; // 2 when K and V scales are interleaved (v_scale == k_scale + 1)
   uint32_t *errors;
   uint32_t hpw; // kv-heads per workgroup, divides Hkv
   uint32_t w8;  // one-round path reads and writes 8-element chunks
@@ -340,7 +341,7 @@ __device__ void scales_from_amax(const AParams &P, PageScales &S, int64_t page, 
   __syncthreads();
   for (uint32_t i = threadIdx.x; i < 2 * hpw; i += kBlock) {
     const uint32_t x = i / hpw, hh = i % hpw;
-    float *slot = (x ? P.v_scale : P.k_scale) + page * P.Hkv + h0 + hh;
+    float *slot = (x ? P.v_scale : P.k_scale) + (page * P.Hkv + h0 + hh) * P.scale_stride;
     set_scale(S, x, hh, slot, *slot, o0);
   }
   __syncthreads();
@@ -599,7 +600,8 @@ __device__ void page_one_round(const AParams &P, PageScales &S, float *stage, in
   // scales; the old values load together with the source
   float *slot = nullptr, s_old = 0.f;
   if (FP8 && threadIdx.x < 2 * hpw) {
-    slot = (threadIdx.x < hpw ? P.k_scale : P.v_scale) + page * P.Hkv + h0 + threadIdx.x % hpw;
+    slot = (threadIdx.x < hpw ? P.k_scale : P.v_scale) +
+           (page * P.Hkv + h0 + threadIdx.x % hpw) * P.scale_stride;
     s_old = *slot;
   }
   Chunk<SRC, W> xk[NB], xv[NB];
@@ -938,6 +940,7 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream) {
   P.vds = vdm ? a->v_dim_stride : 1;
   P.k_scale = a->kv_dtype == SCHED_PD_FP8_E4M3 ? a->k_scale : nullptr;
   P.v_scale = a->kv_dtype == SCHED_PD_FP8_E4M3 ? a->v_scale : nullptr;
+  P.scale_stride = (P.k_scale != nullptr && P.v_scale == P.k_scale + 1) ? 2u : 1u;
   P.errors = a->errors;
 
   const uint32_t max_app = a->max_append ? a->max_append : a->num_tokens;

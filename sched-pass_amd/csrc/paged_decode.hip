@@ -303,6 +303,9 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   kp->vds = a->v_dim_stride;
   kp->k_scale = a->k_scale;
   kp->v_scale = a->v_scale;
+  // K and V scales interleaved as (K, V) pairs per (page, head): the two
+  // loads of a page's scales then fall in one cache line
+  kp->scale_stride = (a->k_scale != nullptr && a->v_scale == a->k_scale + 1) ? 2u : 1u;
   kp->bt = a->block_table;
   kp->indptr = a->page_indptr;
   kp->ctx = a->ctx_lens;

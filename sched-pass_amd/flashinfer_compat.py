@@ -100,18 +100,26 @@ class BatchDecodeWithPagedKVCacheWrapper:
         """FlashInfer's fp8 scales are one float per tensor (default 1); the
         kernels read one per (page, kv-head): expand (kept per value)."""
         n = kv_pool.shape[0] * self._plan["hkv"]
-        out = []
-        for x in (k_scale, v_scale):
-            if isinstance(x, torch.Tensor) and x.numel() == n:
-                out.append(x.to(torch.float32).contiguous())
-                continue
-            val = 1.0 if x is None else float(x)
-            key = (n, val, str(kv_pool.device))
-            cache = self.__dict__.setdefault("_scale_cache", {})
-            if key not in cache:
-                cache[key] = torch.full((n,), val, dtype=torch.float32, device=kv_pool.device)
-            out.append(cache[key])
-        return out
+        if isinstance(k_scale, torch.Tensor) or isinstance(v_scale, torch.Tensor):
+            out = []
+            for x in (k_scale, v_scale):
+                if isinstance(x, torch.Tensor) and x.numel() == n:
+                    out.append(x.to(torch.float32).contiguous())
+                else:
+                    val = 1.0 if x is None else float(x)
+                    out.append(torch.full((n,), val, dtype=torch.float32,
+                                          device=kv_pool.device))
+            return out
+        # two per-tensor values: expanded once into (K, V) pairs per
+        # (page, kv-head), the layout whose two scales share a cache line
+        kv = (1.0 if k_scale is None else float(k_scale),
+              1.0 if v_scale is None else float(v_scale))
+        key = (n, kv, str(kv_pool.device))
+        cache = self.__dict__.setdefault("_scale_cache", {})
+        if key not in cache:
+            pairs = torch.tensor(kv, dtype=torch.float32, device=kv_pool.device).repeat(n, 1)
+            cache[key] = (pairs[:, 0], pairs[:, 1])
+        return list(cache[key])
 
     def run(self, q: torch.Tensor, paged_kv_cache, *, out: torch.Tensor | None = None,
             k_scale=None, v_scale=None, **kw) -> torch.Tensor:

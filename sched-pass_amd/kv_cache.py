@@ -124,10 +124,7 @@ def build_append_args(k_new, v_new, append_indptr, ctx_lens, k_pool, v_pool, blo
     elif page_indptr.numel() != a.num_requests + 1:
         raise ValueError("page_indptr needs num_requests + 1 entries")
     if a.kv_dtype == abi.FP8_E4M3:
-        for t, what in ((k_scale, "k_scale"), (v_scale, "v_scale")):
-            if t is None or t.dtype != torch.float32 or t.numel() < P * hkv \
-                    or not t.is_contiguous():
-                raise ValueError(f"an fp8 pool needs contiguous float32 {what} [P * Hkv]")
+        check_scales(k_scale, v_scale, P * hkv)
     if errors is not None and (errors.dtype not in (torch.int32, torch.uint32)
                                or errors.numel() < 1):
         raise ValueError("errors must be a 32-bit integer tensor")
@@ -222,6 +219,33 @@ class _Lengths(MutableMapping):
         return len(self._c._slot)
 
 
+def paired_scales(n: int, device) -> tuple:
+    """Zeroed fp32 scales for n (page, kv-head)s as (K, V) pairs: one [n, 2]
+    tensor, returned as its two columns (k_scale, v_scale). The kernels see
+    v_scale == k_scale + 1 and read a (page, head)'s two scales from one
+    cache line (separate [n] arrays take a line each)."""
+    pairs = torch.zeros(n, 2, dtype=torch.float32, device=device)
+    return pairs[:, 0], pairs[:, 1]
+
+
+def check_scales(k_scale, v_scale, n: int) -> None:
+    """Raise ValueError unless k_scale / v_scale hold float32 scales for n
+    (page, kv-head)s: two contiguous arrays, or the two columns of one
+    [n, 2] (K, V) pair array (paired_scales)."""
+    for t, what in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+        if t is None or t.dtype != torch.float32 or t.numel() < n:
+            raise ValueError(f"an fp8 pool needs float32 {what} for {n} (page, kv-head)s")
+    if k_scale.is_contiguous() and v_scale.is_contiguous():
+        return
+    paired = (k_scale.dim() >= 1 and k_scale.stride(-1) == 2 and v_scale.stride(-1) == 2
+              and v_scale.data_ptr() == k_scale.data_ptr() + 4
+              and tuple(k_scale.shape) == tuple(v_scale.shape)
+              and (k_scale.dim() == 1 or k_scale.stride(-2) == 2 * k_scale.shape[-1]))
+    if not paired:
+        raise ValueError("k_scale / v_scale must be contiguous, or the (K, V) columns of one "
+                         "pair array")
+
+
 def _on_stream(stream):
     """The stream a step's work goes to: `stream`, or the current one."""
     return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
@@ -276,9 +300,10 @@ class PagedKvCache:
         self.v_pool = torch.zeros(num_pages, num_kv_heads, *vshape, dtype=dtype,
                                   device=self.device)
         fp8 = dtype == getattr(torch, "float8_e4m3fn", None)
-        self.k_scale = torch.zeros(num_pages * num_kv_heads, dtype=torch.float32,
-                                   device=self.device) if fp8 else None
-        self.v_scale = torch.zeros_like(self.k_scale) if fp8 else None
+        # fp8: (K, V) scale pairs per (page, kv-head), k_scale / v_scale
+        # being the pair array's columns
+        self.k_scale, self.v_scale = paired_scales(num_pages * num_kv_heads, self.device) \
+            if fp8 else (None, None)
         self.allocator = PageAllocator(num_pages)
         # Per request: its page list (pages[rid]) and, in arrays indexed by a
         # slot, its token count and page count, so that a step's bookkeeping

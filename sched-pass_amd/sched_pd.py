@@ -561,6 +561,77 @@ def plan_ranges_host(ctx_lens, page_size: int, num_kv_heads: int, task_order=Non
     return np.stack([tasks, chunk | (nch[tasks] << 16), p0, p1], 1).astype(np.int32)
 
 
+def plan_graded_host(ctx_lens, page_size: int, num_kv_heads: int, task_order=None,
+                     sizes=((0.0, 320), (0.9, 128), (0.98, 32)), tau=None) -> np.ndarray:
+    """A task-major ranged plan (int32 [num_tiles, 4] rows (task, chunk |
+    nchunks << 16, p0, p1)) whose chunk size is set per chunk by where the
+    chunk starts in the claim order: `task_order` lists the tasks in the
+    order a ticket queue reaches them (None = task index), so the pages of
+    the step line up in that order, and `sizes` = [(f_0 = 0, s_0), (f_1,
+    s_1), ...] (f ascending) cuts the pages that start in [f_i, f_i+1) of
+    that line into chunks of s_i pages. A task crossing a boundary is cut
+    there and its later pages take the smaller size. Large chunks early
+    keep the per-item cost low; small ones at the very end let the workers
+    finish close together. Each task's last range runs on to its context's
+    last page, so the plan covers the context; a task with no pages has one
+    empty chunk. `tau`: per-task prefix budgets in tokens (0 = no cap), for
+    launches that skip the pages past them: only the pages read are lined
+    up and cut. ctx_lens: the lengths the launch will see."""
+    ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
+                     dtype=np.int64)
+    fr = np.asarray([f for f, _ in sizes], np.float64)
+    sz = np.asarray([p for _, p in sizes], np.int64)
+    if fr.size == 0 or fr[0] != 0.0 or (np.diff(fr) <= 0).any() or fr[-1] >= 1.0 \
+            or (sz < 1).any():
+        raise ValueError("sizes must start at fraction 0, ascend below 1, with sizes >= 1")
+    n = np.repeat(ctx, num_kv_heads)
+    npg_ctx = (n + page_size - 1) // page_size
+    if tau is not None:
+        tau = np.asarray(tau, dtype=np.int64)
+        if tau.shape != n.shape:
+            raise ValueError(f"tau needs one budget per task ({n.size})")
+        n = np.where(tau > 0, np.minimum(n, tau), n)
+    npg = (n + page_size - 1) // page_size
+    ntask = npg.size
+    order = np.arange(ntask) if task_order is None else np.asarray(task_order, dtype=np.int64)
+    if order.shape != (ntask,) or not np.array_equal(np.sort(order), np.arange(ntask)):
+        raise ValueError(f"task_order must be a permutation of the {ntask} tasks")
+    # each task's pages as [a, e) on the line of the step's pages in claim order
+    a = np.empty(ntask, np.int64)
+    a[order] = np.cumsum(npg[order]) - npg[order]
+    e = a + npg
+    bounds = np.ceil(fr * npg.sum()).astype(np.int64)             # level starts on the line
+    ends = np.append(bounds[1:], np.iinfo(np.int64).max)
+    # segment (task, level): the task's pages on that level, then its chunks
+    s0 = np.maximum(a[:, None], bounds[None, :])
+    s1 = np.minimum(e[:, None], ends[None, :])
+    seg = np.maximum(0, s1 - s0)
+    nseg = -(-seg // sz[None, :])
+    nch = np.maximum(1, nseg.sum(1))
+    if nch.max(initial=1) > 0xFFFF:
+        raise ValueError("a task needs more than 65535 chunks; raise the chunk sizes")
+    # rows per (task, level) in task-major, level order; an empty task gets
+    # one chunk of level 0
+    cnt = nseg.copy()
+    cnt[:, 0] += (nseg.sum(1) == 0)
+    flat = cnt.ravel()
+    t_of = np.repeat(np.repeat(np.arange(ntask), sz.size), flat)
+    lv_of = np.repeat(np.tile(np.arange(sz.size), ntask), flat)
+    first = np.cumsum(flat) - flat                               # first row of each segment
+    j = np.arange(flat.sum()) - np.repeat(first, flat)           # chunk index in the segment
+    base = (s0 - a[:, None]).ravel()                             # segment start, task pages
+    seg_end = (s0 - a[:, None] + seg).ravel()
+    p0 = np.repeat(base, flat) + j * sz[lv_of]
+    p1 = np.minimum(p0 + sz[lv_of], np.repeat(seg_end, flat))
+    empty = npg[t_of] == 0
+    p0 = np.where(empty, 0, p0)
+    p1 = np.where(empty, 0, p1)
+    tstart = np.cumsum(nch) - nch
+    chunk = np.arange(t_of.size) - np.repeat(tstart, nch)
+    p1 = np.where(chunk == nch[t_of] - 1, npg_ctx[t_of], p1)
+    return np.stack([t_of, chunk | (nch[t_of] << 16), p0, p1], 1).astype(np.int32)
+
+
 def check_ranged_plan(tiles) -> None:
     """Raise ValueError unless `tiles` ([n, 4] ranged rows) is task-major:
     each task's chunks consecutive, numbered 0..nchunks-1 with one nchunks,

@@ -5,7 +5,8 @@ A batch is a dict of tensors in the kernels' layout:
     k_pool   [num_pages, Hkv, page, d]  token rows
     v_pool   [num_pages, Hkv, d, page]  d-major
     block_table [R, max_pages] int32, ctx_lens [R] int32
-    k_scale, v_scale [num_pages, Hkv] fp32 (fp8 pools only)
+    k_scale, v_scale [num_pages, Hkv] fp32 (fp8 pools only): the K and V
+                columns of one [num_pages, Hkv, 2] pair array
 Pages of a request are distinct pages drawn from a random permutation of the
 pool, so KV reads are scattered over HBM the way a serving cache is.
 
@@ -69,6 +70,10 @@ def make_batch(ctx_lens, *, num_q_heads, num_kv_heads, head_dim=128, page_size=1
         lo, hi = fp8_scale_range
         k_scale = torch.rand((pool_pages, hkv), generator=g, device=device) * (hi - lo) + lo
         v_scale = torch.rand((pool_pages, hkv), generator=g, device=device) * (hi - lo) + lo
+        # stored as (K, V) pairs per (page, kv-head): k_scale / v_scale are
+        # the columns of one [pool_pages, hkv, 2] array
+        pairs = torch.stack([k_scale, v_scale], -1).contiguous()
+        k_scale, v_scale = pairs[..., 0], pairs[..., 1]
 
     perm = torch.randperm(pool_pages, generator=g, device=device).to(torch.int32).cpu().numpy()
     maxp = max(int(npg.max()) if R else 1, 1)
