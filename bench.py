@@ -734,8 +734,10 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
         out_ = {}
         for name, f in (("append", fa), ("decode", fd), ("step", both)):
             out_[name + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
-        if layout == "tokmajor" and k_pool.dtype in (torch.bfloat16, torch.float16):
-            # the same step as one launch (the decode writes the token first)
+        if layout == "tokmajor" and k_pool.dtype in (torch.bfloat16, torch.float16,
+                                                     torch.float8_e4m3fn):
+            # the same step as one launch (the decode writes the token first;
+            # fp8: its page's scale grown as the writer grows it)
             ff = lambda i: sched_pd.launch_with_append(dec[i % tables], ins[i % tables],  # noqa: E731
                                                        stream)
             for i in range(2 * tables):

@@ -101,18 +101,20 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream);
  * same result, pools and output, as sched_kv_append(w) followed by
  * sched_paged_decode(a) on the same stream, in one launch. The decode
  * kernel's work item that holds request r's last position (ctx_lens[r] - 1)
- * writes source row r's K and V for each kv-head into it before reading it.
- * No counterpart in the reference (its decode reads caches an engine filled);
- * for serving loops, where the separate append is a small, launch-bound
- * kernel per step. Supported: softmax decode on the MFMA kernel (head dim
- * 128, bf16 or fp16 cache, token-major V), one token per request
- * (w->num_tokens == w->num_requests; source row r belongs to request r;
- * append_indptr is not read), source dtype fp32 or the cache's; w's pools,
- * strides, page table and ctx_lens must be a's. Anything else returns
- * hipErrorInvalidValue with sched_pd_last_error() set: fp8 caches (whose
- * scales the writer updates) and d-major V take the two calls. The page
- * written must exist (ctx_lens[r] >= 1 and its table entry valid); the
- * writer's error counter is not used. */
+ * writes source row r's K and V for each kv-head into it before reading it;
+ * for an fp8 cache it applies the writer's scale rule above to that
+ * (page, kv-head) first (grow the scale, re-encode the page's earlier slots
+ * when it grew, store the scales). No counterpart in the reference (its
+ * decode reads caches an engine filled); for serving loops, where the
+ * separate append is a small, launch-bound kernel per step. Supported:
+ * softmax decode on the MFMA kernel (head dim 128, bf16, fp16 or fp8 cache,
+ * token-major V), one token per request (w->num_tokens == w->num_requests;
+ * source row r belongs to request r; append_indptr is not read), source
+ * dtype fp32 or the cache's (fp32, bf16 or fp16 for fp8); w's pools,
+ * strides, page table, ctx_lens (and fp8 scales) must be a's. Anything else
+ * returns hipErrorInvalidValue with sched_pd_last_error() set: d-major V
+ * takes the two calls. The page written must exist (ctx_lens[r] >= 1 and its
+ * table entry valid); the writer's error counter is not used. */
 int sched_paged_decode_append(const SchedDecodeArgs *a, const SchedKvAppendArgs *w,
                               void *stream);
 

@@ -46,7 +46,9 @@ struct KParams {
   const void *app_k;
   const void *app_v;
   int64_t app_ts, app_hs; // source strides (elements): row, kv-head
-  uint32_t app_f32;       // fp32 source rows (else the cache's 16-bit type)
+  uint32_t app_f32;       // fp32 source rows (else the cache's 16-bit type, or for an fp8
+                          // cache app_f16 ? fp16 : bf16)
+  uint32_t app_f16;
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -115,6 +117,56 @@ __device__ __forceinline__ unsigned pack_bf16_rne(float lo, float hi) {
 __device__ __forceinline__ unsigned pack_f16_rne(float lo, float hi) {
   const f16x2_t v = {(_Float16)lo, (_Float16)hi};
   return __builtin_bit_cast(unsigned, v);
+}
+
+// fp8 cache scales (the cache writer's rule, also applied by the decode's
+// fused append): the least 2^k (k >= -126) with a <= 448 * 2^k; 0 for a == 0.
+// With a = m * 2^e, m in [0.5, 1): k = e - 9 when m <= 0.875 (448 = 0.875 *
+// 2^9), else e - 8.
+__device__ __forceinline__ float pow2_scale(float a) {
+  if (!(a > 0.f))
+    return 0.f;
+  int e;
+  float m = frexpf(a, &e);
+  int k = e - 9 + (m > 0.875f ? 1 : 0);
+  return ldexpf(1.f, k < -126 ? -126 : k);
+}
+
+// q clamped to the e4m3fn range, round-to-nearest-even, four at once (byte i
+// of the result is element i). Each element rounds on its own, so encoding
+// two at a time (the low half) gives the same bytes.
+__device__ __forceinline__ uint32_t encode4_fp8(const float q[4]) {
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    c[i] = fminf(fmaxf(q[i], -448.f), 448.f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w, true);
+  return (uint32_t)w;
+}
+__device__ __forceinline__ uint32_t encode2_fp8(float q0, float q1) {
+  const float c0 = fminf(fmaxf(q0, -448.f), 448.f), c1 = fminf(fmaxf(q1, -448.f), 448.f);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false) & 0xffffu;
+}
+
+// Max over the 64 lanes of a wave (all lanes active), in VALU cross-lane
+// moves: quad permutes and row rotations (DPP) within each row of 16, then
+// v_permlane16/32_swap across rows. Every lane gets the result.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF,
+                                                          false))); // quad [1,0,3,2]
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF,
+                                                          false))); // quad [2,3,0,1]
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF,
+                                                          false))); // row_ror:4
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF,
+                                                          false))); // row_ror:8
+  const unsigned u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ void store_out(const KParams &P, int64_t idx, float v) {

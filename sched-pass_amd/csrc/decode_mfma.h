@@ -585,9 +585,9 @@ __device__ __forceinline__ void stream_pages(const KParams &P, const MfmaTask &T
 // kv-head h) into slot `slot` of page `page`, in the cache's 16-bit type (an
 // fp32 source rounds to nearest even); lane l writes dims 2l, 2l+1 of both
 // rows (head dim 128). Called by the one wave that streams that page, which
-// waits for its stores before it loads anything, so it reads the token back
-// from the cache like every other token (each page of an item is streamed
-// by exactly one wave, and no other workgroup reads this (page, kv-head)).
+// waits for its stores before it streams, so it reads the token back from
+// the cache like every other token (each page of an item is streamed by
+// exactly one wave, and no other workgroup reads this (page, kv-head)).
 template <bool F16>
 __device__ __forceinline__ void append_token(const KParams &P, uint32_t r, uint32_t h,
                                              int64_t page, uint32_t slot, uint32_t lane) {
@@ -609,7 +609,88 @@ __device__ __forceinline__ void append_token(const KParams &P, uint32_t r, uint3
                  (int64_t)h * P.vhs + (int64_t)slot * P.vts + j;
   *reinterpret_cast<uint32_t *>(kd) = kw;
   *reinterpret_cast<uint32_t *>(vd) = vw;
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
+// Fused append into an fp8 cache: the writer's rule for a one-token append
+// (sched_kv_append) on the token's (page, kv-head h): the new K (and V)
+// scale is pow2_scale of the token row's max |x|, or at least the page's
+// old scale when the token is not the page's first (slot > 0); the row is
+// encoded at it; when the scale grew, the page's earlier rows [0, slot) are
+// re-encoded (decoded at the old scale, encoded at the new one); then the
+// scales are stored. Lane l encodes dims 2l, 2l+1 of the new row (head dim
+// 128, token-major V, one 2-byte store); a re-encode takes 8 bytes of four
+// rows per pass (lanes 16i..16i+15 on row i), loading every row of a group
+// of 16 before storing any. The source and scale loads go out together.
+// The caller waits for the stores (vmcnt 0) before anything reads them.
+__device__ __forceinline__ void regrow_rows_fp8(uint8_t *row0, int64_t tstride, uint32_t slot,
+                                                float s_old, float inv, uint32_t lane) {
+  const uint32_t sub = lane >> 4, off = 8u * (lane & 15u);
+  for (uint32_t t0 = 0; t0 < slot; t0 += 16u) {
+    u32x2_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t t = min(t0 + 4u * k + sub, slot - 1u); // clamped: re-read, not stored
+      w[k] = *reinterpret_cast<const u32x2_t *>(row0 + (int64_t)t * tstride + off);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t t = t0 + 4u * k + sub;
+      float q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        q[i] = fp8e4m3_to_f32((w[k][i >> 2] >> (8 * (i & 3))) & 0xffu) * s_old * inv;
+      if (t < slot)
+        *reinterpret_cast<u32x2_t *>(row0 + (int64_t)t * tstride + off) =
+            u32x2_t{encode4_fp8(q), encode4_fp8(q + 4)};
+    }
+  }
+}
+
+__device__ __forceinline__ void append_token_fp8(const KParams &P, uint32_t r, uint32_t h,
+                                                 int64_t page, uint32_t slot, uint32_t lane) {
+  const uint32_t j = 2u * lane;
+  const int64_t src = (int64_t)r * P.app_ts + (int64_t)h * P.app_hs + j;
+  const int64_t si = (page * P.Hkv + h) * P.scale_stride;
+  float *scl[2] = {const_cast<float *>(P.k_scale) + si, const_cast<float *>(P.v_scale) + si};
+  const float s_old[2] = {*scl[0], *scl[1]};
+  float x[2][2]; // [K, V][dim]
+  for (int t = 0; t < 2; ++t) {
+    const void *base = t ? P.app_v : P.app_k;
+    if (P.app_f32) {
+      const float *f = static_cast<const float *>(base) + src;
+      x[t][0] = f[0], x[t][1] = f[1];
+    } else {
+      const uint32_t w = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(base) +
+                                                            src);
+      if (P.app_f16) {
+        const f16x2_t hv = __builtin_bit_cast(f16x2_t, w);
+        x[t][0] = (float)hv.x, x[t][1] = (float)hv.y;
+      } else {
+        x[t][0] = bf16_bits_to_f32(w & 0xffffu), x[t][1] = bf16_bits_to_f32(w >> 16);
+      }
+    }
+  }
+  uint8_t *row0[2] = {
+      static_cast<uint8_t *>(const_cast<void *>(P.k_pool)) + page * P.kps + (int64_t)h * P.khs,
+      static_cast<uint8_t *>(const_cast<void *>(P.v_pool)) + page * P.vps + (int64_t)h * P.vhs};
+  const int64_t tstride[2] = {P.kts, P.vts};
+  float s_new[2];
+  for (int t = 0; t < 2; ++t) {
+    const float amax = wave_max(fmaxf(fabsf(x[t][0]), fabsf(x[t][1])));
+    const float so = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s_old[t])));
+    const float p = pow2_scale(amax);
+    const float sn = slot == 0u ? p : fmaxf(so, p);
+    const float inv = sn > 0.f ? 1.f / sn : 0.f;
+    s_new[t] = sn;
+    *reinterpret_cast<uint16_t *>(row0[t] + (int64_t)slot * tstride[t] + j) =
+        (uint16_t)encode2_fp8(x[t][0] * inv, x[t][1] * inv);
+    if (slot > 0u && sn != so)
+      regrow_rows_fp8(row0[t], tstride[t], slot, so, inv, lane);
+  }
+  if (lane == 0u) {
+    *scl[0] = s_new[0];
+    *scl[1] = s_new[1];
+  }
 }
 
 // An urgent task's stream at the launch's ring depth: any depth in
@@ -679,12 +760,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       T.p1 = R.p1;
     }
     T.w = w;
-    if constexpr (!FP8 && !LINEAR && VT) {
+    bool wrote = false; // this wave stored the step's token (fused append)
+    if constexpr (!LINEAR && VT) {
       // fused append: the item holding the new token writes it (in the
       // wave that streams its page) before streaming. A stale plan may hold
       // no item for that page; then chunk 0's item writes it too, so the
       // cache gets the token whatever the plan (the task's output is NaN
-      // then, and a second writer stores the same bytes).
+      // then, and a second writer stores the same bytes; an fp8 scale that
+      // the first writer grew is not grown again by the second).
       if (P.app_k != nullptr && T.n > 0u) {
         const uint32_t pos = T.n - 1u, pg = pos / P.ps;
         const bool holds =
@@ -692,10 +775,22 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
             (P.tile_ranged ? pg >= I.p0 && pg < I.p1 : I.chunk == pg / P.tile_pages);
         if (holds || (stale && I.chunk == 0u)) {
           const uint32_t rel = (PG ? pos / 16u : pg) - T.p0;
-          if (rel % (uint32_t)NW == w)
-            append_token<F16>(P, T.r, T.h,
-                              __builtin_amdgcn_readfirstlane(P.bt[T.row + pg]), pos % P.ps,
-                              lane);
+          if (rel % (uint32_t)NW == w) {
+            const int64_t page = __builtin_amdgcn_readfirstlane(P.bt[T.row + pg]);
+            if constexpr (FP8)
+              append_token_fp8(P, T.r, T.h, page, pos % P.ps, lane);
+            else
+              append_token<F16>(P, T.r, T.h, page, pos % P.ps, lane);
+            wrote = true;
+          }
+          // fp8 pages of several 16-token blocks: the re-encoded rows and the
+          // new scale belong to blocks other waves stream
+          if constexpr (FP8 && PG) {
+            if (wrote)
+              __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            wrote = false;
+            __syncthreads();
+          }
         }
       }
     }
@@ -747,6 +842,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
       S.qop[kb] = __builtin_bit_cast(bf16x8_t, qv);
     }
 
+    // the appended token is read back from the cache: its stores complete
+    // first (issued before the Q loads above, so their latency overlaps)
+    if (wrote)
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
       stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.urgent)

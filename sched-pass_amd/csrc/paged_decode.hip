@@ -526,7 +526,7 @@ static uint32_t resident_blocks(const void *fn, int block) {
 struct AppendRows {
   const void *k, *v;
   int64_t ts, hs;
-  bool f32;
+  bool f32, f16; // source fp32, fp16, else bf16 (16-bit caches: the cache's type)
 };
 
 static int launch_decode(const SchedDecodeArgs *a, const AppendRows *app, void *stream) {
@@ -546,6 +546,7 @@ static int launch_decode(const SchedDecodeArgs *a, const AppendRows *app, void *
     kp.app_ts = app->ts;
     kp.app_hs = app->hs;
     kp.app_f32 = app->f32 ? 1u : 0u;
+    kp.app_f16 = app->f16 ? 1u : 0u;
   }
   const uint32_t nitems = kp.L.nitems;
   if (nitems == 0 || kp.ntasks == 0)
@@ -589,14 +590,22 @@ int sched_paged_decode_append(const SchedDecodeArgs *a, const SchedKvAppendArgs 
   if (a->mode != SCHED_PD_SOFTMAX || (a->flags & SCHED_PD_FLAG_CTX_IN_PAGES))
     return set_error(hipErrorInvalidValue,
                      "fused append: softmax decode with ctx_lens in tokens only");
-  if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_F16)
+  const bool fp8 = a->kv_dtype == SCHED_PD_FP8_E4M3;
+  if (a->kv_dtype != SCHED_PD_BF16 && a->kv_dtype != SCHED_PD_F16 && !fp8)
+    return set_error(hipErrorInvalidValue, "fused append: bf16, fp16 or fp8 caches only");
+  if (w->kv_dtype != a->kv_dtype)
+    return set_error(hipErrorInvalidValue, "fused append: the cache dtypes differ");
+  if (fp8 ? (w->src_dtype != SCHED_PD_F32 && w->src_dtype != SCHED_PD_BF16 &&
+             w->src_dtype != SCHED_PD_F16)
+          : (w->src_dtype != a->kv_dtype && w->src_dtype != SCHED_PD_F32))
     return set_error(hipErrorInvalidValue,
-                     "fused append: bf16 or fp16 caches only (an fp8 cache's scales are "
-                     "updated by sched_kv_append)");
-  if (w->kv_dtype != a->kv_dtype || (w->src_dtype != a->kv_dtype && w->src_dtype != SCHED_PD_F32))
+                     "fused append: the source must be fp32 or the cache's dtype (fp32, bf16 "
+                     "or fp16 for an fp8 cache)");
+  if (fp8 && (a->k_scale == nullptr || a->v_scale == nullptr || w->k_scale != a->k_scale ||
+              w->v_scale != a->v_scale))
     return set_error(hipErrorInvalidValue,
-                     "fused append: the cache dtypes differ, or the source is neither fp32 nor "
-                     "the cache's dtype");
+                     "fused append: an fp8 cache needs its k_scale / v_scale, the same in both "
+                     "argument blocks");
   if (a->head_dim != 128 || a->v_dim_stride != 1 || a->v_tok_stride % 2 ||
       a->k_tok_stride % 2 || a->k_page_stride % 2 || a->k_head_stride % 2 ||
       a->v_page_stride % 2 || a->v_head_stride % 2)
@@ -625,7 +634,7 @@ int sched_paged_decode_append(const SchedDecodeArgs *a, const SchedKvAppendArgs 
     return set_error(hipErrorInvalidValue,
                      "fused append: source rows must be 4-byte aligned with even strides");
   AppendRows app{w->k_src, w->v_src, w->src_tok_stride, w->src_head_stride,
-                 w->src_dtype == SCHED_PD_F32};
+                 w->src_dtype == SCHED_PD_F32, w->src_dtype == SCHED_PD_F16};
   return launch_decode(a, &app, stream);
 }
 

@@ -520,9 +520,10 @@ class PagedKvCache:
     def decode_step(self, q, rids, k_new, v_new, **kw):
         """One serving step: append each request's new token (k_new / v_new
         [R, Hkv, d], row i for rids[i]) and decode over the contexts that now
-        hold it. A bf16 / fp16 cache with token-major V and head dim 128 does
-        both in one launch (the decode writes the token into its page before
-        reading it); other caches run the writer, then the decode. Keyword
+        hold it. A bf16, fp16 or fp8 cache with token-major V and head dim
+        128 does both in one launch (the decode writes the token into its
+        page before reading it, an fp8 page's scale grown as the writer
+        grows it); a d-major V runs the writer, then the decode. Keyword
         arguments are those of decode() (`out`, `plane`, `tiles`, ...); a
         split plan must be built from the lengths after the append. With
         `stream`, the step's uploads, table update and launches all go to
@@ -531,10 +532,12 @@ class PagedKvCache:
             return self._decode_step(q, rids, k_new, v_new, **kw)
 
     def _decode_step(self, q, rids, k_new, v_new, **kw):
-        # the MFMA kernel's shapes (16-bit Q of the cache's type, 1..16 q-heads
-        # per kv-head, head dim 128)
+        # the MFMA kernel's shapes (16-bit Q of the cache's type, bf16 Q for
+        # an fp8 cache, 1..16 q-heads per kv-head, head dim 128)
         G = q.shape[1] // self.num_kv_heads if q.shape[1] % self.num_kv_heads == 0 else 0
-        fusable = (self.dtype in (torch.bfloat16, torch.float16) and q.dtype == self.dtype
+        fp8 = self.k_scale is not None
+        q_ok = q.dtype == torch.bfloat16 if fp8 else q.dtype == self.dtype
+        fusable = (q_ok and (fp8 or self.dtype in (torch.bfloat16, torch.float16))
                    and 1 <= G <= 16 and self.v_layout == "tokmajor" and self.head_dim == 128
                    and self.page_size in (16, 32, 64, 128, 256)
                    and kw.get("mode", abi.SOFTMAX) == abi.SOFTMAX
@@ -566,13 +569,15 @@ class PagedKvCache:
                 dt = kw.pop("out_dtype", None) or q.dtype
                 out = torch.empty(len(key), q.shape[1], self.head_dim, dtype=dt,
                                   device=self.device)
-            args = sched_pd.build_args(q, self.k_pool, self.v_pool, bt, ctx, out=out, **kw)
+            args = sched_pd.build_args(q, self.k_pool, self.v_pool, bt, ctx, out=out,
+                                       k_scale=self.k_scale, v_scale=self.v_scale, **kw)
             if getattr(self, "_app_indptr", None) is None or \
                     self._app_indptr.numel() != len(key) + 1:
                 self._app_indptr = torch.arange(len(key) + 1, dtype=torch.int32,
                                                 device=self.device)
             app = build_append_args(k_new, v_new, self._app_indptr, ctx, self.k_pool,
-                                    self.v_pool, bt, v_layout=self.v_layout, max_append=1)
+                                    self.v_pool, bt, v_layout=self.v_layout, max_append=1,
+                                    k_scale=self.k_scale, v_scale=self.v_scale)
             sched_pd.launch_with_append(args, app, kw.get("stream"))
         except Exception:
             self._len[s] -= 1

@@ -786,8 +786,8 @@ def launch(args: abi.SchedDecodeArgs, stream=None) -> None:
 def launch_with_append(args: abi.SchedDecodeArgs, append_args, stream=None) -> None:
     """One launch that writes each request's new token (the one-token-per-
     request append `append_args`, a SchedKvAppendArgs) and decodes `args`
-    over contexts that include it (sched_paged_decode_append): bf16 / fp16
-    caches with token-major V on the MFMA kernel. Raises RuntimeError with
+    over contexts that include it (sched_paged_decode_append): bf16, fp16 or
+    fp8 caches with token-major V on the MFMA kernel. Raises RuntimeError with
     the library's message for anything else."""
     lib = abi.load_library()
     s = torch.cuda.current_stream() if stream is None else stream

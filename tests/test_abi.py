@@ -483,8 +483,16 @@ def test_fused_append_refusals_without_the_gpu(schedlib):
     assert refused("must be the decode's", ctx_lens=ctypes.c_void_p(0x990000))
     assert refused("4-byte aligned", k_src=ctypes.c_void_p(0x70002))
     assert refused("cache dtypes differ", kv_dtype=abi.F16)
+    a.kv_dtype = w.kv_dtype = abi.F32
+    assert refused("bf16, fp16 or fp8 caches only")
     a.kv_dtype = w.kv_dtype = abi.FP8_E4M3
-    assert refused("bf16 or fp16 caches only")
+    assert refused("needs its k_scale / v_scale")                 # no scales
+    a.k_scale, a.v_scale = ctypes.c_void_p(0xB0000), ctypes.c_void_p(0xB0004)
+    w.k_scale, w.v_scale = ctypes.c_void_p(0xB0000), ctypes.c_void_p(0xC0000)
+    assert refused("the same in both")
+    w.v_scale = ctypes.c_void_p(0xB0004)
+    assert refused("fp32, bf16 or fp16 for an fp8 cache", src_dtype=abi.FP8_E4M3)
+    a.k_scale = a.v_scale = w.k_scale = w.v_scale = None
     a.kv_dtype = w.kv_dtype = abi.BF16
     a.v_tok_stride, a.v_dim_stride = 1, 16                  # d-major V
     assert refused("token-major V")

@@ -1,12 +1,13 @@
 """The fused append + decode step (sched_paged_decode_append through
 PagedKvCache.decode_step) against the writer followed by the decode on a
 second cache with the same contents: pools and outputs bitwise equal, over a
-multi-step loop with tokens that open new pages, for bf16 and fp16 caches,
-16- and 64-token pages, 1 and 4 q-heads per kv-head, fp32 and 16-bit source
-rows, with split tiles, the ticket queue and pi; and the oracle on the
-result. Caches the fused path does not take (fp8, d-major V) fall back to
-the two launches with the same result; a direct fused launch on them is
-refused."""
+multi-step loop with tokens that open new pages, for bf16, fp16 and fp8
+caches (fp8: the pages' scales grown and their earlier codes re-encoded as
+the writer does, over steps of growing magnitude), 16- and 64-token pages, 1
+and 4 q-heads per kv-head, fp32 and 16-bit source rows, with split tiles,
+the ticket queue and pi; and the oracle on the result. Caches the fused
+path does not take (d-major V) fall back to the two launches with the same
+result; a direct fused launch on them is refused."""
 import numpy as np
 import pytest
 import torch
@@ -14,7 +15,7 @@ import torch
 import oracle
 import sched_abi as abi
 import sched_pd
-from kv_cache import PagedKvCache, build_append_args
+from kv_cache import PagedKvCache, build_append_args, paired_scales
 from parity import TOL_BF16, par_err
 from sched_rt import SchedPlane
 
@@ -46,10 +47,17 @@ def make_pair(dtype, ps, lens, v_layout="tokmajor", seed=0):
 
 
 def same(a, b):
-    return bool(torch.equal(a.view(torch.uint8), b.view(torch.uint8)))
+    return bool(torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+FP8 = torch.float8_e4m3fn
+
+
+def qdtype(dtype):
+    return torch.bfloat16 if dtype == FP8 else dtype
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, FP8])
 @pytest.mark.parametrize("ps", [16, 64])
 @pytest.mark.parametrize("G", [1, 4])
 @pytest.mark.parametrize("src32", [False, True])
@@ -59,34 +67,43 @@ def test_fused_step_equals_append_then_decode(dtype, ps, G, src32):
     (fa, sep), g = make_pair(dtype, ps, lens, seed=ps + G)
     R = len(lens)
     rids = list(range(R))
-    q = (torch.randn(R, HKV * G, D, device="cuda", generator=g) / D ** 0.5).to(dtype)
+    q = (torch.randn(R, HKV * G, D, device="cuda", generator=g) / D ** 0.5).to(qdtype(dtype))
     for step in range(5):
-        st = torch.float32 if src32 else dtype
-        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(st)
-        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(st)
-        o_fused = fa.decode_step(q, rids, k1, v1)
+        st = torch.float32 if src32 else qdtype(dtype)
+        # fp8: magnitudes grow step by step, so most pages' scales regrow
+        amp = 2.0 ** step if dtype == FP8 else 1.0
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) * amp / D ** 0.5).to(st)
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) * amp / D ** 0.5).to(st)
+        # fp32 output: the oracle check below then measures the kernel, not
+        # the output's rounding (bf16 alone rounds by up to 2^-9 relative)
+        o_fused = fa.decode_step(q, rids, k1, v1, out_dtype=torch.float32)
         sep.append(rids, k1, v1)
-        o_sep = sep.decode(q, rids)
+        o_sep = sep.decode(q, rids, out_dtype=torch.float32)
         torch.cuda.synchronize()
         assert same(o_fused, o_sep), step
         assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
         assert [fa.lens[r] for r in rids] == [sep.lens[r] for r in rids]
+        if dtype == FP8:
+            assert same(fa.k_scale, sep.k_scale) and same(fa.v_scale, sep.v_scale), step
     bt, ctx = fa.block_table(rids)
-    ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor")
+    ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor",
+                        k_scale=fa.k_scale, v_scale=fa.v_scale)
     assert par_err(o_fused.float().cpu(), ref, f"fused {dtype} p{ps} G{G}") <= TOL_BF16
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
 @pytest.mark.parametrize("ranged", [False, True])
-def test_fused_step_with_tiles_queue_and_pi(ranged):
+def test_fused_step_with_tiles_queue_and_pi(ranged, dtype):
     lens = [int(x) for x in np.random.default_rng(2).integers(1, 900, 40)]
-    (fa, sep), g = make_pair(torch.bfloat16, 16, lens, seed=3)
+    (fa, sep), g = make_pair(dtype, 16, lens, seed=3)
     R = len(lens)
     rids = list(range(R))
     q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
     tp = 8
     for step in range(4):
-        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
-        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
+        amp = 2.0 ** step if dtype == FP8 else 1.0
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) * amp / D ** 0.5).bfloat16()
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) * amp / D ** 0.5).bfloat16()
         after = [fa.lens[r] + 1 for r in rids]          # plan from the post-append lengths
         if ranged:     # host rows, chunks of 8 pages and of 3 at the end of pi
             tiles = sched_pd.plan_ranges_host(after, 16, HKV, task_order=np.arange(R * HKV)[::-1],
@@ -106,6 +123,8 @@ def test_fused_step_with_tiles_queue_and_pi(ranged):
         torch.cuda.synchronize()
         assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
         assert same(o_fused, o_sep), step
+        if dtype == FP8:
+            assert same(fa.k_scale, sep.k_scale) and same(fa.v_scale, sep.v_scale), step
 
 
 @pytest.mark.parametrize("layout", ["tokmajor", "dmajor"])
@@ -138,7 +157,7 @@ def test_steps_on_a_side_stream_match_the_current_stream(layout):
 
 def test_caches_without_the_fused_path_fall_back_and_direct_launch_is_refused():
     lens = [5, 16, 40]
-    for dtype, layout in ((torch.float8_e4m3fn, "tokmajor"), (torch.bfloat16, "dmajor")):
+    for dtype, layout in ((torch.float8_e4m3fn, "dmajor"), (torch.bfloat16, "dmajor")):
         (fa, sep), g = make_pair(dtype, 16, lens, v_layout=layout, seed=7)
         rids = [0, 1, 2]
         q = (torch.randn(3, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
@@ -199,8 +218,9 @@ def test_fused_launch_over_a_csr_page_table():
     assert same(pools[0][0], pools[1][0]) and same(pools[0][1], pools[1][1])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
 @pytest.mark.parametrize("ranged", [False, True])
-def test_fused_launch_with_a_stale_plan_still_writes_the_token(ranged):
+def test_fused_launch_with_a_stale_plan_still_writes_the_token(ranged, dtype):
     """A plan built from the lengths before the append, where the new token
     opens a page in a chunk the plan does not hold (64 tokens in 4-page
     chunks of 16-token pages: the 65th token starts chunk 1). The fused
@@ -210,7 +230,7 @@ def test_fused_launch_with_a_stale_plan_still_writes_the_token(ranged):
     this stale is refused before anything is written."""
     from kv_cache import append as kv_append
     lens = [64, 10, 128, 40]          # requests 0 and 2 open a page in a new chunk
-    (c, _), g = make_pair(torch.bfloat16, 16, lens, seed=13)
+    (c, _), g = make_pair(dtype, 16, lens, seed=13)
     rids = list(range(len(lens)))
     R, tp = len(lens), 4
     before = c.lengths(rids)
@@ -236,40 +256,50 @@ def test_fused_launch_with_a_stale_plan_still_writes_the_token(ranged):
     app_ptr = torch.arange(R + 1, dtype=torch.int32, device="cuda")
     plan = torch.from_numpy(plan_h).cuda()
     outs, pools = [], []
+    fp8 = dtype == FP8
     for fused in (True, False):
         kp, vp = c.k_pool.clone(), c.v_pool.clone()
+        sc = {}
+        if fp8:
+            ks, vs = paired_scales(c.k_scale.numel(), "cuda")
+            ks.copy_(c.k_scale)
+            vs.copy_(c.v_scale)
+            sc = dict(k_scale=ks, v_scale=vs)
         out = torch.empty(R, HKV * 4, D, dtype=torch.bfloat16, device="cuda")
         ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
         kw = dict(tiles=plan, workspace=ws) if ranged else \
             dict(tiles=plan, tile_pages=tp, workspace=ws)
-        args = sched_pd.build_args(q, kp, vp, bt, ctx, out=out, v_layout="tokmajor", **kw)
+        args = sched_pd.build_args(q, kp, vp, bt, ctx, out=out, v_layout="tokmajor", **sc, **kw)
         if fused:
             app = build_append_args(k1, v1, app_ptr, ctx, kp, vp, bt, v_layout="tokmajor",
-                                    max_append=1)
+                                    max_append=1, **sc)
             sched_pd.launch_with_append(args, app)
         else:
-            kv_append(k1, v1, app_ptr, ctx, kp, vp, bt, v_layout="tokmajor", max_append=1)
+            kv_append(k1, v1, app_ptr, ctx, kp, vp, bt, v_layout="tokmajor", max_append=1, **sc)
             sched_pd.launch(args)
         torch.cuda.synchronize()
         outs.append(out)
-        pools.append((kp, vp))
+        pools.append((kp, vp) + ((sc["k_scale"], sc["v_scale"]) if fp8 else ()))
         assert sched_pd.stale_plan_count(ws) == 2 * HKV
         assert int(ws[sched_pd.WS_COUNTERS_OFF:sched_pd.WS_COUNTERS_OFF + 4 * R * HKV]
                    .view(torch.int32).abs().sum()) == 0
-    assert same(pools[0][0], pools[1][0]) and same(pools[0][1], pools[1][1])
+    for a_, b_ in zip(pools[0], pools[1]):
+        assert same(a_, b_)
     got = outs[0].float()
     assert torch.isnan(got[[0, 2]]).all() and torch.isfinite(got[[1, 3]]).all()
     assert same(outs[0][[1, 3]], outs[1][[1, 3]])
-    ref = oracle.decode(q, pools[0][0], pools[0][1], bt, ctx, v_layout="tokmajor")
+    ref = oracle.decode(q, pools[0][0], pools[0][1], bt, ctx, v_layout="tokmajor",
+                        **({"k_scale": pools[0][2], "v_scale": pools[0][3]} if fp8 else {}))
     assert par_err(got[[1, 3]].cpu(), np.asarray(ref)[[1, 3]]) <= TOL_BF16
 
 
-def test_fused_step_under_a_shed_budget():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
+def test_fused_step_under_a_shed_budget(dtype):
     """Prefix budgets below the new token's position: the token is still
     written (the pages past the budget are not read), and the output equals
     append-then-decode under the same rows."""
     lens = [30, 100, 250, 17]
-    (fa, sep), g = make_pair(torch.bfloat16, 16, lens, seed=17)
+    (fa, sep), g = make_pair(dtype, 16, lens, seed=17)
     R = len(lens)
     rids = list(range(R))
     q = (torch.randn(R, HKV * 4, D, device="cuda", generator=g) / D ** 0.5).bfloat16()
@@ -285,3 +315,5 @@ def test_fused_step_under_a_shed_budget():
         torch.cuda.synchronize()
         assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
         assert same(o_fused, o_sep), step
+        if dtype == FP8:
+            assert same(fa.k_scale, sep.k_scale) and same(fa.v_scale, sep.v_scale), step
