@@ -759,33 +759,37 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
     st["paged_kv_cache_default"] = kv_cache.PagedKvCache(1, hkv, d, 16, dtype=torch.bfloat16,
                                                          device="cuda").v_layout
     res["serving_step_page16"] = st
-    # MFMA vs VALU kernel below 4 q-heads per kv-head (same KV bytes: Hkv 8)
+    # The kernel by q-heads per kv-head (same KV bytes: Hkv 8, bf16 Q): over
+    # token-major V the MFMA kernel against the one-wave kernel (the default
+    # below 4 q-heads per kv-head); over d-major V the MFMA kernel against the
+    # general VALU kernel
     grp = {}
-    for G in (1, 2, 4):
+    for G in (1, 2, 3, 4):
         qg = (torch.randn(R, 8 * G, d, device="cuda", generator=g) / d ** 0.5).bfloat16()
         og = torch.empty(R, 8 * G, d, dtype=torch.bfloat16, device="cuda")
         row = {}
-        for kern, flags in (("mfma", 0), ("valu", abi.FLAG_FORCE_VALU)):
-            args = [sched_pd.build_args(qg, kp, vp.view(npg, hkv, d, ps), bt, ctx, out=og,
+        for name, vpool, layout, flags in (
+                ("tokmajor_mfma", vp, "tokmajor", abi.FLAG_NO_WAVE),
+                ("tokmajor_wave", vp, "tokmajor", abi.FLAG_NO_MFMA),
+                ("dmajor_mfma", vp.view(npg, hkv, d, ps), "dmajor", 0),
+                ("dmajor_valu", vp.view(npg, hkv, d, ps), "dmajor", abi.FLAG_FORCE_VALU)):
+            args = [sched_pd.build_args(qg, kp, vpool, bt, ctx, out=og, v_layout=layout,
                                         flags=flags) for bt in bts]
+            kind = sched_pd.kernel_kind(args[0])
+            if name.endswith("wave") and kind != "wave":
+                continue                     # G = 4: the one-wave kernel stops at 3
             f = lambda i: sched_pd.launch(args[i % tables], stream)  # noqa: E731
             for i in range(2 * tables):
                 f(i)
             torch.cuda.synchronize()
-            row[kern + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
-            row["default"] = sched_pd.kernel_kind(sched_pd.build_args(
-                qg, kp, vp.view(npg, hkv, d, ps), bts[0], ctx, out=og))
-        if G == 1:
-            # one wave per task, over token-major V (fp32 Q: the MFMA kernel,
-            # which takes bf16 Q, would be chosen otherwise)
-            args = [sched_pd.build_args(qg.float(), kp, vp, bt, ctx, out=og, v_layout="tokmajor")
-                    for bt in bts]
-            assert sched_pd.kernel_kind(args[0]) == "wave"
-            f = lambda i: sched_pd.launch(args[i % tables], stream)  # noqa: E731
-            for i in range(2 * tables):
-                f(i)
-            torch.cuda.synchronize()
-            row["wave_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+            row[name + "_us"] = round(min(time_region(f, 20, stream) for _ in range(3)) * 1e3, 2)
+        for layout, vpool in (("tokmajor", vp), ("dmajor", vp.view(npg, hkv, d, ps))):
+            row[layout + "_default"] = sched_pd.kernel_kind(sched_pd.build_args(
+                qg, kp, vpool, bts[0], ctx, out=og, v_layout=layout))
+        if "tokmajor_wave_us" in row:
+            row["wave_vs_mfma_pct"] = round(
+                100.0 * (row["tokmajor_wave_us"] - row["tokmajor_mfma_us"]) /
+                row["tokmajor_mfma_us"], 2)
         grp[f"G{G}"] = row
     res["kernel_by_group"] = grp
     del kp, vp
@@ -880,6 +884,12 @@ def bench_pi_makespan(torch, sched_pd, batch_sizes=(256, 1024, 4096, 8192)):
     return res
 
 
+# Split work items of the serving-trace eval's one-wave steps: 4 pages of 32
+# tokens (32 KiB of fp32 K and V), about two of a wave's rings in flight
+# (swept 3..12 pages: 4-6 best at 8192 requests, 3-4 at 256).
+SPLIT_PAGES = 4
+
+
 def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
     """The reference's serving-trace evaluation (test/py/eval_trace.py:36-160,
     published at README.md:95-118): NSEQ requests of one fp32 head (d 32)
@@ -897,7 +907,9 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
     does); mean and min per policy, outputs bit-exact against identity, and
     the bound launcher bit-exact against the same plane passed in the
     argument block. The regime map repeats identity against the closed loop
-    at every batch size."""
+    at every batch size. Then the same steps over split work items (a pair
+    plan of SPLIT_PAGES pages, static grid, through the argument block):
+    stock, identity and LPT over the items from the timer, at every size."""
     import ctypes
 
     import numpy as np
@@ -916,7 +928,8 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)
 
-    res = {"regime_lpt_timer_vs_identity_pct": {}}
+    res = {"regime_lpt_timer_vs_identity_pct": {}, "regime_split_lpt_timer_vs_identity_pct": {},
+           "regime_split_identity_vs_identity_pct": {}, "split_pages": SPLIT_PAGES}
     for nseq in batch_sizes:
         gen = torch.Generator().manual_seed(0)
         is_long = torch.rand(nseq, generator=gen) < 0.1
@@ -1009,6 +1022,52 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         base = row["identity"]["mean_us"]
         gain = round(100 * (row["lpt_timer"]["mean_us"] - base) / base, 2)
         res["regime_lpt_timer_vs_identity_pct"][str(nseq)] = gain
+        # the same step over split work items (a pair plan of SPLIT_PAGES
+        # pages, static grid; one wave per item), through the argument block:
+        # stock (no lever tables), and pi (identity, LPT over the items by
+        # the identity step's timer rows) from the plane, bit-exact between
+        # them
+        plane.unbind_launcher()
+        lens_tok = nbl_h.numpy().astype(np.int64) * PT
+        tiles = sched_pd.plan_tiles_host(lens_tok, PT, SPLIT_PAGES, 1)
+        nti = tiles.shape[0]
+        split = {}
+        a_split = sched_pd.build_args(q, k_view, v_view, bt, nbl, tiles=tiles,
+                                      tile_pages=SPLIT_PAGES, **common)
+        for _ in range(3):
+            sched_pd.launch(a_split, stream)
+        t = [step_ms(lambda: sched_pd.launch(a_split, stream)) for _ in range(steps)]
+        split["stock"] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
+                          "min_us": round(1e3 * min(t), 2)}
+        o_split = out.clone()
+        p_items = SchedPlane(max_tasks=max(nti, nseq))
+        p_items.set_num_tasks(0)
+        p_items.push()
+        a_items = sched_pd.build_args(q, k_view, v_view, bt, nbl, tiles=tiles,
+                                      tile_pages=SPLIT_PAGES, plane=p_items, **common)
+        for name in ("identity", "lpt_timer"):
+            if name == "lpt_timer":
+                # closed loop: one identity step fills the per-request rows
+                p_items.clear_timer()
+                sched_pd.launch(a_items, stream)
+                torch.cuda.synchronize()
+                cyc = p_items.read_timer()[:nseq].cpu().numpy().astype(np.float64)
+                p_items.install_order(sched_pd.tile_order_by_task_key(tiles, cyc), nti)
+                p_items.push()
+            for _ in range(3):
+                sched_pd.launch(a_items, stream)
+            t = [step_ms(lambda: sched_pd.launch(a_items, stream)) for _ in range(steps)]
+            split[name] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
+                           "min_us": round(1e3 * min(t), 2)}
+            exact = exact and bool(torch.equal(out, o_split))
+        sb = split["identity"]["mean_us"]
+        res["regime_split_lpt_timer_vs_identity_pct"][str(nseq)] = round(
+            100 * (split["lpt_timer"]["mean_us"] - sb) / sb, 2)
+        res["regime_split_identity_vs_identity_pct"][str(nseq)] = round(
+            100 * (sb - base) / base, 2)
+        split["items"] = nti
+        if nseq == batch_sizes[-1]:
+            row["split"] = split
         if nseq == batch_sizes[-1]:
             for name in ("sorted_ascending", "lpt_oracle", "lpt_timer"):
                 row[name]["vs_identity_pct"] = round(
@@ -1021,11 +1080,14 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
                 gbs = row["kv_bytes"] / row[name]["mean_us"] / 1e3
                 row[name]["gbs"] = round(gbs, 1)
                 row[name]["frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 4)
+            for name in ("stock", "identity", "lpt_timer"):
+                gbs = row["kv_bytes"] / row["split"][name]["mean_us"] / 1e3
+                row["split"][name]["gbs"] = round(gbs, 1)
+                row["split"][name]["frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 4)
             res[str(nseq)] = row
         res.setdefault("bit_exact_vs_identity", True)
         res["bit_exact_vs_identity"] = res["bit_exact_vs_identity"] and exact
-        plane.unbind_launcher()
-        del kv, pages, q, out, plane, stock, armed, by_args, launcher
+        del kv, pages, q, out, plane, stock, armed, by_args, launcher, a_split, a_items, p_items
         torch.cuda.empty_cache()
     return res
 

@@ -108,7 +108,9 @@ int sched_kv_append(const SchedKvAppendArgs *a, void *stream);
  * decode reads caches an engine filled); for serving loops, where the
  * separate append is a small, launch-bound kernel per step. Supported:
  * softmax decode on the MFMA kernel (head dim 128, bf16, fp16 or fp8 cache,
- * token-major V), one token per request (w->num_tokens == w->num_requests;
+ * token-major V) or the one-wave kernel (the same with a 16-bit cache), the
+ * kernel the decode alone would select, so the bits are those of the two
+ * calls; one token per request (w->num_tokens == w->num_requests;
  * source row r belongs to request r; append_indptr is not read), source
  * dtype fp32 or the cache's (fp32, bf16 or fp16 for fp8); w's pools,
  * strides, page table, ctx_lens (and fp8 scales) must be a's. Anything else

@@ -204,8 +204,11 @@ uint64_t sched_rt_timer_host_va(void);
 #define SCHED_PD_FLAG_SHED_LOADS 0x10u  /* load shed tokens and mask them (reference weave,
                                            lib/SchedWeave.cpp:646-651) instead of skipping
                                            the pages past a prefix budget; same output */
-#define SCHED_PD_FLAG_NO_WAVE 0x20u     /* do not use the one-wave-per-task kernel (G = 1):
-                                           take the general VALU kernel instead */
+#define SCHED_PD_FLAG_NO_WAVE 0x20u     /* do not use the one-wave-per-item kernel (G <= 3):
+                                           take the MFMA kernel where it applies, else the
+                                           general VALU kernel */
+#define SCHED_PD_FLAG_NO_MFMA 0x40u     /* do not use the MFMA kernel: the one-wave-per-item
+                                           kernel where it applies, else the VALU kernel */
 
 /* One decode step. Element (page, kv-head h, token t, dim j) of the pools:
  *   K: k_pool + page*k_page_stride + h*k_head_stride + t*k_tok_stride + j
@@ -331,7 +334,8 @@ int64_t sched_paged_decode_workspace_bytes(const SchedDecodeArgs *a);
  * (python/kernels/paged_softmax.cu:61-67), whose CTAs are tasks. */
 int sched_paged_decode_occupancy(const SchedDecodeArgs *a);
 
-/* Policy lever depths of the kernel `a` selects (a->pf_dist ignored): *stock =
+/* Policy lever depths of the kernel a launch with a nonzero pf_dist selects
+ * (a->pf_dist ignored; the one-wave kernel, which has no ring, is set aside): *stock =
  * pages of loads in flight per wave for stock and polite tasks, *deepest = the
  * deepest ring an urgent task may use (its default); pf_dist may be 0 or any
  * value in [*stock, *deepest]. Both 0 for the VALU kernel, which has no ring
@@ -342,8 +346,12 @@ int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
                                       uint32_t *deepest);
 
 /* Which kernel `a` selects: 0 = the general VALU kernel (one workgroup per
- * work item), 1 = MFMA, 2 = one wave per task (G = 1 softmax over token-major
- * rows, no split tiles), -1 = invalid args. */
+ * work item), 1 = MFMA, 2 = one wave per work item (softmax over token-major
+ * K and V rows, 1..3 q-heads per kv-head), -1 = invalid args. Selection: the
+ * one-wave kernel at one q-head per kv-head wherever it applies (unless
+ * pf_dist asks for the MFMA kernel's prefetch ring), else the MFMA kernel
+ * where it applies, else the one-wave kernel where it applies, else the
+ * VALU kernel. */
 int sched_paged_decode_kernel_kind(const SchedDecodeArgs *a);
 
 /* Compute-unit count of the current device (0 on error). */

@@ -22,7 +22,7 @@ SOURCES = ["sched_rt.hip", "paged_decode.hip", "probe.hip", "kv_append.hip", "st
            # the decode kernels, one instantiation group per unit (kernel_set.h)
            "kernels_bf16_page16.hip", "kernels_bf16_pageblocks.hip", "kernels_fp8.hip", "kernels_fp8_tokmajor.hip",
            "kernels_f16.hip", "kernels_f16_pageblocks.hip", "kernels_valu.hip",
-           "kernels_wave.hip"]
+           "kernels_wave.hip", "kernels_wave_groups.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -35,6 +35,77 @@ template <typename T> __device__ __forceinline__ T ld_coherent(const T *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The merge of a task's partials, in the work item that completes it: the
+// partials of chunks 0 .. nchunks-1 (work items base .. base + nchunks - 1)
+// read in chunk order, outputs (orow + g) * D + j for g < G (linear: orow * D
+// + j). Threads tid, tid + nthreads, ... take the G * D outputs. The loads go
+// out kMergeBatch chunks at a time (chunk indices past the last are clamped
+// to it and their terms dropped by a select), so a task of N chunks costs
+// about 2N / kMergeBatch memory round trips instead of 2N; the arithmetic
+// and its order are those of a plain loop over c = 0 .. N-1.
+template <int D, typename AccT, bool LINEAR>
+__device__ __forceinline__ void merge_partials(const KParams &P, uint32_t base, uint32_t nchunks,
+                                               uint32_t G, int64_t orow, uint32_t tid,
+                                               uint32_t nthreads) {
+  constexpr uint32_t kMergeBatch = 8;
+  const uint32_t clast = nchunks - 1u;
+  for (uint32_t idx = tid; idx < G * D; idx += nthreads) {
+    const uint32_t g = idx / D, j = idx % D;
+    if (LINEAR) {
+      const AccT *acc = static_cast<const AccT *>(P.ws_acc) + (size_t)base * G * D + j;
+      AccT a = 0;
+      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
+        AccT v[kMergeBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k)
+          v[k] = ld_coherent(acc + (size_t)min(c0 + k, clast) * G * D);
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k)
+          a = c0 + k < nchunks ? a + v[k] : a;
+      }
+      store_out(P, orow * D + j, (float)a);
+    } else {
+      // (m, l) of a chunk as one 8-byte load
+      const uint64_t *ml = reinterpret_cast<const uint64_t *>(P.ws_ml + (size_t)base * G * 2) + g;
+      const AccT *acc = static_cast<const AccT *>(P.ws_acc) + (size_t)base * G * D + g * D + j;
+      const size_t stride_ml = G; // u64 words per chunk
+      const size_t stride_acc = (size_t)G * D;
+      float M = __uint_as_float((uint32_t)ld_coherent(ml));
+      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
+        uint64_t w[kMergeBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k)
+          w[k] = ld_coherent(ml + min(c0 + k, clast) * stride_ml);
+        // a clamped repeat of the last chunk leaves the max unchanged
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k)
+          M = fmaxf(M, __uint_as_float((uint32_t)w[k]));
+      }
+      float Lt = 0.f, A = 0.f;
+      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
+        uint64_t w[kMergeBatch];
+        AccT v[kMergeBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k) {
+          const size_t c = min(c0 + k, clast);
+          w[k] = ld_coherent(ml + c * stride_ml);
+          v[k] = ld_coherent(acc + c * stride_acc);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; ++k) {
+          const float e = __builtin_amdgcn_exp2f(__uint_as_float((uint32_t)w[k]) - M);
+          const float lt = Lt + __uint_as_float((uint32_t)(w[k] >> 32)) * e;
+          const float at = A + (float)v[k] * e;
+          const bool in = c0 + k < nchunks;
+          Lt = in ? lt : Lt;
+          A = in ? at : A;
+        }
+      }
+      store_out(P, (orow + g) * D + j, A / Lt);
+    }
+  }
+}
+
 // Softmax: acc is unnormalised with running max m and sum l per head.
 // Linear: acc is a plain sum (m, l unused).
 template <int NW, int GMAX, int D, typename AccT, bool LINEAR>
@@ -115,69 +186,7 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
   __syncthreads();
   if (!s_last)
     return;
-  // The merge reads every chunk's partial in chunk order. The loads go out
-  // kMergeBatch chunks at a time (chunk indices past the last are clamped to
-  // it and their terms dropped by a select), so a task of N chunks costs
-  // about 2N / kMergeBatch memory round trips instead of 2N; the arithmetic
-  // and its order are those of a plain loop over c = 0 .. N-1.
-  constexpr uint32_t kMergeBatch = 8;
-  const uint32_t base = wi - chunk; // task-major list: chunk c is work item base + c
-  const uint32_t clast = nchunks - 1u;
-  for (uint32_t idx = threadIdx.x; idx < G * D; idx += NT) {
-    const uint32_t g = idx / D, j = idx % D;
-    if (LINEAR) {
-      const AccT *acc = static_cast<const AccT *>(P.ws_acc) + (size_t)base * G * D + j;
-      AccT a = 0;
-      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
-        AccT v[kMergeBatch];
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          v[k] = ld_coherent(acc + (size_t)min(c0 + k, clast) * G * D);
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          a = c0 + k < nchunks ? a + v[k] : a;
-      }
-      store_out(P, orow * D + j, (float)a);
-    } else {
-      // (m, l) of a chunk as one 8-byte load
-      const uint64_t *ml = reinterpret_cast<const uint64_t *>(P.ws_ml + (size_t)base * G * 2) + g;
-      const AccT *acc = static_cast<const AccT *>(P.ws_acc) + (size_t)base * G * D + g * D + j;
-      const size_t stride_ml = G; // u64 words per chunk
-      const size_t stride_acc = (size_t)G * D;
-      float M = __uint_as_float((uint32_t)ld_coherent(ml));
-      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
-        uint64_t w[kMergeBatch];
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          w[k] = ld_coherent(ml + min(c0 + k, clast) * stride_ml);
-        // a clamped repeat of the last chunk leaves the max unchanged
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          M = fmaxf(M, __uint_as_float((uint32_t)w[k]));
-      }
-      float Lt = 0.f, A = 0.f;
-      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
-        uint64_t w[kMergeBatch];
-        AccT v[kMergeBatch];
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k) {
-          const size_t c = min(c0 + k, clast);
-          w[k] = ld_coherent(ml + c * stride_ml);
-          v[k] = ld_coherent(acc + c * stride_acc);
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k) {
-          const float e = __builtin_amdgcn_exp2f(__uint_as_float((uint32_t)w[k]) - M);
-          const float lt = Lt + __uint_as_float((uint32_t)(w[k] >> 32)) * e;
-          const float at = A + (float)v[k] * e;
-          const bool in = c0 + k < nchunks;
-          Lt = in ? lt : Lt;
-          A = in ? at : A;
-        }
-      }
-      store_out(P, (orow + g) * D + j, A / Lt);
-    }
-  }
+  merge_partials<D, AccT, LINEAR>(P, wi - chunk, nchunks, G, orow, threadIdx.x, NT);
 }
 
 // A work item's plan row. Pair rows (task, chunk) cover pages

@@ -169,6 +169,37 @@ __device__ __forceinline__ float wave_max(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Fused append: the K and V rows of request r's new token (source row r,
+// kv-head h) into slot `slot` of page `page`, in the cache's 16-bit type (an
+// fp32 source rounds to nearest even); lane l writes dims 2l, 2l+1 of both
+// rows (head dim 128). Called by the one wave that streams that page (in
+// either the MFMA or the one-wave kernel), which waits for its stores
+// before it streams, so it reads the token back from the cache like every
+// other token (each page of an item is streamed by exactly one wave, and no
+// other workgroup reads this (page, kv-head)).
+template <bool F16>
+__device__ __forceinline__ void append_token(const KParams &P, uint32_t r, uint32_t h,
+                                             int64_t page, uint32_t slot, uint32_t lane) {
+  const uint32_t j = 2u * lane;
+  const int64_t src = (int64_t)r * P.app_ts + (int64_t)h * P.app_hs + j;
+  uint32_t kw, vw;
+  if (P.app_f32) {
+    const float *ks = static_cast<const float *>(P.app_k) + src;
+    const float *vs = static_cast<const float *>(P.app_v) + src;
+    kw = F16 ? pack_f16_rne(ks[0], ks[1]) : pack_bf16_rne(ks[0], ks[1]);
+    vw = F16 ? pack_f16_rne(vs[0], vs[1]) : pack_bf16_rne(vs[0], vs[1]);
+  } else {
+    kw = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(P.app_k) + src);
+    vw = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(P.app_v) + src);
+  }
+  uint16_t *kd = static_cast<uint16_t *>(const_cast<void *>(P.k_pool)) + page * P.kps +
+                 (int64_t)h * P.khs + (int64_t)slot * P.kts + j;
+  uint16_t *vd = static_cast<uint16_t *>(const_cast<void *>(P.v_pool)) + page * P.vps +
+                 (int64_t)h * P.vhs + (int64_t)slot * P.vts + j;
+  *reinterpret_cast<uint32_t *>(kd) = kw;
+  *reinterpret_cast<uint32_t *>(vd) = vw;
+}
+
 __device__ __forceinline__ void store_out(const KParams &P, int64_t idx, float v) {
   if (P.o_f32)
     static_cast<float *>(P.out)[idx] = v;

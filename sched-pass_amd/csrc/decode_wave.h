@@ -32,7 +32,9 @@
 // The policy lever has no action here (no prefetch ring choice).
 #pragma once
 
-#include "common.h"
+#include <type_traits>
+
+#include "combine.h"
 
 namespace schedpd {
 
@@ -204,7 +206,61 @@ __device__ __forceinline__ void run_wave_tasks(const LeverTables &L, Body &&body
   }
 }
 
-template <typename KVT, int D, int NWT>
+// End of one work item of the one-wave kernel, per head g: the wave's merged
+// state (lanes of token slot 0 hold dims ds*VN..+VN-1 of acc; m and l are
+// the same on every lane) -> the task's output rows, or this item's partial
+// and, in the item that completes the task, the merge of the task's
+// partials in chunk order (merge_partials, all 64 lanes). The wave waits for
+// its partial's stores before its arrival atomic; the reading item loads
+// only after its own arrival has returned (see the handoff note at the top
+// of combine.h).
+template <int G, int VN, int D>
+__device__ __forceinline__ void finish_wave_item(const KParams &P, uint32_t wi, uint32_t task,
+                                                 uint32_t chunk, uint32_t nchunks, uint32_t r,
+                                                 uint32_t h, const WaveState<VN> (&st)[G],
+                                                 uint32_t lane, uint32_t ts, uint32_t ds) {
+  const int64_t orow = (int64_t)r * P.Hq + (int64_t)h * G;
+  if (nchunks <= 1u) {
+    if (ts == 0u) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < VN; ++e)
+          store_out(P, (orow + g) * D + ds * VN + e, st[g].acc[e] / st[g].l);
+    }
+    return;
+  }
+  float *pacc = static_cast<float *>(P.ws_acc) + (size_t)wi * G * D;
+  float *pml = P.ws_ml + (size_t)wi * G * 2;
+  if (ts == 0u) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < VN; ++e)
+        __hip_atomic_store(pacc + g * D + ds * VN + e, st[g].acc[e], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (lane == 0u) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      __hip_atomic_store(pml + 2 * g, st[g].m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pml + 2 * g + 1, st[g].l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  uint32_t last = 0u;
+  if (lane == 0u) {
+    const uint32_t old = __hip_atomic_fetch_add(P.ws_count + task, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    last = old == nchunks - 1u ? 1u : 0u;
+    if (last)
+      __hip_atomic_store(P.ws_count + task, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (__builtin_amdgcn_readfirstlane(last))
+    merge_partials<D, float, false>(P, wi - chunk, nchunks, G, orow, lane, 64u);
+}
+
+template <typename KVT, int D, int NWT, int G>
 __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
   using S = WaveShape<KVT, D>;
   constexpr int VN = S::VN, LPR = S::LPR, TPI = S::TPI, NI = S::NI, DEPTH = S::DEPTH;
@@ -213,30 +269,63 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
   const uint32_t ts = lane / LPR, ds = lane % LPR;
   const bool toff = timer_off_latched(P.L);
 
-  run_wave_tasks<NWT>(P.L, [&](uint32_t task) __attribute__((always_inline)) {
-    if (task >= P.ntasks)
+  run_wave_tasks<NWT>(P.L, [&](uint32_t wi) __attribute__((always_inline)) {
+    if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
+    const ItemRow I = item_row(P, wi);
+    const uint32_t task = I.task;
+    if (task >= P.ntasks)
+      return;
     const uint32_t r = task / P.Hkv, h = task % P.Hkv;
     const TaskPolicy pol = task_policy(P.L, task);
     const uint32_t n = ctx_tokens(P, r);
     const uint32_t nload = load_extent(P, n, pol.budget);
+    const uint32_t ps = P.ps, cpp = ps / 16u; // 16-token chunks per page
+    const ItemRange R = item_range(P, I, n, (nload + ps - 1u) / ps);
+    if (item_skip(P, wi, I, R))
+      return;
+    const bool stale = item_stale(P, wi, I, R, n);
+    // the item's 16-token chunks [c_begin, c_end) of those read
     const uint32_t nchunks = (nload + 15u) / 16u;
+    const uint32_t c_end = min(R.p1 * cpp, nchunks), c_begin = min(R.p0 * cpp, c_end);
     const int64_t row = P.indptr ? (int64_t)__builtin_amdgcn_readfirstlane(P.indptr[r])
                                  : (int64_t)r * P.bt_stride;
+    // fused append (16-bit caches, head dim 128): the item holding the
+    // step's token writes it before streaming, as in the MFMA kernel (a
+    // stale plan's chunk 0 too)
+    bool wrote = false;
+    if constexpr (!std::is_same<KVT, float>::value && D == 128) {
+      if (P.app_k != nullptr && n > 0u) {
+        const uint32_t pos = n - 1u, pg = pos / ps;
+        const bool holds =
+            P.tiles == nullptr ||
+            (P.tile_ranged ? pg >= I.p0 && pg < I.p1 : I.chunk == pg / P.tile_pages);
+        if (holds || (stale && I.chunk == 0u)) {
+          append_token<std::is_same<KVT, _Float16>::value>(
+              P, r, h, __builtin_amdgcn_readfirstlane(P.bt[row + pg]), pos % ps, lane);
+          wrote = true;
+        }
+      }
+    }
 
-    // the lane's VN dims of q, pre-scaled into the exp2 domain
-    float q[VN];
+    // the lane's VN dims of each head's q, pre-scaled into the exp2 domain
+    float q[G][VN];
 #pragma unroll
-    for (int e = 0; e < VN; ++e)
-      q[e] = load_q(P, ((int64_t)r * P.Hq + h) * D + ds * VN + e) * P.scale_log2;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < VN; ++e)
+        q[g][e] = load_q(P, ((int64_t)r * P.Hq + h * G + g) * D + ds * VN + e) * P.scale_log2;
 
-    WaveState<VN> st;
-    st.m = kMInit;
-    st.l = 0.f;
+    WaveState<VN> st[G];
 #pragma unroll
-    for (int e = 0; e < VN; ++e)
-      st.acc[e] = 0.f;
+    for (int g = 0; g < G; ++g) {
+      st[g].m = kMInit;
+      st[g].l = 0.f;
+#pragma unroll
+      for (int e = 0; e < VN; ++e)
+        st[g].acc[e] = 0.f;
+    }
 
     // uniform (scalar) page bases; each lane adds a 32-bit offset (its token
     // slot's row and its 16 bytes of the row), so the loads take the
@@ -247,7 +336,6 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
     const int64_t kstep = (int64_t)TPI * P.kts * EB, vstep = (int64_t)TPI * P.vts * EB;
     const int64_t krow = P.kts * EB, vrow = P.vts * EB;
     const uint32_t klane = ts * (uint32_t)krow + ds * 16u, vlane = ts * (uint32_t)vrow + ds * 16u;
-    const uint32_t ps = P.ps, cpp = ps / 16u; // 16-token chunks per page
     const bool prefix = P.tau_scope == SCHED_PD_TAU_PREFIX;
     const uint32_t budget = pol.budget;
 
@@ -274,51 +362,62 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
       // a chunk wholly inside the context and the budget needs no mask
       const bool full = pos0 + 16u <= n &&
                         (budget == 0xFFFFFFFFu || (prefix ? pos0 : o) + 16u <= budget);
-      float s[NI];
+      float s[G][NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         float f[VN];
         wave_cvt(B.k[i], f, KVT());
-        float dot = 0.f;
 #pragma unroll
-        for (int e = 0; e < VN; ++e)
-          dot = __builtin_fmaf(q[e], f[e], dot);
-        s[i] = slot_sum<LPR>(dot);
+        for (int g = 0; g < G; ++g) {
+          float dot = 0.f;
+#pragma unroll
+          for (int e = 0; e < VN; ++e)
+            dot = __builtin_fmaf(q[g][e], f[e], dot);
+          s[g][i] = slot_sum<LPR>(dot);
+        }
       }
       if (!full) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           const uint32_t k = i * TPI + ts; // token in the chunk
-          if (!(pos0 + k < n && (prefix ? pos0 + k : o + k) < budget))
-            s[i] = kNegInf;
+          if (!(pos0 + k < n && (prefix ? pos0 + k : o + k) < budget)) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+              s[g][i] = kNegInf;
+          }
         }
       }
-      float mc = s[0];
+      float p[G][NI];
 #pragma unroll
-      for (int i = 1; i < NI; ++i)
-        mc = fmaxf(mc, s[i]);
-      const float mn = fmaxf(st.m, mc);
-      const float cf = __builtin_amdgcn_exp2f(st.m - mn);
-      float p[NI];
-      float lsum = 0.f;
+      for (int g = 0; g < G; ++g) {
+        float mc = s[g][0];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(s[i] - mn);
-        lsum += p[i];
+        for (int i = 1; i < NI; ++i)
+          mc = fmaxf(mc, s[g][i]);
+        const float mn = fmaxf(st[g].m, mc);
+        const float cf = __builtin_amdgcn_exp2f(st[g].m - mn);
+        float lsum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          p[g][i] = __builtin_amdgcn_exp2f(s[g][i] - mn);
+          lsum += p[g][i];
+        }
+        st[g].l = st[g].l * cf + lsum;
+#pragma unroll
+        for (int e = 0; e < VN; ++e)
+          st[g].acc[e] *= cf;
+        st[g].m = mn;
       }
-      st.l = st.l * cf + lsum;
-#pragma unroll
-      for (int e = 0; e < VN; ++e)
-        st.acc[e] *= cf;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         float f[VN];
         wave_cvt(B.v[i], f, KVT());
 #pragma unroll
-        for (int e = 0; e < VN; ++e)
-          st.acc[e] = __builtin_fmaf(p[i], f[e], st.acc[e]);
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < VN; ++e)
+            st[g].acc[e] = __builtin_fmaf(p[g][i], f[e], st[g].acc[e]);
       }
-      st.m = mn;
     };
 
     // Segments of up to 64 pages: load the window, then stream its chunks
@@ -326,12 +425,16 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
     // with fewer chunks re-reads its last one into the spare slots) and a
     // branch-free steady loop, so the compiler's vmcnt waits keep DEPTH-1
     // chunks in flight; the tail computes what is left.
-    const uint32_t npages = (nload + ps - 1u) / ps;
-    for (w0 = 0; w0 < npages; w0 += 64u) {
-      const uint32_t wn = min(npages - w0, 64u);
+    // the appended token is read back from the cache: its stores complete
+    // first
+    if (wrote)
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    const uint32_t pg_end = (c_end + cpp - 1u) / cpp;
+    for (w0 = c_begin / cpp; w0 < pg_end; w0 += 64u) {
+      const uint32_t wn = min(pg_end - w0, 64u);
       win = lane < wn ? P.bt[row + w0 + lane] : 0;
-      const uint32_t c0 = w0 * cpp;
-      const uint32_t c1 = min((w0 + wn) * cpp, nchunks);
+      const uint32_t c0 = max(w0 * cpp, c_begin);
+      const uint32_t c1 = min((w0 + wn) * cpp, c_end);
       const uint32_t cnt = c1 - c0, last = c1 - 1u;
       WaveChunk<KVT, D> buf[DEPTH];
 #pragma unroll
@@ -358,17 +461,27 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
     }
 
     // merge the TPI token slots (lanes LPR, 2 LPR, ... apart)
-    if constexpr (TPI >= 8)
-      merge_partner<8, VN>(st);
-    if constexpr (TPI >= 4)
-      merge_partner<16, VN>(st);
-    if constexpr (TPI >= 2)
-      merge_partner<32, VN>(st);
-    if (ts == 0u) {
-      const int64_t o = ((int64_t)r * P.Hq + h) * D + ds * VN;
 #pragma unroll
-      for (int e = 0; e < VN; ++e)
-        store_out(P, o + e, st.acc[e] / st.l);
+    for (int g = 0; g < G; ++g) {
+      if constexpr (TPI >= 8)
+        merge_partner<8, VN>(st[g]);
+      if constexpr (TPI >= 4)
+        merge_partner<16, VN>(st[g]);
+      if constexpr (TPI >= 2)
+        merge_partner<32, VN>(st[g]);
+    }
+    if (stale) {
+      // the plan does not cover the context: chunk 0's item writes the
+      // task's rows as NaN and counts the task; nothing merges
+      if (I.chunk == 0u) {
+        const int64_t orow = (int64_t)r * P.Hq + (int64_t)h * G;
+        for (uint32_t idx = lane; idx < (uint32_t)(G * D); idx += 64u)
+          store_out(P, orow * D + idx, __builtin_nanf(""));
+        if (lane == 0u)
+          __hip_atomic_fetch_add(P.ws_stale, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      finish_wave_item<G, VN, D>(P, wi, task, I.chunk, R.nchunks, r, h, st, lane, ts, ds);
     }
     unsigned long long *timer = lt_timer(P.L);
     if (lane == 0u && timer != nullptr && task < P.L.max_tasks && !toff) {

@@ -115,22 +115,21 @@ constexpr int mfma_du(bool fp8, bool vt, bool pg, bool f16 = false) {
   SCHED_PD_VALU_ONE(PRE, uint8_t, 64)                                                            \
   SCHED_PD_VALU_ONE(PRE, uint8_t, 128)
 
-// One wave per task (G = 1, softmax, token-major rows).
-#define SCHED_PD_WAVE_ALL(PRE)                                                                   \
-  PRE template __global__ void schedpd::decode_wave<float, 32, SCHED_PD_WAVE_NWT>(               \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<float, 64, SCHED_PD_WAVE_NWT>(               \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<float, 128, SCHED_PD_WAVE_NWT>(              \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<uint16_t, 64, SCHED_PD_WAVE_NWT>(            \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<uint16_t, 128, SCHED_PD_WAVE_NWT>(           \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<_Float16, 64, SCHED_PD_WAVE_NWT>(            \
-      schedpd::KParams);                                                                         \
-  PRE template __global__ void schedpd::decode_wave<_Float16, 128, SCHED_PD_WAVE_NWT>(           \
+// One wave per work item (softmax, token-major rows), G = 1..3 q-heads per
+// kv-head: one group per translation unit.
+#define SCHED_PD_WAVE_ONE(PRE, KVT, D, G)                                                        \
+  PRE template __global__ void schedpd::decode_wave<KVT, D, SCHED_PD_WAVE_NWT, G>(               \
       schedpd::KParams);
+#define SCHED_PD_WAVE_G(PRE, G)                                                                  \
+  SCHED_PD_WAVE_ONE(PRE, float, 32, G)                                                           \
+  SCHED_PD_WAVE_ONE(PRE, float, 64, G)                                                           \
+  SCHED_PD_WAVE_ONE(PRE, float, 128, G)                                                          \
+  SCHED_PD_WAVE_ONE(PRE, uint16_t, 64, G)                                                        \
+  SCHED_PD_WAVE_ONE(PRE, uint16_t, 128, G)                                                       \
+  SCHED_PD_WAVE_ONE(PRE, _Float16, 64, G)                                                        \
+  SCHED_PD_WAVE_ONE(PRE, _Float16, 128, G)
+#define SCHED_PD_WAVE_ALL(PRE) SCHED_PD_WAVE_G(PRE, 1)
+#define SCHED_PD_WAVE_GROUPS(PRE) SCHED_PD_WAVE_G(PRE, 2) SCHED_PD_WAVE_G(PRE, 3)
 
 // Declarations for the launcher (paged_decode.hip).
 #define SCHED_PD_DECLARE_ALL_KERNELS                                                             \
@@ -141,4 +140,5 @@ constexpr int mfma_du(bool fp8, bool vt, bool pg, bool f16 = false) {
   SCHED_PD_MFMA_F16(extern)                                                                      \
   SCHED_PD_MFMA_F16_PAGEBLOCKS(extern)                                                           \
   SCHED_PD_VALU_ALL(extern)                                                                      \
-  SCHED_PD_WAVE_ALL(extern)
+  SCHED_PD_WAVE_ALL(extern)                                                                      \
+  SCHED_PD_WAVE_GROUPS(extern)

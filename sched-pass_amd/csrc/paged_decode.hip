@@ -21,6 +21,13 @@ using namespace schedpd;
 
 namespace {
 
+// Fewest q-heads per kv-head that the MFMA kernel takes when the one-wave
+// kernel also applies. Measured on the 64 x 2048-token bf16 step (Hkv 8,
+// token-major V): one wave per item runs within 1.1% of the MFMA kernel at
+// one q-head per kv-head, 25% slower at two and 52% at three (its VALU work
+// grows with the group; the MFMA kernel's does not).
+constexpr uint32_t kMfmaMinGroup = 2;
+
 typedef void (*KernelFn)(KParams);
 
 struct Selected {
@@ -147,13 +154,13 @@ void ring_depths(const SchedDecodeArgs *a, bool mfma, uint32_t *ds, uint32_t *du
                           a->kv_dtype == SCHED_PD_F16);
 }
 
-// The one-wave-per-task kernel's shape: softmax, one q-head per kv-head, no
-// split tiles, fp32 KV (head dim 32/64/128) or bf16 / fp16 KV (64/128), K and
-// V token-major rows (dims contiguous), 16-byte aligned pools and strides.
+// The one-wave-per-item kernel's shape: softmax, 1..3 q-heads per kv-head,
+// fp32 KV (head dim 32/64/128) or bf16 / fp16 KV (64/128), K and V
+// token-major rows (dims contiguous), 16-byte aligned pools and strides.
 bool wave_applies(const SchedDecodeArgs *a) {
   if (a->flags & (SCHED_PD_FLAG_FORCE_VALU | SCHED_PD_FLAG_NO_WAVE))
     return false;
-  if (a->mode != SCHED_PD_SOFTMAX || a->num_q_heads != a->num_kv_heads || a->tiles)
+  if (a->mode != SCHED_PD_SOFTMAX || a->num_q_heads > 3u * a->num_kv_heads)
     return false;
   const uint32_t d = a->head_dim;
   if (a->kv_dtype == SCHED_PD_F32) {
@@ -175,15 +182,22 @@ bool wave_applies(const SchedDecodeArgs *a) {
   return aligned16(a->k_pool) && aligned16(a->v_pool);
 }
 
-KernelFn wave_kernel(const SchedDecodeArgs *a) {
+template <int G> KernelFn wave_kernel_g(const SchedDecodeArgs *a) {
   constexpr int NWT = SCHED_PD_WAVE_NWT;
   if (a->kv_dtype == SCHED_PD_F32)
-    return a->head_dim == 32   ? decode_wave<float, 32, NWT>
-           : a->head_dim == 64 ? decode_wave<float, 64, NWT>
-                               : decode_wave<float, 128, NWT>;
+    return a->head_dim == 32   ? decode_wave<float, 32, NWT, G>
+           : a->head_dim == 64 ? decode_wave<float, 64, NWT, G>
+                               : decode_wave<float, 128, NWT, G>;
   if (a->kv_dtype == SCHED_PD_BF16)
-    return a->head_dim == 64 ? decode_wave<uint16_t, 64, NWT> : decode_wave<uint16_t, 128, NWT>;
-  return a->head_dim == 64 ? decode_wave<_Float16, 64, NWT> : decode_wave<_Float16, 128, NWT>;
+    return a->head_dim == 64 ? decode_wave<uint16_t, 64, NWT, G>
+                             : decode_wave<uint16_t, 128, NWT, G>;
+  return a->head_dim == 64 ? decode_wave<_Float16, 64, NWT, G>
+                           : decode_wave<_Float16, 128, NWT, G>;
+}
+
+KernelFn wave_kernel(const SchedDecodeArgs *a) {
+  const uint32_t G = a->num_q_heads / a->num_kv_heads;
+  return G == 1 ? wave_kernel_g<1>(a) : G == 2 ? wave_kernel_g<2>(a) : wave_kernel_g<3>(a);
 }
 
 // Validate `a`; on success fill *kp (tables resolved) and *sel.
@@ -229,10 +243,16 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     return set_error(hipErrorInvalidValue, "bt_stride is 0 with a 2-D block table");
 
   const int64_t eb = elem_bytes(a->kv_dtype);
-  // MFMA first: at one q-head per kv-head it still streams bf16 faster than
-  // one wave per task (64 x 2048 x 8 heads: 80 vs 96 us)
-  const bool mfma = mfma_applies(a);
-  const bool wave = !mfma && wave_applies(a);
+  // The one-wave kernel at one q-head per kv-head where its shape applies
+  // (token-major V), unless the launch asks for an urgent prefetch depth
+  // (pf_dist), which only the MFMA kernel's ring serves; the matrix cores for
+  // larger groups, and for a d-major V (the general VALU kernel reads it
+  // 3.7x slower); the one-wave kernel for groups of 2-3 the MFMA kernel does
+  // not take (fp32 KV or Q, head dim 64).
+  const bool mfma_ok = !(a->flags & SCHED_PD_FLAG_NO_MFMA) && mfma_applies(a);
+  const bool wave_ok = wave_applies(a);
+  const bool wave = wave_ok && (!mfma_ok || (G < kMfmaMinGroup && a->pf_dist == 0));
+  const bool mfma = mfma_ok && !wave;
   if (!mfma && !linear) {
     // VALU K rows are read with 16-byte vector loads.
     if (!aligned16(a->k_pool) || (a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 ||
@@ -380,8 +400,8 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
   ring_depths(a, mfma, &ds, &du);
   if (a->pf_dist != 0 && !mfma)
     return set_error(hipErrorInvalidValue,
-                     "pf_dist %u: these arguments select a VALU kernel, which has no prefetch "
-                     "ring (pass 0)", a->pf_dist);
+                     "pf_dist %u: these arguments select a VALU or one-wave kernel, which has "
+                     "no prefetch ring (pass 0)", a->pf_dist);
   if (a->pf_dist != 0 && (a->pf_dist < ds || a->pf_dist > du))
     return set_error(hipErrorInvalidValue,
                      "pf_dist %u: the kernel these arguments select keeps %u..%u pages in flight",
@@ -536,11 +556,11 @@ static int launch_decode(const SchedDecodeArgs *a, const AppendRows *app, void *
   if (rc)
     return rc;
   if (app != nullptr) {
-    if (sel.mfma != 1)
+    if (sel.mfma == 0)
       return set_error(hipErrorInvalidValue,
-                       "fused append: these arguments select the %s kernel; the append is "
-                       "fused into the MFMA kernel only (call sched_kv_append, then "
-                       "sched_paged_decode)", sel.mfma == 2 ? "one-wave-per-task" : "VALU");
+                       "fused append: these arguments select the VALU kernel; the append is "
+                       "fused into the MFMA and one-wave kernels only (call sched_kv_append, "
+                       "then sched_paged_decode)");
     kp.app_k = app->k;
     kp.app_v = app->v;
     kp.app_ts = app->ts;
@@ -667,6 +687,9 @@ int sched_paged_decode_prefetch_range(const SchedDecodeArgs *a, uint32_t *stock,
     return set_error(hipErrorInvalidValue, "args is NULL");
   b = *a;
   b.pf_dist = 0;
+  // the depths of the kernel a launch with a nonzero pf_dist selects (the
+  // one-wave kernel, which has no ring, gives way to the MFMA kernel then)
+  b.flags |= SCHED_PD_FLAG_NO_WAVE;
   int rc = prepare(&b, &kp, &sel);
   if (rc)
     return rc;

@@ -39,6 +39,7 @@ FLAG_FORCE_VALU = 0x4
 FLAG_CTX_IN_PAGES = 0x8
 FLAG_SHED_LOADS = 0x10
 FLAG_NO_WAVE = 0x20
+FLAG_NO_MFMA = 0x40
 TILES_PAIRS, TILES_RANGED = 0, 1
 
 _u32, _f32, _i64, _p = ctypes.c_uint32, ctypes.c_float, ctypes.c_int64, ctypes.c_void_p

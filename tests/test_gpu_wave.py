@@ -1,8 +1,10 @@
-"""The one-wave-per-task kernel (G = 1, token-major rows) against the oracle,
-and its levers bitwise: pi, the ticket queue (W above and below the task
-count), the timer rows, both shed scopes with skip and load + mask, windows
-of 64 pages, page sizes that are not powers of two, the reference fixture's
-[token][K|V] pages, and the general VALU kernel on the same inputs."""
+"""The one-wave-per-item kernel (1..3 q-heads per kv-head, token-major rows)
+against the oracle, and its levers bitwise: pi, the ticket queue (W above and
+below the task count), the timer rows, both shed scopes with skip and load +
+mask, windows of 64 pages, page sizes that are not powers of two, the
+reference fixture's [token][K|V] pages, split-KV work items (pair and graded
+plans, stale plans), and the general VALU and MFMA kernels on the same
+inputs."""
 import numpy as np
 import pytest
 import torch
@@ -173,3 +175,111 @@ def test_wave_static_positions_over_several_rounds():
         assert same(o, out), name
         rows = plane.read_timer()[:n].numpy()
         assert (rows > 0).all(), name
+
+
+def batch_g(kv, d, ps, G, heads=4, ctx=CTX, seed=0, q_dtype=torch.float32):
+    b = workloads.make_batch(np.asarray(ctx), num_q_heads=G * heads, num_kv_heads=heads,
+                             head_dim=d, page_size=ps, kv_dtype=kv, q_dtype=q_dtype, seed=seed,
+                             device="cuda")
+    b["v_pool"] = b["v_pool"].permute(0, 1, 3, 2).contiguous()   # token-major V
+    return b
+
+
+@pytest.mark.parametrize("G", [2, 3])
+@pytest.mark.parametrize("kv,d,qd", [(torch.float32, 32, torch.float32),
+                                     (torch.float32, 128, torch.float32),
+                                     (torch.bfloat16, 128, torch.bfloat16),
+                                     (torch.bfloat16, 64, torch.float32),
+                                     (torch.float16, 128, torch.float16)])
+@pytest.mark.parametrize("ps", [16, 32])
+def test_wave_kernel_groups_parity_and_levers(G, kv, d, qd, ps):
+    """2 and 3 q-heads per kv-head on the one-wave kernel (below the MFMA
+    kernel's 4): the oracle, pi and the queue bitwise, one timer row per
+    task, and the MFMA kernel where it applies within the tolerance."""
+    b = batch_g(kv, d, ps, G, seed=G * d + ps, q_dtype=qd)
+    tol = TOL_F32 if kv == torch.float32 else TOL_BF16
+    nm = abi.FLAG_NO_MFMA          # the MFMA kernel is the default where it applies
+    out, kind = run(b, flags=nm)
+    assert kind == "wave"
+    r = ref(b)
+    assert par_err(out.cpu(), r, f"wave G{G} {kv} d{d} p{ps}") <= tol
+    n = len(CTX) * 4
+    plane = SchedPlane(max_tasks=n)
+    plane.set_order(torch.arange(n - 1, -1, -1, dtype=torch.int32))
+    plane.push()
+    plane.clear_timer()
+    o, _ = run(b, plane=plane, flags=nm)
+    assert same(o, out)
+    assert (plane.read_timer()[:n].numpy() > 0).all()
+    plane.set_num_tasks(n)
+    plane.push()
+    o, _ = run(b, plane=plane, workers=7, flags=nm)
+    assert same(o, out)
+    if kv != torch.float32 and d == 128 and qd == kv:
+        m, k2 = run(b)
+        assert k2 == "mfma"
+        assert par_err(m.cpu(), r) <= tol
+
+
+@pytest.mark.parametrize("G", [1, 3])
+@pytest.mark.parametrize("ranged", [False, True])
+def test_wave_kernel_split_items(G, ranged):
+    """Split-KV work items on the one-wave kernel: a pair plan or a graded
+    ranged plan, static grid, pi (reversed over items) and the ticket queue
+    bitwise equal; the oracle; every task's timer row; counters left zero."""
+    ctx = [1, 15, 300, 2049, 5000, 64, 0, 777]
+    b = batch_g(torch.bfloat16, 128, 16, G, heads=2, ctx=ctx, seed=21 + G, q_dtype=torch.float32)
+    if ranged:
+        tiles = sched_pd.plan_graded_host(ctx, 16, 2, sizes=((0.0, 40), (0.5, 12), (0.9, 4)))
+        kw = dict(tiles=tiles)
+    else:
+        tiles = sched_pd.plan_tiles_host(ctx, 16, 24, 2)
+        kw = dict(tiles=tiles, tile_pages=24)
+    nt = tiles.shape[0]
+    ntask = len(ctx) * 2
+    plane = SchedPlane(max_tasks=max(nt, ntask))
+    plane.clear_timer()
+    out, kind = run(b, plane=plane, **kw)
+    assert kind == "wave"
+    assert par_err(out.cpu(), ref(b), f"split G{G} ranged={ranged}") <= TOL_BF16
+    assert (plane.read_timer()[:ntask].numpy()[np.repeat(np.asarray(ctx), 2) > 0] > 0).all()
+    plane.install_order(torch.arange(nt - 1, -1, -1, dtype=torch.int32), nt)
+    plane.push()
+    o, _ = run(b, plane=plane, **kw)
+    assert same(o, out)
+    plane.set_num_tasks(nt)
+    plane.push()
+    for W in (3, 64, nt + 5):
+        o, _ = run(b, plane=plane, workers=W, **kw)
+        assert same(o, out), W
+    ws = sched_pd.workspace_for(0, "cuda")
+    assert int(ws[sched_pd.WS_COUNTERS_OFF:sched_pd.WS_COUNTERS_OFF + 4 * ntask]
+               .view(torch.int32).abs().sum()) == 0
+
+
+def test_wave_kernel_split_items_stale_plan_and_shed():
+    """A plan built for shorter contexts: the grown tasks' rows NaN and
+    counted, the others right; then prefix budgets over a budget-aware
+    graded plan against the oracle."""
+    old_ctx, new_ctx = [100, 900, 40], [100, 1300, 40]
+    b = batch_g(torch.float32, 64, 16, 2, heads=2, ctx=new_ctx, seed=31)
+    fresh, _ = run(b, tiles=sched_pd.plan_tiles_host(new_ctx, 16, 8, 2), tile_pages=8)
+    assert par_err(fresh.cpu(), ref(b)) <= TOL_F32
+    ws = sched_pd.workspace_for(0, "cuda")        # the one the launches use
+    sched_pd.stale_plan_count(ws, reset=True)
+    tiles = sched_pd.plan_tiles_host(old_ctx, 16, 8, 2)
+    out, kind = run(b, tiles=tiles, tile_pages=8)
+    assert kind == "wave"
+    got = out.cpu().numpy()
+    assert np.isnan(got[1]).all()
+    r = ref(b)
+    assert par_err(got[[0, 2]], np.asarray(r)[[0, 2]]) <= TOL_F32
+    assert sched_pd.stale_plan_count(ws, reset=True) == 2
+    ntask = 6
+    tau = np.array([0, 50, 700, 3, 0, 17])
+    plane = SchedPlane(max_tasks=64)
+    plane.set_rows(tau=tau, n=ntask)
+    plane.push()
+    gtiles = sched_pd.plan_graded_host(new_ctx, 16, 2, sizes=((0.0, 16), (0.7, 4)), tau=tau)
+    o, _ = run(b, plane=plane, tiles=gtiles)
+    assert par_err(o.cpu(), ref(b, plane), "split shed") <= TOL_F32
