@@ -35,6 +35,33 @@ template <typename T> __device__ __forceinline__ T ld_coherent(const T *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Build-time choice of the handoff's ordering (above), for measurement: 0 =
+// relaxed arrival (the default); 1 = a release arrival and, in the item that
+// merges, an acquire fence (the HIP memory model's edge); 2 = the release
+// alone; 3 = the acquire alone.
+#ifndef SCHED_PD_HANDOFF_RELACQ
+#define SCHED_PD_HANDOFF_RELACQ 0
+#endif
+
+// One work item's arrival at its task's counter (one thread); true in the
+// item that completes the task, which resets the counter for the next launch
+// (every other chunk has already arrived).
+__device__ __forceinline__ bool arrive(uint32_t *count, uint32_t nchunks) {
+  constexpr int kMode = SCHED_PD_HANDOFF_RELACQ;
+  const uint32_t old = (kMode == 1 || kMode == 2)
+                           ? __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELEASE,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                           : __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = old == nchunks - 1u;
+  if (last) {
+    __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kMode == 1 || kMode == 3)
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  return last;
+}
+
 // The merge of a task's partials, in the work item that completes it: the
 // partials of chunks 0 .. nchunks-1 (work items base .. base + nchunks - 1)
 // read in chunk order, outputs (orow + g) * D + j for g < G (linear: orow * D
@@ -175,14 +202,8 @@ __device__ __forceinline__ void finish_item(const KParams &P, uint32_t wi, uint3
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   __shared__ uint32_t s_last;
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(P.ws_count + task, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == nchunks - 1u;
-    if (last)
-      __hip_atomic_store(P.ws_count + task, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? 1u : 0u;
-  }
+  if (threadIdx.x == 0)
+    s_last = arrive(P.ws_count + task, nchunks) ? 1u : 0u;
   __syncthreads();
   if (!s_last)
     return;

@@ -249,13 +249,8 @@ __device__ __forceinline__ void finish_wave_item(const KParams &P, uint32_t wi, 
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   uint32_t last = 0u;
-  if (lane == 0u) {
-    const uint32_t old = __hip_atomic_fetch_add(P.ws_count + task, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    last = old == nchunks - 1u ? 1u : 0u;
-    if (last)
-      __hip_atomic_store(P.ws_count + task, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (lane == 0u)
+    last = arrive(P.ws_count + task, nchunks) ? 1u : 0u;
   if (__builtin_amdgcn_readfirstlane(last))
     merge_partials<D, float, false>(P, wi - chunk, nchunks, G, orow, lane, 64u);
 }
