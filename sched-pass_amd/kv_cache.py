@@ -360,6 +360,14 @@ class PagedKvCache:
         self._npg[s] = np.minimum(self._npg[s], keep)
         self._table = None
 
+    def _batch_distinct(self) -> bool:
+        """Whether the last batch _slots() looked up names each request once
+        (checked once per batch)."""
+        key, s = self._batch
+        if getattr(self, "_distinct", (None,))[0] is not s:
+            self._distinct = (s, np.unique(s).size == s.size)
+        return self._distinct[1]
+
     def _slots(self, rids) -> tuple:
         """(rids as a tuple, their slots), cached for a repeated list."""
         key = tuple(rids)
@@ -548,7 +556,7 @@ class PagedKvCache:
         key, s = self._slots(rids)
         if k_new.shape[0] != len(key) or v_new.shape[0] != len(key):
             raise ValueError(f"{k_new.shape[0]} source rows for {len(key)} requests")
-        if np.unique(s).size != s.size:
+        if not self._batch_distinct():
             raise ValueError("a request appears twice in one step")
         held = self._npg[s].copy()
         self.reserve(key, np.ones(len(key), np.int64))

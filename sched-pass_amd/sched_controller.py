@@ -176,6 +176,9 @@ class SchedControlPlane:
         self.requests = RequestTable()
         self.gate = OrderGate(deadband)
         self._gamma = 1.0
+        # advanced by every change of the predictions (observe): a caller
+        # holding a decision made from predict / uncertainty compares it
+        self.version = 0
 
     @property
     def deadband(self) -> float:
@@ -199,6 +202,7 @@ class SchedControlPlane:
             return
         x, y = x[keep], y[keep]
         kept = [r for r, k in zip(rids, keep) if k]
+        self.version += 1
         self.model.add(x, y)
         self.requests.blend(kept, y - np.maximum(self.model.predict(x), 0.0), self.ewma)
 

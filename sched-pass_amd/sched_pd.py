@@ -632,15 +632,47 @@ def plan_graded_host(ctx_lens, page_size: int, num_kv_heads: int, task_order=Non
     return np.stack([t_of, chunk | (nch[t_of] << 16), p0, p1], 1).astype(np.int32)
 
 
+class _PlanFacts:
+    """What the host checks established about the last few host plans,
+    keyed by content. A serving loop launches one plan for many steps (a
+    request's chunk count changes every tile_pages * page_size tokens), so
+    a plan is validated once and its per-task reach computed once; a lookup
+    compares the array with the remembered copies (a few microseconds)."""
+    MAX = 4
+
+    def __init__(self):
+        self.items = []          # [(array copy, facts dict)], most recent first
+        self.lock = threading.Lock()
+
+    def get(self, t: np.ndarray) -> dict:
+        with self.lock:
+            for i, (a, f) in enumerate(self.items):
+                if a.shape == t.shape and a.dtype == t.dtype and np.array_equal(a, t):
+                    if i:
+                        self.items.insert(0, self.items.pop(i))
+                    return f
+            f = {}
+            self.items.insert(0, (t.copy(), f))
+            del self.items[self.MAX:]
+            return f
+
+
+_FACTS = _PlanFacts()
+
+
 def check_ranged_plan(tiles) -> None:
     """Raise ValueError unless `tiles` ([n, 4] ranged rows) is task-major:
     each task's chunks consecutive, numbered 0..nchunks-1 with one nchunks,
     their page ranges contiguous from page 0. (Coverage of the context is
     the launch's check: a task whose context passes its last range is
     stale.)"""
-    t = np.asarray(tiles, dtype=np.int64)
-    if t.ndim != 2 or t.shape[1] != 4 or t.shape[0] == 0:
+    raw = np.asarray(tiles)
+    if raw.ndim != 2 or raw.shape[1] != 4 or raw.shape[0] == 0:
         raise ValueError("ranged tiles must be a non-empty [num_tiles, 4] array")
+    facts = _FACTS.get(raw)
+    if facts.get("task_major"):
+        return
+    t = raw.astype(np.int64)
     task, chunk, nch = t[:, 0], t[:, 1] & 0xFFFF, t[:, 1] >> 16
     p0, p1 = t[:, 2], t[:, 3]
     first = chunk == 0
@@ -656,6 +688,7 @@ def check_ranged_plan(tiles) -> None:
         raise ValueError(f"ranged tiles row {i} {t[i].tolist()} is not task-major with "
                          "contiguous ranges from page 0")
     _check_one_group_per_task(task[first], "ranged")
+    facts["task_major"] = True
 
 
 def _check_one_group_per_task(first_tasks, what: str) -> None:
@@ -674,23 +707,29 @@ def check_plan_covers(tiles, ctx_lens, page_size: int, num_kv_heads: int,
     contexts `ctx_lens` (tokens): the check the kernels make per task (a
     task it fails is stale: NaN output rows), made on the host before a
     launch that must not run stale, such as a fused append."""
-    t = np.asarray(tiles, dtype=np.int64)
+    raw = np.asarray(tiles)
     ctx = np.asarray(ctx_lens.cpu() if isinstance(ctx_lens, torch.Tensor) else ctx_lens,
                      dtype=np.int64)
     npg = np.repeat((ctx + page_size - 1) // page_size, num_kv_heads)
     ntask = npg.size
-    if t.shape[1] == 4:
-        last = (t[:, 1] & 0xFFFF) == (t[:, 1] >> 16) - 1
-        reach = np.full(ntask, -1, np.int64)
-        lt = t[last]
-        ok = (lt[:, 0] >= 0) & (lt[:, 0] < ntask)
-        np.maximum.at(reach, lt[ok, 0], lt[ok, 3])
-    else:
-        if tile_pages <= 0:
-            raise ValueError("pair rows need tile_pages > 0")
-        ok = (t[:, 0] >= 0) & (t[:, 0] < ntask)
-        nch = np.bincount(t[ok, 0], minlength=ntask)[:ntask]
-        reach = np.where(nch > 0, nch * tile_pages, -1)
+    if raw.shape[1] != 4 and tile_pages <= 0:
+        raise ValueError("pair rows need tile_pages > 0")
+    facts = _FACTS.get(raw)
+    key = ("reach", ntask, 0 if raw.shape[1] == 4 else int(tile_pages))
+    reach = facts.get(key)
+    if reach is None:
+        t = raw.astype(np.int64)
+        if t.shape[1] == 4:
+            last = (t[:, 1] & 0xFFFF) == (t[:, 1] >> 16) - 1
+            reach = np.full(ntask, -1, np.int64)
+            lt = t[last]
+            ok = (lt[:, 0] >= 0) & (lt[:, 0] < ntask)
+            np.maximum.at(reach, lt[ok, 0], lt[ok, 3])
+        else:
+            ok = (t[:, 0] >= 0) & (t[:, 0] < ntask)
+            nch = np.bincount(t[ok, 0], minlength=ntask)[:ntask]
+            reach = np.where(nch > 0, nch * tile_pages, -1)
+        facts[key] = reach
     short = reach < npg
     if short.any():
         k = int(np.argmax(short))
@@ -702,9 +741,13 @@ def check_pair_plan(tiles) -> None:
     """Raise ValueError unless `tiles` ([n, 2] (task, chunk) rows) is
     task-major: each task's chunks consecutive and numbered from 0, each
     task in one group of rows. (Coverage is the launch's check.)"""
-    t = np.asarray(tiles, dtype=np.int64)
-    if t.ndim != 2 or t.shape[1] != 2 or t.shape[0] == 0:
+    raw = np.asarray(tiles)
+    if raw.ndim != 2 or raw.shape[1] != 2 or raw.shape[0] == 0:
         raise ValueError("pair tiles must be a non-empty [num_tiles, 2] array")
+    facts = _FACTS.get(raw)
+    if facts.get("task_major"):
+        return
+    t = raw.astype(np.int64)
     task, chunk = t[:, 0], t[:, 1]
     first = chunk == 0
     start = np.maximum.accumulate(np.where(first, np.arange(len(t)), 0))
@@ -714,6 +757,7 @@ def check_pair_plan(tiles) -> None:
         i = int(np.flatnonzero(~ok)[0])
         raise ValueError(f"pair tiles row {i} {t[i].tolist()} is not task-major")
     _check_one_group_per_task(task[first], "pair")
+    facts["task_major"] = True
 
 
 def desc_order(cost) -> np.ndarray:

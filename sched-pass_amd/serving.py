@@ -33,7 +33,14 @@ Per step, as in the reference:
     * push; clear the timer on probe steps.
   on_batch_end()
     * record the step's completion event; on a probe step keep (event,
-      binding) pending and switch the timer off for the following steps.
+      binding) pending and switch the timer off for the following steps;
+    * enforcing, host work for the next step while this one is queued on the
+      device: advance the probe readout, and when the next step will
+      re-plan, compute its decision (cost, regime, plan, order) for the
+      batch a decode step predicts (the same requests, one token longer).
+      on_batch_begin installs it if the batch and the controller's version
+      match, else decides afresh: the same tables either way, but the heavy
+      host work no longer sits between a step's start and its launch.
 Observing only, a step without a probe launches without the lever tables,
 and the plane's timer flag stays on, so the hooks publish the plane once
 and then only when the batch's task count or order changes.
@@ -108,6 +115,8 @@ class ServingHooks:
             # probe rows read back on a side stream: the readout waits for the
             # probe step only, not for the kernels queued after it
             plane.use_device_timer()
+        self.last_batch = None   # (rids, kv_lens) of the last step, enforcing
+        self.ahead = None        # a re-plan computed after the last launch
         self.probes_folded = 0
         self.hook_errors = 0
         self._err_sites = set()
@@ -159,11 +168,12 @@ class ServingHooks:
         self.pending = None
         rids, kv_list = b[0], b[1]
         n = len(rids)
-        cyc = (rows if rows is not None else torch.as_tensor(self.plane.read_timer())).to(torch.int64)
-        m = min(n * self.hkv, cyc.numel())
-        per_req = torch.zeros(n, dtype=torch.int64).scatter_add_(
-            0, torch.arange(m) // self.hkv, cyc[:m])
-        self.ctl.observe(rids, kv_list, per_req.tolist())
+        cyc = (rows if rows is not None else torch.as_tensor(self.plane.read_timer()))
+        cyc = cyc.to(torch.int64).numpy()
+        m = min(n * self.hkv, cyc.size)
+        per_task = np.zeros(n * self.hkv, np.int64)   # task = request * hkv + head
+        per_task[:m] = cyc[:m]
+        self.ctl.observe(rids, kv_list, per_task.reshape(n, self.hkv).sum(1).tolist())
         self.probes_folded += 1
 
     # -- the hooks ---------------------------------------------------------------
@@ -174,6 +184,8 @@ class ServingHooks:
         cfg, p = self.cfg, self.plane
         step = self.step
         self.step += 1
+        if not cfg.observe_only:
+            self.last_batch = (tuple(rids), np.array(kv_lens, np.int64))
         self._consume_probe()
         probe = step % cfg.timer_every == 0 and self.pending is None
         live = self.armed_n if self.launch["workers"] else self.order_n
@@ -209,47 +221,10 @@ class ServingHooks:
         workers = 0
         plan = None          # (tiles, cost per item) of the plan the launch takes
         if not cfg.observe_only:
-            # predicted cost per request, spread over its work items by pages
-            # (observing needs no prediction)
-            cost_req = self.ctl.predict(rids, kv_list)
-            req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
-
-            def costed(tile_pages):
-                tiles, item_req, item_pages = self._items(kv_list, tile_pages)
-                return tiles, torch.as_tensor(
-                    cost_req[item_req] * item_pages / req_pages[item_req], dtype=torch.float32)
-
-            R = cfg.resident
-            arm = cfg.clc == "on"
-            if cfg.clc == "auto" and R > 0 and nitems > R and \
-                    self.ctl.uncertainty(rids, kv_list) > cfg.clc_resid:
-                plan = costed(tp)
-                cost_item = plan[1]
-                imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6))
-                arm = imbalance > cfg.clc_imbalance
-            if arm:
-                plan = plan or costed(tp)
-                p.install_order(SchedPlane.region_order(plan[1], R), nitems)
-                self.order_n = nitems
-                p.set_num_tasks(nitems)
-                self.armed_n = nitems
-                workers = R if R > 0 else 2 * p.sm_count()
-                self.plan_tp = tp
-            elif R > 0 and nitems <= R:
-                self._retire_order()
-                p.set_num_tasks(0)
-                self.plan_tp = tp
-            else:
-                # the LPT order, over its own (larger) tiles when configured
-                self.plan_tp = (cfg.lpt_tile_pages or tp) if tp > 0 else 0
-                if plan is None or self.plan_tp != tp:
-                    plan = costed(self.plan_tp)
-                nitems = plan[1].numel()
-                p.install_order(SchedPlane.region_order(plan[1], 0, block=cfg.lpt_block),
-                                nitems)
-                self.order_n = nitems
-                p.set_num_tasks(0)
-            self._hints(kv_list, cost_req)
+            d = self._take_ahead(rids, kv_lens)
+            if d is None:
+                d = self._decide(rids, kv_list, nitems)
+            workers, plan, nitems = self._apply(d, kv_list)
         else:
             self._retire_order()
             p.set_num_tasks(0)
@@ -266,6 +241,109 @@ class ServingHooks:
                        "tile_pages": self.plan_tp if tiles is not None else 0}
         return self._observed(self.launch)
 
+    def _decide(self, rids, kv_list, nitems) -> dict:
+        """The enforcing re-plan for a batch, without writing any table:
+        predicted cost per request spread over the work items by pages, the
+        regime, the plan the launch takes and its order. `nitems` counts the
+        items over the configured tiles."""
+        cfg, p = self.cfg, self.plane
+        tp = cfg.tile_pages
+        cost_req = self.ctl.predict(rids, kv_list)
+        req_pages = np.maximum(-(-np.asarray(kv_list, np.int64) // cfg.page_size), 1)
+
+        def costed(tile_pages):
+            tiles, item_req, item_pages = self._items(kv_list, tile_pages)
+            return tiles, torch.as_tensor(
+                cost_req[item_req] * item_pages / req_pages[item_req], dtype=torch.float32)
+
+        R = cfg.resident
+        arm = cfg.clc == "on"
+        plan = None
+        if cfg.clc == "auto" and R > 0 and nitems > R and \
+                self.ctl.uncertainty(rids, kv_list) > cfg.clc_resid:
+            plan = costed(tp)
+            cost_item = plan[1]
+            imbalance = float(cost_item.max() / max(float(cost_item.mean()), 1e-6))
+            arm = imbalance > cfg.clc_imbalance
+        d = {"cost_req": cost_req, "nitems": nitems}
+        if arm:
+            plan = plan or costed(tp)
+            d.update(regime="queue", plan=plan, plan_tp=tp,
+                     order=SchedPlane.region_order(plan[1], R),
+                     workers=R if R > 0 else 2 * p.sm_count())
+        elif R > 0 and nitems <= R:
+            d.update(regime="one_wave", plan=None, plan_tp=tp)
+        else:
+            # the LPT order, over its own (larger) tiles when configured
+            plan_tp = (cfg.lpt_tile_pages or tp) if tp > 0 else 0
+            if plan is None or plan_tp != tp:
+                plan = costed(plan_tp)
+            d.update(regime="lpt", plan=plan, plan_tp=plan_tp, nitems=plan[1].numel(),
+                     order=SchedPlane.region_order(plan[1], 0, block=cfg.lpt_block))
+        return d
+
+    def _apply(self, d: dict, kv_list) -> tuple:
+        """Install a _decide() result in the plane (tables, item count, hints);
+        returns (workers, plan, work items)."""
+        p = self.plane
+        nitems = d["nitems"]
+        workers = 0
+        if d["regime"] == "queue":
+            p.install_order(d["order"], nitems)
+            self.order_n = nitems
+            p.set_num_tasks(nitems)
+            self.armed_n = nitems
+            workers = d["workers"]
+        elif d["regime"] == "one_wave":
+            self._retire_order()
+            p.set_num_tasks(0)
+        else:
+            p.install_order(d["order"], nitems)
+            self.order_n = nitems
+            p.set_num_tasks(0)
+        self.plan_tp = d["plan_tp"]
+        self._hints(kv_list, d["cost_req"])
+        return workers, d["plan"], nitems
+
+    def _plan_ahead(self) -> None:
+        """Enforcing, after a step's launch: if the next step will re-plan (by
+        cadence, or because its item count changes), compute its decision now
+        for the batch a decode step predicts (the same requests, each one
+        token longer), while the device still has this step queued; the
+        next on_batch_begin uses it only if the batch and the controller's
+        state (its version, which every fold of measurements advances) are
+        those it was computed for."""
+        self.ahead = None
+        last = self.last_batch
+        if self.cfg.observe_only or last is None:
+            return
+        rids, kv = last
+        kv_next = kv + 1
+        nxt = self.step
+        live = self.armed_n if self.launch["workers"] else self.order_n
+        due = nxt % self.cfg.plan_every == 0 or nxt % self.cfg.timer_every == 0
+        if not due and (live is None or live == self._count(kv_next, self.plan_tp)):
+            return
+        kv_list = kv_next.tolist()
+        nitems = self._count(kv_list, self.cfg.tile_pages)
+        if max(nitems, len(rids) * self.hkv) > self.plane.N:
+            return       # on_batch_begin raises for this batch
+        d = self._decide(list(rids), kv_list, nitems)
+        self.ahead = (nxt, rids, kv_next, self.ctl.version, d)
+
+    def _take_ahead(self, rids, kv_lens):
+        """The decision _plan_ahead computed for this step, if it was computed
+        for this batch and no probe was folded since; else None."""
+        a, self.ahead = self.ahead, None
+        if a is None or a[0] != self.step - 1 or a[3] != self.ctl.version:
+            return None
+        if tuple(rids) != a[1]:
+            return None
+        kv = np.asarray(kv_lens, np.int64)
+        if kv.shape != a[2].shape or not np.array_equal(kv, a[2]):
+            return None
+        return a[4]
+
     def _observed(self, launch: dict) -> dict:
         """Observing, a step without a probe has nothing to measure and no
         schedule to change: it launches without the lever tables (the same
@@ -281,12 +359,16 @@ class ServingHooks:
         ev = self._event()
         ev.record()
         self.inflight = ev
+        # host work while this step is queued on the device: an earlier
+        # probe's readout first (this step's probe, if any, is pending next)
+        self._consume_probe()
         if self.timer_armed:
             self.pending = (ev, self.binding, None)
             if not self.cfg.observe_only:
                 # enforcing, the next steps launch with the plane: timer off
                 self.plane.set_timer_enabled(False)
                 self.plane.push()
+        self._plan_ahead()
 
     # -- engine-facing wrappers: a hook never takes the serving loop down --------
     STOCK = {"plane": None, "workers": 0, "tiles": None, "tile_pages": 0}

@@ -292,3 +292,101 @@ def test_observing_publishes_the_plane_once():
     assert gens == [gens[0]] * len(gens)
     assert sum(bound) >= 2 and h.probes_folded >= 1
     assert ctrl_u32(p, abi.CTRL_FLAGS_OFF) & abi.FLAG_TIMER_OFF == 0
+
+
+def _run_steps(h, p, rids, kv0, steps, timer_fill=None):
+    """Decode-style steps (each request one token longer per step); returns
+    per step the launch and the plane's published bytes."""
+    got = []
+    kv = np.asarray(kv0, np.int64)
+    for i in range(steps):
+        launch = h.on_batch_begin(rids, kv + i)
+        if timer_fill is not None and h.timer_armed:
+            n = len(rids)
+            p._timer_view()[:n] = torch.as_tensor(timer_fill(kv + i))
+        h.on_batch_end()
+        got.append((launch["workers"], launch["tile_pages"],
+                    None if launch["tiles"] is None else launch["tiles"].tolist(),
+                    bytes(p._ctrl_dev.numpy()[:4096]), p._order_view()[:4096].tolist()))
+    return got
+
+
+def _hooks(cfg, fresh):
+    p = plane(4096)
+    h = ServingHooks(p, 1, cfg, event_factory=Ev)
+    if fresh:
+        h._plan_ahead = lambda: None          # every re-plan decided at begin
+    return p, h
+
+
+def test_plan_ahead_installs_the_tables_a_fresh_re_plan_would():
+    rng = np.random.default_rng(11)
+    rids = list(range(48))
+    kv0 = rng.integers(16, 3000, 48)
+    fill = lambda kv: (kv * 7 + 1000).tolist()        # noqa: E731  measured cost per request
+    for cfg in (HookConfig(plan_every=4, timer_every=4, resident=16, tile_pages=8,
+                           lpt_tile_pages=12),
+                HookConfig(plan_every=4, timer_every=8, resident=16, clc="on", tile_pages=8),
+                HookConfig(plan_every=3, timer_every=5, resident=512, tile_pages=8)):
+        runs = []
+        for fresh in (False, True):
+            p, h = _hooks(cfg, fresh)
+            where = []                        # "begin" / "end" per decision made
+            decide, begin = h._decide, h.on_batch_begin
+            inside = [False]
+
+            def spy(*a, _d=decide, _w=where, _i=inside):
+                _w.append("begin" if _i[0] else "end")
+                return _d(*a)
+
+            def begin_spy(*a, _b=begin, _i=inside):
+                _i[0] = True
+                try:
+                    return _b(*a)
+                finally:
+                    _i[0] = False
+            h._decide, h.on_batch_begin = spy, begin_spy
+            runs.append((_run_steps(h, p, rids, kv0, 17, fill), where))
+        (ahead, where_ahead), (fresh, where_fresh) = runs
+        assert ahead == fresh, cfg
+        assert where_fresh.count("begin") > 1 and "end" not in where_fresh
+        # ahead: re-plans decided at the previous step's end, except the
+        # first step and those whose decision a probe's fold (a new fit)
+        # made stale
+        assert where_ahead[0] == "begin" and where_ahead.count("end") > 1, where_ahead
+        assert where_ahead.count("begin") < where_fresh.count("begin"), where_ahead
+
+
+def test_plan_ahead_is_dropped_when_the_batch_or_the_fit_differs():
+    cfg = HookConfig(plan_every=2, timer_every=100, resident=4, clc="off", tile_pages=4)
+    p, h = _hooks(cfg, False)
+    rids, kv = [0, 1, 2, 3, 4, 5], np.array([100, 900, 300, 64, 2000, 40])
+    h.on_batch_begin(rids, kv)
+    h.on_batch_end()
+    h.on_batch_begin(rids, kv + 1)            # off cadence
+    h.on_batch_end()
+    assert h.ahead is not None                # the next step re-plans
+    # a batch that is not the predicted one (a request grew by two tokens)
+    other = kv + 2
+    other[1] += 60
+    launch = h.on_batch_begin(rids, other)
+    p2, h2 = _hooks(cfg, True)
+    h2.on_batch_begin(rids, kv)
+    h2.on_batch_end()
+    h2.on_batch_begin(rids, kv + 1)
+    h2.on_batch_end()
+    want = h2.on_batch_begin(rids, other)
+    assert launch["tiles"].tolist() == want["tiles"].tolist()
+    assert order(p, h.order_n) == order(p2, h2.order_n)
+    h.on_batch_end()
+    h.on_batch_begin(rids, other + 1)
+    h.on_batch_end()
+    assert h.ahead is not None
+    ver = h.ctl.version
+    h.ctl.observe(rids, (other + 2).tolist(), [5000, 1, 1, 1, 1, 1])  # the fit moved
+    assert h.ctl.version == ver + 1
+    seen = []
+    decide = h._decide
+    h._decide = lambda *a: seen.append(1) or decide(*a)
+    h.on_batch_begin(rids, other + 2)
+    assert seen == [1]                        # decided afresh at begin
