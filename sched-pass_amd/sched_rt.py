@@ -83,8 +83,9 @@ class SchedPlane:
 
     def __init__(self, max_tasks: int = 4096, device: str = "cuda"):
         if max_tasks > MAX_TASKS_LIMIT:
-            raise ValueError(f"max_tasks {max_tasks} > {MAX_TASKS_LIMIT} "
-                             f"(the arena's per-table window)")
+            raise ValueError(f"a plane holds at most {MAX_TASKS_LIMIT} rows per table "
+                             f"(asked for {max_tasks}): each table sits in a 256 KiB "
+                             "slot of the arena")
         self.N = int(max_tasks)
         self.dev = torch.device(device)
         try:
