@@ -507,3 +507,42 @@ def test_fused_append_refusals_without_the_gpu(schedlib):
     a.kv_dtype = w.kv_dtype = abi.BF16
     a.v_tok_stride, a.v_dim_stride = 1, 16                  # d-major V
     assert refused("token-major V")
+
+
+def test_plan_checks_remember_plans_by_content_only():
+    """The host checks keep what they established about recent plans keyed
+    by the plan's bytes: a plan changed in place after a passing check, or
+    an equal-looking plan of another dtype or shape, is checked again."""
+    import numpy as np
+    import sched_pd
+    ctx = [100, 40, 300]
+    pairs = sched_pd.plan_tiles_host(ctx, 16, 4, 2)
+    sched_pd.check_pair_plan(pairs)
+    sched_pd.check_pair_plan(pairs)                       # remembered
+    sched_pd.check_plan_covers(pairs, ctx, 16, 2, tile_pages=4)
+    pairs[1, 1] = 5                                       # the same array, now malformed
+    with pytest.raises(ValueError):
+        sched_pd.check_pair_plan(pairs)
+    pairs[1, 1] = 1
+    sched_pd.check_pair_plan(pairs)
+    with pytest.raises(ValueError):                       # coverage: a longer context
+        sched_pd.check_plan_covers(pairs, [100, 40, 400], 16, 2, tile_pages=4)
+    with pytest.raises(ValueError):                       # the same rows at another tile size
+        sched_pd.check_plan_covers(pairs, ctx, 16, 2, tile_pages=2)
+    ranged = sched_pd.plan_ranges_host(ctx, 16, 2, tile_pages=3, tail_frac=0.0)
+    sched_pd.check_ranged_plan(ranged)
+    sched_pd.check_plan_covers(ranged, ctx, 16, 2)
+    bad = ranged.copy()
+    bad[[1, 2]] = bad[[2, 1]]
+    with pytest.raises(ValueError):
+        sched_pd.check_ranged_plan(bad)
+    ranged[0, 3] = 1                                      # in place: a gap after row 0
+    with pytest.raises(ValueError):
+        sched_pd.check_ranged_plan(ranged)
+    # more distinct plans than remembered: each still checked correctly
+    for n in range(1, 12):
+        p = sched_pd.plan_tiles_host([16 * n, 40], 16, 2, 1)
+        sched_pd.check_pair_plan(p)
+        sched_pd.check_plan_covers(p, [16 * n, 40], 16, 1, tile_pages=2)
+        with pytest.raises(ValueError):
+            sched_pd.check_plan_covers(p, [16 * n + 33, 40], 16, 1, tile_pages=2)
