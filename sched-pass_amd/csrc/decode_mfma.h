@@ -622,7 +622,13 @@ __device__ __forceinline__ void append_token_fp8(const KParams &P, uint32_t r, u
   const int64_t src = (int64_t)r * P.app_ts + (int64_t)h * P.app_hs + j;
   const int64_t si = (page * P.Hkv + h) * P.scale_stride;
   float *scl[2] = {const_cast<float *>(P.k_scale) + si, const_cast<float *>(P.v_scale) + si};
-  const float s_old[2] = {*scl[0], *scl[1]};
+  // the page's old scales matter only past its first slot (a token in slot
+  // 0 starts the page afresh): not read otherwise
+  float s_old[2] = {0.f, 0.f};
+  if (slot > 0u) {
+    s_old[0] = *scl[0];
+    s_old[1] = *scl[1];
+  }
   float x[2][2]; // [K, V][dim]
   for (int t = 0; t < 2; ++t) {
     const void *base = t ? P.app_v : P.app_k;
