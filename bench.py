@@ -1011,7 +1011,13 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
             else:
                 plane.install_order(order, nseq)
             plane.push()
+            plane.clear_timer()
             t = [step_ms(armed) for _ in range(steps)]
+            if nseq == batch_sizes[-1]:
+                # per-request residency of this policy's steps (timer rows,
+                # averaged over the steps): the tail the order has to hide
+                rows_ = plane.read_timer()[:nseq].cpu().numpy() / steps
+                row.setdefault("residency_cycles", {})[name] = _residency(rows_, is_long)
             o = out.clone()
             if golden is None:
                 golden = o
@@ -1056,7 +1062,11 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
                 p_items.push()
             for _ in range(3):
                 sched_pd.launch(a_items, stream)
+            p_items.clear_timer()
             t = [step_ms(lambda: sched_pd.launch(a_items, stream)) for _ in range(steps)]
+            if nseq == batch_sizes[-1]:
+                rows_ = p_items.read_timer()[:nseq].cpu().numpy() / steps
+                split.setdefault("residency_cycles", {})[name] = _residency(rows_, is_long)
             split[name] = {"mean_us": round(1e3 * float(np.mean(t)), 2),
                            "min_us": round(1e3 * min(t), 2)}
             exact = exact and bool(torch.equal(out, o_split))
@@ -1090,6 +1100,21 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         del kv, pages, q, out, plane, stock, armed, by_args, launcher, a_split, a_items, p_items
         torch.cuda.empty_cache()
     return res
+
+
+def _residency(rows, is_long):
+    """Percentiles of per-request residency (timer rows: the cycles a
+    request's work items were resident, summed over its items) for the
+    short and the long requests of the trace eval."""
+    import numpy as np
+    rows = np.asarray(rows, np.float64)
+    lng = np.asarray(is_long, bool)
+    out = {}
+    for label, sel in (("short", ~lng), ("long", lng)):
+        x = rows[sel]
+        out[label] = {"p50": int(np.percentile(x, 50)), "p90": int(np.percentile(x, 90)),
+                      "max": int(x.max())}
+    return out
 
 
 def _lcg_uniform(n, seed):
