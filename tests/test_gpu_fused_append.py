@@ -317,3 +317,43 @@ def test_fused_step_under_a_shed_budget(dtype):
         assert same(o_fused, o_sep), step
         if dtype == FP8:
             assert same(fa.k_scale, sep.k_scale) and same(fa.v_scale, sep.v_scale), step
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
+@pytest.mark.parametrize("G", [1, 4])
+def test_fused_step_opens_an_empty_requests_first_page(dtype, G):
+    """Requests that hold no token yet (added, nothing appended) take their
+    first token in a fused step beside requests that hold many: the same
+    pools, scales and outputs as the writer followed by the decode."""
+    lens = [0, 40, 0, 17, 300]
+    R = len(lens)
+    g = torch.Generator(device="cuda").manual_seed(29)
+    npages = int(sum(-(-(n + 4) // 16) for n in lens)) + R + 4
+    caches = [PagedKvCache(npages, HKV, D, 16, dtype=dtype) for _ in range(2)]
+    T = int(sum(lens))
+    src = torch.float32 if dtype == FP8 else dtype
+    k = (torch.randn(T, HKV, D, device="cuda", generator=g) / D ** 0.5).to(src)
+    v = (torch.randn(T, HKV, D, device="cuda", generator=g) / D ** 0.5).to(src)
+    for c in caches:
+        for r in range(R):
+            c.add_request(r)
+        c.append(list(range(R)), k, v, list(lens))
+    fa, sep = caches
+    rids = list(range(R))
+    q = (torch.randn(R, HKV * G, D, device="cuda", generator=g) / D ** 0.5).to(qdtype(dtype))
+    for step in range(3):
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(qdtype(dtype))
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(qdtype(dtype))
+        o_f = fa.decode_step(q, rids, k1, v1, out_dtype=torch.float32)
+        sep.append(rids, k1, v1)
+        o_s = sep.decode(q, rids, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert same(o_f, o_s), step
+        assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
+        if dtype == FP8:
+            assert same(fa.k_scale, sep.k_scale) and same(fa.v_scale, sep.v_scale), step
+    assert [fa.lens[r] for r in rids] == [n + 3 for n in lens]
+    bt, ctx = fa.block_table(rids)
+    ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor",
+                        k_scale=fa.k_scale, v_scale=fa.v_scale)
+    assert par_err(o_f.cpu(), ref, f"empty requests {dtype} G{G}") <= TOL_BF16
