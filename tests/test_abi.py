@@ -546,3 +546,44 @@ def test_plan_checks_remember_plans_by_content_only():
         sched_pd.check_plan_covers(p, [16 * n, 40], 16, 1, tile_pages=2)
         with pytest.raises(ValueError):
             sched_pd.check_plan_covers(p, [16 * n + 33, 40], 16, 1, tile_pages=2)
+
+
+def test_graded_plan_rows_by_position_in_the_claim_order():
+    """plan_graded_host against rows derived by hand: 10 + 2 + 20 pages on
+    the claim line (32 pages), sizes 8 before the line's middle and 3 after;
+    a task crossing the middle is cut there."""
+    import numpy as np
+    import sched_pd
+    ctx = [160, 32, 320]                        # 10, 2, 20 pages of 16 tokens
+    got = sched_pd.plan_graded_host(ctx, 16, 1, sizes=((0.0, 8), (0.5, 3)))
+    want = [[0, 0 | 2 << 16, 0, 8], [0, 1 | 2 << 16, 8, 10],
+            [1, 0 | 1 << 16, 0, 2],
+            [2, 0 | 7 << 16, 0, 4], [2, 1 | 7 << 16, 4, 7], [2, 2 | 7 << 16, 7, 10],
+            [2, 3 | 7 << 16, 10, 13], [2, 4 | 7 << 16, 13, 16], [2, 5 | 7 << 16, 16, 19],
+            [2, 6 | 7 << 16, 19, 20]]
+    assert got.tolist() == want
+    sched_pd.check_ranged_plan(got)
+    sched_pd.check_plan_covers(got, ctx, 16, 1)
+    # claimed in reverse: task 2 first (its 20 pages: 16 of them before the
+    # middle), then task 1 and task 0 after it
+    rev = sched_pd.plan_graded_host(ctx, 16, 1, task_order=[2, 1, 0], sizes=((0.0, 8), (0.5, 3)))
+    by_task = {t: rev[rev[:, 0] == t][:, 2:].tolist() for t in range(3)}
+    assert by_task[2] == [[0, 8], [8, 16], [16, 19], [19, 20]]
+    assert by_task[1] == [[0, 2]]
+    assert by_task[0] == [[0, 3], [3, 6], [6, 9], [9, 10]]
+    # budgets: task 2 reads 5 pages (70 tokens); only those are lined up,
+    # and its last range runs on to the context's last page
+    tau = sched_pd.plan_graded_host(ctx, 16, 1, sizes=((0.0, 8), (0.5, 3)),
+                                    tau=np.array([0, 0, 70]))
+    assert tau[tau[:, 0] == 2][:, 2:].tolist() == [[0, 3], [3, 20]]
+    sched_pd.check_plan_covers(tau, ctx, 16, 1)
+    # an empty task keeps one empty chunk; heads repeat each request
+    empty = sched_pd.plan_graded_host([0, 40], 16, 2, sizes=((0.0, 2),))
+    assert empty.tolist() == [[0, 1 << 16, 0, 0], [1, 1 << 16, 0, 0],
+                              [2, 0 | 2 << 16, 0, 2], [2, 1 | 2 << 16, 2, 3],
+                              [3, 0 | 2 << 16, 0, 2], [3, 1 | 2 << 16, 2, 3]]
+    for bad in (((0.1, 8),), ((0.0, 8), (0.0, 4)), ((0.0, 0),), ((0.0, 8), (1.0, 2))):
+        with pytest.raises(ValueError):
+            sched_pd.plan_graded_host(ctx, 16, 1, sizes=bad)
+    with pytest.raises(ValueError):
+        sched_pd.plan_graded_host(ctx, 16, 1, task_order=[0, 0, 1])
