@@ -20,7 +20,6 @@ from __future__ import annotations
 import collections
 import ctypes
 import functools
-import math
 import threading
 
 import numpy as np

@@ -4,7 +4,6 @@ host-side argument validation / kernel selection behave (no device calls)."""
 import ctypes
 import os
 import re
-import struct
 import subprocess
 
 import pytest

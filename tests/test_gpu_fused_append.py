@@ -13,7 +13,6 @@ import pytest
 import torch
 
 import oracle
-import sched_abi as abi
 import sched_pd
 from kv_cache import PagedKvCache, build_append_args, paired_scales
 from parity import TOL_BF16, par_err

@@ -10,7 +10,6 @@ import torch
 
 import kv_cache
 import oracle
-import sched_pd
 from parity import TOL_BF16, par_err
 from sched_rt import SchedPlane
 from serving import HookConfig, ServingHooks
