@@ -929,7 +929,8 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         return e0.elapsed_time(e1)
 
     res = {"regime_lpt_timer_vs_identity_pct": {}, "regime_split_lpt_timer_vs_identity_pct": {},
-           "regime_split_identity_vs_identity_pct": {}, "split_pages": SPLIT_PAGES}
+           "regime_split_identity_vs_identity_pct": {}, "split_pages": SPLIT_PAGES,
+           "step_us": {}}
     for nseq in batch_sizes:
         gen = torch.Generator().manual_seed(0)
         is_long = torch.rand(nseq, generator=gen) < 0.1
@@ -1028,6 +1029,8 @@ def bench_trace_eval(torch, sched_pd, batch_sizes=(256, 2048, 8192), steps=30):
         base = row["identity"]["mean_us"]
         gain = round(100 * (row["lpt_timer"]["mean_us"] - base) / base, 2)
         res["regime_lpt_timer_vs_identity_pct"][str(nseq)] = gain
+        res["step_us"][str(nseq)] = {"identity": row["identity"]["mean_us"],
+                                     "lpt_timer": row["lpt_timer"]["mean_us"]}
         # the same step over split work items (a pair plan of SPLIT_PAGES
         # pages, static grid; one wave per item), through the argument block:
         # stock (no lever tables), and pi (identity, LPT over the items by

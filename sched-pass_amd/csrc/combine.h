@@ -19,7 +19,12 @@
 // invalidates the XCD's L2 once per work item. Measured with that one change
 // on a queue launch over 128-page tiles (256 requests of the Llama-3-8B shape,
 // lognormal contexts, median 1024): 378 -> 478 us; on the fp8 Qwen2-7B queue
-// launch: 356 -> 431 us. The
+// launch: 356 -> 431 us. The other way the memory model allows without L2
+// maintenance -- every published value in a 64-bit word with a "published"
+// tag that the merging item validates word by word and then clears, so that
+// no ordering between words is needed -- was built and measured on the same
+// batch's queue launch over the graded plan: 366 -> 404 us (8-byte words
+// +9 us, the per-word checks +12 us, the clears +17 us). The
 // arrival counter is reset to 0 by the work item that completes the task:
 // every other chunk has already arrived.
 #pragma once
