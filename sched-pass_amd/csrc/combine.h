@@ -73,8 +73,7 @@ __device__ __forceinline__ bool arrive(uint32_t *count, uint32_t nchunks) {
 // + j). Threads tid, tid + nthreads, ... take the G * D outputs. The loads go
 // out kMergeBatch chunks at a time (chunk indices past the last are clamped
 // to it and their terms dropped by a select), so a task of N chunks costs
-// about 2N / kMergeBatch memory round trips instead of 2N; the arithmetic
-// and its order are those of a plain loop over c = 0 .. N-1.
+// about N / kMergeBatch memory round trips; the sums run in chunk order.
 template <int D, typename AccT, bool LINEAR>
 __device__ __forceinline__ void merge_partials(const KParams &P, uint32_t base, uint32_t nchunks,
                                                uint32_t G, int64_t orow, uint32_t tid,
@@ -102,18 +101,11 @@ __device__ __forceinline__ void merge_partials(const KParams &P, uint32_t base, 
       const AccT *acc = static_cast<const AccT *>(P.ws_acc) + (size_t)base * G * D + g * D + j;
       const size_t stride_ml = G; // u64 words per chunk
       const size_t stride_acc = (size_t)G * D;
-      float M = __uint_as_float((uint32_t)ld_coherent(ml));
-      for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
-        uint64_t w[kMergeBatch];
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          w[k] = ld_coherent(ml + min(c0 + k, clast) * stride_ml);
-        // a clamped repeat of the last chunk leaves the max unchanged
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; ++k)
-          M = fmaxf(M, __uint_as_float((uint32_t)w[k]));
-      }
-      float Lt = 0.f, A = 0.f;
+      // one pass: each batch's (m, l) and accumulators load together; the
+      // running max moves per batch and rescales the sums (for up to
+      // kMergeBatch chunks the arithmetic is that of a max pass followed by
+      // a sum pass)
+      float M = 0.f, Lt = 0.f, A = 0.f;
       for (uint32_t c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
         uint64_t w[kMergeBatch];
         AccT v[kMergeBatch];
@@ -122,6 +114,19 @@ __device__ __forceinline__ void merge_partials(const KParams &P, uint32_t base, 
           const size_t c = min(c0 + k, clast);
           w[k] = ld_coherent(ml + c * stride_ml);
           v[k] = ld_coherent(acc + c * stride_acc);
+        }
+        // a clamped repeat of the last chunk leaves the max unchanged
+        float Mb = __uint_as_float((uint32_t)w[0]);
+#pragma unroll
+        for (uint32_t k = 1; k < kMergeBatch; ++k)
+          Mb = fmaxf(Mb, __uint_as_float((uint32_t)w[k]));
+        if (c0 == 0u) {
+          M = Mb;
+        } else if (Mb > M) {
+          const float cf = __builtin_amdgcn_exp2f(M - Mb);
+          Lt *= cf;
+          A *= cf;
+          M = Mb;
         }
 #pragma unroll
         for (uint32_t k = 0; k < kMergeBatch; ++k) {
