@@ -48,8 +48,9 @@
 // [DEPTH_S, DEPTH_U], DEPTH_U by default (deeper KV prefetch). Polite tasks
 // always stream with non-temporal loads (the reference's "do not keep this
 // task's lines"). Stock tasks do too (KV is read once per step), except work
-// items longer than kLongItemPages, which take the deep ring with ordinary
-// loads; so polite and stock differ only on those long items.
+// items longer than kLongItemPages and a queue worker's last item, which take
+// the deep ring with ordinary loads; so polite and stock differ only on
+// those items.
 // fp8: values convert exactly to bf16; the per-(page, head) K scale multiplies
 // the score and the V scale multiplies p before PV, so no element is scaled.
 #pragma once
@@ -97,6 +98,15 @@ constexpr bool kStockNT = SCHED_PD_MFMA_STOCK_NT != 0;
 #define SCHED_PD_MFMA_LONG_ITEM_PAGES 256u
 #endif
 constexpr uint32_t kLongItemPages = SCHED_PD_MFMA_LONG_ITEM_PAGES;
+// A queue worker's last item streams in the launch's run-down, with fewer
+// and fewer items beside it, so a deep ring of ordinary loads serves it
+// better too (measured with 128-page tiles under urgency order: C3 queue
+// 377 -> 363 us; the fp8 Qwen2-7B queue over 256-page tiles 355 -> 343 us;
+// the graded plans, whose last items are small, -1.5% to 0).
+#ifndef SCHED_PD_MFMA_LATE_DEEP
+#define SCHED_PD_MFMA_LATE_DEEP 1
+#endif
+constexpr bool kLateDeep = SCHED_PD_MFMA_LATE_DEEP != 0;
 
 template <bool NT, typename T> __device__ __forceinline__ T gload(const T *p) {
   if constexpr (NT)
@@ -701,7 +711,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
   const bool toff = timer_off_latched(P.L);
   constexpr uint32_t EB = FP8 ? 1u : 2u; // bytes per KV element
 
-  run_tasks(P.L, [&](uint32_t wi) __attribute__((always_inline)) {
+  run_tasks(P.L, [&](uint32_t wi, bool last_round) __attribute__((always_inline)) {
     if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);
@@ -822,7 +832,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma(KParams P) {
     // first (issued before the Q loads above, so their latency overlaps)
     if (wrote)
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    if (T.p1 - T.p0 > kLongItemPages && !pol.polite)
+    if ((T.p1 - T.p0 > kLongItemPages || (kLateDeep && last_round)) && !pol.polite)
       stream_pages<FP8, NW, DEPTH_U, false, LINEAR, VT, PG, F16>(P, T, S, lane, g4);
     else if (pol.urgent)
       stream_urgent<FP8, NW, DEPTH_S, DEPTH_U, kStockNT, LINEAR, VT, PG, F16>(P, T, S, lane, g4);

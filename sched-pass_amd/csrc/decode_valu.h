@@ -110,7 +110,7 @@ __global__ void __launch_bounds__(SCHED_PD_VALU_NW * 64) decode_valu(KParams P) 
   const uint32_t i16 = lane & 15u, slot = lane >> 4;
   const bool toff = timer_off_latched(P.L);
 
-  run_tasks(P.L, [&](uint32_t wi) __attribute__((always_inline)) {
+  run_tasks(P.L, [&](uint32_t wi, bool) __attribute__((always_inline)) {
     if (wi >= P.L.nitems)
       return;
     const unsigned long long t0 = read_clock(P.L.wallclock);

@@ -161,6 +161,8 @@ __device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uin
 // Static launch (wq == 0): one task per workgroup, task = remap_static(ctaid)
 // with the launch's item count as the grid bound (the host launches one
 // workgroup per item).
+// The body gets the item and whether it is a queue worker's last (the
+// launch's run-down).
 // Work-queue launch (wq == 1, grid = W workers):
 //   stock path if queue or ctrl is NULL, the grid is not 1-D, or num_tasks==0;
 //   otherwise raw = ctaid (exit if >= num_tasks), then loop: body(remap(raw)),
@@ -172,6 +174,13 @@ __device__ __forceinline__ void timer_commit(const LeverTables &L, bool off, uin
 // The worker that takes the launch's last ticket (W + num_tasks - 1) stores W
 // back into the counter: every other worker has already made its last claim,
 // so the next launch with the same W needs no host-side reset.
+// Claim rounds at the end of a queue launch whose items the body is told
+// are late (the MFMA kernel streams them with its deep ring): measured on
+// the heterogeneous, shed and fp8 queue launches, 1 is best (2 and 3 slow
+// the fp8 and shed launches by 2-6%).
+#ifndef SCHED_PD_LATE_ROUNDS
+#define SCHED_PD_LATE_ROUNDS 1u
+#endif
 template <class Body>
 __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
   const uint32_t pid = blockIdx.x;
@@ -198,8 +207,14 @@ __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
       return;
     // the item is the same on every lane: keep it (and the addresses derived
     // from it) in scalar registers
+    // a queue worker's last item (fewer tickets left than workers, on a
+    // launch of more items than workers): the launch's run-down, where the
+    // item streams with fewer and fewer others beside it
+    const bool last_round =
+        queue && ntasks > gridDim.x && raw + SCHED_PD_LATE_ROUNDS * gridDim.x >= ntasks;
     body(__builtin_amdgcn_readfirstlane(queue ? remap_wq(L, raw, ntasks)
-                                              : remap_static(L, raw, L.nitems)));
+                                              : remap_static(L, raw, L.nitems)),
+         last_round);
     if (!queue) {
       raw += gridDim.x;
       if (raw < L.nitems)
