@@ -208,10 +208,11 @@ __device__ __forceinline__ void run_tasks(const LeverTables &L, Body &&body) {
     // the item is the same on every lane: keep it (and the addresses derived
     // from it) in scalar registers
     // a queue worker's last item (fewer tickets left than workers, on a
-    // launch of more items than workers): the launch's run-down, where the
-    // item streams with fewer and fewer others beside it
-    const bool last_round =
-        queue && ntasks > gridDim.x && raw + SCHED_PD_LATE_ROUNDS * gridDim.x >= ntasks;
+    // launch of at least twice as many items as workers, so that most items
+    // stream in full rounds): the launch's run-down, where the item streams
+    // with fewer and fewer others beside it
+    const bool last_round = queue && ntasks >= 2u * gridDim.x &&
+                            raw + SCHED_PD_LATE_ROUNDS * gridDim.x >= ntasks;
     body(__builtin_amdgcn_readfirstlane(queue ? remap_wq(L, raw, ntasks)
                                               : remap_static(L, raw, L.nitems)),
          last_round);
