@@ -99,10 +99,13 @@ constexpr bool kStockNT = SCHED_PD_MFMA_STOCK_NT != 0;
 #endif
 constexpr uint32_t kLongItemPages = SCHED_PD_MFMA_LONG_ITEM_PAGES;
 // A queue worker's last item streams in the launch's run-down, with fewer
-// and fewer items beside it, so a deep ring of ordinary loads serves it
-// better too (measured with 128-page tiles under urgency order: C3 queue
-// 377 -> 363 us; the fp8 Qwen2-7B queue over 256-page tiles 355 -> 343 us;
-// the graded plans, whose last items are small, -1.5% to 0).
+// and fewer items beside it, where ordinary loads serve it better than
+// non-temporal ones (measured with 128-page tiles under urgency order: C3
+// queue 377 -> 363 us; the fp8 Qwen2-7B queue over 256-page tiles 355 ->
+// 343 us; the graded plans, whose last items are small, -1.5% to 0). The
+// loads are what matters: the same items on the deep ring with
+// non-temporal loads run as before, on the stock ring with ordinary loads
+// as here. They take the long-item path (deep ring, ordinary loads).
 #ifndef SCHED_PD_MFMA_LATE_DEEP
 #define SCHED_PD_MFMA_LATE_DEEP 1
 #endif
