@@ -53,6 +53,11 @@ struct KParams {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kMInit = -1e30f; // running-max start value (test/paged_decode.cu:94)
+// Buffer resource word 3 for raw buffer loads (GFX9: data format 32, so that
+// a raw load is not treated as an invalid format), and the load's cache
+// policy bits: 2 = nt (streamed, as __builtin_nontemporal_load).
+constexpr int kBufWord3 = 0x00020000;
+constexpr int kBufNT = 2;
 
 __device__ __forceinline__ int32_t page_of(const KParams &P, uint32_t r, uint32_t b) {
   return P.indptr ? P.bt[P.indptr[r] + b] : P.bt[(int64_t)r * P.bt_stride + b];

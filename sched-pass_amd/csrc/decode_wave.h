@@ -354,9 +354,6 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
     };
     auto compute = [&](uint32_t c, const WaveChunk<KVT, D> &B) __attribute__((always_inline)) {
       const uint32_t pos0 = c * 16u, o = (c % cpp) * 16u; // o: chunk offset in its page
-      // a chunk wholly inside the context and the budget needs no mask
-      const bool full = pos0 + 16u <= n &&
-                        (budget == 0xFFFFFFFFu || (prefix ? pos0 : o) + 16u <= budget);
       float s[G][NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -371,16 +368,18 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
           s[g][i] = slot_sum<LPR>(dot);
         }
       }
-      if (!full) {
+      // the mask is a select per token, with no test for a chunk that needs
+      // none (an unshed budget is 0xFFFFFFFF): a branch here splits the
+      // steady loop's body into blocks, the compiler then moves the softmax
+      // and PV of every chunk below the reloads, and the ring's old V
+      // registers are copied at the back edge after waiting for their loads
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const uint32_t k = i * TPI + ts; // token in the chunk
-          if (!(pos0 + k < n && (prefix ? pos0 + k : o + k) < budget)) {
+      for (int i = 0; i < NI; ++i) {
+        const uint32_t k = i * TPI + ts; // token in the chunk
+        const bool keep = (pos0 + k < n) & ((prefix ? pos0 + k : o + k) < budget);
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-              s[g][i] = kNegInf;
-          }
-        }
+        for (int g = 0; g < G; ++g)
+          s[g][i] = keep ? s[g][i] : kNegInf;
       }
       float p[G][NI];
 #pragma unroll
@@ -415,11 +414,34 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
       }
     };
 
+    // The prologue's and the tail's loads: buffer loads over the chunk's own
+    // rows, with an empty range for a chunk past the segment, whose loads
+    // then return 0 and read nothing (the buffer range check). Every path
+    // issues the same loads, with no branch and no re-read: a conditional
+    // load makes the compiler's vmcnt waits drain the ring. Offsets are 32
+    // bits (a chunk's 16 rows span less than 2 GiB; the launcher checks).
+    const uint32_t kstep32 = (uint32_t)kstep, vstep32 = (uint32_t)vstep;
+    auto issue_or_skip = [&](uint32_t c, bool live, uint32_t cfirst,
+                             WaveChunk<KVT, D> &B) __attribute__((always_inline)) {
+      const uint32_t cc = live ? c : cfirst; // a chunk of the window, for the page id
+      const uint32_t b = cc / cpp, o = (cc % cpp) * 16u;
+      const int64_t page = __builtin_amdgcn_readlane(win, (int)(b - w0));
+      const int nrec = live ? 0x7FFFFFFF : 0;
+      const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(kb + page * kps + (int64_t)o * krow), (short)0, nrec, kBufWord3);
+      const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t *>(vb + page * vps + (int64_t)o * vrow), (short)0, nrec, kBufWord3);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        B.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, klane + i * kstep32, 0, kBufNT);
+        B.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vlane + i * vstep32, 0, kBufNT);
+      }
+    };
+
     // Segments of up to 64 pages: load the window, then stream its chunks
-    // through a ring of DEPTH chunks -- an unconditional prologue (a segment
-    // with fewer chunks re-reads its last one into the spare slots) and a
-    // branch-free steady loop, so the compiler's vmcnt waits keep DEPTH-1
-    // chunks in flight; the tail computes what is left.
+    // through a ring of DEPTH chunks -- a prologue, a branch-free steady
+    // loop, so the compiler's vmcnt waits keep DEPTH-1 chunks in flight, and
+    // a tail of fewer than 2 DEPTH chunks with the same waits.
     // the appended token is read back from the cache: its stores complete
     // first
     if (wrote)
@@ -430,29 +452,39 @@ __global__ void __launch_bounds__(NWT * 64) decode_wave(KParams P) {
       win = lane < wn ? P.bt[row + w0 + lane] : 0;
       const uint32_t c0 = max(w0 * cpp, c_begin);
       const uint32_t c1 = min((w0 + wn) * cpp, c_end);
-      const uint32_t cnt = c1 - c0, last = c1 - 1u;
+      const uint32_t cnt = c1 - c0;
       WaveChunk<KVT, D> buf[DEPTH];
 #pragma unroll
       for (int sl = 0; sl < DEPTH; ++sl)
-        issue(min(c0 + sl, last), buf[sl]);
+        issue_or_skip(c0 + sl, sl < cnt, c0, buf[sl]);
       uint32_t j = 0;
       for (; j + 2u * DEPTH <= cnt; j += DEPTH) {
 #pragma unroll
         for (int sl = 0; sl < DEPTH; ++sl) {
           compute(c0 + j + sl, buf[sl]);
+          // the slot's reload after its last use, so that it takes the same
+          // registers (a hoisted load needs others and a copy on the back edge)
+          __builtin_amdgcn_sched_barrier(0);
           issue(c0 + j + DEPTH + sl, buf[sl]);
         }
       }
-      for (; j < cnt; j += DEPTH) {
+      // tail: a round that computes DEPTH chunks and issues the rest (empty
+      // ranges past the segment) when more than DEPTH are left, then a round
+      // that computes what is left; either way the last DEPTH chunks' loads
+      // are outstanding in slot order at the join
+      if (j + DEPTH < cnt) {
 #pragma unroll
         for (int sl = 0; sl < DEPTH; ++sl) {
-          if (j + sl < cnt) {
-            compute(c0 + j + sl, buf[sl]);
-            if (j + DEPTH + sl < cnt)
-              issue(c0 + j + DEPTH + sl, buf[sl]);
-          }
+          compute(c0 + j + sl, buf[sl]);
+          __builtin_amdgcn_sched_barrier(0);
+          issue_or_skip(c0 + j + DEPTH + sl, j + DEPTH + sl < cnt, c0, buf[sl]);
         }
+        j += DEPTH;
       }
+#pragma unroll
+      for (int sl = 0; sl < DEPTH; ++sl)
+        if (j + sl < cnt)
+          compute(c0 + j + sl, buf[sl]);
     }
 
     // merge the TPI token slots (lanes LPR, 2 LPR, ... apart)

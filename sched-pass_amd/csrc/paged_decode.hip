@@ -5,6 +5,7 @@
 // kernels_*.hip (kernel_set.h lists them).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -178,6 +179,10 @@ bool wave_applies(const SchedDecodeArgs *a) {
   if ((a->k_tok_stride * eb) % 16 || (a->k_page_stride * eb) % 16 || (a->k_head_stride * eb) % 16)
     return false;
   if ((a->v_tok_stride * eb) % 16 || (a->v_page_stride * eb) % 16 || (a->v_head_stride * eb) % 16)
+    return false;
+  // a lane's offset into a 16-token chunk is 32 bits (buffer loads)
+  const int64_t span = 16 * std::max(a->k_tok_stride, a->v_tok_stride) * eb + d * eb;
+  if (a->k_tok_stride < 0 || a->v_tok_stride < 0 || span > INT32_MAX)
     return false;
   return aligned16(a->k_pool) && aligned16(a->v_pool);
 }
