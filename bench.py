@@ -761,8 +761,8 @@ def bench_layouts(torch, sched_pd, workloads, tables=4):
     res["serving_step_page16"] = st
     # The kernel by q-heads per kv-head (same KV bytes: Hkv 8, bf16 Q): over
     # token-major V the MFMA kernel against the one-wave kernel (the default
-    # below 4 q-heads per kv-head); over d-major V the MFMA kernel against the
-    # general VALU kernel
+    # for the shapes the MFMA kernel does not take); over d-major V the MFMA
+    # kernel against the general VALU kernel
     grp = {}
     for G in (1, 2, 3, 4):
         qg = (torch.randn(R, 8 * G, d, device="cuda", generator=g) / d ** 0.5).bfloat16()

@@ -24,10 +24,13 @@ namespace {
 
 // Fewest q-heads per kv-head that the MFMA kernel takes when the one-wave
 // kernel also applies. Measured on the 64 x 2048-token bf16 step (Hkv 8,
-// token-major V): one wave per item runs within 1.1% of the MFMA kernel at
-// one q-head per kv-head, 25% slower at two and 52% at three (its VALU work
-// grows with the group; the MFMA kernel's does not).
-constexpr uint32_t kMfmaMinGroup = 2;
+// token-major V): one wave per item runs 4.0-4.6% behind the MFMA kernel at
+// one q-head per kv-head (2.7-3.2% with a 24 KB ring), 25% at two and 55%
+// at three (its VALU work grows with the group; the MFMA kernel's does not),
+// so the MFMA kernel takes every group it applies to and the one-wave kernel
+// the shapes it does not (fp32 KV or Q, head dim 32 / 64, pages that are not
+// a power of two).
+constexpr uint32_t kMfmaMinGroup = 1;
 
 typedef void (*KernelFn)(KParams);
 
@@ -248,12 +251,12 @@ int prepare(const SchedDecodeArgs *a, KParams *kp, Selected *sel) {
     return set_error(hipErrorInvalidValue, "bt_stride is 0 with a 2-D block table");
 
   const int64_t eb = elem_bytes(a->kv_dtype);
-  // The one-wave kernel at one q-head per kv-head where its shape applies
-  // (token-major V), unless the launch asks for an urgent prefetch depth
-  // (pf_dist), which only the MFMA kernel's ring serves; the matrix cores for
-  // larger groups, and for a d-major V (the general VALU kernel reads it
-  // 3.7x slower); the one-wave kernel for groups of 2-3 the MFMA kernel does
-  // not take (fp32 KV or Q, head dim 64).
+  // The matrix cores wherever the MFMA kernel applies (a d-major V included:
+  // the general VALU kernel reads it 3.7x slower); the one-wave kernel for
+  // groups of 1-3 over token-major rows that the MFMA kernel does not take
+  // (fp32 KV or Q, head dim 32 / 64); below kMfmaMinGroup the one-wave
+  // kernel first unless the launch asks for an urgent prefetch depth
+  // (pf_dist), which only the MFMA kernel's ring serves.
   const bool mfma_ok = !(a->flags & SCHED_PD_FLAG_NO_MFMA) && mfma_applies(a);
   const bool wave_ok = wave_applies(a);
   const bool wave = wave_ok && (!mfma_ok || (G < kMfmaMinGroup && a->pf_dist == 0));

@@ -130,10 +130,12 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.BF16)) == 0
     assert kind(schedlib, fake_args(page_size=32, v_dim_stride=32, **f16)) == 1   # fp16, 32-token pages
     assert kind(schedlib, fake_args(kv_dtype=abi.F16, q_dtype=abi.FP8_E4M3)) == -1
-    # 1..3 q-heads per kv-head over token-major rows: one wave per work item
+    # 1..3 q-heads per kv-head over token-major rows: the MFMA kernel where it
+    # applies, else one wave per work item
     mha = dict(num_q_heads=8, num_kv_heads=8, v_tok_stride=128, v_dim_stride=1)
-    assert kind(schedlib, fake_args(**mha)) == 2                             # bf16 d 128
-    assert kind(schedlib, fake_args(**mha, flags=abi.FLAG_NO_WAVE)) == 1     # -> MFMA
+    assert kind(schedlib, fake_args(**mha)) == 1                             # bf16 d 128: MFMA
+    assert kind(schedlib, fake_args(**mha, flags=abi.FLAG_NO_MFMA)) == 2     # -> one wave
+    assert kind(schedlib, fake_args(**mha, flags=abi.FLAG_NO_WAVE)) == 1
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=16))) == 1       # G = 2: MFMA
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=24))) == 1       # G = 3: MFMA
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=24), q_dtype=abi.F32)) == 2
@@ -156,7 +158,8 @@ def test_kernel_selection(schedlib):
                                     lin_w=ctypes.c_void_p(0x80000))) == 1     # linear: not wave
     assert kind(schedlib, fake_args(**mha, tiles=ctypes.c_void_p(0x90000), num_tiles=8,
                                     tile_pages=4, workspace=ctypes.c_void_p(0xA0000),
-                                    workspace_bytes=1 << 20)) == 2            # split plans too
+                                    workspace_bytes=1 << 20,
+                                    flags=abi.FLAG_NO_MFMA)) == 2            # split plans too
     assert kind(schedlib, fake_args(num_q_heads=16, num_kv_heads=8)) == 1  # d-major V: MFMA
 
 

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle
+import sched_abi as abi
 import sched_pd
 from kv_cache import PagedKvCache, build_append_args, paired_scales
 from parity import TOL_BF16, par_err
@@ -88,6 +89,35 @@ def test_fused_step_equals_append_then_decode(dtype, ps, G, src32):
     ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor",
                         k_scale=fa.k_scale, v_scale=fa.v_scale)
     assert par_err(o_fused.float().cpu(), ref, f"fused {dtype} p{ps} G{G}") <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ps", [16, 64])
+def test_fused_step_on_the_one_wave_kernel(dtype, ps):
+    """One q-head per kv-head with the MFMA kernel kept out, so the one-wave
+    kernel streams the step and writes the token: pools and outputs bitwise
+    equal to append-then-decode on the same kernel."""
+    lens = [1, 15, 16, 17, 31, 47, 63, 64, 65, 100, 127, 200]
+    (fa, sep), g = make_pair(dtype, ps, lens, seed=ps + 7)
+    R = len(lens)
+    rids = list(range(R))
+    q = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(qdtype(dtype))
+    for step in range(4):
+        k1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(dtype)
+        v1 = (torch.randn(R, HKV, D, device="cuda", generator=g) / D ** 0.5).to(dtype)
+        o_fused = fa.decode_step(q, rids, k1, v1, out_dtype=torch.float32,
+                                 flags=abi.FLAG_NO_MFMA)
+        sep.append(rids, k1, v1)
+        o_sep = sep.decode(q, rids, out_dtype=torch.float32, flags=abi.FLAG_NO_MFMA)
+        torch.cuda.synchronize()
+        assert same(o_fused, o_sep), step
+        assert same(fa.k_pool, sep.k_pool) and same(fa.v_pool, sep.v_pool), step
+    bt, ctx = fa.block_table(rids)
+    assert sched_pd.kernel_kind(sched_pd.build_args(
+        q, fa.k_pool, fa.v_pool, bt, ctx, out=torch.empty_like(o_fused), v_layout="tokmajor",
+        flags=abi.FLAG_NO_MFMA)) == "wave"
+    ref = oracle.decode(q, fa.k_pool, fa.v_pool, bt, ctx, v_layout="tokmajor")
+    assert par_err(o_fused.float().cpu(), ref, f"fused wave {dtype} p{ps}") <= TOL_BF16
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, FP8])
