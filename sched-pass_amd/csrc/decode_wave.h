@@ -1,7 +1,9 @@
-// decode_wave.h -- one wave per task for one q-head per kv-head (G = 1): the
-// shape of the reference's JIT kernel (python/kernels/paged_softmax.cu:14-45,
-// fp32, head dim 32, [token][K|V] pages) and of MHA caches with token-major
-// rows, fp32 / bf16 / fp16 KV, head dim 32 (fp32) / 64 / 128, softmax mode.
+// decode_wave.h -- one wave per work item for 1-3 q-heads per kv-head (G):
+// the shape of the reference's JIT kernel (python/kernels/paged_softmax.cu:
+// 14-45, fp32, head dim 32, [token][K|V] pages) and of caches with
+// token-major rows that the MFMA kernel does not take (fp32 KV or Q, head
+// dim 32 / 64, pages that are not a power of two); fp32 / bf16 / fp16 KV,
+// head dim 32 (fp32) / 64 / 128, softmax mode.
 //
 // With G = 1 a task is one (request, head) stream of K and V rows and little
 // arithmetic, so what bounds it is how many bytes are in flight and how long
