@@ -140,6 +140,12 @@ def test_kernel_selection(schedlib):
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=24))) == 1       # G = 3: MFMA
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=24), q_dtype=abi.F32)) == 2
     assert kind(schedlib, fake_args(**dict(mha, num_q_heads=32))) == 1       # G = 4: MFMA
+    # the one-wave kernel's lane offsets into a 16-token chunk are 32 bits:
+    # a chunk's rows spanning 2 GiB or more go to the general kernel
+    d64 = dict(mha, head_dim=64)
+    assert kind(schedlib, fake_args(**dict(d64, k_tok_stride=1 << 25, v_tok_stride=1 << 25))) == 2
+    assert kind(schedlib, fake_args(**dict(d64, k_tok_stride=1 << 26, v_tok_stride=128))) == 0
+    assert kind(schedlib, fake_args(**dict(d64, k_tok_stride=128, v_tok_stride=1 << 26))) == 0
     assert kind(schedlib, fake_args(**mha, pf_dist=3)) == 1                  # a prefetch depth
     assert kind(schedlib, fake_args(v_tok_stride=128, v_dim_stride=1,
                                     flags=abi.FLAG_NO_MFMA)) == 0            # G = 4, no MFMA
